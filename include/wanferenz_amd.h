@@ -1,0 +1,153 @@
+/* wanferenz_amd — C ABI of the MI355X (gfx950) MoE + FP8-linear hot path.
+ *
+ * One shared library, libwanferenz_amd.so, replaces the kernel layer the
+ * reference model calls (wanferenz/kernels/reference.py, its CPU twin
+ * wanferenz/kernels/torch_ops.py, and the MoE dispatch patches in
+ * wanferenz/kernels/{fp4_grouped,fp8_vector,expert_dispatch,expert_batch}.py).
+ *
+ * Conventions
+ *   - Every entry point returns 0 on success and a negative code on error;
+ *     wz_last_error() returns a thread-local message for the last failure.
+ *   - All tensor arguments are device pointers to dense row-major storage.
+ *   - Work is enqueued on the given stream.  No entry point allocates device
+ *     memory, synchronises the host or reads device data back, so every call
+ *     can be captured in a HIP graph.  Scratch memory comes in as `ws`.
+ *   - Formats: bf16 activations/outputs; e4m3fn FP8 (OCP); e2m1 MXFP4 packed
+ *     two per byte, low nibble = even element; e8m0 scales (2^(b-127)).
+ */
+#ifndef WANFERENZ_AMD_H
+#define WANFERENZ_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error codes. */
+#define WZ_OK 0
+#define WZ_EINVAL (-1)   /* bad shape / argument */
+#define WZ_ELAUNCH (-2)  /* HIP launch failure */
+#define WZ_ESPACE (-3)   /* workspace too small */
+
+/* Activation scale kinds (act_quant's scale_fmt / scale_dtype pair,
+ * wanferenz/kernels/torch_ops.py:33-49, partition.py:128-134). */
+#define WZ_SCALE_F32 0        /* s = amax/448, stored float32 (scale_fmt=None)       */
+#define WZ_SCALE_UE8M0 1      /* s = 2^ceil(log2(amax/448)), stored as e8m0 bytes    */
+#define WZ_SCALE_UE8M0_F32 2  /* same power-of-two s, stored as float32              */
+
+/* Weight block-scale storage for FP8 weights (128x128 blocks). */
+#define WZ_WSCALE_F32 0
+#define WZ_WSCALE_E8M0 1
+
+/* Gate score functions (ModelArgs.score_func, architecture.py:57). */
+#define WZ_SCORE_SOFTMAX 0
+#define WZ_SCORE_SIGMOID 1
+#define WZ_SCORE_SQRTSOFTPLUS 2
+
+const char* wz_last_error(void);
+
+/* Library / device properties. */
+int wz_device_info(int* cu_count, int* xcd_count);
+
+/* act_quant: per-row, per-128-column dynamic FP8 quantisation.
+ * Replaces act_quant(x, block_size=128, scale_fmt, scale_dtype) —
+ * wanferenz/kernels/reference.py:117-146 (TileLang) / torch_ops.py:33-49 (CPU).
+ * x_bf16 [M, K] -> q_e4m3 [M, K], s [M, K/128] (float32 or e8m0 per scale_kind). */
+int wz_act_quant_fp8(const void* x_bf16, int64_t M, int64_t K, void* q_e4m3, void* s,
+                     int scale_kind, hipStream_t stream);
+
+/* fp8_gemm: C[M,N] bf16 = (a * a_s) @ (w * w_s)^T, K-blocks of 128.
+ * Replaces fp8_gemm(a, a_s, b, b_s, scale_dtype) — reference.py:292-311 / torch_ops.py:93-99,
+ * and the decode retile _fp8_gemm_fast — fp8_vector.py:289-297.
+ * a_e4m3 [M,K], a_s [M,K/128] (act_scale_kind), w_e4m3 [N,K],
+ * w_s [ceil(N/128), ceil(K/128)] (w_scale_kind). */
+int wz_fp8_gemm(const void* a_e4m3, const void* a_s, const void* w_e4m3, const void* w_s,
+                void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
+                int w_scale_kind, hipStream_t stream);
+
+/* fp8 linear with act_quant fused into the GEMM prologue: y = linear(x, w) for an
+ * FP8 weight — architecture.py:121-132 (act_quant + fp8_gemm). */
+int wz_fp8_linear(const void* x_bf16, const void* w_e4m3, const void* w_s, void* y_bf16,
+                  int64_t M, int64_t N, int64_t K, int act_scale_kind, int w_scale_kind,
+                  hipStream_t stream);
+
+/* fp4_gemm: C[M,N] bf16 = (a * a_s) @ (e2m1(w) * w_s)^T, weight scale e8m0 per 32 K.
+ * Replaces fp4_gemm(a, a_s, b, b_s, scale_dtype) — reference.py:572-591 / torch_ops.py:102-108.
+ * a_e4m3 [M,K], a_s [M,K/128], w_fp4x2 [N,K/2], w_s_e8m0 [N,K/32]. */
+int wz_fp4_gemm(const void* a_e4m3, const void* a_s, const void* w_fp4x2, const void* w_s_e8m0,
+                void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
+                hipStream_t stream);
+
+/* One MoE layer (Gate + routed MXFP4 experts + FP8 shared expert + combine).
+ * Mirrors MoE.forward — architecture.py:744-794, Gate.forward :696-718, Expert.forward :729-741,
+ * on the expert-bank layout of fp4_grouped._relayout_moe (fp4_grouped.py:142-188). */
+typedef struct wz_moe_desc {
+  int32_t dim;            /* D */
+  int32_t inter;          /* I (moe_inter_dim) */
+  int32_t n_experts;      /* E */
+  int32_t topk;           /* k (n_activated_experts) */
+  int32_t score_func;     /* WZ_SCORE_* */
+  int32_t act_scale_kind; /* WZ_SCALE_* (module scale_fmt) */
+  int32_t shared_w_scale_kind; /* WZ_WSCALE_* of the shared expert's FP8 weights */
+  float route_scale;
+  float swiglu_limit;     /* <= 0: no clamp */
+  int64_t vocab;          /* rows of tid2eid (hash layers) */
+  const void* gate_w;     /* bf16 [E, D] */
+  const float* gate_bias; /* fp32 [E]; NULL for hash-routed layers */
+  const int32_t* tid2eid; /* int32 [vocab, k] for hash-routed layers, else NULL */
+  const void* w13;        /* fp4x2 [E, 2I, D/2]: rows [0,I) = w1, [I,2I) = w3 */
+  const void* w13_s;      /* e8m0  [E, 2I, D/32] */
+  const void* w2;         /* fp4x2 [E, D, I/2] */
+  const void* w2_s;       /* e8m0  [E, D, I/32] */
+  const void* sh_w1;      /* e4m3 [I, D] */
+  const void* sh_w1_s;    /* [I/128, D/128] */
+  const void* sh_w3;      /* e4m3 [I, D] */
+  const void* sh_w3_s;
+  const void* sh_w2;      /* e4m3 [D, I] */
+  const void* sh_w2_s;    /* [D/128, I/128] */
+} wz_moe_desc;
+
+/* Bytes of scratch wz_moe_forward needs for up to T tokens. */
+size_t wz_moe_workspace_bytes(const wz_moe_desc* d, int64_t T);
+
+/* Zero the parts of a fresh workspace that must start at zero (arrival
+ * counters).  Call once after allocating ws; the kernels leave them at zero. */
+int wz_moe_workspace_init(void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* Full layer: x_bf16 [T, D], input_ids int64 [T] (read only by hash layers) -> y_bf16 [T, D].
+ * Optional routing outputs (may be NULL): weights fp32 [T,k], indices int64 [T,k]. */
+int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids, int64_t T,
+                   void* y_bf16, float* weights_out, int64_t* indices_out, void* ws,
+                   size_t ws_bytes, hipStream_t stream);
+
+/* Routing only (Gate.forward + the canonical permutation of expert_batch.py:24-37):
+ * weights fp32 [T,k], indices int64 [T,k], offsets int32 [E+1],
+ * perm_token int32 [T*k], perm_slot int32 [T*k]. */
+int wz_moe_route(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids, int64_t T,
+                 float* weights, int64_t* indices, int32_t* offsets, int32_t* perm_token,
+                 int32_t* perm_slot, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* RMSNorm (architecture.py:217-230): y = bf16(w * x * rsqrt(mean(x^2) + eps)), fp32 math.
+ * Optional fused residual: if residual != NULL, x := x + residual (bf16 add, written back
+ * to residual_out when non-NULL) before the norm. */
+int wz_rmsnorm(const void* x_bf16, const float* weight, void* y_bf16, int64_t T, int64_t D,
+               float eps, hipStream_t stream);
+
+/* bf16 elementwise add (residual): out = bf16(float(a) + float(b)). */
+int wz_add_bf16(const void* a, const void* b, void* out, int64_t n, hipStream_t stream);
+
+/* Synthetic-input generator (no reference counterpart: fills benchmark and test inputs
+ * with the portable counter-based hash of wanferenz_amd/synth.py).
+ * mode 0: u8 = low byte of draw; 1: e8m0 = lo + draw % (hi-lo+1);
+ * 2: e4m3 = low byte with NaN codes zeroed; 3: f32 = lo + (draw>>41)*2^-23*(hi-lo). */
+int wz_synth_fill(void* dst, int64_t n, uint64_t key, int64_t start, int mode, double lo,
+                  double hi, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WANFERENZ_AMD_H */

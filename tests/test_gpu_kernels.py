@@ -1,0 +1,225 @@
+"""GPU parity of the HIP act_quant / fp8_gemm / fp4_gemm / fp8_linear against the oracle.
+
+Bar: act_quant bit-exact (codes and scales); GEMMs bit-exact on exactness-
+constructed inputs (every partial sum representable in fp32, so any
+accumulation order gives the same fp32 and hence the same bf16), and within
+max|d|/max|ref| <= 1e-2 and cosine >= 0.9999 on random inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as om
+from oracle.numerics import e8m0_decode, from_bf16_bits
+from tests.helpers import bf16_tensor, bits16, bytes8, f32_of_bf16, f32_tensor, u8_tensor
+from wanferenz_amd import kernels, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL_REL = 1e-2
+TOL_COS = 0.9999
+
+
+@pytest.fixture(autouse=True)
+def _bf16_default():
+    """The model runs with torch's default dtype set to bf16 (fp4_grouped.py:451)."""
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    yield
+    torch.set_default_dtype(prev)
+
+
+def _x(seed, M, K, sigma=1.0):
+    return synth.normal_bf16(synth.stream_key(seed, synth.S_FP8_X), (M, K), sigma)
+
+
+def _special_rows(bits):
+    """Overwrite blocks with edge cases: all-zero, exact power-of-two amax, tiny, huge."""
+    from oracle.numerics import bf16_bits
+
+    b = bits.copy()
+    K = b.shape[1]
+    if b.shape[0] >= 4 and K >= 256:
+        b[0, :128] = 0
+        b[1, :128] = bf16_bits(np.full(128, 0.5, np.float32))
+        b[1, 5] = bf16_bits(np.float32(448.0 * 2.0))   # amax exactly 2 * 448 -> s = 2
+        b[2, 128:256] = bf16_bits(np.linspace(-1e-6, 1e-6, 128).astype(np.float32))
+        b[3, :128] = bf16_bits(np.linspace(-3e4, 3e4, 128).astype(np.float32))
+        b[3, 130] = bf16_bits(np.float32(-0.0))
+    return b
+
+
+@pytest.mark.parametrize("scale_fmt,scale_dtype", [
+    ("ue8m0", torch.float8_e8m0fnu), (None, torch.float32), ("ue8m0", torch.float32)])
+@pytest.mark.parametrize("M,K", [(1, 4096), (4, 1024), (37, 2048), (128, 512)])
+def test_act_quant_bit_exact(gpu, scale_fmt, scale_dtype, M, K):
+    xb = _special_rows(_x(M * 7 + K, M, K))
+    x = bf16_tensor(xb, gpu)
+    q, s = kernels.act_quant(x, 128, scale_fmt, scale_dtype)
+    torch.cuda.synchronize()
+    rq, rs = om.act_quant(from_bf16_bits(xb), 128, round_pow2=scale_fmt is not None)
+    got_q = bytes8(q)
+    assert np.array_equal(got_q, rq), f"{(got_q != rq).sum()} code mismatches"
+    if scale_dtype == torch.float8_e8m0fnu:
+        got_s = e8m0_decode(bytes8(s))
+    else:
+        got_s = s.cpu().numpy()
+    assert np.array_equal(got_s.view(np.uint32), rs.view(np.uint32))
+
+
+def _fp4_weight(seed, N, K, e_lo=119, e_hi=123):
+    key = synth.stream_key(seed, synth.S_W13)
+    w = synth.fill_u8(key, 0, N * K // 2).reshape(N, K // 2)
+    ws = synth.fill_e8m0(synth.stream_key(seed, synth.S_W13_S), 0, N * K // 32, e_lo, e_hi).reshape(N, K // 32)
+    return w, ws
+
+
+def _fp8_weight(seed, N, K, fp32_scales):
+    w = synth.fill_e4m3(synth.stream_key(seed, synth.S_FP8_W), 0, N * K).reshape(N, K)
+    nb, kb = (N + 127) // 128, (K + 127) // 128
+    if fp32_scales:
+        ws = synth.fill_f32_uniform(synth.stream_key(seed, synth.S_FP8_W_S), 0, nb * kb, 0.5, 1.5).reshape(nb, kb)
+    else:
+        ws = synth.fill_e8m0(synth.stream_key(seed, synth.S_FP8_W_S), 0, nb * kb, 112, 116).reshape(nb, kb)
+    return w, ws
+
+
+def _close(got, ref):
+    return om.max_rel_err(got, ref), om.cosine(got, ref)
+
+
+@pytest.mark.parametrize("act_fmt", ["ue8m0", None])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (4, 512, 4096), (8, 128, 2048), (33, 256, 512), (130, 128, 1024)])
+def test_fp4_gemm_random(gpu, act_fmt, M, N, K):
+    xb = _x(M + N + K, M, K)
+    sd = torch.float8_e8m0fnu if act_fmt else torch.float32
+    x = bf16_tensor(xb, gpu)
+    q, s = kernels.act_quant(x, 128, act_fmt, sd)
+    w, ws = _fp4_weight(N * 3 + K, N, K)
+    c = kernels.fp4_gemm(q, s, u8_tensor(w, gpu, torch.float4_e2m1fn_x2), u8_tensor(ws, gpu, torch.float8_e8m0fnu), sd)
+    got = f32_of_bf16(c)
+    rq, rs = om.act_quant(from_bf16_bits(xb), 128, act_fmt is not None)
+    ref = om.fp4_gemm(rq, rs, w, e8m0_decode(ws))
+    rel, cos = _close(got, ref)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    assert (got == ref).mean() > 0.9, (got == ref).mean()
+
+
+@pytest.mark.parametrize("w_fp32", [False, True])
+@pytest.mark.parametrize("act_fmt", ["ue8m0", None])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (4, 1024, 4096), (8, 384, 2048), (20, 128, 512), (128, 256, 1024)])
+def test_fp8_gemm_random(gpu, w_fp32, act_fmt, M, N, K):
+    xb = _x(M + 2 * N + K, M, K)
+    sd = torch.float8_e8m0fnu if act_fmt else torch.float32
+    x = bf16_tensor(xb, gpu)
+    q, s = kernels.act_quant(x, 128, act_fmt, sd)
+    w, ws = _fp8_weight(N + K, N, K, w_fp32)
+    wst = f32_tensor(ws, gpu) if w_fp32 else u8_tensor(ws, gpu, torch.float8_e8m0fnu)
+    c = kernels.fp8_gemm(q, s, u8_tensor(w, gpu, torch.float8_e4m3fn), wst, sd)
+    got = f32_of_bf16(c)
+    rq, rs = om.act_quant(from_bf16_bits(xb), 128, act_fmt is not None)
+    ref = om.fp8_gemm(rq, rs, w, ws if w_fp32 else e8m0_decode(ws))
+    rel, cos = _close(got, ref)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    # fused act_quant: same codes, same math
+    y = kernels.fp8_linear(x, u8_tensor(w, gpu, torch.float8_e4m3fn), wst, act_fmt, sd)
+    got2 = f32_of_bf16(y)
+    rel2, cos2 = _close(got2, ref)
+    assert rel2 <= TOL_REL and cos2 >= TOL_COS, (rel2, cos2)
+
+
+def _exact_codes(seed, n, table_codes):
+    d = synth.draws(synth.stream_key(seed, 99), 0, n)
+    return np.asarray(table_codes, np.uint8)[(d % np.uint64(len(table_codes))).astype(np.int64)]
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 1024), (5, 256, 2048), (16, 64, 4096), (40, 128, 512)])
+def test_fp4_gemm_exact(gpu, M, N, K):
+    """Small codes and unit scales: every partial sum is exact in fp32 -> bit-exact bf16."""
+    # e4m3 codes of 0, +-0.5, +-1, +-1.5, +-2 and e2m1 codes 0..15 (|v| <= 6)
+    a_codes = _exact_codes(M * K, M * K, [0x00, 0x30, 0xB0, 0x38, 0xB8, 0x3C, 0xBC, 0x40, 0xC0]).reshape(M, K)
+    w = synth.fill_u8(synth.stream_key(N, 7), 0, N * K // 2).reshape(N, K // 2)
+    ws = np.full((N, K // 32), 127, np.uint8)
+    a_s = np.full((M, K // 128), 127, np.uint8)
+    c = kernels.fp4_gemm(u8_tensor(a_codes, gpu, torch.float8_e4m3fn), u8_tensor(a_s, gpu, torch.float8_e8m0fnu),
+                         u8_tensor(w, gpu, torch.float4_e2m1fn_x2), u8_tensor(ws, gpu, torch.float8_e8m0fnu))
+    got = bits16(c)
+    ref = om.fp4_gemm(a_codes, e8m0_decode(a_s), w, e8m0_decode(ws))
+    from oracle.numerics import bf16_bits
+    assert np.array_equal(got, bf16_bits(ref))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 1024), (7, 256, 2048), (16, 128, 4096)])
+def test_fp8_gemm_exact(gpu, M, N, K):
+    codes = [0x00, 0x30, 0xB0, 0x38, 0xB8, 0x3C, 0xBC, 0x40, 0xC0]
+    a_codes = _exact_codes(M * K + 1, M * K, codes).reshape(M, K)
+    w = _exact_codes(N * K + 2, N * K, codes).reshape(N, K)
+    ws = np.full(((N + 127) // 128, K // 128), 127, np.uint8)
+    a_s = np.full((M, K // 128), 127, np.uint8)
+    c = kernels.fp8_gemm(u8_tensor(a_codes, gpu, torch.float8_e4m3fn), u8_tensor(a_s, gpu, torch.float8_e8m0fnu),
+                         u8_tensor(w, gpu, torch.float8_e4m3fn), u8_tensor(ws, gpu, torch.float8_e8m0fnu))
+    from oracle.numerics import bf16_bits
+    ref = om.fp8_gemm(a_codes, e8m0_decode(a_s), w, e8m0_decode(ws))
+    assert np.array_equal(bits16(c), bf16_bits(ref))
+
+
+def test_fp4_gemm_single_nonzero_layout(gpu):
+    """One nonzero weight nibble at a time: pins row/column/K placement and nibble order."""
+    M, N, K = 16, 16, 128
+    a = np.zeros((M, K), np.uint8)
+    rng = np.random.default_rng(0)
+    for m in range(M):
+        a[m] = np.where(rng.random(K) < 0.5, 0x38, 0x40)  # 1.0 or 2.0
+    a_s = np.full((M, 1), 127, np.uint8)
+    ws = np.full((N, K // 32), 127, np.uint8)
+    for (n, k) in [(0, 0), (0, 1), (3, 37), (15, 127), (9, 64), (4, 95)]:
+        w = np.zeros((N, K // 2), np.uint8)
+        w[n, k // 2] = (0x2 << (4 * (k % 2)))  # e2m1 code 2 = 1.0 at element k
+        c = kernels.fp4_gemm(u8_tensor(a, gpu, torch.float8_e4m3fn), u8_tensor(a_s, gpu, torch.float8_e8m0fnu),
+                             u8_tensor(w, gpu, torch.float4_e2m1fn_x2), u8_tensor(ws, gpu, torch.float8_e8m0fnu))
+        got = f32_of_bf16(c)
+        exp = np.zeros((M, N), np.float32)
+        exp[:, n] = np.where(a[:, k] == 0x38, 1.0, 2.0)
+        assert np.array_equal(got, exp), (n, k)
+
+
+def test_fp8_gemm_single_nonzero_layout(gpu):
+    """One nonzero FP8 weight at a time: pins row/column/K placement of the FP8 operands."""
+    M, N, K = 16, 16, 128
+    rng = np.random.default_rng(1)
+    a = np.where(rng.random((M, K)) < 0.5, 0x38, 0x40).astype(np.uint8)
+    a_s = np.full((M, 1), 127, np.uint8)
+    ws = np.full((1, 1), 127, np.uint8)
+    for (n, k) in [(0, 0), (0, 1), (3, 37), (15, 127), (9, 64), (4, 95)]:
+        w = np.zeros((N, K), np.uint8)
+        w[n, k] = 0x38
+        c = kernels.fp8_gemm(u8_tensor(a, gpu, torch.float8_e4m3fn), u8_tensor(a_s, gpu, torch.float8_e8m0fnu),
+                             u8_tensor(w, gpu, torch.float8_e4m3fn), u8_tensor(ws, gpu, torch.float8_e8m0fnu))
+        got = f32_of_bf16(c)
+        exp = np.zeros((M, N), np.float32)
+        exp[:, n] = np.where(a[:, k] == 0x38, 1.0, 2.0)
+        assert np.array_equal(got, exp), (n, k, got[:, n], np.nonzero(got))
+
+
+def test_fp4_gemm_k_mapping(gpu):
+    """Map each weight element k to the activation column it meets (bits of k' in rows 0..6)."""
+    M, N, K = 16, 16, 128
+    a = np.zeros((M, K), np.uint8)
+    for m in range(7):
+        a[m] = np.where((np.arange(K) >> m) & 1, 0x38, 0x00)
+    a[7] = 0x38
+    a_s = np.full((M, 1), 127, np.uint8)
+    ws = np.full((N, K // 32), 127, np.uint8)
+    bad = []
+    for k in range(K):
+        w = np.zeros((N, K // 2), np.uint8)
+        w[5, k // 2] = (0x2 << (4 * (k % 2)))
+        c = kernels.fp4_gemm(u8_tensor(a, gpu, torch.float8_e4m3fn), u8_tensor(a_s, gpu, torch.float8_e8m0fnu),
+                             u8_tensor(w, gpu, torch.float4_e2m1fn_x2), u8_tensor(ws, gpu, torch.float8_e8m0fnu))
+        got = f32_of_bf16(c)
+        cols = np.nonzero(got[7])[0].tolist()
+        kk = int(sum(int(got[m, 5] != 0) << m for m in range(7)))
+        if cols != [5] or kk != k:
+            bad.append((k, kk, cols))
+    assert not bad, f"k -> (k', cols): {bad}"

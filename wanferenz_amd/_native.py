@@ -1,0 +1,99 @@
+"""ctypes binding of libwanferenz_amd.so (the C ABI in include/wanferenz_amd.h).
+
+The library is built in-tree by ``python -m wanferenz_amd.build``.  Loading
+fails loudly when it is missing: there is no CPU fallback in the product.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libwanferenz_amd.so")
+
+# Symbols declared in include/wanferenz_amd.h, with their ctypes signatures.
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+SIGNATURES = {
+    "wz_last_error": (ctypes.c_char_p, []),
+    "wz_device_info": (_I, [ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "wz_act_quant_fp8": (_I, [_P, _I64, _I64, _P, _P, _I, _P]),
+    "wz_fp8_gemm": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P]),
+    "wz_fp8_linear": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P]),
+    "wz_fp4_gemm": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P]),
+    "wz_moe_workspace_bytes": (ctypes.c_size_t, [_P, _I64]),
+    "wz_moe_workspace_init": (_I, [_P, ctypes.c_size_t, _P]),
+    "wz_moe_forward": (_I, [_P, _P, _P, _I64, _P, _P, _P, _P, ctypes.c_size_t, _P]),
+    "wz_moe_route": (_I, [_P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]),
+    "wz_rmsnorm": (_I, [_P, _P, _P, _I64, _I64, _F, _P]),
+    "wz_add_bf16": (_I, [_P, _P, _P, _I64, _P]),
+    "wz_synth_fill": (_I, [_P, _I64, ctypes.c_uint64, _I64, _I, ctypes.c_double, ctypes.c_double, _P]),
+}
+
+# Scale / format constants (mirrors of the header's #defines).
+WZ_SCALE_F32 = 0
+WZ_SCALE_UE8M0 = 1
+WZ_SCALE_UE8M0_F32 = 2
+WZ_WSCALE_F32 = 0
+WZ_WSCALE_E8M0 = 1
+WZ_SCORE_SOFTMAX = 0
+WZ_SCORE_SIGMOID = 1
+WZ_SCORE_SQRTSOFTPLUS = 2
+
+_LIB = None
+_LOCK = threading.Lock()
+
+
+class WzError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    with _LOCK:
+        if _LIB is None:
+            if not os.path.exists(LIB_PATH):
+                raise WzError(
+                    f"{LIB_PATH} is not built — run `python -m wanferenz_amd.build` "
+                    "(there is no CPU fallback)"
+                )
+            L = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                if not hasattr(L, name):
+                    continue
+                fn = getattr(L, name)
+                fn.restype = res
+                fn.argtypes = args
+            _LIB = L
+    return _LIB
+
+
+def missing_symbols() -> list:
+    L = lib()
+    return [n for n in SIGNATURES if not hasattr(L, n)]
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib().wz_last_error().decode(errors="replace")
+        raise WzError(f"{what}: {msg}" if what else msg)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def ptr(t) -> int:
+    """Device (or host) address of a torch tensor, or None."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device=None) -> int:
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

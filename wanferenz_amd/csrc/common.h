@@ -1,0 +1,129 @@
+// Shared device helpers for the gfx950 (CDNA4) MoE / FP8-linear kernels.
+//
+// Number formats (OCP MX / OCP FP8): e4m3fn activations and FP8 weights,
+// e2m1 (two codes per byte, low nibble = even element) MXFP4 weights with one
+// e8m0 scale per 32 K-elements, bf16 activations and outputs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "wanferenz_amd.h"
+
+namespace wz {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr float kFp8Max = 448.0f;
+
+// MFMA operand formats (cbsz / blgp field values of V_MFMA_SCALE_F32_16X16X128_F8F6F4).
+constexpr int kFmtFp8 = 0;
+constexpr int kFmtFp4 = 4;
+constexpr int kE8m0One = 127;
+
+// ---------------------------------------------------------------- bf16 -------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(uint32_t(b) << 16);
+}
+
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// float32 -> bfloat16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return uint16_t((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_round(float f) {
+  return __uint_as_float(uint32_t(f32_to_bf16(f)) << 16);
+}
+
+// ---------------------------------------------------------------- scales -----
+
+// 2^ceil(log2(t)) for a normal positive float t (the ue8m0 activation scale of
+// wanferenz/kernels/torch_ops.py:17-21: a power of two keeps its exponent,
+// anything else rounds up).  Returns the e8m0 byte (biased exponent).
+__device__ __forceinline__ int pow2_ceil_e8m0(float t) {
+  uint32_t b = __float_as_uint(t);
+  int e = int((b >> 23) & 0xFFu);
+  return e + ((b & 0x7FFFFFu) != 0u ? 1 : 0);
+}
+
+__device__ __forceinline__ float e8m0_to_f32(int e) { return __uint_as_float(uint32_t(e) << 23); }
+
+// Activation block scale from the block's amax (torch_ops.py:38-43):
+// amax floored at 1e-4, then amax/448 (fp32) or its power-of-two ceiling.
+struct ActScale {
+  float s;       // the scale the reference stores
+  float inv;     // exact reciprocal when pow2 (multiply == divide)
+  int e8m0;      // biased exponent byte when pow2, else 127
+};
+
+__device__ __forceinline__ ActScale act_scale(float amax, bool pow2) {
+  amax = fmaxf(amax, 1e-4f);
+  float t = amax * (1.0f / 448.0f);
+  ActScale r;
+  if (pow2) {
+    int e = pow2_ceil_e8m0(t);
+    r.e8m0 = e;
+    r.s = e8m0_to_f32(e);
+    r.inv = e8m0_to_f32(254 - e);
+  } else {
+    r.e8m0 = kE8m0One;
+    r.s = t;
+    r.inv = 0.0f;
+  }
+  return r;
+}
+
+// x / s, clamped to the e4m3 range (torch_ops.py:44).  For a power-of-two
+// scale the reciprocal multiply is exact, so it equals the IEEE quotient.
+__device__ __forceinline__ float quant_div(float x, const ActScale& sc, bool pow2) {
+  float q = pow2 ? x * sc.inv : x / sc.s;
+  return fminf(fmaxf(q, -kFp8Max), kFp8Max);
+}
+
+// Two floats (already within +-448) -> two e4m3fn bytes, RNE, via the
+// hardware converter.  word_sel picks the low or high 16 bits of `old`.
+__device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true));
+}
+
+// ---------------------------------------------------------------- wave ops ---
+
+__device__ __forceinline__ float wave_max_xor(float v, int mask) {
+  return fmaxf(v, __shfl_xor(v, mask, kWave));
+}
+
+// ---------------------------------------------------------------- MFMA -------
+
+template <int FMT_A, int FMT_B>
+__device__ __forceinline__ v4f mfma_scaled(const v8i& a, const v8i& b, v4f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, 0, sa, 0, sb);
+}
+
+// ---------------------------------------------------------------- loads ------
+
+__device__ __forceinline__ v4i load16(const void* p) {
+  return *reinterpret_cast<const v4i*>(p);
+}
+
+__device__ __forceinline__ v4i load16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+}
+
+}  // namespace wz
+
+// Error reporting (errors.cpp).
+namespace wz {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace wz

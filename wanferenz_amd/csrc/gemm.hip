@@ -1,0 +1,184 @@
+// Block-scaled FP8 / MXFP4 GEMV-GEMM for skinny M (decode widths and up).
+//
+// C[M,N] (bf16) = sum over 128-wide K-blocks of (A_blk . W_blk^T) * scales
+// (wanferenz/kernels/reference.py:235-311 fp8_gemm, :506-591 fp4_gemm; the CPU
+// restatement torch_ops.py:93-108).
+//
+// Decode is bound by streaming W from HBM, so the kernel is shaped around the
+// weight stream, not the M dimension:
+//   * a workgroup owns 16 output columns (= 16 weight rows) and its four
+//     waves split K into four contiguous ranges, so every weight byte is read
+//     once, by one lane, in 16-byte loads; partial sums meet in LDS;
+//   * each wave batches the loads of UNROLL K-blocks before issuing the MFMAs
+//     to keep enough bytes in flight per CU;
+//   * tokens ride on the MFMA's M side (16 rows per tile, MT tiles per wave),
+//     padded with zero rows, so an M=1..16 GEMV is one V_MFMA_SCALE 16x16x128
+//     per 16x128 weight block with no per-byte VALU dequantisation.
+#include "mfma_ops.h"
+
+namespace wz {
+
+constexpr int kGemmThreads = 256;
+constexpr int kUnroll = 8;
+
+template <int WF, bool A_BF16, int MT>
+__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(
+    const void* __restrict__ A, const void* __restrict__ As, int act_kind,
+    const uint8_t* __restrict__ W, const void* __restrict__ Ws, int w_kind,
+    uint16_t* __restrict__ C, int M, int N, int K) {
+  __shared__ float red[4][MT][kWave][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nl = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int m_base = blockIdx.y * (16 * MT);
+  const int nkb = K / 128;
+  const int kb0 = (wave * nkb) / 4, kb1 = ((wave + 1) * nkb) / 4;
+  const int ldw = WF == kFmtFp4 ? K / 2 : K;
+  const uint8_t* wrow = W + int64_t(n0 + nl) * ldw;
+  const uint8_t* wsrow = WF == kFmtFp4 ? reinterpret_cast<const uint8_t*>(Ws) + int64_t(n0 + nl) * (K / 32)
+                                       : nullptr;
+  const bool a_pow2 = act_kind != WZ_SCALE_F32;
+  const bool b_pow2 = WF == kFmtFp4 || w_kind == WZ_WSCALE_E8M0;
+
+  v4f acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int kb = kb0; kb < kb1; kb += kUnroll) {
+    v8i bb[kUnroll];
+    int sbe[kUnroll];
+    float sbf[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int k = kb + u;
+      if (k < kb1) {
+        if (WF == kFmtFp4) {
+          bb[u] = b_fp4(wrow, k, g);
+          sbe[u] = b_fp4_scale(wsrow, k, g);
+          sbf[u] = 1.0f;
+        } else {
+          bb[u] = b_fp8(wrow, k, g);
+          fp8_wscale(Ws, int64_t(n0 >> 7) * nkb + k, w_kind, sbe[u], sbf[u]);
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = m_base + t * 16 + nl;
+      const bool live = m < M;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int k = kb + u;
+        if (k < kb1) {
+          AOp a;
+          if (A_BF16)
+            a = a_from_bf16(live ? reinterpret_cast<const uint16_t*>(A) + int64_t(m) * K : nullptr, k, g,
+                            a_pow2);
+          else
+            a = a_from_fp8(live ? reinterpret_cast<const uint8_t*>(A) + int64_t(m) * K : nullptr,
+                           live ? (act_kind == WZ_SCALE_UE8M0
+                                       ? static_cast<const void*>(reinterpret_cast<const uint8_t*>(As) + int64_t(m) * nkb)
+                                       : static_cast<const void*>(reinterpret_cast<const float*>(As) + int64_t(m) * nkb))
+                                : nullptr,
+                           k, g, act_kind);
+          mma_step<kFmtFp8, WF>(acc[t], a, bb[u], sbe[u], sbf[u], a_pow2, b_pow2, lane);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][t][lane][i] = acc[t][i];
+  __syncthreads();
+  // Wave w finishes M-tiles t = w, w+4, ...; partials are summed in wave order.
+  for (int t = wave; t < MT; t += 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = red[0][t][lane][i];
+      v += red[1][t][lane][i];
+      v += red[2][t][lane][i];
+      v += red[3][t][lane][i];
+      const int m = m_base + t * 16 + g * 4 + i;
+      if (m < M) C[int64_t(m) * N + n0 + nl] = f32_to_bf16(v);
+    }
+  }
+}
+
+template <int WF, bool A_BF16>
+static int launch_skinny(const void* A, const void* As, int act_kind, const void* W, const void* Ws,
+                         int w_kind, void* C, int64_t M, int64_t N, int64_t K, hipStream_t stream,
+                         const char* what) {
+  if (M == 0) return WZ_OK;
+  int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+  const int64_t rows_per_block = 16 * mt;
+  dim3 grid(unsigned(N / 16), unsigned((M + rows_per_block - 1) / rows_per_block));
+  const uint8_t* w = static_cast<const uint8_t*>(W);
+  uint16_t* c = static_cast<uint16_t*>(C);
+#define WZ_LAUNCH(MTV)                                                                            \
+  hipLaunchKernelGGL((skinny_gemm_kernel<WF, A_BF16, MTV>), grid, dim3(kGemmThreads), 0, stream, A, \
+                     As, act_kind, w, Ws, w_kind, c, int(M), int(N), int(K))
+  switch (mt) {
+    case 1: WZ_LAUNCH(1); break;
+    case 2: WZ_LAUNCH(2); break;
+    case 4: WZ_LAUNCH(4); break;
+    default: WZ_LAUNCH(8); break;
+  }
+#undef WZ_LAUNCH
+  return check_launch(what);
+}
+
+static int check_dims(const char* what, int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N <= 0 || K <= 0)
+    return set_error(WZ_EINVAL, "%s: bad shape M=%lld N=%lld K=%lld", what, (long long)M,
+                     (long long)N, (long long)K);
+  if (K % 128)
+    return set_error(WZ_EINVAL, "%s: K=%lld must be a multiple of 128", what, (long long)K);
+  if (N % 16)
+    return set_error(WZ_EINVAL, "%s: N=%lld must be a multiple of 16", what, (long long)N);
+  if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
+    return set_error(WZ_EINVAL, "%s: dimension too large", what);
+  return WZ_OK;
+}
+
+}  // namespace wz
+
+extern "C" int wz_fp8_gemm(const void* a_e4m3, const void* a_s, const void* w_e4m3, const void* w_s,
+                           void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
+                           int w_scale_kind, hipStream_t stream) {
+  using namespace wz;
+  if (int rc = check_dims("fp8_gemm", M, N, K)) return rc;
+  if (act_scale_kind < 0 || act_scale_kind > 2 || (w_scale_kind != 0 && w_scale_kind != 1))
+    return set_error(WZ_EINVAL, "fp8_gemm: bad scale kinds %d/%d", act_scale_kind, w_scale_kind);
+  if (M && (!a_e4m3 || !a_s || !w_e4m3 || !w_s || !c_bf16))
+    return set_error(WZ_EINVAL, "fp8_gemm: null pointer");
+  return launch_skinny<kFmtFp8, false>(a_e4m3, a_s, act_scale_kind, w_e4m3, w_s, w_scale_kind,
+                                       c_bf16, M, N, K, stream, "fp8_gemm");
+}
+
+extern "C" int wz_fp8_linear(const void* x_bf16, const void* w_e4m3, const void* w_s, void* y_bf16,
+                             int64_t M, int64_t N, int64_t K, int act_scale_kind, int w_scale_kind,
+                             hipStream_t stream) {
+  using namespace wz;
+  if (int rc = check_dims("fp8_linear", M, N, K)) return rc;
+  if (act_scale_kind < 0 || act_scale_kind > 2 || (w_scale_kind != 0 && w_scale_kind != 1))
+    return set_error(WZ_EINVAL, "fp8_linear: bad scale kinds %d/%d", act_scale_kind, w_scale_kind);
+  if (M && (!x_bf16 || !w_e4m3 || !w_s || !y_bf16))
+    return set_error(WZ_EINVAL, "fp8_linear: null pointer");
+  return launch_skinny<kFmtFp8, true>(x_bf16, nullptr, act_scale_kind, w_e4m3, w_s, w_scale_kind,
+                                      y_bf16, M, N, K, stream, "fp8_linear");
+}
+
+extern "C" int wz_fp4_gemm(const void* a_e4m3, const void* a_s, const void* w_fp4x2,
+                           const void* w_s_e8m0, void* c_bf16, int64_t M, int64_t N, int64_t K,
+                           int act_scale_kind, hipStream_t stream) {
+  using namespace wz;
+  if (int rc = check_dims("fp4_gemm", M, N, K)) return rc;
+  if (act_scale_kind < 0 || act_scale_kind > 2)
+    return set_error(WZ_EINVAL, "fp4_gemm: bad scale kind %d", act_scale_kind);
+  if (M && (!a_e4m3 || !a_s || !w_fp4x2 || !w_s_e8m0 || !c_bf16))
+    return set_error(WZ_EINVAL, "fp4_gemm: null pointer");
+  return launch_skinny<kFmtFp4, false>(a_e4m3, a_s, act_scale_kind, w_fp4x2, w_s_e8m0,
+                                       WZ_WSCALE_E8M0, c_bf16, M, N, K, stream, "fp4_gemm");
+}

@@ -1,0 +1,145 @@
+"""Portable, counter-based synthetic inputs for the MoE / FP8-linear workloads.
+
+Every tensor is a pure function of ``(seed, stream, flat index)`` so that any
+slice of a multi-GB expert bank can be regenerated independently on the CPU
+(numpy here) or on the GPU (``wz_synth_fill`` in the HIP library, which uses
+the same integer hash).  Only integer arithmetic feeds the bytes that are
+generated on the GPU; Gaussian tensors (activations, gate weights) are drawn
+on the host with float64 Box-Muller and rounded to bf16 with round-to-nearest-
+even, then uploaded.
+
+The generators follow the recipes of the reference's own tests and probes:
+
+* MXFP4 expert weights: e2m1 codes uniform over all 16 values, ue8m0 scale
+  bytes uniform in a stated exponent window (reference expert weights are
+  ``float4_e2m1fn_x2`` + ``float8_e8m0fnu`` per 32 K-elements,
+  wanferenz/model/architecture.py:146-157).
+* FP8 weights: e4m3 bytes uniform with the two NaN codes replaced by zero,
+  as in wanferenz/kernels/fp8_vector.py:195-197; fp32 block scales uniform in
+  [0.5, 1.5) as in fp8_vector.py:216-231.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+GOLDEN = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+_MASK64 = (1 << 64) - 1
+
+# Fill modes shared with the HIP generator (wz_synth_fill).
+FILL_U8 = 0          # low byte of the draw
+FILL_E8M0 = 1        # lo + draw % (hi - lo + 1)
+FILL_E4M3 = 2        # low byte, NaN codes (0x7F, 0xFF) -> 0x00
+FILL_F32_UNIFORM = 3  # lo + (draw >> 41) * 2^-23 * (hi - lo), lo/hi floats
+
+
+def _mix64_int(z: int) -> int:
+    z &= _MASK64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _MASK64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _MASK64
+    return z ^ (z >> 31)
+
+
+def stream_key(seed: int, stream: int) -> int:
+    """64-bit key of one named stream (splitmix64 finaliser of seed*phi+stream+1)."""
+    return _mix64_int(seed * 0x9E3779B97F4A7C15 + stream + 1)
+
+
+def draws(key: int, start: int, count: int) -> np.ndarray:
+    """uint64 draws ``mix64(key + (i + 1) * phi)`` for i in [start, start+count)."""
+    with np.errstate(over="ignore"):
+        i = np.arange(start + 1, start + count + 1, dtype=np.uint64)
+        z = np.uint64(key) + i * GOLDEN
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+        return z ^ (z >> np.uint64(31))
+
+
+def fill_u8(key: int, start: int, count: int) -> np.ndarray:
+    return (draws(key, start, count) & np.uint64(0xFF)).astype(np.uint8)
+
+
+def fill_e8m0(key: int, start: int, count: int, lo: int, hi: int) -> np.ndarray:
+    span = np.uint64(hi - lo + 1)
+    return (np.uint64(lo) + draws(key, start, count) % span).astype(np.uint8)
+
+
+def fill_e4m3(key: int, start: int, count: int) -> np.ndarray:
+    b = fill_u8(key, start, count)
+    b[(b & 0x7F) == 0x7F] = 0
+    return b
+
+
+def fill_f32_uniform(key: int, start: int, count: int, lo: float, hi: float) -> np.ndarray:
+    k = (draws(key, start, count) >> np.uint64(41)).astype(np.float64)
+    return (np.float32(lo) + (k * 2.0**-23).astype(np.float32) * np.float32(hi - lo)).astype(np.float32)
+
+
+def bf16_bits_from_f32(x: np.ndarray) -> np.ndarray:
+    """Round float32 to bfloat16 (round-to-nearest-even) and return the uint16 bits."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    bias = np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))
+    r = ((u + bias) >> np.uint32(16)).astype(np.uint16)
+    r[nan] = ((u[nan] >> np.uint32(16)) | np.uint32(0x40)).astype(np.uint16)
+    return r
+
+
+def f32_from_bf16_bits(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def normal_bf16(key: int, shape, sigma: float = 1.0, mean: float = 0.0) -> np.ndarray:
+    """N(mean, sigma) drawn by float64 Box-Muller, cast to float32, then bf16 RNE.
+
+    Returns uint16 bf16 bits of ``shape``.
+    """
+    n = int(np.prod(shape))
+    d = draws(key, 0, 2 * n)
+    u1 = ((d[0::2] >> np.uint64(11)).astype(np.float64) + 1.0) * 2.0**-53
+    u2 = (d[1::2] >> np.uint64(11)).astype(np.float64) * 2.0**-53
+    z = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+    v = (z * sigma + mean).astype(np.float32)
+    return bf16_bits_from_f32(v).reshape(shape)
+
+
+def normal_f32(key: int, shape, sigma: float = 1.0, mean: float = 0.0) -> np.ndarray:
+    n = int(np.prod(shape))
+    d = draws(key, 0, 2 * n)
+    u1 = ((d[0::2] >> np.uint64(11)).astype(np.float64) + 1.0) * 2.0**-53
+    u2 = (d[1::2] >> np.uint64(11)).astype(np.float64) * 2.0**-53
+    z = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+    return (z * sigma + mean).astype(np.float32).reshape(shape)
+
+
+# Stream identifiers.  A layer's streams are offset by ``layer * 64`` so that
+# stacked layers never share bytes.
+S_X = 1
+S_GATE_W = 2
+S_GATE_BIAS = 3
+S_W13 = 4
+S_W13_S = 5
+S_W2 = 6
+S_W2_S = 7
+S_SH_W13 = 8
+S_SH_W13_S = 9
+S_SH_W2 = 10
+S_SH_W2_S = 11
+S_TID2EID = 12
+S_INPUT_IDS = 13
+S_FP8_W = 20
+S_FP8_W_S = 21
+S_FP8_X = 22
+S_NORM = 23
+
+
+def layer_stream(layer: int, stream: int) -> int:
+    return layer * 64 + stream
+
+
+# Exponent windows (ue8m0 byte values) of the synthetic scales.
+ROUTED_E8M0 = (119, 123)   # 2^-8 .. 2^-4 per 32-element block
+SHARED_E8M0 = (112, 116)   # 2^-15 .. 2^-11 per 128x128 block (keeps the shared
+                           # expert's pre-activations O(1) for uniform e4m3 codes)
