@@ -1,0 +1,815 @@
+// MoE layer: gate scoring + top-k routing, canonical permutation, MXFP4 routed
+// experts (w1/w3 SwiGLU, then w2), FP8 shared expert, weighted combine.
+//
+// Semantics: MoE.forward / Gate.forward / Expert.forward of
+// wanferenz/model/architecture.py:696-794, with the canonical pair order of
+// wanferenz/kernels/expert_batch.py:24-37 (experts ascending, then token,
+// then slot) and the combine of fp4_grouped.py:318-324 (fp32 sum of the
+// routed bf16 outputs in ascending expert id, then the shared expert, then
+// bf16).  A token that lists an expert twice (hash-routed layers) receives it
+// once (architecture.py:790 is a non-accumulating index_put).
+//
+// The layer runs as a fixed sequence of stream-ordered launches with no host
+// synchronisation and no allocation, so a decode step can be captured in a
+// HIP graph.  Grids are sized from T on the host; blocks beyond the device-
+// side number of active experts return at once.
+//
+//   gate_dot   scores[T,E] = x . W^T, exact bf16 products summed in fp64, one
+//              wave per (expert, 8 tokens): reads the bf16 gate once.
+//   topk       one wave per token: score function, +bias, top-k (ties -> lower
+//              index), renormalise, x route_scale; hash layers read tid2eid.
+//   perm       one workgroup: expert counts, offsets, active-expert list and
+//              the stable (expert, token, slot) permutation via wave ballots.
+//   w13        per (active expert, 16 intermediate features): w1 and w3 rows
+//              streamed once through V_MFMA_SCALE 16x16x128 (e4m3 x e2m1),
+//              act_quant of x fused into the A-operand load, SwiGLU + routing
+//              weight in registers, bf16 h written in permuted order; plus
+//              the shared expert's FP8 w1/w3 tiles in the same launch.
+//   w2         per (active expert, 16 output rows): act_quant of h fused, w2
+//              rows streamed once; shared expert's FP8 w2 in the same launch.
+//   combine    y[t] = bf16(sum_{experts asc} out[t,e] + shared[t]).
+#include "mfma_ops.h"
+
+namespace wz {
+
+constexpr int kRouteThreads = 1024;
+constexpr int kMaxExperts = 512;
+constexpr int kMaxPairs = 16384;
+constexpr int kGateTok = 8;
+
+struct MoeWs {
+  float* scores;       // [T, E]
+  float* weights;      // [T, k]
+  int32_t* idx;        // [T, k]
+  int32_t* offsets;    // [E + 1]
+  int32_t* active;     // [E] active expert ids, ascending
+  int32_t* act_off;    // [E] first pair of active expert u
+  int32_t* act_cnt;    // [E] pairs of active expert u
+  int32_t* n_active;   // [1]
+  int32_t* perm_token; // [P]
+  int32_t* perm_slot;  // [P]
+  int32_t* pos;        // [P] permuted position of pair t*k + j
+  uint16_t* h;         // [P, I] bf16
+  uint16_t* sh_h;      // [T, I] bf16
+  uint16_t* out2;      // [P, D] bf16
+  uint16_t* sh_out;    // [T, D] bf16
+  size_t bytes;
+};
+
+static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+static MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base) {
+  const int64_t E = d->n_experts, k = d->topk, P = T * k, D = d->dim, I = d->inter;
+  size_t off = 0;
+  MoeWs w;
+  auto take = [&](size_t bytes) {
+    uint8_t* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  w.scores = reinterpret_cast<float*>(take(sizeof(float) * T * E));
+  w.weights = reinterpret_cast<float*>(take(sizeof(float) * P));
+  w.idx = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
+  w.offsets = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (E + 1)));
+  w.active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
+  w.act_off = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
+  w.act_cnt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
+  w.n_active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 64));
+  w.perm_token = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
+  w.perm_slot = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
+  w.pos = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
+  w.h = reinterpret_cast<uint16_t*>(take(2 * size_t(P) * I));
+  w.sh_h = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * I));
+  w.out2 = reinterpret_cast<uint16_t*>(take(2 * size_t(P) * D));
+  w.sh_out = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * D));
+  w.bytes = off;
+  return w;
+}
+
+// ------------------------------------------------------------------ gate ----
+
+// scores[t, e] = fp32(sum_d x[t,d] * W[e,d]).  bf16 x bf16 is exact in fp32;
+// the fp64 running sums make the result the correctly rounded dot product
+// except in vanishingly rare cases, so the GPU and the oracle agree on the
+// fp32 scores that decide the top-k.
+__global__ __launch_bounds__(256) void gate_dot_kernel(const uint16_t* __restrict__ x,
+                                                       const uint16_t* __restrict__ W,
+                                                       float* __restrict__ scores, int T, int E,
+                                                       int D) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x * 4 + wave;
+  const int t0 = blockIdx.y * kGateTok;
+  if (e >= E) return;
+  double acc[kGateTok];
+#pragma unroll
+  for (int i = 0; i < kGateTok; ++i) acc[i] = 0.0;
+  const int nc = D / 8;
+  for (int c = lane; c < nc; c += 64) {
+    const v4i wv = load16(W + int64_t(e) * D + c * 8);
+    float wf[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      wf[2 * j] = bf16lo(uint32_t(wv[j]));
+      wf[2 * j + 1] = bf16hi(uint32_t(wv[j]));
+    }
+#pragma unroll
+    for (int i = 0; i < kGateTok; ++i) {
+      if (t0 + i < T) {
+        const v4i xv = load16(x + int64_t(t0 + i) * D + c * 8);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[i] += double(bf16lo(uint32_t(xv[j])) * wf[2 * j]);
+          acc[i] += double(bf16hi(uint32_t(xv[j])) * wf[2 * j + 1]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kGateTok; ++i) {
+    double v = acc[i];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+    if (lane == 0 && t0 + i < T) scores[int64_t(t0 + i) * E + e] = float(v);
+  }
+}
+
+// ------------------------------------------------------------------ top-k ---
+
+struct Cand {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ Cand cand_better(Cand a, Cand b) {
+  // larger value wins; equal values -> lower expert index (stable descending order)
+  if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+  return a;
+}
+
+__device__ __forceinline__ float softplus_f32(float a) {
+  // torch F.softplus(beta=1, threshold=20) evaluated in fp64, rounded to fp32
+  if (a > 20.0f) return a;
+  return float(log1p(exp(double(a))));
+}
+
+constexpr int kSlots = kMaxExperts / 64;
+
+__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ scores,
+                                                   const float* __restrict__ bias,
+                                                   const int32_t* __restrict__ tid2eid,
+                                                   const int64_t* __restrict__ input_ids,
+                                                   int64_t vocab, int T, int E, int k,
+                                                   int score_func, float route_scale,
+                                                   float* __restrict__ weights,
+                                                   int32_t* __restrict__ idx) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  const float* a = scores + int64_t(t) * E;
+  float s[kSlots], b[kSlots];
+  double mx = -1e300, sum = 0.0;
+  if (score_func == WZ_SCORE_SOFTMAX) {
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) mx = fmax(mx, double(a[e]));
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx = fmax(mx, __shfl_xor(mx, m, kWave));
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) sum += exp(double(a[e]) - mx);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, kWave);
+  }
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    const int e = lane + 64 * i;
+    float v = -INFINITY;
+    if (e < E) {
+      const float ae = a[e];
+      if (score_func == WZ_SCORE_SOFTMAX)
+        v = float(exp(double(ae) - mx) / sum);
+      else if (score_func == WZ_SCORE_SIGMOID)
+        v = float(1.0 / (1.0 + exp(-double(ae))));
+      else
+        v = float(sqrt(double(softplus_f32(ae))));
+    }
+    s[i] = v;
+    b[i] = (e < E && bias != nullptr) ? v + bias[e] : v;
+  }
+  int sel[16];
+  if (tid2eid != nullptr) {
+    int64_t id = input_ids[t];
+    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+    for (int j = 0; j < k; ++j) {
+      int e = tid2eid[id * k + j];
+      sel[j] = e < 0 ? 0 : (e >= E ? E - 1 : e);
+    }
+  } else {
+    unsigned taken = 0u;
+    for (int j = 0; j < k; ++j) {
+      Cand best = {-INFINITY, 0x7FFFFFFF};
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E && !((taken >> i) & 1u)) best = cand_better(best, Cand{b[i], e});
+      }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) {
+        Cand o;
+        o.v = __shfl_xor(best.v, m, kWave);
+        o.i = __shfl_xor(best.i, m, kWave);
+        best = cand_better(best, o);
+      }
+      sel[j] = best.i;
+      if ((best.i & 63) == lane) taken |= 1u << (best.i >> 6);
+    }
+  }
+  // weights = original scores gathered at the selected experts (architecture.py:714-717)
+  float w[16];
+  float tot = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const int e = sel[j];
+    float mine = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i)
+      if ((e >> 6) == i) mine = s[i];
+    w[j] = __shfl(mine, e & 63, kWave);
+    tot += w[j];
+  }
+  for (int j = 0; j < k; ++j) {
+    float v = w[j];
+    if (score_func != WZ_SCORE_SOFTMAX) v = v / tot;
+    v = v * route_scale;
+    if (lane == j) {
+      weights[int64_t(t) * k + j] = v;
+      idx[int64_t(t) * k + j] = sel[j];
+    }
+  }
+}
+
+// ------------------------------------------------------------ permutation ---
+
+__device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
+  // exclusive scan over the 1024 threads of the block
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int o = __shfl_up(inc, d, kWave);
+    if (lane >= d) inc += o;
+  }
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    int x = threadIdx.x < (kRouteThreads / 64) ? wsum[threadIdx.x] : 0;
+    int xi = x;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      int o = __shfl_up(xi, d, kWave);
+      if (threadIdx.x >= d) xi += o;
+    }
+    wsum[32 + threadIdx.x] = xi - x;  // exclusive prefix of wave totals
+    if (threadIdx.x == 63) wsum[31] = xi;
+  }
+  __syncthreads();
+  total = wsum[31];
+  int r = inc - v + wsum[32 + wave];
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __restrict__ idx, int T,
+                                                             int E, int k, int32_t* __restrict__ offsets,
+                                                             int32_t* __restrict__ active,
+                                                             int32_t* __restrict__ act_off,
+                                                             int32_t* __restrict__ act_cnt,
+                                                             int32_t* __restrict__ n_active,
+                                                             int32_t* __restrict__ perm_token,
+                                                             int32_t* __restrict__ perm_slot,
+                                                             int32_t* __restrict__ pos) {
+  __shared__ int cnt[kMaxExperts];
+  __shared__ int base[kMaxExperts];
+  __shared__ int run[kMaxExperts];
+  __shared__ int wcnt[kRouteThreads / 64][kMaxExperts];
+  __shared__ int wsum[128];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int P = T * k;
+  for (int e = tid; e < kMaxExperts; e += kRouteThreads) {
+    cnt[e] = 0;
+    run[e] = 0;
+  }
+  __syncthreads();
+  for (int p = tid; p < P; p += kRouteThreads) atomicAdd(&cnt[idx[p]], 1);
+  __syncthreads();
+  // offsets and the active-expert list (E <= 1024 = block size)
+  int c = tid < E ? cnt[tid] : 0;
+  int total;
+  int ex = block_excl_scan(c, wsum, total);
+  int flag = c > 0 ? 1 : 0;
+  int nact;
+  int u = block_excl_scan(flag, wsum, nact);
+  if (tid < E) {
+    base[tid] = ex;
+    offsets[tid] = ex;
+    if (flag) {
+      active[u] = tid;
+      act_off[u] = ex;
+      act_cnt[u] = c;
+    }
+  }
+  if (tid == 0) {
+    offsets[E] = total;
+    n_active[0] = nact;
+  }
+  __syncthreads();
+  // stable placement, 1024 pairs per round
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int c0 = 0; c0 < P; c0 += kRouteThreads) {
+    const int p = c0 + tid;
+    const bool valid = p < P;
+    const int e = valid ? idx[p] : 0;
+    unsigned long long mask = __ballot(valid);
+    if (!valid) mask = ~mask;
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = (e >> bit) & 1;
+      const unsigned long long m = __ballot(on);
+      mask &= on ? m : ~m;
+    }
+    const int rank = __popcll(mask & lt);
+    const bool leader = (mask & lt) == 0ull;
+    for (int i = tid; i < (kRouteThreads / 64) * kMaxExperts; i += kRouteThreads)
+      (&wcnt[0][0])[i] = 0;
+    __syncthreads();
+    if (valid && leader) wcnt[wave][e] = __popcll(mask);
+    __syncthreads();
+    if (valid) {
+      int before = run[e];
+      for (int w = 0; w < wave; ++w) before += wcnt[w][e];
+      const int q = base[e] + before + rank;
+      perm_token[q] = p / k;
+      perm_slot[q] = p % k;
+      pos[p] = q;
+    }
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += kRouteThreads) {
+      int s = 0;
+      for (int w = 0; w < kRouteThreads / 64; ++w) s += wcnt[w][ee];
+      run[ee] += s;
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------- w13 ----
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+constexpr int kMoeThreads = 256;
+constexpr int kMoeUnroll = 4;
+
+// One work item: 16 intermediate features f0..f0+15 of one expert (or of the
+// shared expert), all of its token rows.  The four waves split K = D.
+// red: LDS [4 waves][2][MT][64][4] floats.
+template <bool SHARED, int kMT>
+__device__ void w13_item(const wz_moe_desc& d, const MoeWs& ws, const uint16_t* __restrict__ x,
+                         int T, int f0, int e, int row0, int nrows, float* red_) {
+  auto red = reinterpret_cast<float(*)[2][kMT][kWave][4]>(red_);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nl = lane & 15, g = lane >> 4;
+  const int D = d.dim, I = d.inter;
+  const int nkb = D / 128;
+  const int kb0 = (wave * nkb) / 4, kb1 = ((wave + 1) * nkb) / 4;
+  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
+  // weight rows of this lane: w1 row (f0 + nl), w3 row (f0 + nl)
+  const uint8_t *w1row, *w3row, *s1row = nullptr, *s3row = nullptr;
+  bool b_pow2;
+  if (SHARED) {
+    w1row = static_cast<const uint8_t*>(d.sh_w1) + int64_t(f0 + nl) * D;
+    w3row = static_cast<const uint8_t*>(d.sh_w3) + int64_t(f0 + nl) * D;
+    b_pow2 = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  } else {
+    const int64_t ebase = int64_t(e) * 2 * I;
+    w1row = static_cast<const uint8_t*>(d.w13) + (ebase + f0 + nl) * (D / 2);
+    w3row = static_cast<const uint8_t*>(d.w13) + (ebase + I + f0 + nl) * (D / 2);
+    s1row = static_cast<const uint8_t*>(d.w13_s) + (ebase + f0 + nl) * (D / 32);
+    s3row = static_cast<const uint8_t*>(d.w13_s) + (ebase + I + f0 + nl) * (D / 32);
+    b_pow2 = true;
+  }
+  for (int r0 = 0; r0 < nrows; r0 += 16 * kMT) {
+    v4f ag[kMT], au[kMT];
+#pragma unroll
+    for (int t = 0; t < kMT; ++t) {
+      ag[t] = v4f{0.f, 0.f, 0.f, 0.f};
+      au[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+    // token row pointer of this lane for each tile (A row = lane & 15)
+    const uint16_t* arow[kMT];
+#pragma unroll
+    for (int t = 0; t < kMT; ++t) {
+      const int r = r0 + t * 16 + nl;
+      int tok = -1;
+      if (r < nrows) tok = SHARED ? r : ws.perm_token[row0 + r];
+      arow[t] = tok >= 0 ? x + int64_t(tok) * D : nullptr;
+    }
+    const int ntiles = min(kMT, (nrows - r0 + 15) / 16);
+    for (int kb = kb0; kb < kb1; kb += kMoeUnroll) {
+      v8i b1[kMoeUnroll], b3[kMoeUnroll];
+      int e1[kMoeUnroll], e3[kMoeUnroll];
+      float f1[kMoeUnroll], f3[kMoeUnroll];
+#pragma unroll
+      for (int q = 0; q < kMoeUnroll; ++q) {
+        const int kk = kb + q;
+        if (kk < kb1) {
+          if (SHARED) {
+            b1[q] = b_fp8(w1row, kk, g);
+            b3[q] = b_fp8(w3row, kk, g);
+            fp8_wscale(d.sh_w1_s, int64_t(f0 >> 7) * nkb + kk, d.shared_w_scale_kind, e1[q], f1[q]);
+            fp8_wscale(d.sh_w3_s, int64_t(f0 >> 7) * nkb + kk, d.shared_w_scale_kind, e3[q], f3[q]);
+          } else {
+            b1[q] = b_fp4(w1row, kk, g);
+            b3[q] = b_fp4(w3row, kk, g);
+            e1[q] = b_fp4_scale(s1row, kk, g);
+            e3[q] = b_fp4_scale(s3row, kk, g);
+            f1[q] = f3[q] = 1.0f;
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kMT; ++t) {
+        if (t >= ntiles) break;
+#pragma unroll
+        for (int q = 0; q < kMoeUnroll; ++q) {
+          const int kk = kb + q;
+          if (kk < kb1) {
+            const AOp a = a_from_bf16(arow[t], kk, g, a_pow2);
+            if (SHARED) {
+              mma_step<kFmtFp8, kFmtFp8>(ag[t], a, b1[q], e1[q], f1[q], a_pow2, b_pow2, lane);
+              mma_step<kFmtFp8, kFmtFp8>(au[t], a, b3[q], e3[q], f3[q], a_pow2, b_pow2, lane);
+            } else {
+              mma_step<kFmtFp8, kFmtFp4>(ag[t], a, b1[q], e1[q], f1[q], a_pow2, true, lane);
+              mma_step<kFmtFp8, kFmtFp4>(au[t], a, b3[q], e3[q], f3[q], a_pow2, true, lane);
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kMT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        red[wave][0][t][lane][i] = ag[t][i];
+        red[wave][1][t][lane][i] = au[t][i];
+      }
+    __syncthreads();
+    // wave w finishes tile w: SwiGLU with clamp, x routing weight, bf16 h
+    if (wave < ntiles) {
+      const int t = wave;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = r0 + t * 16 + g * 4 + i;
+        float gs = red[0][0][t][lane][i];
+        gs += red[1][0][t][lane][i];
+        gs += red[2][0][t][lane][i];
+        gs += red[3][0][t][lane][i];
+        float us = red[0][1][t][lane][i];
+        us += red[1][1][t][lane][i];
+        us += red[2][1][t][lane][i];
+        us += red[3][1][t][lane][i];
+        if (r < nrows) {
+          float gv = bf16_round(gs), uv = bf16_round(us);
+          if (d.swiglu_limit > 0.0f) {
+            uv = fminf(fmaxf(uv, -d.swiglu_limit), d.swiglu_limit);
+            gv = fminf(gv, d.swiglu_limit);
+          }
+          float hv = silu_f32(gv) * uv;
+          if (SHARED) {
+            ws.sh_h[int64_t(r) * I + f0 + nl] = f32_to_bf16(hv);
+          } else {
+            const int p = row0 + r;
+            const float wt = ws.weights[int64_t(ws.perm_token[p]) * d.topk + ws.perm_slot[p]];
+            ws.h[int64_t(p) * I + f0 + nl] = f32_to_bf16(wt * hv);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int MT>
+__global__ __launch_bounds__(kMoeThreads) void w13_kernel(wz_moe_desc d, MoeWs ws,
+                                                          const uint16_t* __restrict__ x, int T,
+                                                          int n_shared_items) {
+  __shared__ float red[4 * 2 * MT * kWave * 4];
+  const int item = blockIdx.x;
+  const int ftiles = d.inter / 16;
+  if (item < n_shared_items) {
+    w13_item<true, MT>(d, ws, x, T, item * 16, -1, 0, T, red);
+    return;
+  }
+  const int r = item - n_shared_items;
+  const int u = r / ftiles, ft = r % ftiles;
+  if (u >= ws.n_active[0]) return;
+  w13_item<false, MT>(d, ws, x, T, ft * 16, ws.active[u], ws.act_off[u], ws.act_cnt[u], red);
+}
+
+// -------------------------------------------------------------------- w2 ----
+
+// red: LDS [4 waves][MT][64][4] floats.
+template <bool SHARED, int kMT>
+__device__ void w2_item(const wz_moe_desc& d, const MoeWs& ws, int T, int n0, int e, int row0,
+                        int nrows, float* red_) {
+  auto red = reinterpret_cast<float(*)[kMT][kWave][4]>(red_);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nl = lane & 15, g = lane >> 4;
+  const int D = d.dim, I = d.inter;
+  const int nkb = I / 128;
+  const int kb0 = (wave * nkb) / 4, kb1 = ((wave + 1) * nkb) / 4;
+  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
+  const uint8_t *wrow, *srow = nullptr;
+  bool b_pow2;
+  if (SHARED) {
+    wrow = static_cast<const uint8_t*>(d.sh_w2) + int64_t(n0 + nl) * I;
+    b_pow2 = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  } else {
+    const int64_t ebase = int64_t(e) * D;
+    wrow = static_cast<const uint8_t*>(d.w2) + (ebase + n0 + nl) * (I / 2);
+    srow = static_cast<const uint8_t*>(d.w2_s) + (ebase + n0 + nl) * (I / 32);
+    b_pow2 = true;
+  }
+  const uint16_t* hbase = SHARED ? ws.sh_h : ws.h + int64_t(row0) * I;
+  for (int r0 = 0; r0 < nrows; r0 += 16 * kMT) {
+    v4f acc[kMT];
+#pragma unroll
+    for (int t = 0; t < kMT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    const uint16_t* arow[kMT];
+#pragma unroll
+    for (int t = 0; t < kMT; ++t) {
+      const int r = r0 + t * 16 + nl;
+      arow[t] = r < nrows ? hbase + int64_t(r) * I : nullptr;
+    }
+    const int ntiles = min(kMT, (nrows - r0 + 15) / 16);
+    for (int kb = kb0; kb < kb1; kb += kMoeUnroll) {
+      v8i bw[kMoeUnroll];
+      int es[kMoeUnroll];
+      float fs[kMoeUnroll];
+#pragma unroll
+      for (int q = 0; q < kMoeUnroll; ++q) {
+        const int kk = kb + q;
+        if (kk < kb1) {
+          if (SHARED) {
+            bw[q] = b_fp8(wrow, kk, g);
+            fp8_wscale(d.sh_w2_s, int64_t(n0 >> 7) * nkb + kk, d.shared_w_scale_kind, es[q], fs[q]);
+          } else {
+            bw[q] = b_fp4(wrow, kk, g);
+            es[q] = b_fp4_scale(srow, kk, g);
+            fs[q] = 1.0f;
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kMT; ++t) {
+        if (t >= ntiles) break;
+#pragma unroll
+        for (int q = 0; q < kMoeUnroll; ++q) {
+          const int kk = kb + q;
+          if (kk < kb1) {
+            const AOp a = a_from_bf16(arow[t], kk, g, a_pow2);
+            if (SHARED)
+              mma_step<kFmtFp8, kFmtFp8>(acc[t], a, bw[q], es[q], fs[q], a_pow2, b_pow2, lane);
+            else
+              mma_step<kFmtFp8, kFmtFp4>(acc[t], a, bw[q], es[q], fs[q], a_pow2, true, lane);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kMT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][t][lane][i] = acc[t][i];
+    __syncthreads();
+    if (wave < ntiles) {
+      const int t = wave;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = r0 + t * 16 + g * 4 + i;
+        float v = red[0][t][lane][i];
+        v += red[1][t][lane][i];
+        v += red[2][t][lane][i];
+        v += red[3][t][lane][i];
+        if (r < nrows) {
+          if (SHARED)
+            ws.sh_out[int64_t(r) * D + n0 + nl] = f32_to_bf16(v);
+          else
+            ws.out2[int64_t(row0 + r) * D + n0 + nl] = f32_to_bf16(v);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int MT>
+__global__ __launch_bounds__(kMoeThreads) void w2_kernel(wz_moe_desc d, MoeWs ws, int T,
+                                                         int n_shared_items) {
+  __shared__ float red[4 * MT * kWave * 4];
+  const int item = blockIdx.x;
+  const int ntiles = d.dim / 16;
+  if (item < n_shared_items) {
+    w2_item<true, MT>(d, ws, T, item * 16, -1, 0, T, red);
+    return;
+  }
+  const int r = item - n_shared_items;
+  const int u = r / ntiles, nt = r % ntiles;
+  if (u >= ws.n_active[0]) return;
+  w2_item<false, MT>(d, ws, T, nt * 16, ws.active[u], ws.act_off[u], ws.act_cnt[u], red);
+}
+
+// --------------------------------------------------------------- combine ----
+
+__global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int D,
+                                                      uint16_t* __restrict__ y) {
+  const int t = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;  // 8-column chunk
+  if (c * 8 >= D) return;
+  int ps[16];
+  for (int j = 0; j < k; ++j) ps[j] = ws.pos[int64_t(t) * k + j];
+  // ascending permuted position == ascending expert id
+  for (int i = 1; i < k; ++i) {
+    int v = ps[i], j = i - 1;
+    while (j >= 0 && ps[j] > v) {
+      ps[j + 1] = ps[j];
+      --j;
+    }
+    ps[j + 1] = v;
+  }
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  int prev_e = -1;
+  for (int j = 0; j < k; ++j) {
+    const int p = ps[j];
+    const int pe = ws.idx[int64_t(ws.perm_token[p]) * k + ws.perm_slot[p]];
+    if (pe == prev_e) continue;  // repeated expert of a hash-routed token: counted once
+    prev_e = pe;
+    const v4i v = load16(ws.out2 + int64_t(p) * D + c * 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] += bf16lo(uint32_t(v[i]));
+      acc[2 * i + 1] += bf16hi(uint32_t(v[i]));
+    }
+  }
+  const v4i sv = load16(ws.sh_out + int64_t(t) * D + c * 8);
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = acc[2 * i] + bf16lo(uint32_t(sv[i]));
+    const float hi = acc[2 * i + 1] + bf16hi(uint32_t(sv[i]));
+    o[i] = uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+  }
+  *reinterpret_cast<v4i*>(y + int64_t(t) * D + c * 8) = v4i{int(o[0]), int(o[1]), int(o[2]), int(o[3])};
+}
+
+__global__ void export_routing_kernel(const MoeWs ws, int P, float* __restrict__ w_out,
+                                      int64_t* __restrict__ i_out) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= P) return;
+  if (w_out) w_out[p] = ws.weights[p];
+  if (i_out) i_out[p] = ws.idx[p];
+}
+
+// ------------------------------------------------------------------ host ----
+
+static int validate(const wz_moe_desc* d, int64_t T, const void* ws, size_t ws_bytes,
+                    const char* what) {
+  if (!d) return set_error(WZ_EINVAL, "%s: null descriptor", what);
+  if (d->dim <= 0 || d->dim % 128 || d->inter <= 0 || d->inter % 128)
+    return set_error(WZ_EINVAL, "%s: dim=%d and inter=%d must be positive multiples of 128", what,
+                     d->dim, d->inter);
+  if (d->n_experts <= 0 || d->n_experts > kMaxExperts)
+    return set_error(WZ_EINVAL, "%s: n_experts=%d outside 1..%d", what, d->n_experts, kMaxExperts);
+  if (d->topk <= 0 || d->topk > 16 || d->topk > d->n_experts)
+    return set_error(WZ_EINVAL, "%s: topk=%d outside 1..min(16, n_experts)", what, d->topk);
+  if (T < 0 || T * d->topk > kMaxPairs)
+    return set_error(WZ_EINVAL, "%s: T=%lld x topk=%d exceeds %d routed pairs", what, (long long)T,
+                     d->topk, kMaxPairs);
+  if (d->score_func < 0 || d->score_func > 2)
+    return set_error(WZ_EINVAL, "%s: unknown score_func %d", what, d->score_func);
+  if (d->act_scale_kind < 0 || d->act_scale_kind > 2)
+    return set_error(WZ_EINVAL, "%s: unknown act_scale_kind %d", what, d->act_scale_kind);
+  if (!d->gate_w) return set_error(WZ_EINVAL, "%s: gate weight missing", what);
+  if (d->tid2eid && d->vocab <= 0) return set_error(WZ_EINVAL, "%s: tid2eid without vocab", what);
+  if (!d->tid2eid && !d->gate_bias && d->score_func == WZ_SCORE_SQRTSOFTPLUS) {
+    // a score-routed layer without bias is legal (bias optional), nothing to check
+  }
+  if (!ws && T > 0) return set_error(WZ_EINVAL, "%s: null workspace", what);
+  const size_t need = moe_ws_layout(d, T, nullptr).bytes;
+  if (ws_bytes < need)
+    return set_error(WZ_ESPACE, "%s: workspace %zu bytes < %zu needed for T=%lld", what, ws_bytes,
+                     need, (long long)T);
+  return WZ_OK;
+}
+
+static int launch_routing(const wz_moe_desc* d, const MoeWs& w, const void* x,
+                          const int64_t* input_ids, int64_t T, hipStream_t stream) {
+  const int E = d->n_experts, k = d->topk, D = d->dim;
+  if (d->tid2eid && !input_ids) return set_error(WZ_EINVAL, "moe: hash-routed layer needs input_ids");
+  hipLaunchKernelGGL(gate_dot_kernel, dim3((E + 3) / 4, unsigned((T + kGateTok - 1) / kGateTok)), dim3(256),
+                     0, stream, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(d->gate_w),
+                     w.scores, int(T), E, D);
+  if (int rc = check_launch("moe gate")) return rc;
+  hipLaunchKernelGGL(topk_kernel, dim3(unsigned((T + 3) / 4)), dim3(256), 0, stream, w.scores,
+                     d->tid2eid ? nullptr : d->gate_bias, d->tid2eid, input_ids, d->vocab, int(T), E,
+                     k, d->score_func, d->route_scale, w.weights, w.idx);
+  if (int rc = check_launch("moe topk")) return rc;
+  hipLaunchKernelGGL(perm_kernel, dim3(1), dim3(kRouteThreads), 0, stream, w.idx, int(T), E, k,
+                     w.offsets, w.active, w.act_off, w.act_cnt, w.n_active, w.perm_token,
+                     w.perm_slot, w.pos);
+  return check_launch("moe perm");
+}
+
+}  // namespace wz
+
+extern "C" size_t wz_moe_workspace_bytes(const wz_moe_desc* d, int64_t T) {
+  if (!d || T < 0) return 0;
+  return wz::moe_ws_layout(d, T, nullptr).bytes;
+}
+
+extern "C" int wz_moe_workspace_init(void* ws, size_t ws_bytes, hipStream_t stream) {
+  (void)ws;
+  (void)ws_bytes;
+  (void)stream;
+  return WZ_OK;
+}
+
+extern "C" int wz_moe_route(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids,
+                            int64_t T, float* weights, int64_t* indices, int32_t* offsets,
+                            int32_t* perm_token, int32_t* perm_slot, void* ws, size_t ws_bytes,
+                            hipStream_t stream) {
+  using namespace wz;
+  if (int rc = validate(d, T, ws, ws_bytes, "moe_route")) return rc;
+  if (T == 0) return WZ_OK;
+  const MoeWs w = moe_ws_layout(d, T, static_cast<uint8_t*>(ws));
+  if (int rc = launch_routing(d, w, x_bf16, input_ids, T, stream)) return rc;
+  const int P = int(T * d->topk);
+  hipLaunchKernelGGL(export_routing_kernel, dim3((P + 255) / 256), dim3(256), 0, stream, w, P, weights,
+                     indices);
+  if (int rc = check_launch("moe_route export")) return rc;
+  if (offsets && hipMemcpyAsync(offsets, w.offsets, sizeof(int32_t) * (d->n_experts + 1),
+                                hipMemcpyDeviceToDevice, stream) != hipSuccess)
+    return set_error(WZ_ELAUNCH, "moe_route: offsets copy failed");
+  if (perm_token && hipMemcpyAsync(perm_token, w.perm_token, sizeof(int32_t) * P,
+                                   hipMemcpyDeviceToDevice, stream) != hipSuccess)
+    return set_error(WZ_ELAUNCH, "moe_route: perm copy failed");
+  if (perm_slot && hipMemcpyAsync(perm_slot, w.perm_slot, sizeof(int32_t) * P,
+                                  hipMemcpyDeviceToDevice, stream) != hipSuccess)
+    return set_error(WZ_ELAUNCH, "moe_route: perm copy failed");
+  return WZ_OK;
+}
+
+extern "C" int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids,
+                              int64_t T, void* y_bf16, float* weights_out, int64_t* indices_out,
+                              void* ws, size_t ws_bytes, hipStream_t stream) {
+  using namespace wz;
+  if (int rc = validate(d, T, ws, ws_bytes, "moe_forward")) return rc;
+  if (T == 0) return WZ_OK;
+  if (!x_bf16 || !y_bf16) return set_error(WZ_EINVAL, "moe_forward: null x or y");
+  if (!d->w13 || !d->w13_s || !d->w2 || !d->w2_s || !d->sh_w1 || !d->sh_w1_s || !d->sh_w3 ||
+      !d->sh_w3_s || !d->sh_w2 || !d->sh_w2_s)
+    return set_error(WZ_EINVAL, "moe_forward: expert weights missing");
+  const MoeWs w = moe_ws_layout(d, T, static_cast<uint8_t*>(ws));
+  if (int rc = launch_routing(d, w, x_bf16, input_ids, T, stream)) return rc;
+  const int E = d->n_experts, k = d->topk, D = d->dim, I = d->inter;
+  const int64_t P = T * k;
+  const int u_max = int(P < E ? P : E);
+  const int sh13 = I / 16, sh2 = D / 16;
+  const dim3 g13(unsigned(sh13 + u_max * (I / 16))), g2(unsigned(sh2 + u_max * (D / 16)));
+  const uint16_t* xb = static_cast<const uint16_t*>(x_bf16);
+  if (T <= 16) {
+    hipLaunchKernelGGL(w13_kernel<1>, g13, dim3(kMoeThreads), 0, stream, *d, w, xb, int(T), sh13);
+  } else {
+    hipLaunchKernelGGL(w13_kernel<4>, g13, dim3(kMoeThreads), 0, stream, *d, w, xb, int(T), sh13);
+  }
+  if (int rc = check_launch("moe w13")) return rc;
+  if (T <= 16) {
+    hipLaunchKernelGGL(w2_kernel<1>, g2, dim3(kMoeThreads), 0, stream, *d, w, int(T), sh2);
+  } else {
+    hipLaunchKernelGGL(w2_kernel<4>, g2, dim3(kMoeThreads), 0, stream, *d, w, int(T), sh2);
+  }
+  if (int rc = check_launch("moe w2")) return rc;
+  hipLaunchKernelGGL(combine_kernel, dim3(unsigned((D / 8 + 255) / 256), unsigned(T)), dim3(256), 0,
+                     stream, w, k, D, static_cast<uint16_t*>(y_bf16));
+  if (int rc = check_launch("moe combine")) return rc;
+  if (weights_out || indices_out) {
+    hipLaunchKernelGGL(export_routing_kernel, dim3(unsigned((P + 255) / 256)), dim3(256), 0, stream, w,
+                       int(P), weights_out, indices_out);
+    if (int rc = check_launch("moe export")) return rc;
+  }
+  return WZ_OK;
+}

@@ -1,0 +1,375 @@
+"""MoE layer on the HIP library: the drop-in for the reference's MoE dispatch chain.
+
+Two ways in:
+
+* :class:`HipMoE` — a standalone layer over expert-bank tensors
+  (w13 ``[E, 2I, D/2]`` packed e2m1 + ``[E, 2I, D/32]`` e8m0, w2 ``[E, D, I/2]``
+  + ``[E, D, I/32]``, the bank layout of wanferenz/kernels/fp4_grouped.py:142-188)
+  with an FP8 shared expert and a bf16 gate.  ``forward(x, input_ids)`` is one
+  stream-ordered sequence of launches with no host sync and no allocation
+  besides its output, so a decode step can be captured in a HIP graph.
+* :func:`install` — replaces ``MoE.forward`` of a loaded reference model module
+  at class level, following the reference's install protocol
+  (fp4_grouped.py:339-351): the previous forward is kept in ``_REF_FORWARD``,
+  the new function carries a ``_v4_hip_moe`` marker and installing twice is a
+  no-op.  A layer the HIP path cannot serve (``world_size > 1``, an expert
+  dtype other than MXFP4, a shared expert other than FP8) declines to
+  ``_REF_FORWARD`` with a reason tally in ``moe._hip_declined``, as
+  fp4_grouped._decline does (fp4_grouped.py:256-262).  The declined path still
+  runs on the HIP library when :func:`wanferenz_amd.kernels.install` has
+  rebound the module's act_quant / fp8_gemm / fp4_gemm.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+from . import _native as N
+
+SCORE_FUNCS = {"softmax": N.WZ_SCORE_SOFTMAX, "sigmoid": N.WZ_SCORE_SIGMOID,
+               "sqrtsoftplus": N.WZ_SCORE_SQRTSOFTPLUS}
+
+
+class WzMoeDesc(ctypes.Structure):
+    """ctypes mirror of ``wz_moe_desc`` (include/wanferenz_amd.h)."""
+
+    _fields_ = [
+        ("dim", ctypes.c_int32), ("inter", ctypes.c_int32), ("n_experts", ctypes.c_int32),
+        ("topk", ctypes.c_int32), ("score_func", ctypes.c_int32),
+        ("act_scale_kind", ctypes.c_int32), ("shared_w_scale_kind", ctypes.c_int32),
+        ("route_scale", ctypes.c_float), ("swiglu_limit", ctypes.c_float),
+        ("vocab", ctypes.c_int64),
+        ("gate_w", ctypes.c_void_p), ("gate_bias", ctypes.c_void_p), ("tid2eid", ctypes.c_void_p),
+        ("w13", ctypes.c_void_p), ("w13_s", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p), ("w2_s", ctypes.c_void_p),
+        ("sh_w1", ctypes.c_void_p), ("sh_w1_s", ctypes.c_void_p),
+        ("sh_w3", ctypes.c_void_p), ("sh_w3_s", ctypes.c_void_p),
+        ("sh_w2", ctypes.c_void_p), ("sh_w2_s", ctypes.c_void_p),
+    ]
+
+
+@dataclass
+class MoEConfig:
+    dim: int
+    inter: int
+    n_experts: int
+    topk: int
+    score_func: str = "sqrtsoftplus"
+    route_scale: float = 1.0
+    swiglu_limit: float = 0.0
+    act_scale_kind: int = N.WZ_SCALE_UE8M0       # reference scale_fmt="ue8m0"
+    shared_w_scale_kind: int = N.WZ_WSCALE_E8M0
+
+
+@dataclass
+class MoEWeights:
+    """Device tensors of one MoE layer (byte views; formats in the module docstring)."""
+
+    gate_w: torch.Tensor                  # bf16 [E, D]
+    gate_bias: Optional[torch.Tensor]     # fp32 [E], None for hash-routed layers
+    w13: torch.Tensor                     # uint8 [E, 2I, D/2]
+    w13_s: torch.Tensor                   # uint8 [E, 2I, D/32]
+    w2: torch.Tensor                      # uint8 [E, D, I/2]
+    w2_s: torch.Tensor                    # uint8 [E, D, I/32]
+    sh_w1: torch.Tensor                   # uint8 (e4m3) [I, D]
+    sh_w1_s: torch.Tensor                 # [I/128, D/128] e8m0 bytes or fp32
+    sh_w3: torch.Tensor
+    sh_w3_s: torch.Tensor
+    sh_w2: torch.Tensor                   # [D, I]
+    sh_w2_s: torch.Tensor                 # [D/128, I/128]
+    tid2eid: Optional[torch.Tensor] = None  # int32 [vocab, k]
+
+
+def _u8(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.uint8) if t.dtype != torch.float32 else t
+
+
+def _check_layout(cfg: MoEConfig, w: MoEWeights):
+    D, I, E, k = cfg.dim, cfg.inter, cfg.n_experts, cfg.topk
+
+    def need(name, t, shape, dtypes=None):
+        if t is None:
+            raise ValueError(f"MoE weights: {name} missing")
+        if tuple(t.shape) != tuple(shape):
+            raise ValueError(f"MoE weights: {name} has shape {tuple(t.shape)}, want {tuple(shape)}")
+        if not t.is_contiguous():
+            raise ValueError(f"MoE weights: {name} must be contiguous")
+        if not t.is_cuda:
+            raise RuntimeError(f"MoE weights: {name} must be on the GPU (no CPU fallback)")
+        if dtypes and t.dtype not in dtypes:
+            raise TypeError(f"MoE weights: {name} dtype {t.dtype} not in {dtypes}")
+
+    byte_types = (torch.uint8, torch.float4_e2m1fn_x2, torch.float8_e8m0fnu, torch.float8_e4m3fn, torch.int8)
+    need("gate_w", w.gate_w, (E, D), (torch.bfloat16,))
+    if w.tid2eid is None:
+        if w.gate_bias is not None:
+            need("gate_bias", w.gate_bias, (E,), (torch.float32,))
+    else:
+        if w.tid2eid.dim() != 2 or w.tid2eid.size(1) != k or w.tid2eid.dtype != torch.int32:
+            raise ValueError("MoE weights: tid2eid must be int32 [vocab, k]")
+    need("w13", w.w13, (E, 2 * I, D // 2), byte_types)
+    need("w13_s", w.w13_s, (E, 2 * I, D // 32), byte_types)
+    need("w2", w.w2, (E, D, I // 2), byte_types)
+    need("w2_s", w.w2_s, (E, D, I // 32), byte_types)
+    sdt = (torch.float32,) if cfg.shared_w_scale_kind == N.WZ_WSCALE_F32 else byte_types
+    need("sh_w1", w.sh_w1, (I, D), byte_types)
+    need("sh_w3", w.sh_w3, (I, D), byte_types)
+    need("sh_w2", w.sh_w2, (D, I), byte_types)
+    need("sh_w1_s", w.sh_w1_s, ((I + 127) // 128, (D + 127) // 128), sdt)
+    need("sh_w3_s", w.sh_w3_s, ((I + 127) // 128, (D + 127) // 128), sdt)
+    need("sh_w2_s", w.sh_w2_s, ((D + 127) // 128, (I + 127) // 128), sdt)
+
+
+class HipMoE:
+    """One MoE layer served by the HIP library (see module docstring)."""
+
+    def __init__(self, cfg: MoEConfig, weights: MoEWeights, max_tokens: int = 16):
+        if cfg.score_func not in SCORE_FUNCS:
+            raise ValueError(f"unknown score_func {cfg.score_func!r}")
+        _check_layout(cfg, weights)
+        self.cfg = cfg
+        self.weights = weights
+        w = weights
+        d = WzMoeDesc()
+        d.dim, d.inter, d.n_experts, d.topk = cfg.dim, cfg.inter, cfg.n_experts, cfg.topk
+        d.score_func = SCORE_FUNCS[cfg.score_func]
+        d.act_scale_kind = cfg.act_scale_kind
+        d.shared_w_scale_kind = cfg.shared_w_scale_kind
+        d.route_scale = cfg.route_scale
+        d.swiglu_limit = cfg.swiglu_limit
+        d.vocab = 0 if w.tid2eid is None else w.tid2eid.size(0)
+        d.gate_w = w.gate_w.data_ptr()
+        d.gate_bias = None if (w.gate_bias is None or w.tid2eid is not None) else w.gate_bias.data_ptr()
+        d.tid2eid = None if w.tid2eid is None else w.tid2eid.data_ptr()
+        for name in ("w13", "w13_s", "w2", "w2_s", "sh_w1", "sh_w1_s", "sh_w3", "sh_w3_s", "sh_w2", "sh_w2_s"):
+            setattr(d, name, getattr(w, name).data_ptr())
+        self.desc = d
+        self.device = w.gate_w.device
+        self._ws = None
+        self._ws_tokens = 0
+        self.reserve(max_tokens)
+
+    # -- workspace -----------------------------------------------------------
+    def workspace_bytes(self, T: int) -> int:
+        return int(N.lib().wz_moe_workspace_bytes(ctypes.byref(self.desc), T))
+
+    def reserve(self, T: int):
+        """Allocate scratch for up to T tokens (outside any graph capture)."""
+        if T <= self._ws_tokens and self._ws is not None:
+            return
+        nbytes = max(self.workspace_bytes(T), 256)
+        self._ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        N.call("wz_moe_workspace_init", self._ws.data_ptr(), nbytes, N.stream_handle(self.device))
+        self._ws_tokens = T
+
+    def _ws_for(self, T: int):
+        if T > self._ws_tokens:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    f"HipMoE: T={T} exceeds the reserved workspace ({self._ws_tokens} tokens) "
+                    "inside graph capture; call reserve() before capturing")
+            self.reserve(T)
+        return self._ws
+
+    # -- compute -------------------------------------------------------------
+    def forward(self, x: torch.Tensor, input_ids: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None, routing_out=None) -> torch.Tensor:
+        """x [..., D] bf16 -> y [..., D] bf16 (MoE.forward, architecture.py:777-794)."""
+        D = self.cfg.dim
+        if x.dtype != torch.bfloat16:
+            raise TypeError(f"HipMoE: x must be bf16, got {x.dtype}")
+        if not x.is_cuda:
+            raise RuntimeError("HipMoE: x must be on the GPU (no CPU fallback)")
+        xv = x.reshape(-1, D)
+        if not xv.is_contiguous():
+            xv = xv.contiguous()
+        T = xv.size(0)
+        ids = None
+        if self.weights.tid2eid is not None:
+            if input_ids is None:
+                raise ValueError("HipMoE: a hash-routed layer needs input_ids")
+            ids = input_ids.reshape(-1).to(torch.int64)
+            if ids.numel() != T:
+                raise ValueError("HipMoE: input_ids must have one id per token")
+            ids = ids.contiguous()
+        y = out if out is not None else torch.empty_like(xv)
+        ws = self._ws_for(T)
+        wp = ip = None
+        if routing_out is not None:
+            wp, ip = routing_out[0].data_ptr(), routing_out[1].data_ptr()
+        N.call("wz_moe_forward", ctypes.byref(self.desc), xv.data_ptr(),
+               None if ids is None else ids.data_ptr(), T, y.data_ptr(), wp, ip,
+               ws.data_ptr(), ws.numel(), N.stream_handle(self.device))
+        return y.view(x.shape)
+
+    __call__ = forward
+
+    def route(self, x: torch.Tensor, input_ids: Optional[torch.Tensor] = None):
+        """Gate.forward + canonical permutation: (weights, indices, offsets, perm_token, perm_slot)."""
+        D, E, k = self.cfg.dim, self.cfg.n_experts, self.cfg.topk
+        xv = x.reshape(-1, D).contiguous()
+        T = xv.size(0)
+        ids = None
+        if self.weights.tid2eid is not None:
+            ids = input_ids.reshape(-1).to(torch.int64).contiguous()
+        dev = self.device
+        weights = torch.empty(T, k, dtype=torch.float32, device=dev)
+        indices = torch.empty(T, k, dtype=torch.int64, device=dev)
+        offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        ptok = torch.empty(T * k, dtype=torch.int32, device=dev)
+        pslot = torch.empty(T * k, dtype=torch.int32, device=dev)
+        ws = self._ws_for(T)
+        N.call("wz_moe_route", ctypes.byref(self.desc), xv.data_ptr(),
+               None if ids is None else ids.data_ptr(), T, weights.data_ptr(), indices.data_ptr(),
+               offsets.data_ptr(), ptok.data_ptr(), pslot.data_ptr(), ws.data_ptr(), ws.numel(),
+               N.stream_handle(dev))
+        return weights, indices, offsets, ptok, pslot
+
+
+# ---------------------------------------------------------------- drop-in -----
+
+_REF_FORWARD = None
+_MOD = None
+
+
+def _act_kind_of_module(mod) -> int:
+    scale_fmt = getattr(mod, "scale_fmt", None)
+    scale_dtype = getattr(mod, "scale_dtype", torch.float32)
+    if scale_fmt is None:
+        return N.WZ_SCALE_F32
+    return N.WZ_SCALE_UE8M0 if scale_dtype == torch.float8_e8m0fnu else N.WZ_SCALE_UE8M0_F32
+
+
+def bank_of(moe) -> Optional[dict]:
+    """The expert bank of a reference MoE, building it the way _relayout_moe does.
+
+    Per-expert parameters become views into one contiguous bank per group
+    (w13 = w1 rows then w3 rows; w2), fp4_grouped.py:142-188, so the routed
+    experts ARE the bank and no duplicate is kept.
+    """
+    bank = getattr(moe, "_grouped_bank", None)
+    if bank:
+        return bank
+    lo, hi = moe.experts_start_idx, moe.experts_end_idx
+    experts = [moe.experts[i] for i in range(lo, hi)]
+    if not experts or experts[0].w1.weight.dtype != torch.float4_e2m1fn_x2:
+        return None
+    groups = (("w13", ("w1", "w3")), ("w2", ("w2",)))
+    bank = {}
+    with torch.no_grad():
+        for key, kinds in groups:
+            for attr, suffix in (("weight", ""), ("scale", "_s")):
+                first = [getattr(getattr(experts[0], kk), attr) for kk in kinds]
+                rows = [t.shape[0] for t in first]
+                shape = (len(experts), sum(rows)) + tuple(first[0].shape[1:])
+                b = torch.empty(shape, dtype=first[0].dtype, device=first[0].device)
+                bu = b.view(torch.uint8)
+                for j, e in enumerate(experts):
+                    off = 0
+                    for n, kk in zip(rows, kinds):
+                        p = getattr(getattr(e, kk), attr)
+                        bu[j, off:off + n].copy_(p.detach().view(torch.uint8))
+                        p.data = b[j, off:off + n]
+                        off += n
+                bank[key + suffix] = b
+    moe._grouped_bank = bank
+    return bank
+
+
+def hip_moe_of(moe, mod=None) -> Optional[HipMoE]:
+    """Build (once) and cache the HipMoE view of a reference MoE module."""
+    h = getattr(moe, "_hip_moe", None)
+    if h is not None:
+        return h
+    mod = mod or _MOD
+    bank = bank_of(moe)
+    if bank is None:
+        return None
+    sh = moe.shared_experts
+    if sh.w1.weight.dtype != torch.float8_e4m3fn:
+        return None
+    e0 = moe.experts[moe.experts_start_idx]
+    gate = moe.gate
+    cfg = MoEConfig(
+        dim=moe.dim, inter=e0.w1.weight.shape[0], n_experts=moe.n_routed_experts,
+        topk=moe.n_activated_experts, score_func=gate.score_func,
+        route_scale=float(gate.route_scale), swiglu_limit=float(e0.swiglu_limit),
+        act_scale_kind=_act_kind_of_module(mod),
+        shared_w_scale_kind=N.WZ_WSCALE_E8M0 if sh.w1.scale.dtype == torch.float8_e8m0fnu else N.WZ_WSCALE_F32,
+    )
+    w = MoEWeights(
+        gate_w=gate.weight.data, gate_bias=None if gate.bias is None else gate.bias.data,
+        w13=bank["w13"], w13_s=bank["w13_s"], w2=bank["w2"], w2_s=bank["w2_s"],
+        sh_w1=sh.w1.weight.data, sh_w1_s=sh.w1.scale.data, sh_w3=sh.w3.weight.data,
+        sh_w3_s=sh.w3.scale.data, sh_w2=sh.w2.weight.data, sh_w2_s=sh.w2.scale.data,
+        tid2eid=gate.tid2eid.data if getattr(gate, "hash", False) else None,
+    )
+    h = HipMoE(cfg, w)
+    moe._hip_moe = h
+    return h
+
+
+def _decline(moe, why, x, input_ids):
+    tally = getattr(moe, "_hip_declined", None)
+    if tally is None:
+        tally = moe._hip_declined = {}
+    tally[why] = tally.get(why, 0) + 1
+    return _REF_FORWARD(moe, x, input_ids)
+
+
+def hip_forward(self, x, input_ids):
+    """Replacement for MoE.forward(self, x, input_ids) (architecture.py:777-794)."""
+    if int(getattr(_MOD, "world_size", 1) or 1) > 1:
+        return _decline(self, "world_size>1", x, input_ids)
+    if self.experts_start_idx != 0 or self.experts_end_idx != self.n_routed_experts:
+        return _decline(self, "partial-experts", x, input_ids)
+    h = hip_moe_of(self)
+    if h is None:
+        return _decline(self, "not-mxfp4-bank", x, input_ids)
+    y = h.forward(x, input_ids)
+    self._hip_steps = getattr(self, "_hip_steps", 0) + 1
+    return y
+
+
+hip_forward._v4_hip_moe = True
+
+
+def install(mod) -> bool:
+    """Replace mod.MoE.forward with the HIP layer (idempotent, marker ``_v4_hip_moe``)."""
+    global _REF_FORWARD, _MOD
+    _MOD = mod
+    if getattr(mod.MoE.forward, "_v4_hip_moe", False):
+        return False
+    _REF_FORWARD = mod.MoE.forward
+    mod.MoE.forward = hip_forward
+    return True
+
+
+def uninstall(mod) -> bool:
+    global _REF_FORWARD
+    if _REF_FORWARD is None or not getattr(mod.MoE.forward, "_v4_hip_moe", False):
+        return False
+    mod.MoE.forward = _REF_FORWARD
+    _REF_FORWARD = None
+    return True
+
+
+def coverage(module) -> dict:
+    """Per-layer (steps served, declines by reason), like fp4_grouped.coverage (:327-336)."""
+    out = {}
+    mods = module.modules() if hasattr(module, "modules") else [module]
+    for m in mods:
+        if hasattr(m, "experts") and hasattr(m, "experts_start_idx"):
+            out[getattr(m, "layer_id", len(out))] = (
+                getattr(m, "_hip_steps", 0), dict(getattr(m, "_hip_declined", {})))
+    return out
+
+
+def moe_chain(mod) -> str:
+    """Status string of the installed MoE chain (controls.moe_chain, controls.py:38-68)."""
+    f = mod.MoE.forward
+    return "hip>ref" if getattr(f, "_v4_hip_moe", False) else "ref"

@@ -143,3 +143,80 @@ def layer_stream(layer: int, stream: int) -> int:
 ROUTED_E8M0 = (119, 123)   # 2^-8 .. 2^-4 per 32-element block
 SHARED_E8M0 = (112, 116)   # 2^-15 .. 2^-11 per 128x128 block (keeps the shared
                            # expert's pre-activations O(1) for uniform e4m3 codes)
+
+
+# ------------------------------------------------------------ device fills ----
+
+
+def device_fill(t, key: int, mode: int, lo: float = 0.0, hi: float = 0.0, start: int = 0):
+    """Fill a contiguous device tensor (bytes, or float32 for mode 3) with the hash stream."""
+    from . import _native as N
+
+    if not t.is_contiguous():
+        raise ValueError("device_fill: tensor must be contiguous")
+    n = t.numel() if mode != FILL_F32_UNIFORM else t.numel()
+    N.call("wz_synth_fill", t.data_ptr(), n, key & 0xFFFFFFFFFFFFFFFF, start, mode, float(lo), float(hi),
+           N.stream_handle(t.device))
+    return t
+
+
+def synthetic_moe(cfg, seed: int = 0, layer: int = 0, device="cuda", hash_layer: bool = False,
+                  vocab: int = 64, bias_sigma: float = 0.01, bias=None):
+    """MoEWeights of one synthetic layer (streams as tests/golden/cases.make_inputs).
+
+    Expert banks and the FP8 shared expert are generated on the device by the
+    integer hash; the bf16 gate weight and fp32 bias are drawn on the host
+    (Box-Muller) and uploaded.  Returns (weights, host) where host holds the
+    host-side gate weight bits and bias.
+    """
+    import torch
+
+    from .moe import MoEWeights
+
+    D, I, E, k = cfg.dim, cfg.inter, cfg.n_experts, cfg.topk
+
+    def key(stream):
+        return stream_key(seed, layer_stream(layer, stream))
+
+    u8 = dict(dtype=torch.uint8, device=device)
+    lo, hi = ROUTED_E8M0
+    w13 = device_fill(torch.empty(E, 2 * I, D // 2, **u8), key(S_W13), FILL_U8)
+    w13_s = device_fill(torch.empty(E, 2 * I, D // 32, **u8), key(S_W13_S), FILL_E8M0, lo, hi)
+    w2 = device_fill(torch.empty(E, D, I // 2, **u8), key(S_W2), FILL_U8)
+    w2_s = device_fill(torch.empty(E, D, I // 32, **u8), key(S_W2_S), FILL_E8M0, lo, hi)
+    slo, shi = SHARED_E8M0
+    sh13 = device_fill(torch.empty(2 * I, D, **u8), key(S_SH_W13), FILL_E4M3)
+    sh13_s = device_fill(torch.empty(2 * I // 128, D // 128, **u8), key(S_SH_W13_S), FILL_E8M0, slo, shi)
+    sh2 = device_fill(torch.empty(D, I, **u8), key(S_SH_W2), FILL_E4M3)
+    sh2_s = device_fill(torch.empty(D // 128, I // 128, **u8), key(S_SH_W2_S), FILL_E8M0, slo, shi)
+    gw_bits = normal_bf16(key(S_GATE_W), (E, D), 0.02)
+    gate_w = torch.from_numpy(gw_bits.view(np.int16)).view(torch.bfloat16).to(device)
+    host = {"gate_w": gw_bits}
+    gate_bias = None
+    tid2eid = None
+    if hash_layer:
+        t2e = (draws(key(S_TID2EID), 0, vocab * k) % np.uint64(E)).astype(np.int32).reshape(vocab, k)
+        host["tid2eid"] = t2e
+        tid2eid = torch.from_numpy(t2e).to(device)
+    else:
+        b = normal_f32(key(S_GATE_BIAS), (E,), bias_sigma) if bias is None else np.asarray(bias, np.float32)
+        host["gate_bias"] = b
+        gate_bias = torch.from_numpy(b).to(device)
+    nb = I // 128
+    w = MoEWeights(gate_w=gate_w, gate_bias=gate_bias, w13=w13, w13_s=w13_s, w2=w2, w2_s=w2_s,
+                   sh_w1=sh13[:I], sh_w1_s=sh13_s[:nb], sh_w3=sh13[I:], sh_w3_s=sh13_s[nb:],
+                   sh_w2=sh2, sh_w2_s=sh2_s, tid2eid=tid2eid)
+    return w, host
+
+
+def zipf_bias(n_experts: int, s: float = 1.1, beta: float = 0.05, seed: int = 1) -> np.ndarray:
+    """Gate bias that skews expert popularity towards a Zipf(s) law.
+
+    bias_e = beta * log(p_e) with p_e proportional to rank_e^-s, where rank is a
+    seeded random permutation of the experts; beta sets the strength.
+    """
+    d = draws(stream_key(seed, 77), 0, n_experts)
+    rank = np.argsort(np.argsort(d)) + 1
+    p = rank.astype(np.float64) ** (-s)
+    p /= p.sum()
+    return (beta * np.log(p)).astype(np.float32)
