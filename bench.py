@@ -1,0 +1,269 @@
+"""Benchmark: DeepSeek-V4-Flash-shape MoE layer, decode, on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--T 4] [--layers 12] [--no-cpu]
+
+A step is one MoE layer forward (gate + top-6 routing + permute + MXFP4 routed
+experts + FP8 shared expert + combine) over T synthetic tokens, replayed from
+a HIP graph captured per layer.  Steps rotate over ``--layers`` independent
+layers (12 x 3.45 GB of expert banks resident in HBM) with a different input
+per layer, so the 256 MB Infinity Cache cannot serve repeated expert reads.
+
+Printed JSON line (one):
+  value       algorithmic HBM GB/s of the layer = sum over steps of
+              (U*13,369,344 + 25,167,360 + 2,098,176 + 4*T*D) bytes / time,
+              U = distinct experts the step's routing selected
+  ms_per_step layer latency (µs/layer = 1000 * ms_per_step)
+  roofline    the dominant kernel (moe_w13: routed w1/w3 + shared w1/w3),
+              algorithmic bytes per launch / its mean duration measured live
+              with HIP events on the launch stream
+  cpu_baseline the oracle (numpy restatement of the reference CPU path) on one
+              T-token layer, single thread
+  per_T       the same layer measured at T = 1, 2, 4, 8
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE layer µs + HBM GB/s (decode T=1-8); FP4 MFMA util (prefill T=2048)"
+HBM_PEAK_GBS = 8000.0
+D, I, E, K_TOP = 4096, 2048, 256, 6
+ROUTED_EXPERT_BYTES = 3 * (I * D // 2) + 3 * (I * D // 32)          # 13,369,344
+SHARED_BYTES = 3 * I * D + 3 * (I // 128) * (D // 128)              # 25,167,360
+GATE_BYTES = E * D * 2 + E * 4                                       # 2,098,176
+W13_ROUTED_BYTES = 2 * (I * D // 2) + 2 * (I * D // 32)             # 8,912,896
+W13_SHARED_BYTES = 2 * I * D + 2 * (I // 128) * (D // 128)          # 16,778,240
+
+
+def layer_bytes(U: int, T: int) -> int:
+    return U * ROUTED_EXPERT_BYTES + SHARED_BYTES + GATE_BYTES + 4 * T * D
+
+
+def w13_bytes(U: int, T: int) -> int:
+    # weights + x read (bf16) + h written (bf16, routed pairs and shared rows)
+    return U * W13_ROUTED_BYTES + W13_SHARED_BYTES + 2 * T * D + 2 * (T * K_TOP + T) * I
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--T", type=int, default=4)
+    ap.add_argument("--layers", type=int, default=12)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    return ap.parse_args()
+
+
+def build_layers(n_layers, dev, tmax):
+    from wanferenz_amd import _native as N
+    from wanferenz_amd import synth
+    from wanferenz_amd.moe import HipMoE, MoEConfig
+
+    cfg = MoEConfig(D, I, E, K_TOP, "sqrtsoftplus", 1.5, 10.0, N.WZ_SCALE_UE8M0, N.WZ_WSCALE_E8M0)
+    layers = []
+    for l in range(n_layers):
+        w, host = synth.synthetic_moe(cfg, seed=0, layer=l, device=dev)
+        layers.append((HipMoE(cfg, w, max_tokens=tmax), host))
+    return cfg, layers
+
+
+def make_inputs(n_layers, T, dev, salt=0):
+    import torch
+
+    from wanferenz_amd import synth
+
+    xs = []
+    for l in range(n_layers):
+        bits = synth.normal_bf16(synth.stream_key(1000 + salt, synth.layer_stream(l, synth.S_X)), (T, D), 1.0)
+        xs.append((bits, torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).to(dev)))
+    return xs
+
+
+def distinct_experts(layers, xs):
+    import torch
+
+    Us = []
+    for (moe, _), (_, x) in zip(layers, xs):
+        _, idx, _, _, _ = moe.route(x)
+        torch.cuda.synchronize()
+        Us.append(len(set(idx.cpu().numpy().ravel().tolist())))
+    return Us
+
+
+def capture(layers, xs):
+    import torch
+
+    graphs, outs = [], []
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for (moe, _), (_, x) in zip(layers, xs):
+            out = torch.empty_like(x)
+            for _ in range(2):
+                moe.forward(x, out=out)
+            outs.append(out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for (moe, _), (_, x), out in zip(layers, xs, outs):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            moe.forward(x, out=out)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    return graphs, outs
+
+
+def time_steps(graphs, steps, warmup):
+    import torch
+
+    L = len(graphs)
+    for i in range(warmup):
+        graphs[i % L].replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        graphs[i % L].replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / 1000.0, wall
+
+
+def kernel_times(layers, xs, reps=2):
+    """Eager pass with every library launch bracketed by HIP events."""
+    import torch
+
+    from wanferenz_amd._native import KernelTimer
+
+    for (moe, _), (_, x) in zip(layers, xs):
+        moe.forward(x)
+    torch.cuda.synchronize()
+    with KernelTimer(64 * len(layers) * reps) as kt:
+        for _ in range(reps):
+            for (moe, _), (_, x) in zip(layers, xs):
+                moe.forward(x)
+    torch.cuda.synchronize()
+    return kt.mean_ms()
+
+
+def measure_T(layers, T, steps, warmup, dev, salt):
+    xs = make_inputs(len(layers), T, dev, salt)
+    Us = distinct_experts(layers, xs)
+    graphs, _ = capture(layers, xs)
+    secs, wall = time_steps(graphs, steps, warmup)
+    L = len(layers)
+    total_bytes = sum(layer_bytes(Us[i % L], T) for i in range(steps))
+    kt = kernel_times(layers, xs)
+    return dict(T=T, secs=secs, wall=wall, Us=Us, total_bytes=total_bytes, kernels=kt, xs=xs)
+
+
+def cpu_baseline(layers, cfg, T, dev):
+    """Oracle on one T-token step of layer 0 (weights of the touched experts copied from HBM)."""
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    from oracle import moe as om
+    from oracle.numerics import e8m0_decode, from_bf16_bits
+    from wanferenz_amd import synth
+
+    moe, host = layers[0]
+    w = moe.weights
+    xb = synth.normal_bf16(synth.stream_key(1000, synth.layer_stream(0, synth.S_X)), (T, D), 1.0)
+    xf = from_bf16_bits(xb)
+    g = om.gate(xf, from_bf16_bits(host["gate_w"]), host["gate_bias"], K_TOP, "sqrtsoftplus", 1.5)
+    used = sorted(set(g.indices.ravel().tolist()))
+    ex = [None] * E
+    for e in used:
+        w13 = w.w13[e].cpu().numpy()
+        s13 = e8m0_decode(w.w13_s[e].cpu().numpy())
+        ex[e] = (om.Fp4Linear(w13[:I], s13[:I]), om.Fp4Linear(w13[I:], s13[I:]),
+                 om.Fp4Linear(w.w2[e].cpu().numpy(), e8m0_decode(w.w2_s[e].cpu().numpy())))
+    shared = (om.Fp8Linear(w.sh_w1.cpu().numpy(), e8m0_decode(w.sh_w1_s.cpu().numpy())),
+              om.Fp8Linear(w.sh_w3.cpu().numpy(), e8m0_decode(w.sh_w3_s.cpu().numpy())),
+              om.Fp8Linear(w.sh_w2.cpu().numpy(), e8m0_decode(w.sh_w2_s.cpu().numpy())))
+    p = om.MoEParams(D, I, E, K_TOP, from_bf16_bits(host["gate_w"]), host["gate_bias"], ex, shared,
+                     "sqrtsoftplus", 1.5, 10.0, True, None)
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        om.moe_forward(p, xf)
+        secs = time.perf_counter() - t0
+    nbytes = layer_bytes(len(used), T)
+    return {"value": round(nbytes / secs / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"one V4 MoE layer at T={T} (U={len(used)} experts, {nbytes/1e6:.1f} MB "
+                      f"algorithmic) through the numpy oracle, 1 thread: {secs:.2f} s",
+            "us_per_layer": round(secs * 1e6, 1)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(no multi-GPU path is built)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from wanferenz_amd import _native
+
+    _native.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg, layers = build_layers(args.layers, dev, 16)
+    torch.cuda.synchronize()
+    main_run = measure_T(layers, args.T, args.steps, args.warmup, dev, 0)
+    secs, T = main_run["secs"], args.T
+    value = main_run["total_bytes"] / secs / 1e9
+    ms = secs / args.steps * 1000.0
+    Umean = float(np.mean(main_run["Us"]))
+    kt = main_run["kernels"]
+    w13_ms = kt.get("moe_w13", float("nan"))
+    w13_b = float(np.mean([w13_bytes(u, T) for u in main_run["Us"]]))
+    achieved = w13_b / (w13_ms / 1000.0) / 1e9
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "mxfp4(e2m1)*fp8(e4m3)->fp32", "data": "synthetic",
+        "config": {"workload": f"DeepSeek-V4-Flash MoE layer decode, T={T} tokens: hidden 4096, "
+                               f"256 routed MXFP4 experts + 1 FP8 shared, top-6, intermediate 2048; "
+                               f"{args.layers} layers rotated, hipGraph per layer",
+                   "T": T, "layers": args.layers, "mean_distinct_experts": Umean},
+        "us_per_layer": round(ms * 1000.0, 2),
+        "tokens_per_s": round(T * args.steps / secs, 1),
+        "hbm_frac_layer": round(value / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": "moe_w13", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": round(w13_b),
+                     "mean_us": round(w13_ms * 1000.0, 2)},
+        "kernel_us": {k: round(v * 1000.0, 2) for k, v in sorted(kt.items())},
+    }
+    if not args.no_sweep:
+        sweep = {}
+        for Ts in (1, 2, 4, 8):
+            r = main_run if Ts == T else measure_T(layers, Ts, 120, 12, dev, Ts)
+            v = r["total_bytes"] / r["secs"] / 1e9
+            n = 120 if Ts != T else args.steps
+            sweep[str(Ts)] = {"us_per_layer": round(r["secs"] / n * 1e6, 2), "GB_s": round(v, 1),
+                              "hbm_frac": round(v / HBM_PEAK_GBS, 4),
+                              "mean_U": round(float(np.mean(r["Us"])), 1),
+                              "kernel_us": {k: round(x * 1000.0, 2) for k, x in sorted(r["kernels"].items())}}
+        out["per_T"] = sweep
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(layers, cfg, T, dev)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

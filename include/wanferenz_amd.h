@@ -130,9 +130,8 @@ int wz_moe_route(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_
                  float* weights, int64_t* indices, int32_t* offsets, int32_t* perm_token,
                  int32_t* perm_slot, void* ws, size_t ws_bytes, hipStream_t stream);
 
-/* RMSNorm (architecture.py:217-230): y = bf16(w * x * rsqrt(mean(x^2) + eps)), fp32 math.
- * Optional fused residual: if residual != NULL, x := x + residual (bf16 add, written back
- * to residual_out when non-NULL) before the norm. */
+/* RMSNorm (architecture.py:217-230): y = bf16(w * x * rsqrt(mean(x^2) + eps)), fp32 math;
+ * x_bf16 [T, D], weight fp32 [D]. */
 int wz_rmsnorm(const void* x_bf16, const float* weight, void* y_bf16, int64_t T, int64_t D,
                float eps, hipStream_t stream);
 
@@ -145,6 +144,15 @@ int wz_add_bf16(const void* a, const void* b, void* out, int64_t n, hipStream_t 
  * 2: e4m3 = low byte with NaN codes zeroed; 3: f32 = lo + (draw>>41)*2^-23*(hi-lo). */
 int wz_synth_fill(void* dst, int64_t n, uint64_t key, int64_t start, int mode, double lo,
                   double hi, hipStream_t stream);
+
+/* Live kernel timing (no reference counterpart; used by bench.py): while enabled,
+ * every launch of this library made outside graph capture is bracketed by two
+ * HIP events on its stream.  wz_prof_end() disables and returns the number of
+ * recorded launches; wz_prof_get(i) synchronises launch i and returns its name
+ * and elapsed milliseconds. */
+int wz_prof_begin(int max_launches);
+int wz_prof_end(void);
+int wz_prof_get(int i, const char** name, float* ms);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,9 @@ SIGNATURES = {
     "wz_rmsnorm": (_I, [_P, _P, _P, _I64, _I64, _F, _P]),
     "wz_add_bf16": (_I, [_P, _P, _P, _I64, _P]),
     "wz_synth_fill": (_I, [_P, _I64, ctypes.c_uint64, _I64, _I, ctypes.c_double, ctypes.c_double, _P]),
+    "wz_prof_begin": (_I, [_I]),
+    "wz_prof_end": (_I, []),
+    "wz_prof_get": (_I, [_I, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_F)]),
 }
 
 # Scale / format constants (mirrors of the header's #defines).
@@ -97,3 +100,35 @@ def stream_handle(device=None) -> int:
     import torch
 
     return torch.cuda.current_stream(device).cuda_stream
+
+
+class KernelTimer:
+    """Live per-launch timing of the library's kernels with HIP events.
+
+    Usage: ``with KernelTimer(max_launches) as kt: ...`` then ``kt.records``
+    holds (kernel name, milliseconds) for every launch made inside the block
+    (graph captures are never instrumented).
+    """
+
+    def __init__(self, max_launches: int = 4096):
+        self.max_launches = max_launches
+        self.records = []
+
+    def __enter__(self):
+        check(lib().wz_prof_begin(self.max_launches), "wz_prof_begin")
+        return self
+
+    def __exit__(self, *exc):
+        n = lib().wz_prof_end()
+        name = ctypes.c_char_p()
+        ms = ctypes.c_float()
+        for i in range(n):
+            check(lib().wz_prof_get(i, ctypes.byref(name), ctypes.byref(ms)), "wz_prof_get")
+            self.records.append((name.value.decode(), float(ms.value)))
+        return False
+
+    def mean_ms(self) -> dict:
+        out = {}
+        for n, ms in self.records:
+            out.setdefault(n, []).append(ms)
+        return {n: sum(v) / len(v) for n, v in out.items()}

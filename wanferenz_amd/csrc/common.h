@@ -122,8 +122,18 @@ __device__ __forceinline__ v4i load16_nt(const void* p) {
 
 }  // namespace wz
 
-// Error reporting (errors.cpp).
+// Error reporting (errors.hip) and optional launch timing (prof.hip).
 namespace wz {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+int prof_pre(hipStream_t s);
+void prof_post(int slot, const char* name, hipStream_t s);
 }  // namespace wz
+
+// Launch with optional event bracketing: WZ_LAUNCH("name", stream, kernel, grid, block, lds, args...)
+#define WZ_LAUNCH(NAME, STREAM, KERNEL, GRID, BLOCK, LDS, ...)                 \
+  do {                                                                         \
+    const int wz_prof_slot_ = ::wz::prof_pre(STREAM);                          \
+    hipLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, STREAM, __VA_ARGS__);         \
+    ::wz::prof_post(wz_prof_slot_, NAME, STREAM);                              \
+  } while (0)

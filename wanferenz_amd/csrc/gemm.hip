@@ -116,16 +116,16 @@ static int launch_skinny(const void* A, const void* As, int act_kind, const void
   dim3 grid(unsigned(N / 16), unsigned((M + rows_per_block - 1) / rows_per_block));
   const uint8_t* w = static_cast<const uint8_t*>(W);
   uint16_t* c = static_cast<uint16_t*>(C);
-#define WZ_LAUNCH(MTV)                                                                            \
-  hipLaunchKernelGGL((skinny_gemm_kernel<WF, A_BF16, MTV>), grid, dim3(kGemmThreads), 0, stream, A, \
-                     As, act_kind, w, Ws, w_kind, c, int(M), int(N), int(K))
+#define WZ_SKINNY(MTV)                                                                           \
+  WZ_LAUNCH(what, stream, (skinny_gemm_kernel<WF, A_BF16, MTV>), grid, dim3(kGemmThreads), 0, A, As, \
+            act_kind, w, Ws, w_kind, c, int(M), int(N), int(K))
   switch (mt) {
-    case 1: WZ_LAUNCH(1); break;
-    case 2: WZ_LAUNCH(2); break;
-    case 4: WZ_LAUNCH(4); break;
-    default: WZ_LAUNCH(8); break;
+    case 1: WZ_SKINNY(1); break;
+    case 2: WZ_SKINNY(2); break;
+    case 4: WZ_SKINNY(4); break;
+    default: WZ_SKINNY(8); break;
   }
-#undef WZ_LAUNCH
+#undef WZ_SKINNY
   return check_launch(what);
 }
 

@@ -28,63 +28,9 @@
 //   w2         per (active expert, 16 output rows): act_quant of h fused, w2
 //              rows streamed once; shared expert's FP8 w2 in the same launch.
 //   combine    y[t] = bf16(sum_{experts asc} out[t,e] + shared[t]).
-#include "mfma_ops.h"
+#include "moe_common.h"
 
 namespace wz {
-
-constexpr int kRouteThreads = 1024;
-constexpr int kMaxExperts = 512;
-constexpr int kMaxPairs = 16384;
-constexpr int kGateTok = 8;
-
-struct MoeWs {
-  float* scores;       // [T, E]
-  float* weights;      // [T, k]
-  int32_t* idx;        // [T, k]
-  int32_t* offsets;    // [E + 1]
-  int32_t* active;     // [E] active expert ids, ascending
-  int32_t* act_off;    // [E] first pair of active expert u
-  int32_t* act_cnt;    // [E] pairs of active expert u
-  int32_t* n_active;   // [1]
-  int32_t* perm_token; // [P]
-  int32_t* perm_slot;  // [P]
-  int32_t* pos;        // [P] permuted position of pair t*k + j
-  uint16_t* h;         // [P, I] bf16
-  uint16_t* sh_h;      // [T, I] bf16
-  uint16_t* out2;      // [P, D] bf16
-  uint16_t* sh_out;    // [T, D] bf16
-  size_t bytes;
-};
-
-static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
-
-static MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base) {
-  const int64_t E = d->n_experts, k = d->topk, P = T * k, D = d->dim, I = d->inter;
-  size_t off = 0;
-  MoeWs w;
-  auto take = [&](size_t bytes) {
-    uint8_t* p = base ? base + off : nullptr;
-    off += align256(bytes);
-    return p;
-  };
-  w.scores = reinterpret_cast<float*>(take(sizeof(float) * T * E));
-  w.weights = reinterpret_cast<float*>(take(sizeof(float) * P));
-  w.idx = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
-  w.offsets = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (E + 1)));
-  w.active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
-  w.act_off = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
-  w.act_cnt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
-  w.n_active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 64));
-  w.perm_token = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
-  w.perm_slot = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
-  w.pos = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
-  w.h = reinterpret_cast<uint16_t*>(take(2 * size_t(P) * I));
-  w.sh_h = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * I));
-  w.out2 = reinterpret_cast<uint16_t*>(take(2 * size_t(P) * D));
-  w.sh_out = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * D));
-  w.bytes = off;
-  return w;
-}
 
 // ------------------------------------------------------------------ gate ----
 
@@ -135,23 +81,6 @@ __global__ __launch_bounds__(256) void gate_dot_kernel(const uint16_t* __restric
 
 // ------------------------------------------------------------------ top-k ---
 
-struct Cand {
-  float v;
-  int i;
-};
-
-__device__ __forceinline__ Cand cand_better(Cand a, Cand b) {
-  // larger value wins; equal values -> lower expert index (stable descending order)
-  if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
-  return a;
-}
-
-__device__ __forceinline__ float softplus_f32(float a) {
-  // torch F.softplus(beta=1, threshold=20) evaluated in fp64, rounded to fp32
-  if (a > 20.0f) return a;
-  return float(log1p(exp(double(a))));
-}
-
 constexpr int kSlots = kMaxExperts / 64;
 
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ scores,
@@ -200,13 +129,14 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ sco
     s[i] = v;
     b[i] = (e < E && bias != nullptr) ? v + bias[e] : v;
   }
-  int sel[16];
+  // lane j < k ends up holding the j-th selected expert
+  int my_sel = 0;
   if (tid2eid != nullptr) {
     int64_t id = input_ids[t];
     id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
-    for (int j = 0; j < k; ++j) {
-      int e = tid2eid[id * k + j];
-      sel[j] = e < 0 ? 0 : (e >= E ? E - 1 : e);
+    if (lane < k) {
+      const int e = tid2eid[id * k + lane];
+      my_sel = e < 0 ? 0 : (e >= E ? E - 1 : e);
     }
   } else {
     unsigned taken = 0u;
@@ -217,37 +147,26 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ sco
         const int e = lane + 64 * i;
         if (e < E && !((taken >> i) & 1u)) best = cand_better(best, Cand{b[i], e});
       }
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) {
-        Cand o;
-        o.v = __shfl_xor(best.v, m, kWave);
-        o.i = __shfl_xor(best.i, m, kWave);
-        best = cand_better(best, o);
-      }
-      sel[j] = best.i;
+      best = wave_argmax(best);
+      if (lane == j) my_sel = best.i;
       if ((best.i & 63) == lane) taken |= 1u << (best.i >> 6);
     }
   }
   // weights = original scores gathered at the selected experts (architecture.py:714-717)
-  float w[16];
-  float tot = 0.0f;
-  for (int j = 0; j < k; ++j) {
-    const int e = sel[j];
-    float mine = 0.0f;
+  float mine = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kSlots; ++i)
-      if ((e >> 6) == i) mine = s[i];
-    w[j] = __shfl(mine, e & 63, kWave);
-    tot += w[j];
+  for (int i = 0; i < kSlots; ++i) {
+    const float v = __shfl(s[i], my_sel & 63, kWave);
+    if ((my_sel >> 6) == i) mine = v;
   }
-  for (int j = 0; j < k; ++j) {
-    float v = w[j];
-    if (score_func != WZ_SCORE_SOFTMAX) v = v / tot;
-    v = v * route_scale;
-    if (lane == j) {
-      weights[int64_t(t) * k + j] = v;
-      idx[int64_t(t) * k + j] = sel[j];
-    }
+  float tot = 0.0f;
+  for (int j = 0; j < k; ++j) tot += __shfl(mine, j, kWave);  // slot order, fp32
+  float v = mine;
+  if (score_func != WZ_SCORE_SOFTMAX) v = v / tot;
+  v = v * route_scale;
+  if (lane < k) {
+    weights[int64_t(t) * k + lane] = v;
+    idx[int64_t(t) * k + lane] = my_sel;
   }
 }
 
@@ -368,7 +287,6 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
 
 // ------------------------------------------------------------------- w13 ----
 
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
 constexpr int kMoeThreads = 256;
 constexpr int kMoeUnroll = 4;
@@ -686,6 +604,9 @@ __global__ void export_routing_kernel(const MoeWs ws, int P, float* __restrict__
 
 // ------------------------------------------------------------------ host ----
 
+int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* ids, int64_t T,
+                  void* y, hipStream_t stream);
+
 static int validate(const wz_moe_desc* d, int64_t T, const void* ws, size_t ws_bytes,
                     const char* what) {
   if (!d) return set_error(WZ_EINVAL, "%s: null descriptor", what);
@@ -720,15 +641,14 @@ static int launch_routing(const wz_moe_desc* d, const MoeWs& w, const void* x,
                           const int64_t* input_ids, int64_t T, hipStream_t stream) {
   const int E = d->n_experts, k = d->topk, D = d->dim;
   if (d->tid2eid && !input_ids) return set_error(WZ_EINVAL, "moe: hash-routed layer needs input_ids");
-  hipLaunchKernelGGL(gate_dot_kernel, dim3((E + 3) / 4, unsigned((T + kGateTok - 1) / kGateTok)), dim3(256),
-                     0, stream, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(d->gate_w),
+  WZ_LAUNCH("moe_gate", stream, gate_dot_kernel, dim3((E + 3) / 4, unsigned((T + kGateTok - 1) / kGateTok)), dim3(256), 0, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(d->gate_w),
                      w.scores, int(T), E, D);
   if (int rc = check_launch("moe gate")) return rc;
-  hipLaunchKernelGGL(topk_kernel, dim3(unsigned((T + 3) / 4)), dim3(256), 0, stream, w.scores,
+  WZ_LAUNCH("moe_topk", stream, topk_kernel, dim3(unsigned((T + 3) / 4)), dim3(256), 0, w.scores,
                      d->tid2eid ? nullptr : d->gate_bias, d->tid2eid, input_ids, d->vocab, int(T), E,
                      k, d->score_func, d->route_scale, w.weights, w.idx);
   if (int rc = check_launch("moe topk")) return rc;
-  hipLaunchKernelGGL(perm_kernel, dim3(1), dim3(kRouteThreads), 0, stream, w.idx, int(T), E, k,
+  WZ_LAUNCH("moe_perm", stream, perm_kernel, dim3(1), dim3(kRouteThreads), 0, w.idx, int(T), E, k,
                      w.offsets, w.active, w.act_off, w.act_cnt, w.n_active, w.perm_token,
                      w.perm_slot, w.pos);
   return check_launch("moe perm");
@@ -741,11 +661,19 @@ extern "C" size_t wz_moe_workspace_bytes(const wz_moe_desc* d, int64_t T) {
   return wz::moe_ws_layout(d, T, nullptr).bytes;
 }
 
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
 extern "C" int wz_moe_workspace_init(void* ws, size_t ws_bytes, hipStream_t stream) {
-  (void)ws;
-  (void)ws_bytes;
-  (void)stream;
-  return WZ_OK;
+  using namespace wz;
+  if (!ws || ws_bytes < sizeof(uint32_t) * kCounterWords)
+    return set_error(WZ_ESPACE, "moe_workspace_init: workspace smaller than the %zu-byte counter block",
+                     sizeof(uint32_t) * kCounterWords);
+  WZ_LAUNCH("moe_ws_init", stream, zero_words_kernel, dim3(kCounterWords / 256), dim3(256), 0,
+            static_cast<uint32_t*>(ws), kCounterWords);
+  return check_launch("moe_workspace_init");
 }
 
 extern "C" int wz_moe_route(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids,
@@ -758,7 +686,7 @@ extern "C" int wz_moe_route(const wz_moe_desc* d, const void* x_bf16, const int6
   const MoeWs w = moe_ws_layout(d, T, static_cast<uint8_t*>(ws));
   if (int rc = launch_routing(d, w, x_bf16, input_ids, T, stream)) return rc;
   const int P = int(T * d->topk);
-  hipLaunchKernelGGL(export_routing_kernel, dim3((P + 255) / 256), dim3(256), 0, stream, w, P, weights,
+  WZ_LAUNCH("moe_export", stream, export_routing_kernel, dim3((P + 255) / 256), dim3(256), 0, w, P, weights,
                      indices);
   if (int rc = check_launch("moe_route export")) return rc;
   if (offsets && hipMemcpyAsync(offsets, w.offsets, sizeof(int32_t) * (d->n_experts + 1),
@@ -784,6 +712,17 @@ extern "C" int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const in
       !d->sh_w3_s || !d->sh_w2 || !d->sh_w2_s)
     return set_error(WZ_EINVAL, "moe_forward: expert weights missing");
   const MoeWs w = moe_ws_layout(d, T, static_cast<uint8_t*>(ws));
+  if (T <= kDecodeMaxT && d->n_experts <= kMaxExperts) {
+    if (d->tid2eid && !input_ids) return set_error(WZ_EINVAL, "moe: hash-routed layer needs input_ids");
+    if (int rc = launch_decode(d, w, x_bf16, input_ids, T, y_bf16, stream)) return rc;
+    if (weights_out || indices_out) {
+      const int P = int(T * d->topk);
+      WZ_LAUNCH("moe_export", stream, export_routing_kernel, dim3(unsigned((P + 255) / 256)), dim3(256), 0, w,
+                P, weights_out, indices_out);
+      if (int rc = check_launch("moe export")) return rc;
+    }
+    return WZ_OK;
+  }
   if (int rc = launch_routing(d, w, x_bf16, input_ids, T, stream)) return rc;
   const int E = d->n_experts, k = d->topk, D = d->dim, I = d->inter;
   const int64_t P = T * k;
@@ -792,22 +731,22 @@ extern "C" int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const in
   const dim3 g13(unsigned(sh13 + u_max * (I / 16))), g2(unsigned(sh2 + u_max * (D / 16)));
   const uint16_t* xb = static_cast<const uint16_t*>(x_bf16);
   if (T <= 16) {
-    hipLaunchKernelGGL(w13_kernel<1>, g13, dim3(kMoeThreads), 0, stream, *d, w, xb, int(T), sh13);
+    WZ_LAUNCH("moe_w13", stream, w13_kernel<1>, g13, dim3(kMoeThreads), 0, *d, w, xb, int(T), sh13);
   } else {
-    hipLaunchKernelGGL(w13_kernel<4>, g13, dim3(kMoeThreads), 0, stream, *d, w, xb, int(T), sh13);
+    WZ_LAUNCH("moe_w13", stream, w13_kernel<4>, g13, dim3(kMoeThreads), 0, *d, w, xb, int(T), sh13);
   }
   if (int rc = check_launch("moe w13")) return rc;
   if (T <= 16) {
-    hipLaunchKernelGGL(w2_kernel<1>, g2, dim3(kMoeThreads), 0, stream, *d, w, int(T), sh2);
+    WZ_LAUNCH("moe_w2", stream, w2_kernel<1>, g2, dim3(kMoeThreads), 0, *d, w, int(T), sh2);
   } else {
-    hipLaunchKernelGGL(w2_kernel<4>, g2, dim3(kMoeThreads), 0, stream, *d, w, int(T), sh2);
+    WZ_LAUNCH("moe_w2", stream, w2_kernel<4>, g2, dim3(kMoeThreads), 0, *d, w, int(T), sh2);
   }
   if (int rc = check_launch("moe w2")) return rc;
-  hipLaunchKernelGGL(combine_kernel, dim3(unsigned((D / 8 + 255) / 256), unsigned(T)), dim3(256), 0,
-                     stream, w, k, D, static_cast<uint16_t*>(y_bf16));
+  WZ_LAUNCH("moe_combine", stream, combine_kernel, dim3(unsigned((D / 8 + 255) / 256), unsigned(T)), dim3(256),
+                     0, w, k, D, static_cast<uint16_t*>(y_bf16));
   if (int rc = check_launch("moe combine")) return rc;
   if (weights_out || indices_out) {
-    hipLaunchKernelGGL(export_routing_kernel, dim3(unsigned((P + 255) / 256)), dim3(256), 0, stream, w,
+    WZ_LAUNCH("moe_export", stream, export_routing_kernel, dim3(unsigned((P + 255) / 256)), dim3(256), 0, w,
                        int(P), weights_out, indices_out);
     if (int rc = check_launch("moe export")) return rc;
   }

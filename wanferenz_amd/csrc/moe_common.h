@@ -1,0 +1,135 @@
+// Workspace layout and helpers shared by the MoE kernels (moe.hip, moe_decode.hip).
+#pragma once
+
+#include "mfma_ops.h"
+
+namespace wz {
+
+constexpr int kRouteThreads = 1024;
+constexpr int kMaxExperts = 512;
+constexpr int kMaxPairs = 16384;
+constexpr int kGateTok = 8;
+constexpr int kDecodeMaxT = 16;       // tokens served by the decode kernels
+constexpr int kCounterWords = 4096;   // arrival counters at the start of the workspace
+
+// Scratch of one MoE layer call, carved from the caller's workspace.  The
+// arrival counters sit at offset 0 so wz_moe_workspace_init can zero them
+// without knowing T; every kernel that bumps a counter resets it to zero.
+struct MoeWs {
+  uint32_t* counters;  // [kCounterWords]: [0] route, [1 + d_tile] combine
+  float* scores;       // [T, E]
+  float* weights;      // [T, k]
+  int32_t* idx;        // [T, k]
+  int32_t* offsets;    // [E + 1]
+  int32_t* active;     // [E] active expert ids, ascending
+  int32_t* act_off;    // [E] first pair of active expert u
+  int32_t* act_cnt;    // [E] pairs of active expert u
+  int32_t* n_active;   // [1]
+  int32_t* perm_token; // [P]
+  int32_t* perm_slot;  // [P]
+  int32_t* pos;        // [P] permuted position of pair t*k + j
+  int32_t* tok_pos;    // [T, k] a token's positions, ascending, one per distinct expert
+  int32_t* tok_n;      // [T]
+  uint8_t* xq;         // [T, D] e4m3 act_quant(x)
+  float* xs;           // [T, D/128] its block scales
+  uint8_t* hq;         // [P + T, I] e4m3 act_quant(h) (routed pairs, then shared rows)
+  float* hs;           // [P + T, I/128]
+  uint16_t* h;         // [P, I] bf16
+  uint16_t* sh_h;      // [T, I] bf16
+  uint16_t* out2;      // [P, D] bf16
+  uint16_t* sh_out;    // [T, D] bf16
+  size_t bytes;
+};
+
+static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+static inline MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base) {
+  const int64_t E = d->n_experts, k = d->topk, P = T * k, D = d->dim, I = d->inter;
+  size_t off = 0;
+  MoeWs w;
+  auto take = [&](size_t bytes) {
+    uint8_t* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  w.counters = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * kCounterWords));
+  w.scores = reinterpret_cast<float*>(take(sizeof(float) * T * E));
+  w.weights = reinterpret_cast<float*>(take(sizeof(float) * P));
+  w.idx = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
+  w.offsets = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (E + 1)));
+  w.active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
+  w.act_off = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
+  w.act_cnt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
+  w.n_active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 64));
+  w.perm_token = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
+  w.perm_slot = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
+  w.pos = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
+  w.tok_pos = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
+  w.tok_n = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * T));
+  w.xq = take(size_t(T) * D);
+  w.xs = reinterpret_cast<float*>(take(sizeof(float) * T * (D / 128)));
+  w.hq = take(size_t(P + T) * I);
+  w.hs = reinterpret_cast<float*>(take(sizeof(float) * (P + T) * (I / 128)));
+  w.h = reinterpret_cast<uint16_t*>(take(2 * size_t(P) * I));
+  w.sh_h = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * I));
+  w.out2 = reinterpret_cast<uint16_t*>(take(2 * size_t(P) * D));
+  w.sh_out = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * D));
+  w.bytes = off;
+  return w;
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+// torch F.softplus(beta=1, threshold=20) evaluated in fp64, rounded to fp32
+__device__ __forceinline__ float softplus_f32(float a) {
+  if (a > 20.0f) return a;
+  return float(log1p(exp(double(a))));
+}
+
+// Routing score of one raw gate logit (Gate.forward, architecture.py:700-705);
+// softmax is handled by the caller (it needs the row max and sum).
+__device__ __forceinline__ float score_of(float a, int score_func) {
+  if (score_func == WZ_SCORE_SIGMOID) return float(1.0 / (1.0 + exp(-double(a))));
+  return float(sqrt(double(softplus_f32(a))));
+}
+
+struct Cand {
+  float v;
+  int i;
+};
+
+// larger value wins; equal values -> lower expert index (stable descending order)
+__device__ __forceinline__ Cand cand_better(Cand a, Cand b) {
+  if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+  return a;
+}
+
+__device__ __forceinline__ Cand wave_argmax(Cand c) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    Cand o;
+    o.v = __shfl_xor(c.v, m, kWave);
+    o.i = __shfl_xor(c.i, m, kWave);
+    c = cand_better(c, o);
+  }
+  return c;
+}
+
+// Agent-scope arrival counter: returns true in the last of `n` arrivals and
+// resets the counter for the next launch.  Producers publish their global
+// writes with release_agent() before arriving; the last arrival calls
+// acquire_agent() before reading them.  (An agent-scope release writes back
+// this XCD's L2 and the acquire invalidates it, so keep arrivals few.)
+__device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t n) {
+  const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old == n - 1) {
+    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  }
+  return false;
+}
+
+__device__ __forceinline__ void release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
+}  // namespace wz

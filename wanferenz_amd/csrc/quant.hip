@@ -62,7 +62,7 @@ extern "C" int wz_act_quant_fp8(const void* x_bf16, int64_t M, int64_t K, void* 
   if (!x_bf16 || !q_e4m3 || !s) return set_error(WZ_EINVAL, "act_quant: null pointer");
   const int64_t n8 = M * K / 8;
   const int64_t blocks = (n8 + 255) / 256;
-  hipLaunchKernelGGL(act_quant_kernel, dim3(unsigned(blocks)), dim3(256), 0, stream,
+  WZ_LAUNCH("act_quant", stream, act_quant_kernel, dim3(unsigned(blocks)), dim3(256), 0,
                      static_cast<const uint16_t*>(x_bf16), n8, static_cast<uint8_t*>(q_e4m3), s,
                      scale_kind);
   return check_launch("act_quant");
