@@ -108,7 +108,25 @@ typedef struct wz_moe_desc {
   const void* sh_w3_s;
   const void* sh_w2;      /* e4m3 [D, I] */
   const void* sh_w2_s;    /* [D/128, I/128] */
+  /* Packed banks (wz_moe_pack): MFMA-ready 16-row x 128-K tiles stored as 1 KB blocks in
+   * lane order, so each weight load instruction of a wave reads 1 KB contiguous.  The
+   * decode path (T <= 16) reads these; NULL -> wz_moe_forward rejects T <= 16. */
+  const void* w13p;       /* [E][I/16][D/128][2 (w1,w3)][1024] */
+  const void* w13p_s;     /* [E][I/16][ceil(D/512)][2][64 x 4]: 4 K-blocks of e8m0 per lane */
+  const void* w2p;        /* [E][D/16][I/128][1024] */
+  const void* w2p_s;      /* [E][D/16][ceil(I/512)][64 x 4] */
+  const void* sh13p;      /* [I/16][D/128][2 (w1,w3)][2 halves][1024] */
+  const void* sh2p;       /* [D/16][I/128][2 halves][1024] */
 } wz_moe_desc;
+
+/* Bytes of each packed bank (which: 0 w13p, 1 w13p_s, 2 w2p, 3 w2p_s, 4 sh13p, 5 sh2p). */
+size_t wz_moe_packed_bytes(const wz_moe_desc* d, int which);
+
+/* Build the packed banks from the reference-layout pointers of d (a one-time
+ * load-step relayout, the role of fp4_grouped._relayout_moe, fp4_grouped.py:142-188).
+ * Outputs are the six buffers of wz_moe_packed_bytes; d itself is not modified. */
+int wz_moe_pack(const wz_moe_desc* d, void* w13p, void* w13p_s, void* w2p, void* w2p_s, void* sh13p,
+                void* sh2p, hipStream_t stream);
 
 /* Bytes of scratch wz_moe_forward needs for up to T tokens. */
 size_t wz_moe_workspace_bytes(const wz_moe_desc* d, int64_t T);

@@ -174,3 +174,38 @@ def test_v4_decode_graph_replay(v4_layer):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i} differs from eager"
         _ = moe.forward(x)  # eager work between replays
+
+
+def _expected_pack_w13(w13, w13_s, D, I):
+    """numpy statement of the packed w13 layout (pack.hip): [E][I/16][D/128][2][64 lanes][16 B]."""
+    E = w13.shape[0]
+    KB = D // 128
+    out = np.empty((E, I // 16, KB, 2, 64, 16), np.uint8)
+    lanes = np.arange(64)
+    r, g = lanes & 15, lanes >> 4
+    for m in range(2):
+        rows = w13[:, m * I:(m + 1) * I].reshape(E, I // 16, 16, D // 2)  # [E, FT, 16, D/2]
+        for kb in range(KB):
+            for ln in range(64):
+                out[:, :, kb, m, ln] = rows[:, :, r[ln], kb * 64 + g[ln] * 16: kb * 64 + g[ln] * 16 + 16]
+    KG = (KB + 3) // 4
+    sc = np.zeros((E, I // 16, KG, 2, 64, 4), np.uint8)
+    for m in range(2):
+        srows = w13_s[:, m * I:(m + 1) * I].reshape(E, I // 16, 16, D // 32)
+        for kg in range(KG):
+            for j in range(4):
+                kb = kg * 4 + j
+                if kb < KB:
+                    for ln in range(64):
+                        sc[:, :, kg, m, ln, j] = srows[:, :, r[ln], kb * 4 + g[ln]]
+    return out.reshape(-1), sc.reshape(-1)
+
+
+def test_pack_layout_matches_statement(gpu):
+    case = CASES["toy_t4"]
+    inp = make_inputs(case)
+    moe = upload_case(case, inp, gpu)
+    torch.cuda.synchronize()
+    exp_w, exp_s = _expected_pack_w13(inp.w13, inp.w13_s, case.dim, case.inter)
+    assert np.array_equal(moe.packed["w13p"].cpu().numpy(), exp_w)
+    assert np.array_equal(moe.packed["w13p_s"].cpu().numpy(), exp_s)

@@ -30,11 +30,13 @@ struct MoeWs {
   int32_t* pos;        // [P] permuted position of pair t*k + j
   int32_t* tok_pos;    // [T, k] a token's positions, ascending, one per distinct expert
   int32_t* tok_n;      // [T]
+  int32_t* umap;       // [U_max, T] decode: permuted position of (active expert u, token t), -1 if unrouted
+  float* uwt;          // [U_max, T] decode: its routing weight
   uint8_t* xq;         // [T, D] e4m3 act_quant(x)
   float* xs;           // [T, D/128] its block scales
-  uint8_t* hq;         // [P + T, I] e4m3 act_quant(h) (routed pairs, then shared rows)
-  float* hs;           // [P + T, I/128]
-  uint16_t* h;         // [P, I] bf16
+  uint8_t* hq;         // decode: [U_max*T + T, I] e4m3 act_quant(h) (rows (u, t), then shared t)
+  float* hs;           // [U_max*T + T, I/128]
+  uint16_t* h;         // [P, I] bf16 (general path) / [U_max*T, I] rows (u, t) (decode path)
   uint16_t* sh_h;      // [T, I] bf16
   uint16_t* out2;      // [P, D] bf16
   uint16_t* sh_out;    // [T, D] bf16
@@ -45,6 +47,8 @@ static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 static inline MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base) {
   const int64_t E = d->n_experts, k = d->topk, P = T * k, D = d->dim, I = d->inter;
+  const int64_t UT = T <= kDecodeMaxT ? (P < E ? P : E) * T : 0;  // decode tables only
+  const int64_t HR = UT > P ? UT : P;
   size_t off = 0;
   MoeWs w;
   auto take = [&](size_t bytes) {
@@ -66,11 +70,13 @@ static inline MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base
   w.pos = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
   w.tok_pos = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
   w.tok_n = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * T));
+  w.umap = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * UT));
+  w.uwt = reinterpret_cast<float*>(take(sizeof(float) * UT));
   w.xq = take(size_t(T) * D);
   w.xs = reinterpret_cast<float*>(take(sizeof(float) * T * (D / 128)));
-  w.hq = take(size_t(P + T) * I);
-  w.hs = reinterpret_cast<float*>(take(sizeof(float) * (P + T) * (I / 128)));
-  w.h = reinterpret_cast<uint16_t*>(take(2 * size_t(P) * I));
+  w.hq = take(size_t(UT + T) * I);
+  w.hs = reinterpret_cast<float*>(take(sizeof(float) * (UT + T) * (I / 128)));
+  w.h = reinterpret_cast<uint16_t*>(take(2 * size_t(HR) * I));
   w.sh_h = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * I));
   w.out2 = reinterpret_cast<uint16_t*>(take(2 * size_t(P) * D));
   w.sh_out = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * D));

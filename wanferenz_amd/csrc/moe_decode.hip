@@ -2,91 +2,46 @@
 //
 // Four stream-ordered launches, no host sync, no allocation (graph-capturable):
 //
-//   route   WG per 4 experts: gate logits x.W^T (exact bf16 products, fp64
+//   route   WGs of 4 gate experts: logits x.W^T (exact bf16 products, fp64
 //           sums); the last gate WG to arrive (agent-scope counter) does score
-//           function + bias + top-k + renormalise for every token, the
-//           canonical (expert, token, slot) permutation, the active-expert
-//           list and per-token combine lists.  T more WGs quantise x
-//           (act_quant, one token each).
-//   w13     per (expert, 16 intermediate features), routed MXFP4 experts and
-//           the FP8 shared expert alike: w1 and w3 rows streamed once, A =
-//           act_quant(x) rows of the expert's tokens, SwiGLU + clamp (+ the
-//           routing weight), bf16 h.
-//   hquant  act_quant of every h row (routed pairs and shared rows).
+//           function + bias + top-k + renormalise for every token
+//           (Gate.forward, architecture.py:696-718), the canonical (expert,
+//           token, slot) permutation (expert_batch.py:24-37), the active-
+//           expert list and the per-token combine lists.  In the same launch,
+//           T WGs quantise x (act_quant) and I/16 WGs run the shared
+//           expert's FP8 w1/w3 + SwiGLU, which need only x.
+//   w13     per (active expert, 16 intermediate features): MXFP4 w1 and w3
+//           tiles streamed once, SwiGLU + clamp + routing weight, bf16 h.
+//   hquant  act_quant of the h rows that are routed, and of the shared rows.
 //   w2      one WG per 16 output columns; each wave computes one expert's
-//           [rows x 16] tile over the full K (MXFP4 w2, or FP8 for the shared
+//           16-column tile over the full K (MXFP4, or FP8 for the shared
 //           expert) into LDS, then the WG sums each token's experts in
 //           ascending id, adds the shared expert and writes bf16 y
-//           (architecture.py:781-794, fp4_grouped.py:318-324) — the combine
-//           never leaves the workgroup.
+//           (architecture.py:781-794, fp4_grouped.py:318-324).
 //
-// Weight tiles are consumed with 16-byte loads, the loads of up to eight
-// 128-wide K-blocks issued before the first MFMA, non-temporal (read once).
+// Tokens ride on the MFMA's 16-row side: the A operand of every expert is
+// the whole (<= 16 token) batch, row t = token t, and only the rows of the
+// tokens routed to that expert are kept.  So a workgroup needs one table
+// lookup (its expert id) before its weight stream starts, and no per-lane
+// token gather.  Weights come from the packed banks (pack.hip): every load
+// instruction reads 1 KB contiguous, non-temporal (read once).
 #include "moe_common.h"
 
 namespace wz {
 
 constexpr int kDecThreads = 256;
 
-__device__ __forceinline__ v8i b_fp4_nt(const uint8_t* wrow, int kb, int g) {
-  v4i x = load16_nt(wrow + kb * 64 + g * 16);
+__device__ __forceinline__ v8i pk_fp4(const uint8_t* tile, int lane) {
+  const v4i x = load16_nt(tile + lane * 16);
   return v8i{x[0], x[1], x[2], x[3], 0, 0, 0, 0};
 }
 
-__device__ __forceinline__ v8i b_fp8_nt(const uint8_t* wrow, int kb, int g) {
-  const uint8_t* p = wrow + kb * 128 + g * 16;
-  v4i lo = load16_nt(p), hi = load16_nt(p + 64);
+__device__ __forceinline__ v8i pk_fp8(const uint8_t* tile, int lane) {
+  const v4i lo = load16_nt(tile + lane * 16), hi = load16_nt(tile + 1024 + lane * 16);
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// Accumulate NB weight matrices (rows of this lane: wrow[m]) against one
-// 16-row A tile over K-blocks [kb0, kb1).  WF: weight format.  A is either
-// pre-quantised e4m3 (arow/asrow, float scales) or bf16 with act_quant fused.
-template <int NB, int WF, bool A_BF16, int B>
-__device__ __forceinline__ void tile_accum(v4f (&acc)[NB], const uint8_t* const (&wrow)[NB],
-                                           const uint8_t* const (&srow)[NB], const void* const (&ws8)[NB],
-                                           const int64_t (&ws8_base)[NB], int ws8_kind,
-                                           const void* arow, const float* asrow, bool a_pow2,
-                                           int kb0, int kb1, int g, int lane) {
-  const bool b_pow2 = WF == kFmtFp4 || ws8_kind == WZ_WSCALE_E8M0;
-  const int a_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
-  for (int kb = kb0; kb < kb1; kb += B) {
-    v8i w[NB][B];
-    int se[NB][B];
-    float sf[NB][B];
-#pragma unroll
-    for (int q = 0; q < B; ++q) {
-      const int kk = kb + q;
-      if (kk < kb1) {
-#pragma unroll
-        for (int m = 0; m < NB; ++m) {
-          if (WF == kFmtFp4) {
-            w[m][q] = b_fp4_nt(wrow[m], kk, g);
-            se[m][q] = b_fp4_scale(srow[m], kk, g);
-            sf[m][q] = 1.0f;
-          } else {
-            w[m][q] = b_fp8_nt(wrow[m], kk, g);
-            fp8_wscale(ws8[m], ws8_base[m] + kk, ws8_kind, se[m][q], sf[m][q]);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < B; ++q) {
-      const int kk = kb + q;
-      if (kk < kb1) {
-        const AOp a = A_BF16 ? a_from_bf16(static_cast<const uint16_t*>(arow), kk, g, a_pow2)
-                             : a_from_fp8(static_cast<const uint8_t*>(arow), asrow, kk, g, a_kind);
-#pragma unroll
-        for (int m = 0; m < NB; ++m)
-          mma_step<kFmtFp8, WF>(acc[m], a, w[m][q], se[m][q], sf[m][q], a_pow2, b_pow2, lane);
-      }
-    }
-  }
-}
-
-// Cross-wave K reduction through LDS: returns, in every wave, the sum of the
-// four waves' accumulators (summed in wave order) for matrix m.
+// Cross-wave K reduction through LDS (partials summed in wave order).
 template <int NB>
 __device__ __forceinline__ void reduce_waves(v4f (&acc)[NB], float* red, int wave, int lane) {
 #pragma unroll
@@ -106,8 +61,8 @@ __device__ __forceinline__ void reduce_waves(v4f (&acc)[NB], float* red, int wav
     }
 }
 
-// SwiGLU with clamp (Expert.forward, architecture.py:733-739) on bf16-rounded
-// linear outputs.
+// SwiGLU with clamp (Expert.forward, architecture.py:733-739) on the
+// bf16-rounded outputs of w1 and w3.
 __device__ __forceinline__ float swiglu(float gs, float us, float limit) {
   float gv = bf16_round(gs), uv = bf16_round(us);
   if (limit > 0.0f) {
@@ -119,15 +74,23 @@ __device__ __forceinline__ float swiglu(float gs, float us, float limit) {
 
 // ------------------------------------------------------------------ route ---
 
-__device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t* ids, int T) {
-  __shared__ int s_idx[kDecodeMaxT * 16];
+constexpr int kMaxDecPairs = kDecodeMaxT * 16;
+constexpr int kMaxUT = kDecodeMaxT * kMaxDecPairs;
+
+__device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t* ids, int T, int u_max) {
+  __shared__ int s_e[kMaxDecPairs];
+  __shared__ int s_q[kMaxDecPairs];
+  __shared__ float s_w[kMaxDecPairs];
   __shared__ int cnt[kMaxExperts];
   __shared__ int base[kMaxExperts];
+  __shared__ int ucode[kMaxExperts];
   __shared__ int wc[4][kMaxExperts];
-  const int E = d.n_experts, k = d.topk, P = T * k;
+  __shared__ int s_umap[kMaxUT];
+  __shared__ float s_uwt[kMaxUT];
+  const int E = d.n_experts, k = d.topk, P = T * k, UT = u_max * T;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr int kSlots = kMaxExperts / 64;
-  // top-k per token, one wave per token
+  // ---- top-k, one wave per token ----
   for (int t = wave; t < T; t += 4) {
     const float* a = ws.scores + int64_t(t) * E;
     float s[kSlots], b[kSlots];
@@ -148,10 +111,8 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
     for (int i = 0; i < kSlots; ++i) {
       const int e = lane + 64 * i;
       float v = -INFINITY;
-      if (e < E) {
-        v = d.score_func == WZ_SCORE_SOFTMAX ? float(exp(double(a[e]) - mx) / sum)
-                                             : score_of(a[e], d.score_func);
-      }
+      if (e < E)
+        v = d.score_func == WZ_SCORE_SOFTMAX ? float(exp(double(a[e]) - mx) / sum) : score_of(a[e], d.score_func);
       s[i] = v;
       b[i] = (e < E && d.tid2eid == nullptr && d.gate_bias != nullptr) ? v + d.gate_bias[e] : v;
     }
@@ -184,26 +145,27 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       if ((my_sel >> 6) == i) mine = v;
     }
     float tot = 0.0f;
-    for (int j = 0; j < k; ++j) tot += __shfl(mine, j, kWave);
+    for (int j = 0; j < k; ++j) tot += __shfl(mine, j, kWave);  // slot order, fp32
     float v = mine;
     if (d.score_func != WZ_SCORE_SOFTMAX) v = v / tot;
     v = v * d.route_scale;
     if (lane < k) {
       ws.weights[t * k + lane] = v;
       ws.idx[t * k + lane] = my_sel;
-      s_idx[t * k + lane] = my_sel;
+      s_e[t * k + lane] = my_sel;
+      s_w[t * k + lane] = v;
     }
   }
   for (int e = tid; e < kMaxExperts; e += kDecThreads) cnt[e] = 0;
+  for (int i = tid; i < UT; i += kDecThreads) s_umap[i] = -1;
   __syncthreads();
-  for (int p = tid; p < P; p += kDecThreads) atomicAdd(&cnt[s_idx[p]], 1);
+  for (int p = tid; p < P; p += kDecThreads) atomicAdd(&cnt[s_e[p]], 1);
   __syncthreads();
-  // exclusive scan of counts and of (count > 0) over E <= 512 experts, 2 per thread
+  // ---- exclusive scans of counts and of (count > 0), 2 experts per thread ----
   {
     const int e0 = 2 * tid, e1 = 2 * tid + 1;
     const int c0 = e0 < E ? cnt[e0] : 0, c1 = e1 < E ? cnt[e1] : 0;
-    int v = c0 + c1;
-    int f = (c0 > 0) + (c1 > 0);
+    const int v = c0 + c1, f = (c0 > 0) + (c1 > 0);
     int vi = v, fi = f;
 #pragma unroll
     for (int dd = 1; dd < 64; dd <<= 1) {
@@ -228,6 +190,7 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       base[e0] = ex0;
       ws.offsets[e0] = ex0;
       if (c0 > 0) {
+        ucode[e0] = fx0;
         ws.active[fx0] = e0;
         ws.act_off[fx0] = ex0;
         ws.act_cnt[fx0] = c0;
@@ -238,6 +201,7 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       ws.offsets[e1] = ex0 + c0;
       if (c1 > 0) {
         const int u = fx0 + (c0 > 0);
+        ucode[e1] = u;
         ws.active[u] = e1;
         ws.act_off[u] = ex0 + c0;
         ws.act_cnt[u] = c1;
@@ -249,14 +213,14 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
     }
   }
   __syncthreads();
-  // stable placement of the P <= 256 pairs (one pass)
+  // ---- stable placement of the P <= 256 pairs: one pair per thread ----
   {
     int nbits = 1;
     while ((1 << nbits) < E) ++nbits;
     const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     const int p = tid;
     const bool valid = p < P;
-    const int e = valid ? s_idx[p] : 0;
+    const int e = valid ? s_e[p] : 0;
     unsigned long long mask = __ballot(valid);
     if (!valid) mask = ~mask;
     for (int bit = 0; bit < nbits; ++bit) {
@@ -277,46 +241,49 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       ws.perm_token[q] = p / k;
       ws.perm_slot[q] = p % k;
       ws.pos[p] = q;
-      s_idx[p] = q | (e << 16);  // position and expert, for the combine lists
+      s_q[p] = q;
     }
   }
   __syncthreads();
-  // per-token combine list: positions ascending (== experts ascending), one per expert
-  if (tid < T) {
-    int ps[16];
-    for (int j = 0; j < k; ++j) ps[j] = s_idx[tid * k + j];
-    for (int i = 1; i < k; ++i) {
-      const int v = ps[i];
-      int j = i - 1;
-      while (j >= 0 && (ps[j] & 0xFFFF) > (v & 0xFFFF)) {
-        ps[j + 1] = ps[j];
-        --j;
+  // ---- (expert, token) map and per-token combine lists.  A token that lists an
+  // expert twice keeps its last slot (architecture.py:790 index_put semantics). ----
+  if (tid < P) {
+    const int p = tid, t = p / k, j = p % k, e = s_e[p];
+    bool last = true;
+    for (int jj = j + 1; jj < k; ++jj) last = last && (s_e[t * k + jj] != e);
+    if (last) {
+      const int q = s_q[p];
+      s_umap[ucode[e] * T + t] = q;
+      s_uwt[ucode[e] * T + t] = s_w[p];
+      int rank = 0, n = 0;
+      for (int jj = 0; jj < k; ++jj) {
+        const int pe = s_e[t * k + jj];
+        bool l2 = true;
+        for (int j3 = jj + 1; j3 < k; ++j3) l2 = l2 && (s_e[t * k + j3] != pe);
+        if (l2) {
+          ++n;
+          if (s_q[t * k + jj] < q) ++rank;
+        }
       }
-      ps[j + 1] = v;
+      ws.tok_pos[t * k + rank] = q;
+      if (rank == 0) ws.tok_n[t] = n;
     }
-    int n = 0, prev_e = -1;
-    for (int j = 0; j < k; ++j) {
-      const int e = ps[j] >> 16;
-      if (e == prev_e) {
-        ws.tok_pos[tid * k + n - 1] = ps[j] & 0xFFFF;  // repeated expert: keep the last slot
-        continue;
-      }
-      prev_e = e;
-      ws.tok_pos[tid * k + n] = ps[j] & 0xFFFF;
-      ++n;
-    }
-    ws.tok_n[tid] = n;
+  }
+  __syncthreads();
+  for (int i = tid; i < UT; i += kDecThreads) {
+    ws.umap[i] = s_umap[i];
+    ws.uwt[i] = s_uwt[i];
   }
 }
 
-__device__ void quant_row(const MoeWs& ws, const uint16_t* x, int t, int D, bool pow2) {
-  // act_quant of one token row (torch_ops.py:33-49): 8 elements per lane,
-  // 16 lanes per 128-block.
-  for (int c0 = 0; c0 < D; c0 += kDecThreads * 8) {
+__device__ void quant_row(uint8_t* __restrict__ q, float* __restrict__ s, const uint16_t* __restrict__ x,
+                          int K, bool pow2) {
+  // act_quant of one row (torch_ops.py:33-49): 8 elements per lane, 16 lanes per 128-block.
+  for (int c0 = 0; c0 < K; c0 += kDecThreads * 8) {
     const int c = c0 + threadIdx.x * 8;
-    const bool valid = c < D;
+    const bool valid = c < K;
     v4i w = {0, 0, 0, 0};
-    if (valid) w = load16(x + int64_t(t) * D + c);
+    if (valid) w = load16(x + c);
     float f[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -336,20 +303,22 @@ __device__ void quant_row(const MoeWs& ws, const uint16_t* x, int t, int D, bool
                                      quant_div(f[2], sc, pow2), quant_div(f[3], sc, pow2));
       const uint32_t hi = pack_fp8x4(quant_div(f[4], sc, pow2), quant_div(f[5], sc, pow2),
                                      quant_div(f[6], sc, pow2), quant_div(f[7], sc, pow2));
-      *reinterpret_cast<uint2*>(ws.xq + int64_t(t) * D + c) = make_uint2(lo, hi);
-      if ((threadIdx.x & 15) == 0) ws.xs[int64_t(t) * (D / 128) + c / 128] = sc.s;
+      *reinterpret_cast<uint2*>(q + c) = make_uint2(lo, hi);
+      if ((threadIdx.x & 15) == 0) s[c / 128] = sc.s;
     }
   }
 }
 
 __global__ __launch_bounds__(kDecThreads) void route_decode_kernel(wz_moe_desc d, MoeWs ws,
                                                                    const uint16_t* __restrict__ x,
-                                                                   const int64_t* __restrict__ ids,
-                                                                   int T, int n_gate) {
+                                                                   const int64_t* __restrict__ ids, int T,
+                                                                   int n_gate, int u_max) {
+  __shared__ float red[4 * 2 * 4 * kWave];
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nl = lane & 15, g = lane >> 4;
   const int D = d.dim, I = d.inter, E = d.n_experts;
+  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
   int b = blockIdx.x;
   if (b < n_gate) {
     // ---- gate logits: one expert per wave, all T tokens ----
@@ -401,133 +370,137 @@ __global__ __launch_bounds__(kDecThreads) void route_decode_kernel(wz_moe_desc d
     __syncthreads();
     if (!s_last) return;
     acquire_agent();
-    route_last(d, ws, ids, T);
+    route_last(d, ws, ids, T, u_max);
     return;
   }
   b -= n_gate;
-  quant_row(ws, x, b, D, d.act_scale_kind != WZ_SCALE_F32);
+  if (b < T) {
+    quant_row(ws.xq + int64_t(b) * D, ws.xs + int64_t(b) * (D / 128), x + int64_t(b) * D, D, a_pow2);
+    return;
+  }
+  b -= T;
+  // ---- shared expert w1 / w3 (FP8, packed) + SwiGLU for features f0..f0+15 ----
+  const int f0 = b * 16;
+  const int KB = D / 128;
+  const int kb0 = (wave * KB) / 4, kb1 = ((wave + 1) * KB) / 4;
+  const uint8_t* tiles = static_cast<const uint8_t*>(d.sh13p) + int64_t(b) * KB * 4096;
+  const uint16_t* arow = nl < T ? x + int64_t(nl) * D : nullptr;
+  const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  const int64_t sbase = int64_t(f0 >> 7) * KB;
+  v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  for (int kb = kb0; kb < kb1; kb += 4) {
+    v8i w[2][4];
+    int se[2][4];
+    float sf[2][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (kb + q < kb1) {
+        w[0][q] = pk_fp8(tiles + int64_t(kb + q) * 4096, lane);
+        w[1][q] = pk_fp8(tiles + int64_t(kb + q) * 4096 + 2048, lane);
+        fp8_wscale(d.sh_w1_s, sbase + kb + q, d.shared_w_scale_kind, se[0][q], sf[0][q]);
+        fp8_wscale(d.sh_w3_s, sbase + kb + q, d.shared_w_scale_kind, se[1][q], sf[1][q]);
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (kb + q < kb1) {
+        const AOp a = a_from_bf16(arow, kb + q, g, a_pow2);
+        mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], a_pow2, bp, lane);
+        mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], a_pow2, bp, lane);
+      }
+  }
+  reduce_waves<2>(acc, red, wave, lane);
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = g * 4 + i;
+      if (t < T) ws.sh_h[int64_t(t) * I + f0 + nl] = f32_to_bf16(swiglu(acc[0][i], acc[1][i], d.swiglu_limit));
+    }
+  }
 }
 
 // -------------------------------------------------------------------- w13 ---
 
-__global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, MoeWs ws, int T,
-                                                                 int n_sh) {
+__global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, MoeWs ws, int T) {
   __shared__ float red[4 * 2 * 4 * kWave];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nl = lane & 15, g = lane >> 4;
-  const int D = d.dim, I = d.inter, k = d.topk;
+  const int D = d.dim, I = d.inter;
   const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
-  const int nkb = D / 128;
-  const int kb0 = (wave * nkb) / 4, kb1 = ((wave + 1) * nkb) / 4;
-  const int ftiles = I / 16;
-  int b = blockIdx.x;
-  const bool shared = b < n_sh;
-  int f0, row0, nrows;
-  const uint8_t* wrow[2];
-  const uint8_t* srow[2] = {nullptr, nullptr};
-  const void* ws8[2] = {nullptr, nullptr};
-  int64_t sb[2] = {0, 0};
-  if (shared) {
-    f0 = b * 16;
-    row0 = 0;
-    nrows = T;
-    wrow[0] = static_cast<const uint8_t*>(d.sh_w1) + int64_t(f0 + nl) * D;
-    wrow[1] = static_cast<const uint8_t*>(d.sh_w3) + int64_t(f0 + nl) * D;
-    ws8[0] = d.sh_w1_s;
-    ws8[1] = d.sh_w3_s;
-    sb[0] = sb[1] = int64_t(f0 >> 7) * nkb;
-  } else {
-    b -= n_sh;
-    const int u = b / ftiles;
-    f0 = (b % ftiles) * 16;
-    if (u >= ws.n_active[0]) return;
-    const int e = ws.active[u];
-    row0 = ws.act_off[u];
-    nrows = ws.act_cnt[u];
-    const int64_t ebase = int64_t(e) * 2 * I;
-    const uint8_t* w13 = static_cast<const uint8_t*>(d.w13);
-    const uint8_t* w13s = static_cast<const uint8_t*>(d.w13_s);
-    wrow[0] = w13 + (ebase + f0 + nl) * (D / 2);
-    wrow[1] = w13 + (ebase + I + f0 + nl) * (D / 2);
-    srow[0] = w13s + (ebase + f0 + nl) * (D / 32);
-    srow[1] = w13s + (ebase + I + f0 + nl) * (D / 32);
+  const int a_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
+  const int KB = D / 128, KG = (KB + 3) / 4, FT = I / 16;
+  const int u = blockIdx.x / FT, ft = blockIdx.x % FT;
+  if (u >= ws.n_active[0]) return;
+  const int e = ws.active[u];
+  const int kb0 = (wave * KB) / 4, kb1 = ((wave + 1) * KB) / 4;
+  const int64_t tile0 = (int64_t(e) * FT + ft) * KB;  // first K-block of (e, ft)
+  const uint8_t* wt = static_cast<const uint8_t*>(d.w13p) + tile0 * 2048;
+  const uint32_t* st = static_cast<const uint32_t*>(d.w13p_s) + (int64_t(e) * FT + ft) * KG * 2 * 64 + lane;
+  const uint8_t* arow = nl < T ? ws.xq + int64_t(nl) * D : nullptr;
+  const float* asrow = nl < T ? ws.xs + int64_t(nl) * (D / 128) : nullptr;
+  // epilogue data for this lane's output rows (token 4g + i), fetched early
+  int qrow[4];
+  float wrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = g * 4 + i;
+    qrow[i] = t < T ? ws.umap[u * T + t] : -1;
+    wrow[i] = t < T ? ws.uwt[u * T + t] : 0.0f;
   }
-  for (int r0 = 0; r0 < nrows; r0 += 16) {
-    // this lane's A row (token) and, for the epilogue, the routing weight of its output rows
-    const int r = r0 + nl;
-    const int tok = r < nrows ? (shared ? r : ws.perm_token[row0 + r]) : -1;
-    float wt[4] = {1.f, 1.f, 1.f, 1.f};
-    if (!shared && wave == 0) {
+  v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  for (int kb = kb0; kb < kb1; kb += 8) {
+    v8i w[2][8];
+    uint32_t s1[3], s3[3];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rr = r0 + g * 4 + i;
-        if (rr < nrows) {
-          const int p = row0 + rr;
-          wt[i] = ws.weights[ws.perm_token[p] * k + ws.perm_slot[p]];
-        }
+    for (int q = 0; q < 3; ++q) {
+      const int kg = (kb >> 2) + q;
+      s1[q] = kg < KG ? st[(kg * 2 + 0) * 64] : 0u;
+      s3[q] = kg < KG ? st[(kg * 2 + 1) * 64] : 0u;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (kb + q < kb1) {
+        w[0][q] = pk_fp4(wt + int64_t(kb + q) * 2048, lane);
+        w[1][q] = pk_fp4(wt + int64_t(kb + q) * 2048 + 1024, lane);
+      }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int kk = kb + q;
+      if (kk < kb1) {
+        const AOp a = a_from_fp8(arow, asrow, kk, g, a_kind);
+        const int sh = 8 * (kk & 3), qi = (kk >> 2) - (kb >> 2);
+        const int e1 = int((s1[qi] >> sh) & 0xFFu), e3 = int((s3[qi] >> sh) & 0xFFu);
+        mma_step<kFmtFp8, kFmtFp4>(acc[0], a, w[0][q], e1, 1.0f, a_pow2, true, lane);
+        mma_step<kFmtFp8, kFmtFp4>(acc[1], a, w[1][q], e3, 1.0f, a_pow2, true, lane);
       }
     }
-    const uint8_t* arow = tok >= 0 ? ws.xq + int64_t(tok) * D : nullptr;
-    const float* asrow = tok >= 0 ? ws.xs + int64_t(tok) * (D / 128) : nullptr;
-    v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    if (shared)
-      tile_accum<2, kFmtFp8, false, 4>(acc, wrow, srow, ws8, sb, d.shared_w_scale_kind, arow, asrow, a_pow2,
-                                       kb0, kb1, g, lane);
-    else
-      tile_accum<2, kFmtFp4, false, 8>(acc, wrow, srow, ws8, sb, 0, arow, asrow, a_pow2, kb0, kb1, g, lane);
-    reduce_waves<2>(acc, red, wave, lane);
-    if (wave == 0) {
+  }
+  reduce_waves<2>(acc, red, wave, lane);
+  if (wave == 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rr = r0 + g * 4 + i;
-        if (rr < nrows) {
-          const float hv = swiglu(acc[0][i], acc[1][i], d.swiglu_limit);
-          if (shared)
-            ws.sh_h[int64_t(rr) * I + f0 + nl] = f32_to_bf16(hv);
-          else
-            ws.h[int64_t(row0 + rr) * I + f0 + nl] = f32_to_bf16(wt[i] * hv);
-        }
+    for (int i = 0; i < 4; ++i) {
+      if (qrow[i] >= 0) {
+        const int t = g * 4 + i;
+        ws.h[(int64_t(u) * T + t) * I + ft * 16 + nl] =
+            f32_to_bf16(wrow[i] * swiglu(acc[0][i], acc[1][i], d.swiglu_limit));
       }
     }
-    __syncthreads();
   }
 }
 
 // ----------------------------------------------------------------- hquant ---
 
-// act_quant of one h row per WG: rows [0, P) are routed pairs (h), [P, P+T)
-// the shared expert's rows (sh_h).
-__global__ __launch_bounds__(kDecThreads) void hquant_kernel(MoeWs ws, int P, int I, bool pow2) {
-  const int row = blockIdx.x;
-  const uint16_t* src = row < P ? ws.h + int64_t(row) * I : ws.sh_h + int64_t(row - P) * I;
-  for (int c0 = 0; c0 < I; c0 += kDecThreads * 8) {
-    const int c = c0 + threadIdx.x * 8;
-    const bool valid = c < I;
-    v4i w = {0, 0, 0, 0};
-    if (valid) w = load16(src + c);
-    float f[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[2 * i] = bf16lo(uint32_t(w[i]));
-      f[2 * i + 1] = bf16hi(uint32_t(w[i]));
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
-    amax = wave_max_xor(amax, 1);
-    amax = wave_max_xor(amax, 2);
-    amax = wave_max_xor(amax, 4);
-    amax = wave_max_xor(amax, 8);
-    const ActScale sc = act_scale(amax, pow2);
-    if (valid) {
-      const uint32_t lo = pack_fp8x4(quant_div(f[0], sc, pow2), quant_div(f[1], sc, pow2),
-                                     quant_div(f[2], sc, pow2), quant_div(f[3], sc, pow2));
-      const uint32_t hi = pack_fp8x4(quant_div(f[4], sc, pow2), quant_div(f[5], sc, pow2),
-                                     quant_div(f[6], sc, pow2), quant_div(f[7], sc, pow2));
-      *reinterpret_cast<uint2*>(ws.hq + int64_t(row) * I + c) = make_uint2(lo, hi);
-      if ((threadIdx.x & 15) == 0) ws.hs[int64_t(row) * (I / 128) + c / 128] = sc.s;
-    }
+// Row r < u_max*T: h row (u, t), quantised only when routed; row u_max*T + t:
+// the shared expert's row t.
+__global__ __launch_bounds__(kDecThreads) void hquant_kernel(MoeWs ws, int T, int I, int u_max, bool pow2) {
+  const int r = blockIdx.x, UT = u_max * T;
+  const uint16_t* src;
+  if (r < UT) {
+    if (r / T >= ws.n_active[0] || ws.umap[r] < 0) return;
+    src = ws.h + int64_t(r) * I;
+  } else {
+    src = ws.sh_h + int64_t(r - UT) * I;
   }
+  quant_row(ws.hq + int64_t(r) * I, ws.hs + int64_t(r) * (I / 128), src, I, pow2);
 }
 
 // --------------------------------------------------------------------- w2 ---
@@ -535,60 +508,77 @@ __global__ __launch_bounds__(kDecThreads) void hquant_kernel(MoeWs ws, int P, in
 constexpr int kW2Waves = 16;
 constexpr int kW2Threads = kW2Waves * 64;
 
-__global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, MoeWs ws, int T,
+__global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, MoeWs ws, int T, int u_max,
                                                                 uint16_t* __restrict__ y) {
-  __shared__ float out_s[kDecodeMaxT * 16][16];   // routed pair rows (permuted order) x 16 columns
+  __shared__ float out_s[kMaxDecPairs][16];  // routed pair (permuted position) x 16 columns
   __shared__ float sh_s[kDecodeMaxT][16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nl = lane & 15, g = lane >> 4;
   const int D = d.dim, I = d.inter, k = d.topk;
-  const int P = T * k;
   const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
-  const int n0 = blockIdx.x * 16;
-  const int nkb = I / 128;
+  const int a_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
+  const int dt = blockIdx.x, n0 = dt * 16;
+  const int KB = I / 128, KG = (KB + 3) / 4, DT = D / 16, UT = u_max * T;
   const int n_act = ws.n_active[0];
   for (int job = wave; job <= n_act; job += kW2Waves) {
     const bool shared = job == n_act;
-    int row0, nrows;
-    const uint8_t* wrow[1];
-    const uint8_t* srow[1] = {nullptr};
-    const void* ws8[1] = {nullptr};
-    int64_t sb[1] = {0};
+    const int arow0 = shared ? UT : job * T;
+    const uint8_t* arow = nl < T ? ws.hq + int64_t(arow0 + nl) * I : nullptr;
+    const float* asrow = nl < T ? ws.hs + int64_t(arow0 + nl) * (I / 128) : nullptr;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
     if (shared) {
-      row0 = P;  // shared rows follow the pairs in hq
-      nrows = T;
-      wrow[0] = static_cast<const uint8_t*>(d.sh_w2) + int64_t(n0 + nl) * I;
-      ws8[0] = d.sh_w2_s;
-      sb[0] = int64_t(n0 >> 7) * nkb;
+      const uint8_t* tiles = static_cast<const uint8_t*>(d.sh2p) + int64_t(dt) * KB * 2048;
+      const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+      const int64_t sbase = int64_t(n0 >> 7) * KB;
+      for (int kb = 0; kb < KB; kb += 4) {
+        v8i w[4];
+        int se[4];
+        float sf[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (kb + q < KB) {
+            w[q] = pk_fp8(tiles + int64_t(kb + q) * 2048, lane);
+            fp8_wscale(d.sh_w2_s, sbase + kb + q, d.shared_w_scale_kind, se[q], sf[q]);
+          }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (kb + q < KB) {
+            const AOp a = a_from_fp8(arow, asrow, kb + q, g, a_kind);
+            mma_step<kFmtFp8, kFmtFp8>(acc, a, w[q], se[q], sf[q], a_pow2, bp, lane);
+          }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (g * 4 + i < T) sh_s[g * 4 + i][nl] = bf16_round(acc[i]);
     } else {
       const int e = ws.active[job];
-      row0 = ws.act_off[job];
-      nrows = ws.act_cnt[job];
-      const int64_t ebase = int64_t(e) * D;
-      wrow[0] = static_cast<const uint8_t*>(d.w2) + (ebase + n0 + nl) * (I / 2);
-      srow[0] = static_cast<const uint8_t*>(d.w2_s) + (ebase + n0 + nl) * (I / 32);
-    }
-    for (int r0 = 0; r0 < nrows; r0 += 16) {
-      const int r = r0 + nl;
-      const uint8_t* arow = r < nrows ? ws.hq + int64_t(row0 + r) * I : nullptr;
-      const float* asrow = r < nrows ? ws.hs + int64_t(row0 + r) * (I / 128) : nullptr;
-      v4f acc[1] = {{0.f, 0.f, 0.f, 0.f}};
-      if (shared)
-        tile_accum<1, kFmtFp8, false, 4>(acc, wrow, srow, ws8, sb, d.shared_w_scale_kind, arow, asrow, a_pow2,
-                                         0, nkb, g, lane);
-      else
-        tile_accum<1, kFmtFp4, false, 8>(acc, wrow, srow, ws8, sb, 0, arow, asrow, a_pow2, 0, nkb, g, lane);
+      const uint8_t* wt = static_cast<const uint8_t*>(d.w2p) + (int64_t(e) * DT + dt) * KB * 1024;
+      const uint32_t* st = static_cast<const uint32_t*>(d.w2p_s) + (int64_t(e) * DT + dt) * KG * 64 + lane;
+      int qrow[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rr = r0 + g * 4 + i;
-        if (rr < nrows) {
-          const float v = bf16_round(acc[0][i]);  // each linear's output is bf16 (architecture.py:741)
-          if (shared)
-            sh_s[rr][nl] = v;
-          else
-            out_s[row0 + rr][nl] = v;
+      for (int i = 0; i < 4; ++i) qrow[i] = g * 4 + i < T ? ws.umap[job * T + g * 4 + i] : -1;
+      for (int kb = 0; kb < KB; kb += 8) {
+        v8i w[8];
+        uint32_t sc[3];
+#pragma unroll
+        for (int q = 0; q < 3; ++q) sc[q] = (kb >> 2) + q < KG ? st[((kb >> 2) + q) * 64] : 0u;
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (kb + q < KB) w[q] = pk_fp4(wt + int64_t(kb + q) * 1024, lane);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int kk = kb + q;
+          if (kk < KB) {
+            const AOp a = a_from_fp8(arow, asrow, kk, g, a_kind);
+            const int es = int((sc[(kk >> 2) - (kb >> 2)] >> (8 * (kk & 3))) & 0xFFu);
+            mma_step<kFmtFp8, kFmtFp4>(acc, a, w[q], es, 1.0f, a_pow2, true, lane);
+          }
         }
       }
+      // each linear's output is bf16 (architecture.py:741)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (qrow[i] >= 0) out_s[qrow[i]][nl] = bf16_round(acc[i]);
     }
   }
   __syncthreads();
@@ -608,18 +598,19 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
   const int n_gate = (E + 3) / 4;
   const int64_t P = T * k;
   const int u_max = int(P < E ? P : E);
-  if (P > kDecodeMaxT * 16) return set_error(WZ_EINVAL, "moe decode: T*topk=%lld exceeds %d", (long long)P,
-                                             kDecodeMaxT * 16);
-  WZ_LAUNCH("moe_route", stream, route_decode_kernel, dim3(unsigned(n_gate + T)), dim3(kDecThreads), 0, *d, w,
-            static_cast<const uint16_t*>(x), ids, int(T), n_gate);
+  if (P > kMaxDecPairs) return set_error(WZ_EINVAL, "moe decode: T*topk=%lld exceeds %d", (long long)P, kMaxDecPairs);
+  if (!d->w13p || !d->w13p_s || !d->w2p || !d->w2p_s || !d->sh13p || !d->sh2p)
+    return set_error(WZ_EINVAL, "moe decode: packed banks missing (wz_moe_pack)");
+  WZ_LAUNCH("moe_route", stream, route_decode_kernel, dim3(unsigned(n_gate + T + I / 16)), dim3(kDecThreads), 0,
+            *d, w, static_cast<const uint16_t*>(x), ids, int(T), n_gate, u_max);
   if (int rc = check_launch("moe route")) return rc;
-  WZ_LAUNCH("moe_w13", stream, w13_decode_kernel, dim3(unsigned(I / 16 + u_max * (I / 16))), dim3(kDecThreads),
-            0, *d, w, int(T), I / 16);
+  WZ_LAUNCH("moe_w13", stream, w13_decode_kernel, dim3(unsigned(u_max * (I / 16))), dim3(kDecThreads), 0, *d, w,
+            int(T));
   if (int rc = check_launch("moe w13")) return rc;
-  WZ_LAUNCH("moe_hquant", stream, hquant_kernel, dim3(unsigned(P + T)), dim3(kDecThreads), 0, w, int(P), I,
-            d->act_scale_kind != WZ_SCALE_F32);
+  WZ_LAUNCH("moe_hquant", stream, hquant_kernel, dim3(unsigned(u_max * T + T)), dim3(kDecThreads), 0, w, int(T), I,
+            u_max, d->act_scale_kind != WZ_SCALE_F32);
   if (int rc = check_launch("moe hquant")) return rc;
-  WZ_LAUNCH("moe_w2", stream, w2_combine_kernel, dim3(unsigned(D / 16)), dim3(kW2Threads), 0, *d, w, int(T),
+  WZ_LAUNCH("moe_w2", stream, w2_combine_kernel, dim3(unsigned(D / 16)), dim3(kW2Threads), 0, *d, w, int(T), u_max,
             static_cast<uint16_t*>(y));
   return check_launch("moe w2");
 }

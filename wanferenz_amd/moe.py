@@ -49,7 +49,12 @@ class WzMoeDesc(ctypes.Structure):
         ("sh_w1", ctypes.c_void_p), ("sh_w1_s", ctypes.c_void_p),
         ("sh_w3", ctypes.c_void_p), ("sh_w3_s", ctypes.c_void_p),
         ("sh_w2", ctypes.c_void_p), ("sh_w2_s", ctypes.c_void_p),
+        ("w13p", ctypes.c_void_p), ("w13p_s", ctypes.c_void_p),
+        ("w2p", ctypes.c_void_p), ("w2p_s", ctypes.c_void_p),
+        ("sh13p", ctypes.c_void_p), ("sh2p", ctypes.c_void_p),
     ]
+
+PACKED_NAMES = ("w13p", "w13p_s", "w2p", "w2p_s", "sh13p", "sh2p")
 
 
 @dataclass
@@ -149,9 +154,23 @@ class HipMoE:
             setattr(d, name, getattr(w, name).data_ptr())
         self.desc = d
         self.device = w.gate_w.device
+        self.packed = self._pack()
         self._ws = None
         self._ws_tokens = 0
         self.reserve(max_tokens)
+
+    def _pack(self) -> dict:
+        """Build the MFMA-ready packed banks the decode kernels stream (pack.hip)."""
+        d = self.desc
+        bufs = {}
+        for i, name in enumerate(PACKED_NAMES):
+            n = int(N.lib().wz_moe_packed_bytes(ctypes.byref(d), i))
+            bufs[name] = torch.empty(n, dtype=torch.uint8, device=self.device)
+        N.call("wz_moe_pack", ctypes.byref(d), *(bufs[n].data_ptr() for n in PACKED_NAMES),
+               N.stream_handle(self.device))
+        for name in PACKED_NAMES:
+            setattr(d, name, bufs[name].data_ptr())
+        return bufs
 
     # -- workspace -----------------------------------------------------------
     def workspace_bytes(self, T: int) -> int:
