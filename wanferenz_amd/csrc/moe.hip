@@ -332,7 +332,7 @@ __device__ void w13_item(const wz_moe_desc& d, const MoeWs& ws, const uint16_t* 
     for (int t = 0; t < kMT; ++t) {
       const int r = r0 + t * 16 + nl;
       int tok = -1;
-      if (r < nrows) tok = SHARED ? r : ws.perm_token[row0 + r];
+      if (r < nrows) tok = SHARED ? r : clampi(ws.perm_token[row0 + r], 0, T - 1);
       arow[t] = tok >= 0 ? x + int64_t(tok) * D : nullptr;
     }
     const int ntiles = min(kMT, (nrows - r0 + 15) / 16);
@@ -410,7 +410,8 @@ __device__ void w13_item(const wz_moe_desc& d, const MoeWs& ws, const uint16_t* 
             ws.sh_h[int64_t(r) * I + f0 + nl] = f32_to_bf16(hv);
           } else {
             const int p = row0 + r;
-            const float wt = ws.weights[int64_t(ws.perm_token[p]) * d.topk + ws.perm_slot[p]];
+            const float wt = ws.weights[int64_t(clampi(ws.perm_token[p], 0, T - 1)) * d.topk +
+                                        clampi(ws.perm_slot[p], 0, d.topk - 1)];
             ws.h[int64_t(p) * I + f0 + nl] = f32_to_bf16(wt * hv);
           }
         }
@@ -433,8 +434,11 @@ __global__ __launch_bounds__(kMoeThreads) void w13_kernel(wz_moe_desc d, MoeWs w
   }
   const int r = item - n_shared_items;
   const int u = r / ftiles, ft = r % ftiles;
-  if (u >= ws.n_active[0]) return;
-  w13_item<false, MT>(d, ws, x, T, ft * 16, ws.active[u], ws.act_off[u], ws.act_cnt[u], red);
+  if (u >= min(ws.n_active[0], d.n_experts)) return;
+  const int P = T * d.topk;
+  const int row0 = clampi(ws.act_off[u], 0, P);
+  w13_item<false, MT>(d, ws, x, T, ft * 16, clampi(ws.active[u], 0, d.n_experts - 1), row0,
+                      clampi(ws.act_cnt[u], 0, P - row0), red);
 }
 
 // -------------------------------------------------------------------- w2 ----
@@ -545,8 +549,11 @@ __global__ __launch_bounds__(kMoeThreads) void w2_kernel(wz_moe_desc d, MoeWs ws
   }
   const int r = item - n_shared_items;
   const int u = r / ntiles, nt = r % ntiles;
-  if (u >= ws.n_active[0]) return;
-  w2_item<false, MT>(d, ws, T, nt * 16, ws.active[u], ws.act_off[u], ws.act_cnt[u], red);
+  if (u >= min(ws.n_active[0], d.n_experts)) return;
+  const int P = T * d.topk;
+  const int row0 = clampi(ws.act_off[u], 0, P);
+  w2_item<false, MT>(d, ws, T, nt * 16, clampi(ws.active[u], 0, d.n_experts - 1), row0,
+                     clampi(ws.act_cnt[u], 0, P - row0), red);
 }
 
 // --------------------------------------------------------------- combine ----
@@ -557,7 +564,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int
   const int c = blockIdx.x * 256 + threadIdx.x;  // 8-column chunk
   if (c * 8 >= D) return;
   int ps[16];
-  for (int j = 0; j < k; ++j) ps[j] = ws.pos[int64_t(t) * k + j];
+  const int P = gridDim.y * k;
+  for (int j = 0; j < k; ++j) ps[j] = clampi(ws.pos[int64_t(t) * k + j], 0, P - 1);
   // ascending permuted position == ascending expert id
   for (int i = 1; i < k; ++i) {
     int v = ps[i], j = i - 1;
@@ -573,7 +581,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int
   int prev_e = -1;
   for (int j = 0; j < k; ++j) {
     const int p = ps[j];
-    const int pe = ws.idx[int64_t(ws.perm_token[p]) * k + ws.perm_slot[p]];
+    const int pe = ws.idx[int64_t(clampi(ws.perm_token[p], 0, gridDim.y - 1)) * k + clampi(ws.perm_slot[p], 0, k - 1)];
     if (pe == prev_e) continue;  // repeated expert of a hash-routed token: counted once
     prev_e = pe;
     const v4i v = load16(ws.out2 + int64_t(p) * D + c * 8);

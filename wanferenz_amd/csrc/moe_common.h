@@ -17,7 +17,8 @@ constexpr int kCounterWords = 4096;   // arrival counters at the start of the wo
 // without knowing T; every kernel that bumps a counter resets it to zero.
 struct MoeWs {
   uint32_t* counters;  // [kCounterWords]: [0] route, [1 + d_tile] combine
-  float* scores;       // [T, E]
+  float* scores;       // [T, E] gate logits (general path) / scores (decode path)
+  float* biased;       // [T, E] decode path: scores + bias (the selection key)
   float* weights;      // [T, k]
   int32_t* idx;        // [T, k]
   int32_t* offsets;    // [E + 1]
@@ -58,6 +59,7 @@ static inline MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base
   };
   w.counters = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * kCounterWords));
   w.scores = reinterpret_cast<float*>(take(sizeof(float) * T * E));
+  w.biased = reinterpret_cast<float*>(take(sizeof(float) * T * E));
   w.weights = reinterpret_cast<float*>(take(sizeof(float) * P));
   w.idx = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * P));
   w.offsets = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (E + 1)));
@@ -83,6 +85,11 @@ static inline MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base
   w.bytes = off;
   return w;
 }
+
+// Routing tables live in device memory and are produced by an earlier kernel;
+// every consumer clamps what it reads so that no table value can address
+// outside the weight banks, the workspace or LDS.
+__device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
@@ -120,6 +127,27 @@ __device__ __forceinline__ Cand wave_argmax(Cand c) {
   }
   return c;
 }
+
+// Order-preserving map float -> uint32 (larger float -> larger key; -inf lowest).
+__device__ __forceinline__ uint32_t f32_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Wave-wide max of a uint32 through DPP row ops (no LDS round trips): quad
+// swaps and row mirrors give every lane its row's max, row_bcast15/31 fold
+// the four rows into lane 63, readlane broadcasts it.
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0xB1, 0xF, 0xF, false)));   // quad_perm 1,0,3,2
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x4E, 0xF, 0xF, false)));   // quad_perm 2,3,0,1
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x141, 0xF, 0xF, false)));  // row_half_mirror
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x140, 0xF, 0xF, false)));  // row_mirror
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x142, 0xA, 0xF, false)));  // row_bcast:15
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x143, 0xC, 0xF, false)));  // row_bcast:31
+  return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
+}
+
+__device__ __forceinline__ uint32_t dpp_min_u32(uint32_t v) { return ~dpp_max_u32(~v); }
 
 // Agent-scope arrival counter: returns true in the last of `n` arrivals and
 // resets the counter for the next launch.  Producers publish their global

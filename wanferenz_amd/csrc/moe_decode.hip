@@ -2,16 +2,18 @@
 //
 // Four stream-ordered launches, no host sync, no allocation (graph-capturable):
 //
-//   route   WGs of 4 gate experts: logits x.W^T (exact bf16 products, fp64
+//   route   WGs of 16 gate experts x one token: logits x.W^T (exact bf16 products, fp64
 //           sums); the last gate WG to arrive (agent-scope counter) does score
 //           function + bias + top-k + renormalise for every token
 //           (Gate.forward, architecture.py:696-718), the canonical (expert,
 //           token, slot) permutation (expert_batch.py:24-37), the active-
-//           expert list and the per-token combine lists.  In the same launch,
-//           T WGs quantise x (act_quant) and I/16 WGs run the shared
-//           expert's FP8 w1/w3 + SwiGLU, which need only x.
+//           expert list and the per-token combine lists.  Each gate wave
+//           evaluates the score function for its expert (lane t = token t),
+//           so the last WG only selects: top-k is k rounds of a DPP wave-max.
+//           In the same launch, T WGs quantise x (act_quant).
 //   w13     per (active expert, 16 intermediate features): MXFP4 w1 and w3
-//           tiles streamed once, SwiGLU + clamp + routing weight, bf16 h.
+//           tiles streamed once, SwiGLU + clamp + routing weight, bf16 h;
+//           the shared expert's FP8 w1/w3 tiles run first in the same grid.
 //   hquant  act_quant of the h rows that are routed, and of the shared rows.
 //   w2      one WG per 16 output columns; each wave computes one expert's
 //           16-column tile over the full K (MXFP4, or FP8 for the shared
@@ -30,6 +32,8 @@
 namespace wz {
 
 constexpr int kDecThreads = 256;
+constexpr int kRouteWaves = 16;                 // one wave per decode token in the routing phase
+constexpr int kRouteThreads_ = kRouteWaves * 64;
 
 __device__ __forceinline__ v8i pk_fp4(const uint8_t* tile, int lane) {
   const v4i x = load16_nt(tile + lane * 16);
@@ -84,18 +88,23 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
   __shared__ int cnt[kMaxExperts];
   __shared__ int base[kMaxExperts];
   __shared__ int ucode[kMaxExperts];
-  __shared__ int wc[4][kMaxExperts];
+  __shared__ int wc[kRouteWaves][kMaxExperts];
   __shared__ int s_umap[kMaxUT];
   __shared__ float s_uwt[kMaxUT];
   const int E = d.n_experts, k = d.topk, P = T * k, UT = u_max * T;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr int kSlots = kMaxExperts / 64;
-  // ---- top-k, one wave per token ----
-  for (int t = wave; t < T; t += 4) {
-    const float* a = ws.scores + int64_t(t) * E;
-    float s[kSlots], b[kSlots];
+  // ---- top-k, one wave per token.  The gate waves already wrote each
+  // expert's score and biased score; softmax needs the whole row here.
+  // (Loops in this single-workgroup phase stay rolled: it runs once per
+  // launch, so its code is fetched cold and code size is its latency.) ----
+#pragma unroll 1
+  for (int t = wave; t < T; t += kRouteWaves) {
+    float sv[kSlots];
+    uint32_t key[kSlots];
     double mx = -1e300, sum = 0.0;
     if (d.score_func == WZ_SCORE_SOFTMAX) {
+      const float* a = ws.scores + int64_t(t) * E;
 #pragma unroll
       for (int i = 0; i < kSlots; ++i)
         if (lane + 64 * i < E) mx = fmax(mx, double(a[lane + 64 * i]));
@@ -110,11 +119,17 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       const int e = lane + 64 * i;
-      float v = -INFINITY;
-      if (e < E)
-        v = d.score_func == WZ_SCORE_SOFTMAX ? float(exp(double(a[e]) - mx) / sum) : score_of(a[e], d.score_func);
-      s[i] = v;
-      b[i] = (e < E && d.tid2eid == nullptr && d.gate_bias != nullptr) ? v + d.gate_bias[e] : v;
+      sv[i] = 0.0f;
+      key[i] = 0u;
+      if (e < E) {
+        if (d.score_func == WZ_SCORE_SOFTMAX) {
+          sv[i] = float(exp(double(ws.scores[int64_t(t) * E + e]) - mx) / sum);
+          key[i] = f32_key((d.tid2eid == nullptr && d.gate_bias != nullptr) ? sv[i] + d.gate_bias[e] : sv[i]);
+        } else {
+          sv[i] = ws.scores[int64_t(t) * E + e];
+          key[i] = f32_key(ws.biased[int64_t(t) * E + e]);
+        }
+      }
     }
     int my_sel = 0;
     if (d.tid2eid != nullptr) {
@@ -126,22 +141,35 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       }
     } else {
       unsigned taken = 0u;
+#pragma unroll 1
       for (int j = 0; j < k; ++j) {
-        Cand best = {-INFINITY, 0x7FFFFFFF};
+        // this lane's best remaining expert (lowest slot on equal keys = lowest id)
+        uint32_t best = 0u;
+        int bi = -1;
 #pragma unroll
-        for (int i = 0; i < kSlots; ++i) {
-          const int e = lane + 64 * i;
-          if (e < E && !((taken >> i) & 1u)) best = cand_better(best, Cand{b[i], e});
+        for (int i = 0; i < kSlots; ++i)
+          if (lane + 64 * i < E && !((taken >> i) & 1u) && (bi < 0 || key[i] > best)) {
+            best = key[i];
+            bi = i;
+          }
+        const uint32_t m = dpp_max_u32(bi >= 0 ? best : 0u);
+        const bool cand = bi >= 0 && best == m;
+        const unsigned long long mask = __ballot(cand);
+        int we;
+        if (__popcll(mask) == 1) {
+          const int wl = __ffsll((long long)mask) - 1;
+          we = wl + 64 * __builtin_amdgcn_readlane(bi, wl);
+        } else {  // equal keys: the lowest expert id wins (torch.topk keeps the earlier index)
+          we = int(dpp_min_u32(cand ? uint32_t(lane + 64 * bi) : 0xFFFFFFFFu));
         }
-        best = wave_argmax(best);
-        if (lane == j) my_sel = best.i;
-        if ((best.i & 63) == lane) taken |= 1u << (best.i >> 6);
+        if ((we & 63) == lane) taken |= 1u << (we >> 6);
+        if (lane == j) my_sel = we;
       }
     }
     float mine = 0.0f;
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
-      const float v = __shfl(s[i], my_sel & 63, kWave);
+      const float v = __shfl(sv[i], my_sel & 63, kWave);
       if ((my_sel >> 6) == i) mine = v;
     }
     float tot = 0.0f;
@@ -156,17 +184,16 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       s_w[t * k + lane] = v;
     }
   }
-  for (int e = tid; e < kMaxExperts; e += kDecThreads) cnt[e] = 0;
-  for (int i = tid; i < UT; i += kDecThreads) s_umap[i] = -1;
+  for (int e = tid; e < kMaxExperts; e += kRouteThreads_) cnt[e] = 0;
+  for (int i = tid; i < UT; i += kRouteThreads_) s_umap[i] = -1;
   __syncthreads();
-  for (int p = tid; p < P; p += kDecThreads) atomicAdd(&cnt[s_e[p]], 1);
+  for (int p = tid; p < P; p += kRouteThreads_) atomicAdd(&cnt[s_e[p]], 1);
   __syncthreads();
-  // ---- exclusive scans of counts and of (count > 0), 2 experts per thread ----
+  // ---- exclusive scans of counts and of (count > 0), one expert per thread ----
   {
-    const int e0 = 2 * tid, e1 = 2 * tid + 1;
-    const int c0 = e0 < E ? cnt[e0] : 0, c1 = e1 < E ? cnt[e1] : 0;
-    const int v = c0 + c1, f = (c0 > 0) + (c1 > 0);
-    int vi = v, fi = f;
+    const int c = tid < E ? cnt[tid] : 0;
+    const int f = c > 0 ? 1 : 0;
+    int vi = c, fi = f;
 #pragma unroll
     for (int dd = 1; dd < 64; dd <<= 1) {
       const int ov = __shfl_up(vi, dd, kWave), of = __shfl_up(fi, dd, kWave);
@@ -181,33 +208,23 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
     }
     __syncthreads();
     int vb = 0, fb = 0;
+#pragma unroll 1
     for (int w = 0; w < wave; ++w) {
       vb += wc[0][w];
       fb += wc[1][w];
     }
-    const int ex0 = vb + vi - v, fx0 = fb + fi - f;
-    if (e0 < E) {
-      base[e0] = ex0;
-      ws.offsets[e0] = ex0;
-      if (c0 > 0) {
-        ucode[e0] = fx0;
-        ws.active[fx0] = e0;
-        ws.act_off[fx0] = ex0;
-        ws.act_cnt[fx0] = c0;
+    const int ex = vb + vi - c, fx = fb + fi - f;
+    if (tid < E) {
+      base[tid] = ex;
+      ws.offsets[tid] = ex;
+      if (c > 0) {
+        ucode[tid] = fx;
+        ws.active[fx] = tid;
+        ws.act_off[fx] = ex;
+        ws.act_cnt[fx] = c;
       }
     }
-    if (e1 < E) {
-      base[e1] = ex0 + c0;
-      ws.offsets[e1] = ex0 + c0;
-      if (c1 > 0) {
-        const int u = fx0 + (c0 > 0);
-        ucode[e1] = u;
-        ws.active[u] = e1;
-        ws.act_off[u] = ex0 + c0;
-        ws.act_cnt[u] = c1;
-      }
-    }
-    if (tid == kDecThreads - 1) {
+    if (tid == kRouteThreads_ - 1) {
       ws.offsets[E] = vb + vi;
       ws.n_active[0] = fb + fi;
     }
@@ -230,12 +247,13 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
     }
     const int rank = __popcll(mask & lt);
     const bool leader = (mask & lt) == 0ull;
-    for (int i = tid; i < 4 * kMaxExperts; i += kDecThreads) (&wc[0][0])[i] = 0;
+    for (int i = tid; i < kRouteWaves * kMaxExperts; i += kRouteThreads_) (&wc[0][0])[i] = 0;
     __syncthreads();
     if (valid && leader) wc[wave][e] = __popcll(mask);
     __syncthreads();
     if (valid) {
       int before = 0;
+#pragma unroll 1
       for (int w = 0; w < wave; ++w) before += wc[w][e];
       const int q = base[e] + before + rank;
       ws.perm_token[q] = p / k;
@@ -247,30 +265,31 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
   __syncthreads();
   // ---- (expert, token) map and per-token combine lists.  A token that lists an
   // expert twice keeps its last slot (architecture.py:790 index_put semantics). ----
+  __shared__ int s_last_of[kMaxDecPairs];
   if (tid < P) {
     const int p = tid, t = p / k, j = p % k, e = s_e[p];
-    bool last = true;
-    for (int jj = j + 1; jj < k; ++jj) last = last && (s_e[t * k + jj] != e);
-    if (last) {
-      const int q = s_q[p];
-      s_umap[ucode[e] * T + t] = q;
-      s_uwt[ucode[e] * T + t] = s_w[p];
-      int rank = 0, n = 0;
-      for (int jj = 0; jj < k; ++jj) {
-        const int pe = s_e[t * k + jj];
-        bool l2 = true;
-        for (int j3 = jj + 1; j3 < k; ++j3) l2 = l2 && (s_e[t * k + j3] != pe);
-        if (l2) {
-          ++n;
-          if (s_q[t * k + jj] < q) ++rank;
-        }
-      }
-      ws.tok_pos[t * k + rank] = q;
-      if (rank == 0) ws.tok_n[t] = n;
-    }
+    int last = 1;
+#pragma unroll 1
+    for (int jj = j + 1; jj < k; ++jj) last &= (s_e[t * k + jj] != e) ? 1 : 0;
+    s_last_of[p] = last;
   }
   __syncthreads();
-  for (int i = tid; i < UT; i += kDecThreads) {
+  if (tid < P && s_last_of[tid]) {
+    const int p = tid, t = p / k, e = s_e[p], q = s_q[p];
+    int n = 0, rank = 0;
+#pragma unroll 1
+    for (int jj = 0; jj < k; ++jj) {
+      const int o = s_last_of[t * k + jj];
+      n += o;
+      rank += (o && s_q[t * k + jj] < q) ? 1 : 0;
+    }
+    s_umap[ucode[e] * T + t] = q;
+    s_uwt[ucode[e] * T + t] = s_w[p];
+    ws.tok_pos[t * k + rank] = q;
+    if (rank == 0) ws.tok_n[t] = n;
+  }
+  __syncthreads();
+  for (int i = tid; i < UT; i += kRouteThreads_) {
     ws.umap[i] = s_umap[i];
     ws.uwt[i] = s_uwt[i];
   }
@@ -279,7 +298,7 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
 __device__ void quant_row(uint8_t* __restrict__ q, float* __restrict__ s, const uint16_t* __restrict__ x,
                           int K, bool pow2) {
   // act_quant of one row (torch_ops.py:33-49): 8 elements per lane, 16 lanes per 128-block.
-  for (int c0 = 0; c0 < K; c0 += kDecThreads * 8) {
+  for (int c0 = 0; c0 < K; c0 += int(blockDim.x) * 8) {
     const int c = c0 + threadIdx.x * 8;
     const bool valid = c < K;
     v4i w = {0, 0, 0, 0};
@@ -309,118 +328,71 @@ __device__ void quant_row(uint8_t* __restrict__ q, float* __restrict__ s, const 
   }
 }
 
-__global__ __launch_bounds__(kDecThreads) void route_decode_kernel(wz_moe_desc d, MoeWs ws,
+__global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_desc d, MoeWs ws,
                                                                    const uint16_t* __restrict__ x,
                                                                    const int64_t* __restrict__ ids, int T,
                                                                    int n_gate, int u_max) {
-  __shared__ float red[4 * 2 * 4 * kWave];
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nl = lane & 15, g = lane >> 4;
-  const int D = d.dim, I = d.inter, E = d.n_experts;
+  const int D = d.dim, E = d.n_experts;
   const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
   int b = blockIdx.x;
-  if (b < n_gate) {
-    // ---- gate logits: one expert per wave, all T tokens ----
-    const int e = b * 4 + wave;
+  if (b < n_gate * T) {
+    // ---- gate logit of one (expert, token) per wave; lane 0 applies the score
+    // function and the bias (the selection key) ----
+    const int e = (b % n_gate) * kRouteWaves + wave, t = b / n_gate;
     if (e < E) {
       const uint16_t* wr = static_cast<const uint16_t*>(d.gate_w) + int64_t(e) * D;
+      const uint16_t* xr = x + int64_t(t) * D;
       const int nc = D / 8;
-      double acc[kDecodeMaxT];
-#pragma unroll
-      for (int t = 0; t < kDecodeMaxT; ++t) acc[t] = 0.0;
+      double acc = 0.0;
+#pragma unroll 1
       for (int c0 = 0; c0 < nc; c0 += 64 * 8) {
-        v4i wv[8];
+        v4i wv[8], xv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int c = c0 + lane + 64 * i;
           wv[i] = c < nc ? load16(wr + c * 8) : v4i{0, 0, 0, 0};
+          xv[i] = c < nc ? load16(xr + c * 8) : v4i{0, 0, 0, 0};
         }
 #pragma unroll
-        for (int t = 0; t < kDecodeMaxT; ++t) {
-          if (t < T) {
+        for (int i = 0; i < 8; ++i)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const int c = c0 + lane + 64 * i;
-              if (c < nc) {
-                const v4i xv = load16(x + int64_t(t) * D + c * 8);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                  acc[t] += double(bf16lo(uint32_t(xv[j])) * bf16lo(uint32_t(wv[i][j])));
-                  acc[t] += double(bf16hi(uint32_t(xv[j])) * bf16hi(uint32_t(wv[i][j])));
-                }
-              }
-            }
+          for (int j = 0; j < 4; ++j) {
+            acc += double(bf16lo(uint32_t(xv[i][j])) * bf16lo(uint32_t(wv[i][j])));
+            acc += double(bf16hi(uint32_t(xv[i][j])) * bf16hi(uint32_t(wv[i][j])));
           }
-        }
       }
 #pragma unroll
-      for (int t = 0; t < kDecodeMaxT; ++t) {
-        if (t < T) {
-          double v = acc[t];
-#pragma unroll
-          for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-          if (lane == 0) ws.scores[int64_t(t) * E + e] = float(v);
+      for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, kWave);
+      if (lane == 0) {
+        const int64_t o = int64_t(t) * E + e;
+        const float logit = float(acc);
+        if (d.score_func == WZ_SCORE_SOFTMAX) {
+          ws.scores[o] = logit;
+        } else {
+          const float sc = score_of(logit, d.score_func);
+          ws.scores[o] = sc;
+          ws.biased[o] = (d.tid2eid == nullptr && d.gate_bias != nullptr) ? sc + d.gate_bias[e] : sc;
         }
       }
     }
     release_agent();
     __syncthreads();
-    if (tid == 0) s_last = arrive_last(&ws.counters[0], uint32_t(n_gate)) ? 1 : 0;
+    if (tid == 0) s_last = arrive_last(&ws.counters[0], uint32_t(n_gate * T)) ? 1 : 0;
     __syncthreads();
     if (!s_last) return;
     acquire_agent();
     route_last(d, ws, ids, T, u_max);
     return;
   }
-  b -= n_gate;
-  if (b < T) {
-    quant_row(ws.xq + int64_t(b) * D, ws.xs + int64_t(b) * (D / 128), x + int64_t(b) * D, D, a_pow2);
-    return;
-  }
-  b -= T;
-  // ---- shared expert w1 / w3 (FP8, packed) + SwiGLU for features f0..f0+15 ----
-  const int f0 = b * 16;
-  const int KB = D / 128;
-  const int kb0 = (wave * KB) / 4, kb1 = ((wave + 1) * KB) / 4;
-  const uint8_t* tiles = static_cast<const uint8_t*>(d.sh13p) + int64_t(b) * KB * 4096;
-  const uint16_t* arow = nl < T ? x + int64_t(nl) * D : nullptr;
-  const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
-  const int64_t sbase = int64_t(f0 >> 7) * KB;
-  v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  for (int kb = kb0; kb < kb1; kb += 4) {
-    v8i w[2][4];
-    int se[2][4];
-    float sf[2][4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (kb + q < kb1) {
-        w[0][q] = pk_fp8(tiles + int64_t(kb + q) * 4096, lane);
-        w[1][q] = pk_fp8(tiles + int64_t(kb + q) * 4096 + 2048, lane);
-        fp8_wscale(d.sh_w1_s, sbase + kb + q, d.shared_w_scale_kind, se[0][q], sf[0][q]);
-        fp8_wscale(d.sh_w3_s, sbase + kb + q, d.shared_w_scale_kind, se[1][q], sf[1][q]);
-      }
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (kb + q < kb1) {
-        const AOp a = a_from_bf16(arow, kb + q, g, a_pow2);
-        mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], a_pow2, bp, lane);
-        mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], a_pow2, bp, lane);
-      }
-  }
-  reduce_waves<2>(acc, red, wave, lane);
-  if (wave == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = g * 4 + i;
-      if (t < T) ws.sh_h[int64_t(t) * I + f0 + nl] = f32_to_bf16(swiglu(acc[0][i], acc[1][i], d.swiglu_limit));
-    }
-  }
+  b -= n_gate * T;
+  if (b < T) quant_row(ws.xq + int64_t(b) * D, ws.xs + int64_t(b) * (D / 128), x + int64_t(b) * D, D, a_pow2);
 }
 
 // -------------------------------------------------------------------- w13 ---
 
-__global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, MoeWs ws, int T) {
+__global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, MoeWs ws, int T, int u_max) {
   __shared__ float red[4 * 2 * 4 * kWave];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nl = lane & 15, g = lane >> 4;
@@ -428,15 +400,56 @@ __global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, 
   const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
   const int a_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
   const int KB = D / 128, KG = (KB + 3) / 4, FT = I / 16;
-  const int u = blockIdx.x / FT, ft = blockIdx.x % FT;
-  if (u >= ws.n_active[0]) return;
-  const int e = ws.active[u];
   const int kb0 = (wave * KB) / 4, kb1 = ((wave + 1) * KB) / 4;
+  // A operand: the token batch, row t = token t (act_quant(x) from the route kernel)
+  const uint8_t* arow = nl < T ? ws.xq + int64_t(nl) * D : nullptr;
+  const float* asrow = nl < T ? ws.xs + int64_t(nl) * (D / 128) : nullptr;
+  v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  int b = blockIdx.x;
+  if (b < FT) {
+    // ---- shared expert w1 / w3 (FP8, packed) for features f0..f0+15 ----
+    const int f0 = b * 16;
+    const uint8_t* tiles = static_cast<const uint8_t*>(d.sh13p) + int64_t(b) * KB * 4096;
+    const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+    const int64_t sbase = int64_t(f0 >> 7) * KB;
+    for (int kb = kb0; kb < kb1; kb += 4) {
+      v8i w[2][4];
+      int se[2][4];
+      float sf[2][4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (kb + q < kb1) {
+          w[0][q] = pk_fp8(tiles + int64_t(kb + q) * 4096, lane);
+          w[1][q] = pk_fp8(tiles + int64_t(kb + q) * 4096 + 2048, lane);
+          fp8_wscale(d.sh_w1_s, sbase + kb + q, d.shared_w_scale_kind, se[0][q], sf[0][q]);
+          fp8_wscale(d.sh_w3_s, sbase + kb + q, d.shared_w_scale_kind, se[1][q], sf[1][q]);
+        }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (kb + q < kb1) {
+          const AOp a = a_from_fp8(arow, asrow, kb + q, g, a_kind);
+          mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], a_pow2, bp, lane);
+          mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], a_pow2, bp, lane);
+        }
+    }
+    reduce_waves<2>(acc, red, wave, lane);
+    if (wave == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = g * 4 + i;
+        if (t < T) ws.sh_h[int64_t(t) * I + f0 + nl] = f32_to_bf16(swiglu(acc[0][i], acc[1][i], d.swiglu_limit));
+      }
+    }
+    return;
+  }
+  b -= FT;
+  // ---- routed expert: MXFP4 w1 / w3 for features ft*16 .. +15 ----
+  const int u = b / FT, ft = b % FT;
+  if (u >= min(ws.n_active[0], u_max)) return;
+  const int e = clampi(ws.active[u], 0, d.n_experts - 1);
   const int64_t tile0 = (int64_t(e) * FT + ft) * KB;  // first K-block of (e, ft)
   const uint8_t* wt = static_cast<const uint8_t*>(d.w13p) + tile0 * 2048;
   const uint32_t* st = static_cast<const uint32_t*>(d.w13p_s) + (int64_t(e) * FT + ft) * KG * 2 * 64 + lane;
-  const uint8_t* arow = nl < T ? ws.xq + int64_t(nl) * D : nullptr;
-  const float* asrow = nl < T ? ws.xs + int64_t(nl) * (D / 128) : nullptr;
   // epilogue data for this lane's output rows (token 4g + i), fetched early
   int qrow[4];
   float wrow[4];
@@ -446,7 +459,6 @@ __global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, 
     qrow[i] = t < T ? ws.umap[u * T + t] : -1;
     wrow[i] = t < T ? ws.uwt[u * T + t] : 0.0f;
   }
-  v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
   for (int kb = kb0; kb < kb1; kb += 8) {
     v8i w[2][8];
     uint32_t s1[3], s3[3];
@@ -495,7 +507,7 @@ __global__ __launch_bounds__(kDecThreads) void hquant_kernel(MoeWs ws, int T, in
   const int r = blockIdx.x, UT = u_max * T;
   const uint16_t* src;
   if (r < UT) {
-    if (r / T >= ws.n_active[0] || ws.umap[r] < 0) return;
+    if (r / T >= min(ws.n_active[0], u_max) || ws.umap[r] < 0) return;
     src = ws.h + int64_t(r) * I;
   } else {
     src = ws.sh_h + int64_t(r - UT) * I;
@@ -519,7 +531,8 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
   const int a_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
   const int dt = blockIdx.x, n0 = dt * 16;
   const int KB = I / 128, KG = (KB + 3) / 4, DT = D / 16, UT = u_max * T;
-  const int n_act = ws.n_active[0];
+  const int P = T * k;
+  const int n_act = min(ws.n_active[0], u_max);
   for (int job = wave; job <= n_act; job += kW2Waves) {
     const bool shared = job == n_act;
     const int arow0 = shared ? UT : job * T;
@@ -551,7 +564,7 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
       for (int i = 0; i < 4; ++i)
         if (g * 4 + i < T) sh_s[g * 4 + i][nl] = bf16_round(acc[i]);
     } else {
-      const int e = ws.active[job];
+      const int e = clampi(ws.active[job], 0, d.n_experts - 1);
       const uint8_t* wt = static_cast<const uint8_t*>(d.w2p) + (int64_t(e) * DT + dt) * KB * 1024;
       const uint32_t* st = static_cast<const uint32_t*>(d.w2p_s) + (int64_t(e) * DT + dt) * KG * 64 + lane;
       int qrow[4];
@@ -578,15 +591,15 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
       // each linear's output is bf16 (architecture.py:741)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (qrow[i] >= 0) out_s[qrow[i]][nl] = bf16_round(acc[i]);
+        if (qrow[i] >= 0 && qrow[i] < P) out_s[qrow[i]][nl] = bf16_round(acc[i]);
     }
   }
   __syncthreads();
   if (tid < 16 * T) {
     const int t = tid >> 4, col = tid & 15;
-    const int n = ws.tok_n[t];
+    const int n = clampi(ws.tok_n[t], 0, k);
     float acc = 0.0f;
-    for (int j = 0; j < n; ++j) acc += out_s[ws.tok_pos[t * k + j]][col];
+    for (int j = 0; j < n; ++j) acc += out_s[clampi(ws.tok_pos[t * k + j], 0, P - 1)][col];
     acc += sh_s[t][col];
     y[int64_t(t) * D + n0 + col] = f32_to_bf16(acc);
   }
@@ -595,17 +608,17 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
 int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* ids, int64_t T,
                   void* y, hipStream_t stream) {
   const int E = d->n_experts, k = d->topk, D = d->dim, I = d->inter;
-  const int n_gate = (E + 3) / 4;
+  const int n_gate = (E + kRouteWaves - 1) / kRouteWaves;
   const int64_t P = T * k;
   const int u_max = int(P < E ? P : E);
   if (P > kMaxDecPairs) return set_error(WZ_EINVAL, "moe decode: T*topk=%lld exceeds %d", (long long)P, kMaxDecPairs);
   if (!d->w13p || !d->w13p_s || !d->w2p || !d->w2p_s || !d->sh13p || !d->sh2p)
     return set_error(WZ_EINVAL, "moe decode: packed banks missing (wz_moe_pack)");
-  WZ_LAUNCH("moe_route", stream, route_decode_kernel, dim3(unsigned(n_gate + T + I / 16)), dim3(kDecThreads), 0,
+  WZ_LAUNCH("moe_route", stream, route_decode_kernel, dim3(unsigned(n_gate * T + T)), dim3(kRouteThreads_), 0,
             *d, w, static_cast<const uint16_t*>(x), ids, int(T), n_gate, u_max);
   if (int rc = check_launch("moe route")) return rc;
-  WZ_LAUNCH("moe_w13", stream, w13_decode_kernel, dim3(unsigned(u_max * (I / 16))), dim3(kDecThreads), 0, *d, w,
-            int(T));
+  WZ_LAUNCH("moe_w13", stream, w13_decode_kernel, dim3(unsigned((u_max + 1) * (I / 16))), dim3(kDecThreads), 0, *d,
+            w, int(T), u_max);
   if (int rc = check_launch("moe w13")) return rc;
   WZ_LAUNCH("moe_hquant", stream, hquant_kernel, dim3(unsigned(u_max * T + T)), dim3(kDecThreads), 0, w, int(T), I,
             u_max, d->act_scale_kind != WZ_SCALE_F32);
