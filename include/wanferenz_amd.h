@@ -110,7 +110,7 @@ typedef struct wz_moe_desc {
   const void* sh_w2_s;    /* [D/128, I/128] */
   /* Packed banks (wz_moe_pack): MFMA-ready 16-row x 128-K tiles stored as 1 KB blocks in
    * lane order, so each weight load instruction of a wave reads 1 KB contiguous.  The
-   * decode path (T <= 16) reads these; NULL -> wz_moe_forward rejects T <= 16. */
+   * expert kernels of wz_moe_forward read only these; NULL -> wz_moe_forward fails. */
   const void* w13p;       /* [E][I/16][D/128][2 (w1,w3)][1024] */
   const void* w13p_s;     /* [E][I/16][ceil(D/512)][2][64 x 4]: 4 K-blocks of e8m0 per lane */
   const void* w2p;        /* [E][D/16][I/128][1024] */
@@ -128,7 +128,8 @@ size_t wz_moe_packed_bytes(const wz_moe_desc* d, int which);
 int wz_moe_pack(const wz_moe_desc* d, void* w13p, void* w13p_s, void* w2p, void* w2p_s, void* sh13p,
                 void* sh2p, hipStream_t stream);
 
-/* Bytes of scratch wz_moe_forward needs for up to T tokens. */
+/* Bytes of scratch that serve every wz_moe_forward / wz_moe_route call of 1..T
+ * tokens (the decode tables of T <= 16 can outgrow a small prefill's needs). */
 size_t wz_moe_workspace_bytes(const wz_moe_desc* d, int64_t T);
 
 /* Zero the parts of a fresh workspace that must start at zero (arrival

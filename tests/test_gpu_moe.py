@@ -46,23 +46,24 @@ def upload_case(case, inp, dev):
     return HipMoE(cfg, w, max_tokens=case.T)
 
 
-def check_routing(moe, x, ids, ref, E):
+def check_routing(moe, x, ids, gate, E):
+    """Routing of all rows vs the oracle's GateResult; returns the near-tie tokens."""
     w, idx, off, ptok, pslot = moe.route(x, ids)
     torch.cuda.synchronize()
     idx = idx.cpu().numpy()
     near = []
     for t in range(idx.shape[0]):
-        if not np.array_equal(idx[t], ref.gate.indices[t]):
-            rel = ref.gate.margin[t] / max(abs(ref.gate.biased[t]).max(), 1e-30)
-            assert rel < NEAR_TIE, f"token {t}: {idx[t]} != {ref.gate.indices[t]} (margin {ref.gate.margin[t]})"
+        if not np.array_equal(idx[t], gate.indices[t]):
+            rel = gate.margin[t] / max(abs(gate.biased[t]).max(), 1e-30)
+            assert rel < NEAR_TIE, f"token {t}: {idx[t]} != {gate.indices[t]} (margin {gate.margin[t]})"
             near.append(t)
     if near:
         print(f"near-tie tokens (margin < {NEAR_TIE} rel): {near}")
         return near
-    wd = np.abs(w.cpu().numpy() - ref.gate.weights)
-    ulp = np.spacing(np.abs(ref.gate.weights).astype(np.float32))
+    wd = np.abs(w.cpu().numpy() - gate.weights)
+    ulp = np.spacing(np.abs(gate.weights).astype(np.float32))
     assert (wd <= 4 * ulp).all(), wd.max()
-    counts, offsets, rt, rs = om.permutation(ref.gate.indices, E)
+    counts, offsets, rt, rs = om.permutation(gate.indices, E)
     assert np.array_equal(off.cpu().numpy(), offsets)
     assert np.array_equal(ptok.cpu().numpy(), rt)
     assert np.array_equal(pslot.cpu().numpy(), rs)
@@ -77,7 +78,7 @@ def test_moe_golden_cases(gpu, name):
     x = bf16_tensor(inp.x, gpu)
     ids = torch.from_numpy(inp.input_ids).to(gpu)
     ref = om.moe_forward(oracle_params(case, inp), from_bf16_bits(inp.x), inp.input_ids)
-    near = check_routing(moe, x, ids, ref, case.n_experts)
+    near = check_routing(moe, x, ids, ref.gate, case.n_experts)
     y = moe.forward(x, ids)
     got = f32_of_bf16(y)
     rel, cos = om.max_rel_err(got, ref.y), om.cosine(got, ref.y)
@@ -105,7 +106,7 @@ def v4_layer(gpu):
     return cfg, w, host, moe
 
 
-def _oracle_params_from_device(cfg, w, host, experts):
+def _oracle_params_from_device(cfg, w, host, experts, bias=None):
     """Oracle parameters for the experts a routing touched, copied back from HBM."""
     I = cfg.inter
     ex = [None] * cfg.n_experts
@@ -118,7 +119,8 @@ def _oracle_params_from_device(cfg, w, host, experts):
               om.Fp8Linear(w.sh_w3.cpu().numpy(), e8m0_decode(w.sh_w3_s.cpu().numpy())),
               om.Fp8Linear(w.sh_w2.cpu().numpy(), e8m0_decode(w.sh_w2_s.cpu().numpy())))
     return om.MoEParams(cfg.dim, I, cfg.n_experts, cfg.topk, from_bf16_bits(host["gate_w"]),
-                        host.get("gate_bias"), ex, shared, cfg.score_func, cfg.route_scale,
+                        host.get("gate_bias") if bias is None else bias, ex, shared, cfg.score_func,
+                        cfg.route_scale,
                         cfg.swiglu_limit, True, None)
 
 
@@ -144,8 +146,15 @@ def test_v4_decode_parity(v4_layer, T):
                 cfg.score_func, cfg.route_scale)
     p = _oracle_params_from_device(cfg, w, host, sorted(set(g.indices.ravel().tolist())))
     ref = om.moe_forward(p, from_bf16_bits(xb))
-    near = check_routing(moe, x, None, ref, cfg.n_experts)
-    y = moe.forward(x)
+    near = check_routing(moe, x, None, ref.gate, cfg.n_experts)
+    # the decode kernels route on their own (route_decode_kernel): check what they export
+    rw = torch.empty(T, cfg.topk, dtype=torch.float32, device="cuda")
+    ri = torch.empty(T, cfg.topk, dtype=torch.int64, device="cuda")
+    y = moe.forward(x, routing_out=(rw, ri))
+    if not near:
+        assert np.array_equal(ri.cpu().numpy(), ref.gate.indices)
+        wd = np.abs(rw.cpu().numpy() - ref.gate.weights)
+        assert (wd <= 4 * np.spacing(np.abs(ref.gate.weights).astype(np.float32))).all(), wd.max()
     got = f32_of_bf16(y)
     rel, cos = om.max_rel_err(got, ref.y), om.cosine(got, ref.y)
     assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
@@ -209,3 +218,78 @@ def test_pack_layout_matches_statement(gpu):
     exp_w, exp_s = _expected_pack_w13(inp.w13, inp.w13_s, case.dim, case.inter)
     assert np.array_equal(moe.packed["w13p"].cpu().numpy(), exp_w)
     assert np.array_equal(moe.packed["w13p_s"].cpu().numpy(), exp_s)
+
+
+# ------------------------------------------------------------------ prefill ---
+# T > 16 runs the expert-grouped MFMA GEMM path (moe_prefill.hip).  The layer is
+# token-local, so at large T the oracle is evaluated on sampled rows (all
+# routing is still checked in full), and every row is compared with the decode
+# path run over 16-token chunks of the same input.
+
+PREFILL_CASES = {
+    # oracle-only cases (no reference golden at these T): fp32 scales, hash routing, top-6
+    "toy_t40_fp32scale": dict(case="toy_t4_fp32scale", T=40),
+    "hash_t48": dict(case="hash_t3", T=48),
+    "top6_t100": dict(case="top6_t8", T=100),
+}
+
+
+@pytest.mark.parametrize("name", list(PREFILL_CASES))
+def test_moe_prefill_oracle_cases(gpu, name):
+    import dataclasses
+    spec = PREFILL_CASES[name]
+    case = dataclasses.replace(CASES[spec["case"]], name=name, T=spec["T"])
+    inp = make_inputs(case)
+    moe = upload_case(case, inp, gpu)
+    x = bf16_tensor(inp.x, gpu)
+    ids = torch.from_numpy(inp.input_ids).to(gpu)
+    ref = om.moe_forward(oracle_params(case, inp), from_bf16_bits(inp.x), inp.input_ids)
+    near = check_routing(moe, x, ids, ref.gate, case.n_experts)
+    rw = torch.empty(case.T, case.topk, dtype=torch.float32, device=gpu)
+    ri = torch.empty(case.T, case.topk, dtype=torch.int64, device=gpu)
+    y = moe.forward(x, ids, routing_out=(rw, ri))
+    if not near:
+        assert np.array_equal(ri.cpu().numpy(), ref.gate.indices)
+    got = f32_of_bf16(y)
+    rel, cos = om.max_rel_err(got, ref.y), om.cosine(got, ref.y)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    print(f"{name}: rel {rel:.2e} cos {cos:.8f} bit-equal {np.mean(got == ref.y):.4f} near-ties {near}")
+
+
+def _decode_chunks(moe, x, chunk=16):
+    return torch.cat([moe.forward(x[i:i + chunk]) for i in range(0, x.size(0), chunk)])
+
+
+@pytest.mark.parametrize("T,bias", [(64, "normal"), (300, "normal"), (2048, "zipf")])
+def test_v4_prefill_parity(v4_layer, T, bias):
+    import dataclasses
+    cfg, w, host, moe = v4_layer
+    b = host["gate_bias"]
+    if bias == "zipf":
+        b = synth.zipf_bias(cfg.n_experts)
+        w = dataclasses.replace(w, gate_bias=torch.from_numpy(b).to("cuda"))
+        moe = HipMoE(cfg, w, max_tokens=T)
+    xb = synth.normal_bf16(synth.stream_key(500 + T, synth.S_X), (T, cfg.dim), 1.0)
+    x = bf16_tensor(xb, "cuda")
+    g = om.gate(from_bf16_bits(xb), from_bf16_bits(host["gate_w"]), b, cfg.topk, cfg.score_func,
+                cfg.route_scale)
+    counts = np.bincount(g.indices.ravel(), minlength=cfg.n_experts)
+    near = check_routing(moe, x, None, g, cfg.n_experts)
+    y = moe.forward(x)
+    got = f32_of_bf16(y)
+    # oracle on sampled rows
+    rows = sorted({0, 1, T // 2, T - 1})
+    xs = xb[rows]
+    gs = om.gate(from_bf16_bits(xs), from_bf16_bits(host["gate_w"]), b, cfg.topk, cfg.score_func,
+                 cfg.route_scale)
+    p = _oracle_params_from_device(cfg, w, host, sorted(set(gs.indices.ravel().tolist())), bias=b)
+    ref = om.moe_forward(p, from_bf16_bits(xs))
+    rel, cos = om.max_rel_err(got[rows], ref.y), om.cosine(got[rows], ref.y)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    # every row against the decode path on 16-token chunks
+    dec = f32_of_bf16(_decode_chunks(moe, x))
+    rel_d, cos_d = om.max_rel_err(got, dec), om.cosine(got, dec)
+    assert rel_d <= TOL_REL and cos_d >= TOL_COS, (rel_d, cos_d)
+    print(f"V4 prefill T={T} ({bias} bias, experts hit {int((counts > 0).sum())}, max rows "
+          f"{int(counts.max())}): sampled rows vs oracle rel {rel:.2e} cos {cos:.8f}; vs decode "
+          f"rel {rel_d:.2e} cos {cos_d:.8f} bit-equal {np.mean(got == dec):.4f}; near-ties {near}")

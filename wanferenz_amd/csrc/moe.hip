@@ -10,9 +10,11 @@
 // once (architecture.py:790 is a non-accumulating index_put).
 //
 // The layer runs as a fixed sequence of stream-ordered launches with no host
-// synchronisation and no allocation, so a decode step can be captured in a
-// HIP graph.  Grids are sized from T on the host; blocks beyond the device-
-// side number of active experts return at once.
+// synchronisation and no allocation, so a step can be captured in a HIP
+// graph.  Grids are sized from T on the host; blocks beyond the device-side
+// number of active experts return at once.  T <= 16 runs the decode kernels
+// (moe_decode.hip); larger T runs the routing below and the expert-grouped
+// GEMMs of moe_prefill.hip.
 //
 //   gate_dot   scores[T,E] = x . W^T, exact bf16 products summed in fp64, one
 //              wave per (expert, 8 tokens): reads the bf16 gate once.
@@ -20,13 +22,6 @@
 //              index), renormalise, x route_scale; hash layers read tid2eid.
 //   perm       one workgroup: expert counts, offsets, active-expert list and
 //              the stable (expert, token, slot) permutation via wave ballots.
-//   w13        per (active expert, 16 intermediate features): w1 and w3 rows
-//              streamed once through V_MFMA_SCALE 16x16x128 (e4m3 x e2m1),
-//              act_quant of x fused into the A-operand load, SwiGLU + routing
-//              weight in registers, bf16 h written in permuted order; plus
-//              the shared expert's FP8 w1/w3 tiles in the same launch.
-//   w2         per (active expert, 16 output rows): act_quant of h fused, w2
-//              rows streamed once; shared expert's FP8 w2 in the same launch.
 //   combine    y[t] = bf16(sum_{experts asc} out[t,e] + shared[t]).
 #include "moe_common.h"
 
@@ -285,277 +280,6 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
   }
 }
 
-// ------------------------------------------------------------------- w13 ----
-
-
-constexpr int kMoeThreads = 256;
-constexpr int kMoeUnroll = 4;
-
-// One work item: 16 intermediate features f0..f0+15 of one expert (or of the
-// shared expert), all of its token rows.  The four waves split K = D.
-// red: LDS [4 waves][2][MT][64][4] floats.
-template <bool SHARED, int kMT>
-__device__ void w13_item(const wz_moe_desc& d, const MoeWs& ws, const uint16_t* __restrict__ x,
-                         int T, int f0, int e, int row0, int nrows, float* red_) {
-  auto red = reinterpret_cast<float(*)[2][kMT][kWave][4]>(red_);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nl = lane & 15, g = lane >> 4;
-  const int D = d.dim, I = d.inter;
-  const int nkb = D / 128;
-  const int kb0 = (wave * nkb) / 4, kb1 = ((wave + 1) * nkb) / 4;
-  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
-  // weight rows of this lane: w1 row (f0 + nl), w3 row (f0 + nl)
-  const uint8_t *w1row, *w3row, *s1row = nullptr, *s3row = nullptr;
-  bool b_pow2;
-  if (SHARED) {
-    w1row = static_cast<const uint8_t*>(d.sh_w1) + int64_t(f0 + nl) * D;
-    w3row = static_cast<const uint8_t*>(d.sh_w3) + int64_t(f0 + nl) * D;
-    b_pow2 = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
-  } else {
-    const int64_t ebase = int64_t(e) * 2 * I;
-    w1row = static_cast<const uint8_t*>(d.w13) + (ebase + f0 + nl) * (D / 2);
-    w3row = static_cast<const uint8_t*>(d.w13) + (ebase + I + f0 + nl) * (D / 2);
-    s1row = static_cast<const uint8_t*>(d.w13_s) + (ebase + f0 + nl) * (D / 32);
-    s3row = static_cast<const uint8_t*>(d.w13_s) + (ebase + I + f0 + nl) * (D / 32);
-    b_pow2 = true;
-  }
-  for (int r0 = 0; r0 < nrows; r0 += 16 * kMT) {
-    v4f ag[kMT], au[kMT];
-#pragma unroll
-    for (int t = 0; t < kMT; ++t) {
-      ag[t] = v4f{0.f, 0.f, 0.f, 0.f};
-      au[t] = v4f{0.f, 0.f, 0.f, 0.f};
-    }
-    // token row pointer of this lane for each tile (A row = lane & 15)
-    const uint16_t* arow[kMT];
-#pragma unroll
-    for (int t = 0; t < kMT; ++t) {
-      const int r = r0 + t * 16 + nl;
-      int tok = -1;
-      if (r < nrows) tok = SHARED ? r : clampi(ws.perm_token[row0 + r], 0, T - 1);
-      arow[t] = tok >= 0 ? x + int64_t(tok) * D : nullptr;
-    }
-    const int ntiles = min(kMT, (nrows - r0 + 15) / 16);
-    for (int kb = kb0; kb < kb1; kb += kMoeUnroll) {
-      v8i b1[kMoeUnroll], b3[kMoeUnroll];
-      int e1[kMoeUnroll], e3[kMoeUnroll];
-      float f1[kMoeUnroll], f3[kMoeUnroll];
-#pragma unroll
-      for (int q = 0; q < kMoeUnroll; ++q) {
-        const int kk = kb + q;
-        if (kk < kb1) {
-          if (SHARED) {
-            b1[q] = b_fp8(w1row, kk, g);
-            b3[q] = b_fp8(w3row, kk, g);
-            fp8_wscale(d.sh_w1_s, int64_t(f0 >> 7) * nkb + kk, d.shared_w_scale_kind, e1[q], f1[q]);
-            fp8_wscale(d.sh_w3_s, int64_t(f0 >> 7) * nkb + kk, d.shared_w_scale_kind, e3[q], f3[q]);
-          } else {
-            b1[q] = b_fp4(w1row, kk, g);
-            b3[q] = b_fp4(w3row, kk, g);
-            e1[q] = b_fp4_scale(s1row, kk, g);
-            e3[q] = b_fp4_scale(s3row, kk, g);
-            f1[q] = f3[q] = 1.0f;
-          }
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < kMT; ++t) {
-        if (t >= ntiles) break;
-#pragma unroll
-        for (int q = 0; q < kMoeUnroll; ++q) {
-          const int kk = kb + q;
-          if (kk < kb1) {
-            const AOp a = a_from_bf16(arow[t], kk, g, a_pow2);
-            if (SHARED) {
-              mma_step<kFmtFp8, kFmtFp8>(ag[t], a, b1[q], e1[q], f1[q], a_pow2, b_pow2, lane);
-              mma_step<kFmtFp8, kFmtFp8>(au[t], a, b3[q], e3[q], f3[q], a_pow2, b_pow2, lane);
-            } else {
-              mma_step<kFmtFp8, kFmtFp4>(ag[t], a, b1[q], e1[q], f1[q], a_pow2, true, lane);
-              mma_step<kFmtFp8, kFmtFp4>(au[t], a, b3[q], e3[q], f3[q], a_pow2, true, lane);
-            }
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < kMT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        red[wave][0][t][lane][i] = ag[t][i];
-        red[wave][1][t][lane][i] = au[t][i];
-      }
-    __syncthreads();
-    // wave w finishes tile w: SwiGLU with clamp, x routing weight, bf16 h
-    if (wave < ntiles) {
-      const int t = wave;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = r0 + t * 16 + g * 4 + i;
-        float gs = red[0][0][t][lane][i];
-        gs += red[1][0][t][lane][i];
-        gs += red[2][0][t][lane][i];
-        gs += red[3][0][t][lane][i];
-        float us = red[0][1][t][lane][i];
-        us += red[1][1][t][lane][i];
-        us += red[2][1][t][lane][i];
-        us += red[3][1][t][lane][i];
-        if (r < nrows) {
-          float gv = bf16_round(gs), uv = bf16_round(us);
-          if (d.swiglu_limit > 0.0f) {
-            uv = fminf(fmaxf(uv, -d.swiglu_limit), d.swiglu_limit);
-            gv = fminf(gv, d.swiglu_limit);
-          }
-          float hv = silu_f32(gv) * uv;
-          if (SHARED) {
-            ws.sh_h[int64_t(r) * I + f0 + nl] = f32_to_bf16(hv);
-          } else {
-            const int p = row0 + r;
-            const float wt = ws.weights[int64_t(clampi(ws.perm_token[p], 0, T - 1)) * d.topk +
-                                        clampi(ws.perm_slot[p], 0, d.topk - 1)];
-            ws.h[int64_t(p) * I + f0 + nl] = f32_to_bf16(wt * hv);
-          }
-        }
-      }
-    }
-    __syncthreads();
-  }
-}
-
-template <int MT>
-__global__ __launch_bounds__(kMoeThreads) void w13_kernel(wz_moe_desc d, MoeWs ws,
-                                                          const uint16_t* __restrict__ x, int T,
-                                                          int n_shared_items) {
-  __shared__ float red[4 * 2 * MT * kWave * 4];
-  const int item = blockIdx.x;
-  const int ftiles = d.inter / 16;
-  if (item < n_shared_items) {
-    w13_item<true, MT>(d, ws, x, T, item * 16, -1, 0, T, red);
-    return;
-  }
-  const int r = item - n_shared_items;
-  const int u = r / ftiles, ft = r % ftiles;
-  if (u >= min(ws.n_active[0], d.n_experts)) return;
-  const int P = T * d.topk;
-  const int row0 = clampi(ws.act_off[u], 0, P);
-  w13_item<false, MT>(d, ws, x, T, ft * 16, clampi(ws.active[u], 0, d.n_experts - 1), row0,
-                      clampi(ws.act_cnt[u], 0, P - row0), red);
-}
-
-// -------------------------------------------------------------------- w2 ----
-
-// red: LDS [4 waves][MT][64][4] floats.
-template <bool SHARED, int kMT>
-__device__ void w2_item(const wz_moe_desc& d, const MoeWs& ws, int T, int n0, int e, int row0,
-                        int nrows, float* red_) {
-  auto red = reinterpret_cast<float(*)[kMT][kWave][4]>(red_);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nl = lane & 15, g = lane >> 4;
-  const int D = d.dim, I = d.inter;
-  const int nkb = I / 128;
-  const int kb0 = (wave * nkb) / 4, kb1 = ((wave + 1) * nkb) / 4;
-  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
-  const uint8_t *wrow, *srow = nullptr;
-  bool b_pow2;
-  if (SHARED) {
-    wrow = static_cast<const uint8_t*>(d.sh_w2) + int64_t(n0 + nl) * I;
-    b_pow2 = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
-  } else {
-    const int64_t ebase = int64_t(e) * D;
-    wrow = static_cast<const uint8_t*>(d.w2) + (ebase + n0 + nl) * (I / 2);
-    srow = static_cast<const uint8_t*>(d.w2_s) + (ebase + n0 + nl) * (I / 32);
-    b_pow2 = true;
-  }
-  const uint16_t* hbase = SHARED ? ws.sh_h : ws.h + int64_t(row0) * I;
-  for (int r0 = 0; r0 < nrows; r0 += 16 * kMT) {
-    v4f acc[kMT];
-#pragma unroll
-    for (int t = 0; t < kMT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-    const uint16_t* arow[kMT];
-#pragma unroll
-    for (int t = 0; t < kMT; ++t) {
-      const int r = r0 + t * 16 + nl;
-      arow[t] = r < nrows ? hbase + int64_t(r) * I : nullptr;
-    }
-    const int ntiles = min(kMT, (nrows - r0 + 15) / 16);
-    for (int kb = kb0; kb < kb1; kb += kMoeUnroll) {
-      v8i bw[kMoeUnroll];
-      int es[kMoeUnroll];
-      float fs[kMoeUnroll];
-#pragma unroll
-      for (int q = 0; q < kMoeUnroll; ++q) {
-        const int kk = kb + q;
-        if (kk < kb1) {
-          if (SHARED) {
-            bw[q] = b_fp8(wrow, kk, g);
-            fp8_wscale(d.sh_w2_s, int64_t(n0 >> 7) * nkb + kk, d.shared_w_scale_kind, es[q], fs[q]);
-          } else {
-            bw[q] = b_fp4(wrow, kk, g);
-            es[q] = b_fp4_scale(srow, kk, g);
-            fs[q] = 1.0f;
-          }
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < kMT; ++t) {
-        if (t >= ntiles) break;
-#pragma unroll
-        for (int q = 0; q < kMoeUnroll; ++q) {
-          const int kk = kb + q;
-          if (kk < kb1) {
-            const AOp a = a_from_bf16(arow[t], kk, g, a_pow2);
-            if (SHARED)
-              mma_step<kFmtFp8, kFmtFp8>(acc[t], a, bw[q], es[q], fs[q], a_pow2, b_pow2, lane);
-            else
-              mma_step<kFmtFp8, kFmtFp4>(acc[t], a, bw[q], es[q], fs[q], a_pow2, true, lane);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < kMT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) red[wave][t][lane][i] = acc[t][i];
-    __syncthreads();
-    if (wave < ntiles) {
-      const int t = wave;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = r0 + t * 16 + g * 4 + i;
-        float v = red[0][t][lane][i];
-        v += red[1][t][lane][i];
-        v += red[2][t][lane][i];
-        v += red[3][t][lane][i];
-        if (r < nrows) {
-          if (SHARED)
-            ws.sh_out[int64_t(r) * D + n0 + nl] = f32_to_bf16(v);
-          else
-            ws.out2[int64_t(row0 + r) * D + n0 + nl] = f32_to_bf16(v);
-        }
-      }
-    }
-    __syncthreads();
-  }
-}
-
-template <int MT>
-__global__ __launch_bounds__(kMoeThreads) void w2_kernel(wz_moe_desc d, MoeWs ws, int T,
-                                                         int n_shared_items) {
-  __shared__ float red[4 * MT * kWave * 4];
-  const int item = blockIdx.x;
-  const int ntiles = d.dim / 16;
-  if (item < n_shared_items) {
-    w2_item<true, MT>(d, ws, T, item * 16, -1, 0, T, red);
-    return;
-  }
-  const int r = item - n_shared_items;
-  const int u = r / ntiles, nt = r % ntiles;
-  if (u >= min(ws.n_active[0], d.n_experts)) return;
-  const int P = T * d.topk;
-  const int row0 = clampi(ws.act_off[u], 0, P);
-  w2_item<false, MT>(d, ws, T, nt * 16, clampi(ws.active[u], 0, d.n_experts - 1), row0,
-                     clampi(ws.act_cnt[u], 0, P - row0), red);
-}
-
 // --------------------------------------------------------------- combine ----
 
 __global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int D,
@@ -614,6 +338,7 @@ __global__ void export_routing_kernel(const MoeWs ws, int P, float* __restrict__
 
 int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* ids, int64_t T,
                   void* y, hipStream_t stream);
+int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, int64_t T, hipStream_t stream);
 
 static int validate(const wz_moe_desc* d, int64_t T, const void* ws, size_t ws_bytes,
                     const char* what) {
@@ -666,7 +391,9 @@ static int launch_routing(const wz_moe_desc* d, const MoeWs& w, const void* x,
 
 extern "C" size_t wz_moe_workspace_bytes(const wz_moe_desc* d, int64_t T) {
   if (!d || T < 0) return 0;
-  return wz::moe_ws_layout(d, T, nullptr).bytes;
+  const size_t big = wz::moe_ws_layout(d, T, nullptr).bytes;
+  const size_t dec = wz::moe_ws_layout(d, T < wz::kDecodeMaxT ? T : wz::kDecodeMaxT, nullptr).bytes;
+  return big > dec ? big : dec;
 }
 
 __global__ void zero_words_kernel(uint32_t* p, int n) {
@@ -732,24 +459,9 @@ extern "C" int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const in
     return WZ_OK;
   }
   if (int rc = launch_routing(d, w, x_bf16, input_ids, T, stream)) return rc;
-  const int E = d->n_experts, k = d->topk, D = d->dim, I = d->inter;
+  const int k = d->topk, D = d->dim;
   const int64_t P = T * k;
-  const int u_max = int(P < E ? P : E);
-  const int sh13 = I / 16, sh2 = D / 16;
-  const dim3 g13(unsigned(sh13 + u_max * (I / 16))), g2(unsigned(sh2 + u_max * (D / 16)));
-  const uint16_t* xb = static_cast<const uint16_t*>(x_bf16);
-  if (T <= 16) {
-    WZ_LAUNCH("moe_w13", stream, w13_kernel<1>, g13, dim3(kMoeThreads), 0, *d, w, xb, int(T), sh13);
-  } else {
-    WZ_LAUNCH("moe_w13", stream, w13_kernel<4>, g13, dim3(kMoeThreads), 0, *d, w, xb, int(T), sh13);
-  }
-  if (int rc = check_launch("moe w13")) return rc;
-  if (T <= 16) {
-    WZ_LAUNCH("moe_w2", stream, w2_kernel<1>, g2, dim3(kMoeThreads), 0, *d, w, int(T), sh2);
-  } else {
-    WZ_LAUNCH("moe_w2", stream, w2_kernel<4>, g2, dim3(kMoeThreads), 0, *d, w, int(T), sh2);
-  }
-  if (int rc = check_launch("moe w2")) return rc;
+  if (int rc = launch_prefill_experts(d, w, x_bf16, T, stream)) return rc;
   WZ_LAUNCH("moe_combine", stream, combine_kernel, dim3(unsigned((D / 8 + 255) / 256), unsigned(T)), dim3(256),
                      0, w, k, D, static_cast<uint16_t*>(y_bf16));
   if (int rc = check_launch("moe combine")) return rc;

@@ -38,6 +38,10 @@ struct MoeWs {
   uint8_t* hq;         // decode: [U_max*T + T, I] e4m3 act_quant(h) (rows (u, t), then shared t)
   float* hs;           // [U_max*T + T, I/128]
   uint16_t* h;         // [P, I] bf16 (general path) / [U_max*T, I] rows (u, t) (decode path)
+  int32_t* mt_u;       // prefill M-tile table: active expert of tile
+  int32_t* mt_row0;    //   first pair row of tile
+  int32_t* mt_n;       //   rows in tile (<= 128)
+  int32_t* n_mt;       //   number of tiles
   uint16_t* sh_h;      // [T, I] bf16
   uint16_t* out2;      // [P, D] bf16
   uint16_t* sh_out;    // [T, D] bf16
@@ -76,8 +80,14 @@ static inline MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base
   w.uwt = reinterpret_cast<float*>(take(sizeof(float) * UT));
   w.xq = take(size_t(T) * D);
   w.xs = reinterpret_cast<float*>(take(sizeof(float) * T * (D / 128)));
-  w.hq = take(size_t(UT + T) * I);
-  w.hs = reinterpret_cast<float*>(take(sizeof(float) * (UT + T) * (I / 128)));
+  const int64_t HQ = (T <= kDecodeMaxT ? UT : P) + T;  // decode rows (u, t) / prefill pairs, then shared rows
+  w.hq = take(size_t(HQ) * I);
+  w.hs = reinterpret_cast<float*>(take(sizeof(float) * HQ * (I / 128)));
+  const int64_t MT = P / 128 + (P < E ? P : E) + 1;     // M-tiles of 128 pair rows (prefill)
+  w.mt_u = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * MT));
+  w.mt_row0 = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * MT));
+  w.mt_n = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * MT));
+  w.n_mt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 64));
   w.h = reinterpret_cast<uint16_t*>(take(2 * size_t(HR) * I));
   w.sh_h = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * I));
   w.out2 = reinterpret_cast<uint16_t*>(take(2 * size_t(P) * D));

@@ -49,6 +49,15 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   }
 }
 
+// Stream-ordered act_quant of `rows` rows of K bf16 for the MoE kernels.
+int launch_act_quant(const void* x, int64_t rows, int64_t K, uint8_t* q, void* s, int kind, hipStream_t stream) {
+  const int64_t n8 = rows * K / 8;
+  if (n8 == 0) return WZ_OK;
+  WZ_LAUNCH("act_quant", stream, act_quant_kernel, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0,
+            static_cast<const uint16_t*>(x), n8, q, s, kind);
+  return check_launch("act_quant");
+}
+
 }  // namespace wz
 
 extern "C" int wz_act_quant_fp8(const void* x_bf16, int64_t M, int64_t K, void* q_e4m3, void* s,
