@@ -19,6 +19,11 @@ Printed JSON line (one):
   cpu_baseline the oracle (numpy restatement of the reference CPU path) on one
               T-token layer, single thread
   per_T       the same layer measured at T = 1, 2, 4, 8
+  prefill     the same layer at T = 128, 512, 2048 with a Zipf(1.1) gate bias
+              (load-imbalanced experts): µs/layer, tokens/s, algorithmic HBM
+              GB/s, and MFMA utilisation = 6*D*I*(T*k + T) flops / time against
+              the dense FP8 (5.0 PFLOP/s, the rate of an e4m3 x e2m1 scaled
+              MFMA) and FP4 (10.1 PFLOP/s) peaks
 """
 
 from __future__ import annotations
@@ -36,6 +41,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "MoE layer µs + HBM GB/s (decode T=1-8); FP4 MFMA util (prefill T=2048)"
 HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+FP4_PEAK_TFLOPS = 10100.0
 D, I, E, K_TOP = 4096, 2048, 256, 6
 ROUTED_EXPERT_BYTES = 3 * (I * D // 2) + 3 * (I * D // 32)          # 13,369,344
 SHARED_BYTES = 3 * I * D + 3 * (I // 128) * (D // 128)              # 25,167,360
@@ -62,6 +69,9 @@ def parse():
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--prefill", default="128,512,2048",
+                    help="comma-separated prefill T values ('' to skip)")
+    ap.add_argument("--prefill-layers", type=int, default=3)
     return ap.parse_args()
 
 
@@ -170,6 +180,48 @@ def measure_T(layers, T, steps, warmup, dev, salt):
     return dict(T=T, secs=secs, wall=wall, Us=Us, total_bytes=total_bytes, kernels=kt, xs=xs)
 
 
+def prefill_flops(T: int) -> float:
+    return 6.0 * D * I * (T * K_TOP + T)
+
+
+def measure_prefill(layers, Ts, dev):
+    """Prefill T-token layers with a Zipf gate bias over the first layers' banks."""
+    import torch
+
+    from wanferenz_amd import synth
+
+    zb = torch.from_numpy(synth.zipf_bias(E)).to(dev)
+    tmax = max(Ts)
+    players = [(moe.with_gate_bias(zb, max_tokens=tmax), host) for moe, host in layers]
+    res = {}
+    for T in Ts:
+        xs = make_inputs(len(players), T, dev, salt=5000 + T)
+        loads = []
+        for (moe, _), (_, x) in zip(players, xs):
+            _, idx, _, _, _ = moe.route(x)
+            torch.cuda.synchronize()
+            loads.append(np.bincount(idx.cpu().numpy().ravel(), minlength=E))
+        graphs, _ = capture(players, xs)
+        steps = max(6, min(60, 24576 // T))
+        secs, _ = time_steps(graphs, steps, max(2, steps // 4))
+        kt = kernel_times(players, xs, reps=1)
+        L = len(players)
+        nbytes = sum(layer_bytes(int((loads[i % L] > 0).sum()), T) for i in range(steps))
+        us = secs / steps * 1e6
+        tflops = prefill_flops(T) / (us * 1e-6) / 1e12
+        res[str(T)] = {"us_per_layer": round(us, 1), "tokens_per_s": round(T / (us * 1e-6), 1),
+                       "GB_s": round(nbytes / secs / 1e9, 1),
+                       "hbm_frac": round(nbytes / secs / 1e9 / HBM_PEAK_GBS, 4),
+                       "TFLOP_s": round(tflops, 1),
+                       "mfma_frac_fp8": round(tflops / FP8_PEAK_TFLOPS, 4),
+                       "mfma_frac_fp4": round(tflops / FP4_PEAK_TFLOPS, 4),
+                       "max_expert_rows": int(max(l.max() for l in loads)),
+                       "mean_active_experts": round(float(np.mean([(l > 0).sum() for l in loads])), 1),
+                       "steps": steps,
+                       "kernel_us": {k: round(v * 1000.0, 2) for k, v in sorted(kt.items())}}
+    return res
+
+
 def cpu_baseline(layers, cfg, T, dev):
     """Oracle on one T-token step of layer 0 (weights of the touched experts copied from HBM)."""
     import torch
@@ -260,6 +312,9 @@ def main():
                               "mean_U": round(float(np.mean(r["Us"])), 1),
                               "kernel_us": {k: round(x * 1000.0, 2) for k, x in sorted(r["kernels"].items())}}
         out["per_T"] = sweep
+    if args.prefill:
+        Ts = [int(t) for t in args.prefill.split(",") if t]
+        out["prefill"] = measure_prefill(layers[:max(1, args.prefill_layers)], Ts, dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(layers, cfg, T, dev)
     print(json.dumps(out), flush=True)

@@ -23,7 +23,7 @@
 namespace wz {
 
 constexpr int kPM = 128;          // pair rows per M-tile
-constexpr int kPThreads = 256;    // 4 waves, 16 features (or columns) each
+constexpr int kPThreads = 256;    // 4 waves
 constexpr int kARow = 144;        // LDS row stride of the staged A tile (bytes)
 
 // ----------------------------------------------------------- M-tile table ---
@@ -78,25 +78,6 @@ __device__ __forceinline__ bool tile_of(const MoeWs& ws, int mt, bool dense, int
   return tr.nrows > 0;
 }
 
-// Stage one 128-row x 128-K fp8 A tile (+ its block scales) into LDS.
-// src_row(r) gives the source row of tile row r (or -1 for a zero row).
-template <typename RowFn>
-__device__ __forceinline__ void stage_a(uint8_t* a_s, float* as_s, const uint8_t* A, const float* As, int K, int kb,
-                                        int nrows, RowFn src_row) {
-  const int tid = threadIdx.x;
-  const int r = tid >> 1, h = tid & 1;
-  const int sr = r < nrows ? src_row(r) : -1;
-  v4i v[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-  if (sr >= 0) {
-    const uint8_t* p = A + int64_t(sr) * K + kb * 128 + h * 64;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = load16(p + 16 * i);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(a_s + r * kARow + h * 64 + 16 * i) = v[i];
-  if (h == 0) as_s[r] = sr >= 0 ? As[int64_t(sr) * (K / 128) + kb] : 1.0f;
-}
-
 __device__ __forceinline__ AOp a_from_lds(const uint8_t* a_s, const float* as_s, int row, int g, bool pow2) {
   AOp a;
   const uint8_t* p = a_s + row * kARow + g * 16;
@@ -108,163 +89,244 @@ __device__ __forceinline__ AOp a_from_lds(const uint8_t* a_s, const float* as_s,
   return a;
 }
 
-// w1/w3 + SwiGLU.  WF = kFmtFp4: routed experts (packed MXFP4 bank);
-// WF = kFmtFp8: the shared expert over the T token rows (DENSE).
-template <int WF>
-__global__ __launch_bounds__(kPThreads) void prefill_w13_kernel(wz_moe_desc d, MoeWs ws, int T) {
-  __shared__ __align__(16) uint8_t a_s[kPM * kARow];
-  __shared__ float as_s[kPM];
-  constexpr bool DENSE = WF == kFmtFp8;
+// B operands of one K-block for the NT weight tiles a wave owns (fp4: lo only).
+// The MXFP4 scale stays the raw packed dword until the MFMA needs its byte:
+// extracting it at fetch time would make the fetch wait for its own loads.
+template <int NT>
+struct BTiles {
+  v4i lo[NT], hi[NT];
+  uint32_t sw[NT];  // fp4: packed e8m0 dword (byte kb & 3); fp8: the e8m0 byte
+  float f[NT];
+};
+
+// Expert-grouped tile GEMM over one M-tile (<= 128 rows) and one N-block.
+//   MODE 0: routed w1/w3 (packed MXFP4) over gathered x rows -> SwiGLU -> h
+//   MODE 1: shared w1/w3 (packed FP8) over token rows        -> SwiGLU -> sh_h
+//   MODE 2: routed w2 (packed MXFP4) over h rows             -> out2
+//   MODE 3: shared w2 (packed FP8) over shared h rows        -> sh_out
+// A wave owns NTW weight tiles of 16 output columns (routed: 4, i.e. w13: 2
+// feature tiles x {w1, w3}, w2: 4 column tiles; shared FP8 tiles are twice
+// the bytes, so 2), and one A operand read from LDS feeds NTW MFMAs.
+// The K loop is software-pipelined: the A block of K-step kb+1 is fetched to
+// registers and the B tiles of kb+2 are in flight while kb computes; A goes
+// through two LDS buffers with one barrier per K-step.
+//
+// CHAIN: activation and weight scales are both powers of two, so they ride in
+// the MFMA's e8m0 scale operands and the accumulators chain over K; otherwise
+// each K-block partial is scaled on the VALU (mma_step).
+template <int MODE, bool CHAIN>
+__device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws, int T, int mt, int nt,
+                                          uint8_t (*a_s)[kPM * kARow], float (*as_s)[kPM]) {
+  constexpr bool W13 = MODE < 2, DENSE = (MODE & 1) != 0;
+  constexpr int WF = DENSE ? kFmtFp8 : kFmtFp4;
+  constexpr int NTW = DENSE ? 2 : 4;          // weight tiles per wave
+  constexpr int CPW = W13 ? NTW / 2 : NTW;    // 16-column output tiles per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nl = lane & 15, g = lane >> 4;
   const int D = d.dim, I = d.inter, E = d.n_experts, k = d.topk, P = T * k;
-  const int KB = D / 128, KG = (KB + 3) / 4, FT = I / 16, NT = I / 64;
-  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
-  const int mt = blockIdx.x / NT, nt = blockIdx.x % NT;
+  const int K = W13 ? D : I, KB = K / 128, KG = (KB + 3) / 4;
+  const int NCT = (W13 ? I : D) / 16;  // 16-column tiles of the output
+  const bool a_pow2 = CHAIN || d.act_scale_kind != WZ_SCALE_F32;
+  const bool bp = CHAIN || !DENSE || d.shared_w_scale_kind == WZ_WSCALE_E8M0;
   TileRows tr;
   if (!tile_of(ws, mt, DENSE, T, P, E, tr)) return;
-  const int ft = nt * 4 + wave, f0 = ft * 16;
-  v4f acc[2][8];
+  const int row0 = tr.row0, nrows = tr.nrows, e = tr.e;
+  const int ct0 = (nt * 4 + wave) * CPW;  // first column tile of this wave
+
+  // weight tile j of this wave: column tile ct(j), w1/w3 selector which(j)
+  int ct[NTW], which[NTW];
+  bool jv[NTW];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) acc[0][m] = acc[1][m] = v4f{0.f, 0.f, 0.f, 0.f};
-  const uint8_t* wt;
-  const uint32_t* st = nullptr;
-  if (DENSE) {
-    wt = static_cast<const uint8_t*>(d.sh13p) + int64_t(ft) * KB * 4096;
-  } else {
-    wt = static_cast<const uint8_t*>(d.w13p) + (int64_t(tr.e) * FT + ft) * KB * 2048;
-    st = static_cast<const uint32_t*>(d.w13p_s) + (int64_t(tr.e) * FT + ft) * KG * 2 * 64 + lane;
+  for (int j = 0; j < NTW; ++j) {
+    ct[j] = W13 ? ct0 + (j >> 1) : ct0 + j;
+    which[j] = W13 ? (j & 1) : 0;
+    jv[j] = ct[j] < NCT;
   }
-  const bool bp = !DENSE || d.shared_w_scale_kind == WZ_WSCALE_E8M0;
-  const int64_t sbase = int64_t(f0 >> 7) * KB;
-  const int32_t* ptok = ws.perm_token;
-  const int row0 = tr.row0;
-  for (int kb = 0; kb < KB; ++kb) {
-    __syncthreads();
-    stage_a(a_s, as_s, ws.xq, ws.xs, D, kb, tr.nrows,
-            [&](int r) { return DENSE ? row0 + r : clampi(ptok[row0 + r], 0, T - 1); });
-    v8i b1, b3;
-    int e1, e3;
-    float f1 = 1.0f, f3 = 1.0f;
-    if (DENSE) {
-      const uint8_t* tp = wt + int64_t(kb) * 4096;
-      const v4i l1 = load16_nt(tp + lane * 16), h1 = load16_nt(tp + 1024 + lane * 16);
-      const v4i l3 = load16_nt(tp + 2048 + lane * 16), h3 = load16_nt(tp + 3072 + lane * 16);
-      b1 = v8i{l1[0], l1[1], l1[2], l1[3], h1[0], h1[1], h1[2], h1[3]};
-      b3 = v8i{l3[0], l3[1], l3[2], l3[3], h3[0], h3[1], h3[2], h3[3]};
-      fp8_wscale(d.sh_w1_s, sbase + kb, d.shared_w_scale_kind, e1, f1);
-      fp8_wscale(d.sh_w3_s, sbase + kb, d.shared_w_scale_kind, e3, f3);
-    } else {
-      const uint8_t* tp = wt + int64_t(kb) * 2048;
-      const v4i x1 = load16_nt(tp + lane * 16), x3 = load16_nt(tp + 1024 + lane * 16);
-      b1 = v8i{x1[0], x1[1], x1[2], x1[3], 0, 0, 0, 0};
-      b3 = v8i{x3[0], x3[1], x3[2], x3[3], 0, 0, 0, 0};
-      const int kg = kb >> 2, sh = 8 * (kb & 3);
-      e1 = int((st[(kg * 2 + 0) * 64] >> sh) & 0xFFu);
-      e3 = int((st[(kg * 2 + 1) * 64] >> sh) & 0xFFu);
+
+  // A staging: thread -> (row, half of the 128-byte K-block)
+  const int sr = tid >> 1, sh = tid & 1;
+  const uint8_t* arow = nullptr;
+  const float* asrow = nullptr;
+  if (sr < nrows) {
+    int src;
+    if (MODE == 0) src = clampi(ws.perm_token[row0 + sr], 0, T - 1);
+    else if (MODE == 1) src = row0 + sr;
+    else if (MODE == 2) src = row0 + sr;
+    else src = P + row0 + sr;
+    const uint8_t* A = W13 ? ws.xq : ws.hq;
+    const float* As = W13 ? ws.xs : ws.hs;
+    arow = A + int64_t(src) * K + sh * 64;
+    asrow = As + int64_t(src) * KB;
+  }
+  v4i av[4];
+  float asv = 1.0f;
+  auto a_fetch = [&](int kb) {
+    if (arow) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = load16(arow + kb * 128 + 16 * i);
+      asv = asrow[kb];
     }
-    __syncthreads();
+  };
+  auto a_put = [&](int buf) {
+    if (arow) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(&a_s[buf][sr * kARow + sh * 64 + 16 * i]) = av[i];
+      if (sh == 0) as_s[buf][sr] = asv;
+    }
+  };
+
+  auto b_fetch = [&](BTiles<NTW>& b, int kb) {
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      if (!jv[j]) continue;
+      if (MODE == 0) {
+        const int64_t t = int64_t(e) * NCT + ct[j];
+        const uint8_t* w = static_cast<const uint8_t*>(d.w13p) + ((t * KB + kb) * 2 + which[j]) * 1024;
+        b.lo[j] = load16_nt(w + lane * 16);
+        const uint32_t* sw = static_cast<const uint32_t*>(d.w13p_s) + ((t * KG + (kb >> 2)) * 2 + which[j]) * 64;
+        b.sw[j] = sw[lane];
+        b.f[j] = 1.0f;
+      } else if (MODE == 2) {
+        const int64_t t = int64_t(e) * NCT + ct[j];
+        const uint8_t* w = static_cast<const uint8_t*>(d.w2p) + (t * KB + kb) * 1024;
+        b.lo[j] = load16_nt(w + lane * 16);
+        const uint32_t* sw = static_cast<const uint32_t*>(d.w2p_s) + (t * KG + (kb >> 2)) * 64;
+        b.sw[j] = sw[lane];
+        b.f[j] = 1.0f;
+      } else {
+        const uint8_t* w;
+        const void* s;
+        if (MODE == 1) {
+          w = static_cast<const uint8_t*>(d.sh13p) + ((int64_t(ct[j]) * KB + kb) * 2 + which[j]) * 2048;
+          s = which[j] ? d.sh_w3_s : d.sh_w1_s;
+        } else {
+          w = static_cast<const uint8_t*>(d.sh2p) + (int64_t(ct[j]) * KB + kb) * 2048;
+          s = d.sh_w2_s;
+        }
+        b.lo[j] = load16_nt(w + lane * 16);
+        b.hi[j] = load16_nt(w + 1024 + lane * 16);
+        int se8;
+        fp8_wscale(s, int64_t(ct[j] >> 3) * KB + kb, d.shared_w_scale_kind, se8, b.f[j]);
+        b.sw[j] = uint32_t(se8);
+      }
+    }
+  };
+
+  v4f acc[NTW][8];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j)
+#pragma unroll
+    for (int m = 0; m < 8; ++m) acc[j][m] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int buf, const BTiles<NTW>& b, int kb) {
+    int e8[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) e8[j] = DENSE ? int(b.sw[j]) : int((b.sw[j] >> (8 * (kb & 3))) & 0xFFu);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      if (m * 16 < tr.nrows) {
-        const AOp a = a_from_lds(a_s, as_s, m * 16 + nl, g, a_pow2);
-        mma_step<kFmtFp8, WF>(acc[0][m], a, b1, e1, f1, a_pow2, bp, lane);
-        mma_step<kFmtFp8, WF>(acc[1][m], a, b3, e3, f3, a_pow2, bp, lane);
+      if (m * 16 < nrows) {
+        const AOp a = a_from_lds(a_s[buf], as_s[buf], m * 16 + nl, g, CHAIN || a_pow2);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          if (!jv[j]) continue;
+          const v8i bv = DENSE ? v8i{b.lo[j][0], b.lo[j][1], b.lo[j][2], b.lo[j][3], b.hi[j][0], b.hi[j][1],
+                                     b.hi[j][2], b.hi[j][3]}
+                               : v8i{b.lo[j][0], b.lo[j][1], b.lo[j][2], b.lo[j][3], 0, 0, 0, 0};
+          if (CHAIN)
+            acc[j][m] = mfma_scaled<kFmtFp8, WF>(a.v, bv, acc[j][m], a.se8, e8[j]);
+          else
+            mma_step<kFmtFp8, WF>(acc[j][m], a, bv, e8[j], b.f[j], a_pow2, bp, lane);
+        }
       }
     }
+  };
+
+  BTiles<NTW> b0, b1;
+  a_fetch(0);
+  b_fetch(b0, 0);
+  a_put(0);
+  if (KB > 1) {
+    a_fetch(1);
+    b_fetch(b1, 1);
   }
-  // epilogue: SwiGLU (+ routing weight) -> bf16 h
+  __syncthreads();
+  for (int kb = 0; kb < KB; kb += 2) {
+    compute(0, b0, kb);
+    if (kb + 1 < KB) a_put(1);
+    if (kb + 2 < KB) {
+      a_fetch(kb + 2);
+      b_fetch(b0, kb + 2);
+    }
+    __syncthreads();
+    if (kb + 1 >= KB) break;
+    compute(1, b1, kb + 1);
+    if (kb + 2 < KB) a_put(0);
+    if (kb + 3 < KB) {
+      a_fetch(kb + 3);
+      b_fetch(b1, kb + 3);
+    }
+    __syncthreads();
+  }
+
+  // epilogue
+  if (W13) {
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
+    for (int q = 0; q < CPW; ++q) {
+      if (!jv[2 * q]) continue;
+      const int f = ct[2 * q] * 16 + nl;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = m * 16 + g * 4 + i;
-      if (r < tr.nrows) {
-        float gs = acc[0][m][i], us = acc[1][m][i];
-        float gv = bf16_round(gs), uv = bf16_round(us);
-        if (d.swiglu_limit > 0.0f) {
-          uv = fminf(fmaxf(uv, -d.swiglu_limit), d.swiglu_limit);
-          gv = fminf(gv, d.swiglu_limit);
+      for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = m * 16 + g * 4 + i;
+          if (r < nrows) {
+            float gv = bf16_round(acc[2 * q][m][i]), uv = bf16_round(acc[2 * q + 1][m][i]);
+            if (d.swiglu_limit > 0.0f) {
+              uv = fminf(fmaxf(uv, -d.swiglu_limit), d.swiglu_limit);
+              gv = fminf(gv, d.swiglu_limit);
+            }
+            const float hv = silu_f32(gv) * uv;
+            if (DENSE) {
+              ws.sh_h[int64_t(row0 + r) * I + f] = f32_to_bf16(hv);
+            } else {
+              const int p = row0 + r;
+              const float wt =
+                  ws.weights[int64_t(clampi(ws.perm_token[p], 0, T - 1)) * k + clampi(ws.perm_slot[p], 0, k - 1)];
+              ws.h[int64_t(p) * I + f] = f32_to_bf16(wt * hv);
+            }
+          }
         }
-        const float hv = silu_f32(gv) * uv;
-        if (DENSE) {
-          ws.sh_h[int64_t(row0 + r) * I + f0 + nl] = f32_to_bf16(hv);
-        } else {
-          const int p = row0 + r;
-          const float wt_ = ws.weights[int64_t(clampi(ptok[p], 0, T - 1)) * k + clampi(ws.perm_slot[p], 0, k - 1)];
-          ws.h[int64_t(p) * I + f0 + nl] = f32_to_bf16(wt_ * hv);
+    }
+  } else {
+    uint16_t* out = DENSE ? ws.sh_out : ws.out2;
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      if (!jv[j]) continue;
+      const int c = ct[j] * 16 + nl;
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = m * 16 + g * 4 + i;
+          if (r < nrows) out[int64_t(row0 + r) * D + c] = f32_to_bf16(acc[j][m][i]);
         }
-      }
     }
   }
 }
 
-// w2: A rows are contiguous hq rows (pairs of the tile, or shared rows P + t).
-template <int WF>
-__global__ __launch_bounds__(kPThreads) void prefill_w2_kernel(wz_moe_desc d, MoeWs ws, int T) {
-  __shared__ __align__(16) uint8_t a_s[kPM * kARow];
-  __shared__ float as_s[kPM];
-  constexpr bool DENSE = WF == kFmtFp8;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nl = lane & 15, g = lane >> 4;
-  const int D = d.dim, I = d.inter, E = d.n_experts, k = d.topk, P = T * k;
-  const int KB = I / 128, KG = (KB + 3) / 4, DT = D / 16, NT = D / 64;
-  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
-  const int mt = blockIdx.x / NT, nt = blockIdx.x % NT;
-  TileRows tr;
-  if (!tile_of(ws, mt, DENSE, T, P, E, tr)) return;
-  const int dt = nt * 4 + wave, n0 = dt * 16;
-  v4f acc[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) acc[m] = v4f{0.f, 0.f, 0.f, 0.f};
-  const uint8_t* wt;
-  const uint32_t* st = nullptr;
-  if (DENSE) {
-    wt = static_cast<const uint8_t*>(d.sh2p) + int64_t(dt) * KB * 2048;
-  } else {
-    wt = static_cast<const uint8_t*>(d.w2p) + (int64_t(tr.e) * DT + dt) * KB * 1024;
-    st = static_cast<const uint32_t*>(d.w2p_s) + (int64_t(tr.e) * DT + dt) * KG * 64 + lane;
-  }
-  const bool bp = !DENSE || d.shared_w_scale_kind == WZ_WSCALE_E8M0;
-  const int64_t sbase = int64_t(n0 >> 7) * KB;
-  const int arow0 = DENSE ? P + tr.row0 : tr.row0;
-  for (int kb = 0; kb < KB; ++kb) {
-    __syncthreads();
-    stage_a(a_s, as_s, ws.hq, ws.hs, I, kb, tr.nrows, [&](int r) { return arow0 + r; });
-    v8i b;
-    int es;
-    float fs = 1.0f;
-    if (DENSE) {
-      const uint8_t* tp = wt + int64_t(kb) * 2048;
-      const v4i lo = load16_nt(tp + lane * 16), hi = load16_nt(tp + 1024 + lane * 16);
-      b = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      fp8_wscale(d.sh_w2_s, sbase + kb, d.shared_w_scale_kind, es, fs);
-    } else {
-      const v4i x = load16_nt(wt + int64_t(kb) * 1024 + lane * 16);
-      b = v8i{x[0], x[1], x[2], x[3], 0, 0, 0, 0};
-      es = int((st[(kb >> 2) * 64] >> (8 * (kb & 3))) & 0xFFu);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      if (m * 16 < tr.nrows) {
-        const AOp a = a_from_lds(a_s, as_s, m * 16 + nl, g, a_pow2);
-        mma_step<kFmtFp8, WF>(acc[m], a, b, es, fs, a_pow2, bp, lane);
-      }
-    }
-  }
-#pragma unroll
-  for (int m = 0; m < 8; ++m)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = m * 16 + g * 4 + i;
-      if (r < tr.nrows) {
-        if (DENSE)
-          ws.sh_out[int64_t(tr.row0 + r) * D + n0 + nl] = f32_to_bf16(acc[m][i]);
-        else
-          ws.out2[int64_t(tr.row0 + r) * D + n0 + nl] = f32_to_bf16(acc[m][i]);
-      }
-    }
+// One launch serves the shared expert's dense tiles (block ids first, so the
+// few long-running shared tiles start early) and the routed experts' M-tiles.
+// W13 selects w1/w3 + SwiGLU or w2; CR / CS: scale chaining of routed / shared.
+template <bool W13, bool CR, bool CS>
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_gemm_kernel(
+    wz_moe_desc d, MoeWs ws, int T, int nblk, int nblk_dense, int dense_blocks) {
+  __shared__ __align__(16) uint8_t a_s[2][kPM * kARow];
+  __shared__ float as_s[2][kPM];
+  const int b = blockIdx.x;
+  if (b < dense_blocks)
+    gemm_tile<W13 ? 1 : 3, CS>(d, ws, T, b / nblk_dense, b % nblk_dense, a_s, as_s);
+  else
+    gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, (b - dense_blocks) / nblk, (b - dense_blocks) % nblk, a_s, as_s);
 }
 
 int launch_act_quant(const void* x, int64_t rows, int64_t K, uint8_t* q, void* s, int kind, hipStream_t stream);
@@ -277,26 +339,36 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
   const int64_t P = T * k;
   if (!d->w13p || !d->w13p_s || !d->w2p || !d->w2p_s || !d->sh13p || !d->sh2p)
     return set_error(WZ_EINVAL, "moe prefill: packed banks missing (call wz_moe_pack)");
-  if (D % 64 || I % 64) return set_error(WZ_EINVAL, "moe prefill: dim and inter must be multiples of 64");
   const int qkind = d->act_scale_kind == WZ_SCALE_F32 ? WZ_SCALE_F32 : WZ_SCALE_UE8M0_F32;
   const int64_t mt_max = prefill_mt_max(P, E), mt_dense = (T + kPM - 1) / kPM;
   WZ_LAUNCH("moe_mtile", stream, mtile_kernel, dim3(1), dim3(1024), 0, w, E, int(P), int(mt_max));
   if (int rc = check_launch("moe mtile")) return rc;
   if (int rc = launch_act_quant(x, T, D, w.xq, w.xs, qkind, stream)) return rc;
-  WZ_LAUNCH("moe_w13", stream, prefill_w13_kernel<kFmtFp4>, dim3(unsigned(mt_max * (I / 64))), dim3(kPThreads), 0,
-            *d, w, int(T));
+  // column tiles of 16 per WG: routed 4 waves x 4 weight tiles, shared 4 x 2
+  const int nb13 = (I / 16 + 7) / 8, nb13d = (I / 16 + 3) / 4;
+  const int nb2 = (D / 16 + 15) / 16, nb2d = (D / 16 + 7) / 8;
+  const bool cr = d->act_scale_kind != WZ_SCALE_F32;
+  const bool cs = cr && d->shared_w_scale_kind == WZ_WSCALE_E8M0;
+  const int Ti = int(T), dn13 = int(mt_dense * nb13d), dn2 = int(mt_dense * nb2d);
+  const dim3 blk(kPThreads), g13(unsigned(dn13 + mt_max * nb13)), g2(unsigned(dn2 + mt_max * nb2));
+  if (cr && cs) {
+    WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, true, true>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13);
+  } else if (cr) {
+    WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, true, false>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13);
+  } else {
+    WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, false, false>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13);
+  }
   if (int rc = check_launch("moe w13")) return rc;
-  WZ_LAUNCH("moe_sh13", stream, prefill_w13_kernel<kFmtFp8>, dim3(unsigned(mt_dense * (I / 64))), dim3(kPThreads),
-            0, *d, w, int(T));
-  if (int rc = check_launch("moe sh13")) return rc;
   if (int rc = launch_act_quant(w.h, P, I, w.hq, w.hs, qkind, stream)) return rc;
   if (int rc = launch_act_quant(w.sh_h, T, I, w.hq + P * I, w.hs + P * (I / 128), qkind, stream)) return rc;
-  WZ_LAUNCH("moe_w2", stream, prefill_w2_kernel<kFmtFp4>, dim3(unsigned(mt_max * (D / 64))), dim3(kPThreads), 0, *d,
-            w, int(T));
-  if (int rc = check_launch("moe w2")) return rc;
-  WZ_LAUNCH("moe_sh2", stream, prefill_w2_kernel<kFmtFp8>, dim3(unsigned(mt_dense * (D / 64))), dim3(kPThreads), 0,
-            *d, w, int(T));
-  return check_launch("moe sh2");
+  if (cr && cs) {
+    WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, true, true>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
+  } else if (cr) {
+    WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, true, false>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
+  } else {
+    WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, false, false>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
+  }
+  return check_launch("moe w2");
 }
 
 }  // namespace wz

@@ -172,6 +172,28 @@ class HipMoE:
             setattr(d, name, bufs[name].data_ptr())
         return bufs
 
+    def with_gate_bias(self, bias: torch.Tensor, max_tokens: int = 16) -> "HipMoE":
+        """A layer over the same expert banks (packed once) with another fp32 gate bias [E]."""
+        import dataclasses
+
+        if self.weights.tid2eid is not None:
+            raise ValueError("HipMoE: a hash-routed layer has no gate bias")
+        bias = bias.to(device=self.device, dtype=torch.float32).contiguous()
+        if bias.shape != (self.cfg.n_experts,):
+            raise ValueError(f"HipMoE: gate bias must be [{self.cfg.n_experts}], got {tuple(bias.shape)}")
+        other = object.__new__(HipMoE)
+        other.cfg = self.cfg
+        other.weights = dataclasses.replace(self.weights, gate_bias=bias)
+        other.desc = WzMoeDesc()
+        ctypes.memmove(ctypes.byref(other.desc), ctypes.byref(self.desc), ctypes.sizeof(WzMoeDesc))
+        other.desc.gate_bias = bias.data_ptr()
+        other.device = self.device
+        other.packed = self.packed
+        other._ws = None
+        other._ws_tokens = 0
+        other.reserve(max_tokens)
+        return other
+
     # -- workspace -----------------------------------------------------------
     def workspace_bytes(self, T: int) -> int:
         return int(N.lib().wz_moe_workspace_bytes(ctypes.byref(self.desc), T))
