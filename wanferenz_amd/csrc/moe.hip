@@ -339,6 +339,8 @@ __global__ void export_routing_kernel(const MoeWs ws, int P, float* __restrict__
 int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* ids, int64_t T,
                   void* y, hipStream_t stream);
 int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, int64_t T, hipStream_t stream);
+int launch_prefill_gate(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* input_ids, int64_t T,
+                        hipStream_t stream);
 
 static int validate(const wz_moe_desc* d, int64_t T, const void* ws, size_t ws_bytes,
                     const char* what) {
@@ -374,16 +376,21 @@ static int launch_routing(const wz_moe_desc* d, const MoeWs& w, const void* x,
                           const int64_t* input_ids, int64_t T, hipStream_t stream) {
   const int E = d->n_experts, k = d->topk, D = d->dim;
   if (d->tid2eid && !input_ids) return set_error(WZ_EINVAL, "moe: hash-routed layer needs input_ids");
-  WZ_LAUNCH("moe_gate", stream, gate_dot_kernel, dim3((E + 3) / 4, unsigned((T + kGateTok - 1) / kGateTok)), dim3(256), 0, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(d->gate_w),
-                     w.scores, int(T), E, D);
-  if (int rc = check_launch("moe gate")) return rc;
-  WZ_LAUNCH("moe_topk", stream, topk_kernel, dim3(unsigned((T + 3) / 4)), dim3(256), 0, w.scores,
-                     d->tid2eid ? nullptr : d->gate_bias, d->tid2eid, input_ids, d->vocab, int(T), E,
-                     k, d->score_func, d->route_scale, w.weights, w.idx);
-  if (int rc = check_launch("moe topk")) return rc;
-  WZ_LAUNCH("moe_perm", stream, perm_kernel, dim3(1), dim3(kRouteThreads), 0, w.idx, int(T), E, k,
-                     w.offsets, w.active, w.act_off, w.act_cnt, w.n_active, w.perm_token,
-                     w.perm_slot, w.pos);
+  if (T > kDecodeMaxT && d->score_func != WZ_SCORE_SOFTMAX) {
+    // MFMA gate + exact refinement at the top-k boundary (moe_prefill.hip)
+    if (int rc = launch_prefill_gate(d, w, x, input_ids, T, stream)) return rc;
+  } else {
+    WZ_LAUNCH("moe_gate", stream, gate_dot_kernel, dim3((E + 3) / 4, unsigned((T + kGateTok - 1) / kGateTok)),
+              dim3(256), 0, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(d->gate_w), w.scores,
+              int(T), E, D);
+    if (int rc = check_launch("moe gate")) return rc;
+    WZ_LAUNCH("moe_topk", stream, topk_kernel, dim3(unsigned((T + 3) / 4)), dim3(256), 0, w.scores,
+              d->tid2eid ? nullptr : d->gate_bias, d->tid2eid, input_ids, d->vocab, int(T), E, k, d->score_func,
+              d->route_scale, w.weights, w.idx);
+    if (int rc = check_launch("moe topk")) return rc;
+  }
+  WZ_LAUNCH("moe_perm", stream, perm_kernel, dim3(1), dim3(kRouteThreads), 0, w.idx, int(T), E, k, w.offsets,
+            w.active, w.act_off, w.act_cnt, w.n_active, w.perm_token, w.perm_slot, w.pos);
   return check_launch("moe perm");
 }
 

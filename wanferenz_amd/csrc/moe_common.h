@@ -18,7 +18,7 @@ constexpr int kCounterWords = 4096;   // arrival counters at the start of the wo
 struct MoeWs {
   uint32_t* counters;  // [kCounterWords]: [0] route, [1 + d_tile] combine
   float* scores;       // [T, E] gate logits (general path) / scores (decode path)
-  float* biased;       // [T, E] decode path: scores + bias (the selection key)
+  float* biased;       // [T, E] decode: scores + bias (the selection key); prefill: sum |x||w| (gate error bound)
   float* weights;      // [T, k]
   int32_t* idx;        // [T, k]
   int32_t* offsets;    // [E + 1]

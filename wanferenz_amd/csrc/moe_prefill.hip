@@ -26,6 +26,263 @@ constexpr int kPM = 128;          // pair rows per M-tile
 constexpr int kPThreads = 256;    // 4 waves
 constexpr int kARow = 144;        // LDS row stride of the staged A tile (bytes)
 
+// ------------------------------------------------------------------- gate ---
+//
+// Prefill routing must pick exactly the experts the exact fp32 logits pick
+// (the reference evaluates the gate as one fp32 GEMM; the oracle and the
+// decode path use the correctly rounded dot product).  Two passes:
+//
+//  gate_mfma   approximate logits a~[t,e] with V_MFMA_F32_16X16X16_BF16: each
+//              32-wide K chunk is summed by two MFMAs from zero and added to
+//              an fp64 accumulator, so |a~ - a| <= 33 * 2^-23 * S + (fp64
+//              terms), S = sum_d |x_d w_d|, whatever order or rounding mode
+//              the MFMA uses inside a chunk (bf16 x bf16 products are exact
+//              in fp32).  S itself comes from the same MFMA on |x|, |w|.
+//  topk_refine one wave per token: key bounds [b~ - G, b~ + G] from the logit
+//              bound through the score function's slope (sigmoid <= 1/4,
+//              sqrt(softplus) <= 0.61); theta = k-th largest lower bound; every
+//              expert whose upper bound reaches theta is a candidate (the
+//              exact top-k is among them); candidates get the exact fp64 dot,
+//              exact keys pick the top-k (ties -> lower index) and the
+//              weights come from exact scores.  Hash-routed layers take the
+//              table's experts and compute only their exact scores.
+// Softmax gates need every logit exactly (the denominator) and use the
+// fp64 gate of moe.hip.
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4s v4s_lo(v4i a) {
+  return v4s{short(a[0] & 0xFFFF), short(uint32_t(a[0]) >> 16), short(a[1] & 0xFFFF), short(uint32_t(a[1]) >> 16)};
+}
+__device__ __forceinline__ v4s v4s_hi(v4i a) {
+  return v4s{short(a[2] & 0xFFFF), short(uint32_t(a[2]) >> 16), short(a[3] & 0xFFFF), short(uint32_t(a[3]) >> 16)};
+}
+__device__ __forceinline__ v4i abs_bf16x8(v4i a) {
+  return v4i{a[0] & 0x7FFF7FFF, a[1] & 0x7FFF7FFF, a[2] & 0x7FFF7FFF, a[3] & 0x7FFF7FFF};
+}
+
+// One workgroup per (16 tokens, 16 experts) tile; its 4 waves split K and
+// meet in LDS.  A lane loads 8 consecutive bf16 of its row for two 16x16x16
+// MFMAs; A and B use the same lane -> K assignment, so each K element's two
+// factors meet in one product.
+__global__ __launch_bounds__(256) void gate_mfma_kernel(const uint16_t* __restrict__ x,
+                                                        const uint16_t* __restrict__ W,
+                                                        float* __restrict__ approx, float* __restrict__ absdot,
+                                                        int T, int E, int D) {
+  __shared__ double red[3][64][4];
+  __shared__ float reds[3][64][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int etiles = (E + 15) / 16;
+  const int tt = blockIdx.x / etiles, et = blockIdx.x % etiles;
+  const int nl = lane & 15, g = lane >> 4;
+  const int tok = tt * 16 + nl, ex = et * 16 + nl;
+  const uint16_t* xr = tok < T ? x + int64_t(tok) * D : nullptr;
+  const uint16_t* wr = ex < E ? W + int64_t(ex) * D : nullptr;
+  const int nsteps = D / 32, s0 = (wave * nsteps) / 4, s1 = ((wave + 1) * nsteps) / 4;
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  v4f sabs = {0.f, 0.f, 0.f, 0.f};
+  const v4f z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+  for (int st = s0; st < s1; ++st) {
+    const int k0 = st * 32;
+    const v4i a = xr ? load16(xr + k0 + 8 * g) : v4i{0, 0, 0, 0};
+    const v4i b = wr ? load16(wr + k0 + 8 * g) : v4i{0, 0, 0, 0};
+    v4f p = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a), v4s_lo(b), z, 0, 0, 0);
+    p = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a), v4s_hi(b), p, 0, 0, 0);
+    const v4i aa = abs_bf16x8(a), ba = abs_bf16x8(b);
+    sabs = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(aa), v4s_lo(ba), sabs, 0, 0, 0);
+    sabs = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(aa), v4s_hi(ba), sabs, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += double(p[i]);
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red[wave - 1][lane][i] = acc[i];
+      reds[wave - 1][lane][i] = sabs[i];
+    }
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  const int e = et * 16 + nl;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const double v = acc[i] + red[0][lane][i] + red[1][lane][i] + red[2][lane][i];
+    const float sv = sabs[i] + reds[0][lane][i] + reds[1][lane][i] + reds[2][lane][i];
+    const int t = tt * 16 + g * 4 + i;
+    if (t < T && e < E) {
+      approx[int64_t(t) * E + e] = float(v);
+      absdot[int64_t(t) * E + e] = sv;
+    }
+  }
+}
+
+// Exact logit of (token row, expert row w): fp32-exact products summed in fp64
+// across the wave (the arithmetic of gate_dot_kernel in moe.hip).  xv holds
+// the token row's first kXC * 512 elements (8 per lane per chunk); all weight
+// loads of a chunk group are issued before the products.
+constexpr int kXC = 8;
+
+__device__ __forceinline__ float exact_logit(const v4i (&xv)[kXC], const uint16_t* __restrict__ xrow,
+                                             const uint16_t* __restrict__ w, int D, int lane) {
+  double acc = 0.0;
+  for (int base = 0; base < D; base += kXC * 512) {
+    v4i wv[kXC], xb[kXC];
+#pragma unroll
+    for (int c = 0; c < kXC; ++c) {
+      const int off = base + (lane + 64 * c) * 8;
+      wv[c] = off < D ? load16(w + off) : v4i{0, 0, 0, 0};
+      xb[c] = base == 0 ? xv[c] : (off < D ? load16(xrow + off) : v4i{0, 0, 0, 0});
+    }
+#pragma unroll
+    for (int c = 0; c < kXC; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc += double(bf16lo(uint32_t(xb[c][j])) * bf16lo(uint32_t(wv[c][j])));
+        acc += double(bf16hi(uint32_t(xb[c][j])) * bf16hi(uint32_t(wv[c][j])));
+      }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, kWave);
+  return float(acc);
+}
+
+constexpr int kRSlots = kMaxExperts / 64;
+constexpr float kChunkErr = 33.0f / 8388608.0f;  // 33 * 2^-23
+
+__global__ __launch_bounds__(256) void topk_refine_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ W,
+                                                          const float* __restrict__ approx,
+                                                          const float* __restrict__ absdot,
+                                                          const float* __restrict__ bias,
+                                                          const int32_t* __restrict__ tid2eid,
+                                                          const int64_t* __restrict__ input_ids, int64_t vocab,
+                                                          int T, int E, int D, int k, int score_func,
+                                                          float route_scale, float* __restrict__ weights,
+                                                          int32_t* __restrict__ idx) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  const uint16_t* xr = x + int64_t(t) * D;
+  v4i xv[kXC];
+#pragma unroll
+  for (int c = 0; c < kXC; ++c) {
+    const int off = (lane + 64 * c) * 8;
+    xv[c] = off < D ? load16(xr + off) : v4i{0, 0, 0, 0};
+  }
+  int my_sel = 0;
+  float mine = 0.0f;  // exact score of the lane's slot (lane < k)
+  if (tid2eid != nullptr) {
+    int64_t id = input_ids[t];
+    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+    for (int j = 0; j < k; ++j) {
+      int e = tid2eid[id * k + j];
+      e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+      const float s = score_of(exact_logit(xv, xr, W + int64_t(e) * D, D, lane), score_func);
+      if (lane == j) {
+        my_sel = e;
+        mine = s;
+      }
+    }
+  } else {
+    const float L = score_func == WZ_SCORE_SIGMOID ? 0.25f : 0.61f;
+    float lo[kRSlots], hi[kRSlots];
+#pragma unroll
+    for (int i = 0; i < kRSlots; ++i) {
+      const int e = lane + 64 * i;
+      lo[i] = hi[i] = -INFINITY;
+      if (e < E) {
+        const float a = approx[int64_t(t) * E + e];
+        const float S = absdot[int64_t(t) * E + e] * 1.001f;
+        const float f = score_of(a, score_func);
+        const float key = bias ? f + bias[e] : f;
+        const float G = L * (kChunkErr * S + 2.4e-7f * fabsf(a)) + 4.8e-7f * (fabsf(f) + fabsf(key)) + 1e-30f;
+        lo[i] = key - G;
+        hi[i] = key + G;
+      }
+    }
+    // theta = k-th largest lower bound
+    unsigned taken = 0u;
+    float theta = -INFINITY;
+    for (int j = 0; j < k; ++j) {
+      Cand best = {-INFINITY, 0x7FFFFFFF};
+#pragma unroll
+      for (int i = 0; i < kRSlots; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E && !((taken >> i) & 1u)) best = cand_better(best, Cand{lo[i], e});
+      }
+      best = wave_argmax(best);
+      theta = best.v;
+      if ((best.i & 63) == lane) taken |= 1u << (best.i >> 6);
+    }
+    // exact keys of the candidates (upper bound reaches theta)
+    float sx[kRSlots], kx[kRSlots];
+#pragma unroll
+    for (int i = 0; i < kRSlots; ++i) {
+      sx[i] = 0.0f;
+      kx[i] = -INFINITY;
+      unsigned long long m = __ballot(lane + 64 * i < E && hi[i] >= theta);
+      while (m) {
+        const int l = __ffsll(static_cast<long long>(m)) - 1;
+        m &= m - 1;
+        const int e = l + 64 * i;
+        const float s = score_of(exact_logit(xv, xr, W + int64_t(e) * D, D, lane), score_func);
+        if (lane == l) {
+          sx[i] = s;
+          kx[i] = bias ? s + bias[e] : s;
+        }
+      }
+    }
+    // top-k of the exact keys (ties -> lower index)
+    taken = 0u;
+    for (int j = 0; j < k; ++j) {
+      Cand best = {-INFINITY, 0x7FFFFFFF};
+#pragma unroll
+      for (int i = 0; i < kRSlots; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E && !((taken >> i) & 1u) && kx[i] != -INFINITY) best = cand_better(best, Cand{kx[i], e});
+      }
+      best = wave_argmax(best);
+      const int bi = clampi(best.i, 0, E - 1);
+      float sv = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kRSlots; ++i) {
+        const float v = __shfl(sx[i], bi & 63, kWave);
+        if ((bi >> 6) == i) sv = v;
+      }
+      if (lane == j) {
+        my_sel = bi;
+        mine = sv;
+      }
+      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    }
+  }
+  float tot = 0.0f;
+  for (int j = 0; j < k; ++j) tot += __shfl(mine, j, kWave);  // slot order, fp32
+  const float v = mine / tot * route_scale;
+  if (lane < k) {
+    weights[int64_t(t) * k + lane] = v;
+    idx[int64_t(t) * k + lane] = my_sel;
+  }
+}
+
+int launch_prefill_gate(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* input_ids, int64_t T,
+                        hipStream_t stream) {
+  const int E = d->n_experts, D = d->dim;
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const uint16_t* gw = static_cast<const uint16_t*>(d->gate_w);
+  if (!d->tid2eid) {
+    const int64_t tiles = ((T + 15) / 16) * ((E + 15) / 16);
+    WZ_LAUNCH("moe_gate", stream, gate_mfma_kernel, dim3(unsigned(tiles)), dim3(256), 0, xb, gw, w.scores,
+              w.biased, int(T), E, D);
+    if (int rc = check_launch("moe gate")) return rc;
+  }
+  WZ_LAUNCH("moe_topk", stream, topk_refine_kernel, dim3(unsigned((T + 3) / 4)), dim3(256), 0, xb, gw, w.scores,
+            w.biased, d->tid2eid ? nullptr : d->gate_bias, d->tid2eid, input_ids, d->vocab, int(T), E, D, d->topk,
+            d->score_func, d->route_scale, w.weights, w.idx);
+  return check_launch("moe topk");
+}
+
 // ----------------------------------------------------------- M-tile table ---
 
 // One workgroup: cut each active expert's pair rows into tiles of kPM.
@@ -107,87 +364,80 @@ struct BTiles {
 // A wave owns NTW weight tiles of 16 output columns (routed: 4, i.e. w13: 2
 // feature tiles x {w1, w3}, w2: 4 column tiles; shared FP8 tiles are twice
 // the bytes, so 2), and one A operand read from LDS feeds NTW MFMAs.
-// The K loop is software-pipelined: the A block of K-step kb+1 is fetched to
-// registers and the B tiles of kb+2 are in flight while kb computes; A goes
-// through two LDS buffers with one barrier per K-step.
+// The K loop is software-pipelined: the B tiles of K-steps kb+1 and kb+2 are
+// in flight while kb computes, and the A block of kb+1 sits in registers on
+// its way to LDS; A goes through three LDS buffers with one barrier per step.
 //
 // CHAIN: activation and weight scales are both powers of two, so they ride in
 // the MFMA's e8m0 scale operands and the accumulators chain over K; otherwise
 // each K-block partial is scaled on the VALU (mma_step).
-template <int MODE, bool CHAIN>
-__device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws, int T, int mt, int nt,
-                                          uint8_t (*a_s)[kPM * kARow], float (*as_s)[kPM]) {
+template <int MODE, bool CHAIN, int NM>
+__device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs& ws, int T, const TileRows& tr,
+                                               int nt, uint8_t (*a_s)[kPM * kARow], float (*as_s)[kPM]) {
   constexpr bool W13 = MODE < 2, DENSE = (MODE & 1) != 0;
   constexpr int WF = DENSE ? kFmtFp8 : kFmtFp4;
   constexpr int NTW = DENSE ? 2 : 4;          // weight tiles per wave
   constexpr int CPW = W13 ? NTW / 2 : NTW;    // 16-column output tiles per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nl = lane & 15, g = lane >> 4;
-  const int D = d.dim, I = d.inter, E = d.n_experts, k = d.topk, P = T * k;
+  const int D = d.dim, I = d.inter, k = d.topk, P = T * k;
   const int K = W13 ? D : I, KB = K / 128, KG = (KB + 3) / 4;
   const int NCT = (W13 ? I : D) / 16;  // 16-column tiles of the output
   const bool a_pow2 = CHAIN || d.act_scale_kind != WZ_SCALE_F32;
   const bool bp = CHAIN || !DENSE || d.shared_w_scale_kind == WZ_WSCALE_E8M0;
-  TileRows tr;
-  if (!tile_of(ws, mt, DENSE, T, P, E, tr)) return;
   const int row0 = tr.row0, nrows = tr.nrows, e = tr.e;
   const int ct0 = (nt * 4 + wave) * CPW;  // first column tile of this wave
 
-  // weight tile j of this wave: column tile ct(j), w1/w3 selector which(j)
-  int ct[NTW], which[NTW];
+  // weight tile j of this wave: column tile ct(j), w1/w3 selector which(j).
+  // Every load of the K loop is unconditional (tiles past the last column
+  // re-read the last one; rows past nrows re-read the last row), so the
+  // compiler can count outstanding loads exactly and keep the prefetches in
+  // flight across the barriers; only the epilogue looks at validity.
+  int ct[NTW], cl[NTW], which[NTW];
   bool jv[NTW];
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
     ct[j] = W13 ? ct0 + (j >> 1) : ct0 + j;
+    cl[j] = min(ct[j], NCT - 1);
     which[j] = W13 ? (j & 1) : 0;
     jv[j] = ct[j] < NCT;
   }
 
   // A staging: thread -> (row, half of the 128-byte K-block)
   const int sr = tid >> 1, sh = tid & 1;
-  const uint8_t* arow = nullptr;
-  const float* asrow = nullptr;
-  if (sr < nrows) {
-    int src;
-    if (MODE == 0) src = clampi(ws.perm_token[row0 + sr], 0, T - 1);
-    else if (MODE == 1) src = row0 + sr;
-    else if (MODE == 2) src = row0 + sr;
-    else src = P + row0 + sr;
-    const uint8_t* A = W13 ? ws.xq : ws.hq;
-    const float* As = W13 ? ws.xs : ws.hs;
-    arow = A + int64_t(src) * K + sh * 64;
-    asrow = As + int64_t(src) * KB;
-  }
+  const int rr = min(sr, nrows - 1);
+  int src;
+  if (MODE == 0) src = clampi(ws.perm_token[row0 + rr], 0, T - 1);
+  else if (MODE == 1) src = row0 + rr;
+  else if (MODE == 2) src = row0 + rr;
+  else src = P + row0 + rr;
+  const uint8_t* arow = (W13 ? ws.xq : ws.hq) + int64_t(src) * K + sh * 64;
+  const float* asrow = (W13 ? ws.xs : ws.hs) + int64_t(src) * KB;
   v4i av[4];
-  float asv = 1.0f;
+  float asv;
   auto a_fetch = [&](int kb) {
-    if (arow) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = load16(arow + kb * 128 + 16 * i);
-      asv = asrow[kb];
-    }
+    for (int i = 0; i < 4; ++i) av[i] = load16(arow + kb * 128 + 16 * i);
+    asv = asrow[kb];
   };
   auto a_put = [&](int buf) {
-    if (arow) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(&a_s[buf][sr * kARow + sh * 64 + 16 * i]) = av[i];
-      if (sh == 0) as_s[buf][sr] = asv;
-    }
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(&a_s[buf][sr * kARow + sh * 64 + 16 * i]) = av[i];
+    as_s[buf][sr] = asv;  // both halves of the row store the same scale: no divergent branch
   };
 
   auto b_fetch = [&](BTiles<NTW>& b, int kb) {
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
-      if (!jv[j]) continue;
       if (MODE == 0) {
-        const int64_t t = int64_t(e) * NCT + ct[j];
+        const int64_t t = int64_t(e) * NCT + cl[j];
         const uint8_t* w = static_cast<const uint8_t*>(d.w13p) + ((t * KB + kb) * 2 + which[j]) * 1024;
         b.lo[j] = load16_nt(w + lane * 16);
         const uint32_t* sw = static_cast<const uint32_t*>(d.w13p_s) + ((t * KG + (kb >> 2)) * 2 + which[j]) * 64;
         b.sw[j] = sw[lane];
         b.f[j] = 1.0f;
       } else if (MODE == 2) {
-        const int64_t t = int64_t(e) * NCT + ct[j];
+        const int64_t t = int64_t(e) * NCT + cl[j];
         const uint8_t* w = static_cast<const uint8_t*>(d.w2p) + (t * KB + kb) * 1024;
         b.lo[j] = load16_nt(w + lane * 16);
         const uint32_t* sw = static_cast<const uint32_t*>(d.w2p_s) + (t * KG + (kb >> 2)) * 64;
@@ -197,51 +447,56 @@ __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws,
         const uint8_t* w;
         const void* s;
         if (MODE == 1) {
-          w = static_cast<const uint8_t*>(d.sh13p) + ((int64_t(ct[j]) * KB + kb) * 2 + which[j]) * 2048;
+          w = static_cast<const uint8_t*>(d.sh13p) + ((int64_t(cl[j]) * KB + kb) * 2 + which[j]) * 2048;
           s = which[j] ? d.sh_w3_s : d.sh_w1_s;
         } else {
-          w = static_cast<const uint8_t*>(d.sh2p) + (int64_t(ct[j]) * KB + kb) * 2048;
+          w = static_cast<const uint8_t*>(d.sh2p) + (int64_t(cl[j]) * KB + kb) * 2048;
           s = d.sh_w2_s;
         }
         b.lo[j] = load16_nt(w + lane * 16);
         b.hi[j] = load16_nt(w + 1024 + lane * 16);
-        int se8;
-        fp8_wscale(s, int64_t(ct[j] >> 3) * KB + kb, d.shared_w_scale_kind, se8, b.f[j]);
-        b.sw[j] = uint32_t(se8);
+        const int64_t si = int64_t(cl[j] >> 3) * KB + kb;
+        if (CHAIN) {
+          b.sw[j] = static_cast<const uint8_t*>(s)[si];
+          b.f[j] = 1.0f;
+        } else {
+          int se8;
+          fp8_wscale(s, si, d.shared_w_scale_kind, se8, b.f[j]);
+          b.sw[j] = uint32_t(se8);
+        }
       }
     }
   };
 
-  v4f acc[NTW][8];
+  v4f acc[NTW][NM];
 #pragma unroll
   for (int j = 0; j < NTW; ++j)
 #pragma unroll
-    for (int m = 0; m < 8; ++m) acc[j][m] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < NM; ++m) acc[j][m] = v4f{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](int buf, const BTiles<NTW>& b, int kb) {
     int e8[NTW];
 #pragma unroll
     for (int j = 0; j < NTW; ++j) e8[j] = DENSE ? int(b.sw[j]) : int((b.sw[j] >> (8 * (kb & 3))) & 0xFFu);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      if (m * 16 < nrows) {
-        const AOp a = a_from_lds(a_s[buf], as_s[buf], m * 16 + nl, g, CHAIN || a_pow2);
+    for (int m = 0; m < NM; ++m) {
+      const AOp a = a_from_lds(a_s[buf], as_s[buf], m * 16 + nl, g, CHAIN || a_pow2);
 #pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-          if (!jv[j]) continue;
-          const v8i bv = DENSE ? v8i{b.lo[j][0], b.lo[j][1], b.lo[j][2], b.lo[j][3], b.hi[j][0], b.hi[j][1],
-                                     b.hi[j][2], b.hi[j][3]}
-                               : v8i{b.lo[j][0], b.lo[j][1], b.lo[j][2], b.lo[j][3], 0, 0, 0, 0};
-          if (CHAIN)
-            acc[j][m] = mfma_scaled<kFmtFp8, WF>(a.v, bv, acc[j][m], a.se8, e8[j]);
-          else
-            mma_step<kFmtFp8, WF>(acc[j][m], a, bv, e8[j], b.f[j], a_pow2, bp, lane);
-        }
+      for (int j = 0; j < NTW; ++j) {
+        const v8i bv = DENSE ? v8i{b.lo[j][0], b.lo[j][1], b.lo[j][2], b.lo[j][3], b.hi[j][0], b.hi[j][1],
+                                   b.hi[j][2], b.hi[j][3]}
+                             : v8i{b.lo[j][0], b.lo[j][1], b.lo[j][2], b.lo[j][3], 0, 0, 0, 0};
+        if (CHAIN)
+          acc[j][m] = mfma_scaled<kFmtFp8, WF>(a.v, bv, acc[j][m], a.se8, e8[j]);
+        else
+          mma_step<kFmtFp8, WF>(acc[j][m], a, bv, e8[j], b.f[j], a_pow2, bp, lane);
       }
     }
   };
 
-  BTiles<NTW> b0, b1;
+  // Invariant at step kb: LDS buffer kb % 3 holds A(kb), av holds A(kb+1),
+  // B registers hold B(kb) (landed), B(kb+1) and B(kb+2) (in flight).
+  BTiles<NTW> b0, b1, b2;
   a_fetch(0);
   b_fetch(b0, 0);
   a_put(0);
@@ -249,22 +504,49 @@ __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws,
     a_fetch(1);
     b_fetch(b1, 1);
   }
+  if (KB > 2) b_fetch(b2, 2);
   __syncthreads();
-  for (int kb = 0; kb < KB; kb += 2) {
+  int kb = 0;
+  // steady state: every step refills, no conditional loads (sched_barrier keeps
+  // each step's MFMAs ahead of the loads that refill their B registers)
+  for (; kb + 5 < KB; kb += 3) {
+    compute(0, b0, kb);
+    __builtin_amdgcn_sched_barrier(0);
+    a_put(1);
+    a_fetch(kb + 2);
+    b_fetch(b0, kb + 3);
+    __syncthreads();
+    compute(1, b1, kb + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    a_put(2);
+    a_fetch(kb + 3);
+    b_fetch(b1, kb + 4);
+    __syncthreads();
+    compute(2, b2, kb + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    a_put(0);
+    a_fetch(kb + 4);
+    b_fetch(b2, kb + 5);
+    __syncthreads();
+  }
+  // last K-steps
+  for (; kb < KB; kb += 3) {
     compute(0, b0, kb);
     if (kb + 1 < KB) a_put(1);
-    if (kb + 2 < KB) {
-      a_fetch(kb + 2);
-      b_fetch(b0, kb + 2);
-    }
+    if (kb + 2 < KB) a_fetch(kb + 2);
+    if (kb + 3 < KB) b_fetch(b0, kb + 3);
     __syncthreads();
     if (kb + 1 >= KB) break;
     compute(1, b1, kb + 1);
-    if (kb + 2 < KB) a_put(0);
-    if (kb + 3 < KB) {
-      a_fetch(kb + 3);
-      b_fetch(b1, kb + 3);
-    }
+    if (kb + 2 < KB) a_put(2);
+    if (kb + 3 < KB) a_fetch(kb + 3);
+    if (kb + 4 < KB) b_fetch(b1, kb + 4);
+    __syncthreads();
+    if (kb + 2 >= KB) break;
+    compute(2, b2, kb + 2);
+    if (kb + 3 < KB) a_put(0);
+    if (kb + 4 < KB) a_fetch(kb + 4);
+    if (kb + 5 < KB) b_fetch(b2, kb + 5);
     __syncthreads();
   }
 
@@ -275,7 +557,7 @@ __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws,
       if (!jv[2 * q]) continue;
       const int f = ct[2 * q] * 16 + nl;
 #pragma unroll
-      for (int m = 0; m < 8; ++m)
+      for (int m = 0; m < NM; ++m)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = m * 16 + g * 4 + i;
@@ -304,7 +586,7 @@ __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws,
       if (!jv[j]) continue;
       const int c = ct[j] * 16 + nl;
 #pragma unroll
-      for (int m = 0; m < 8; ++m)
+      for (int m = 0; m < NM; ++m)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = m * 16 + g * 4 + i;
@@ -314,14 +596,31 @@ __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws,
   }
 }
 
+// Tile dispatch on its height: the body is compiled for 1, 2, 4 or 8 row
+// tiles of 16, so its MFMA loops carry no row branches.
+template <int MODE, bool CHAIN>
+__device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws, int T, int mt, int nt,
+                                          uint8_t (*a_s)[kPM * kARow], float (*as_s)[kPM]) {
+  TileRows tr;
+  if (!tile_of(ws, mt, (MODE & 1) != 0, T, T * d.topk, d.n_experts, tr)) return;
+  if (tr.nrows <= 16)
+    gemm_tile_body<MODE, CHAIN, 1>(d, ws, T, tr, nt, a_s, as_s);
+  else if (tr.nrows <= 32)
+    gemm_tile_body<MODE, CHAIN, 2>(d, ws, T, tr, nt, a_s, as_s);
+  else if (tr.nrows <= 64)
+    gemm_tile_body<MODE, CHAIN, 4>(d, ws, T, tr, nt, a_s, as_s);
+  else
+    gemm_tile_body<MODE, CHAIN, 8>(d, ws, T, tr, nt, a_s, as_s);
+}
+
 // One launch serves the shared expert's dense tiles (block ids first, so the
 // few long-running shared tiles start early) and the routed experts' M-tiles.
 // W13 selects w1/w3 + SwiGLU or w2; CR / CS: scale chaining of routed / shared.
 template <bool W13, bool CR, bool CS>
-__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_gemm_kernel(
+__global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(
     wz_moe_desc d, MoeWs ws, int T, int nblk, int nblk_dense, int dense_blocks) {
-  __shared__ __align__(16) uint8_t a_s[2][kPM * kARow];
-  __shared__ float as_s[2][kPM];
+  __shared__ __align__(16) uint8_t a_s[3][kPM * kARow];
+  __shared__ float as_s[3][kPM];
   const int b = blockIdx.x;
   if (b < dense_blocks)
     gemm_tile<W13 ? 1 : 3, CS>(d, ws, T, b / nblk_dense, b % nblk_dense, a_s, as_s);
