@@ -85,7 +85,8 @@ def e2m1_decode_nibbles(packed: np.ndarray) -> np.ndarray:
 
 def e8m0_decode(b: np.ndarray) -> np.ndarray:
     b = np.asarray(b, dtype=np.uint8)
-    out = np.ldexp(np.float32(1.0), b.astype(np.int32) - 127).astype(np.float32)
+    with np.errstate(over="ignore"):  # code 0xFF overflows before it is set to NaN
+        out = np.ldexp(np.float32(1.0), b.astype(np.int32) - 127).astype(np.float32)
     out[b == 0xFF] = np.nan
     return out
 

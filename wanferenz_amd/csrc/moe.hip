@@ -364,7 +364,8 @@ static int validate(const wz_moe_desc* d, int64_t T, const void* ws, size_t ws_b
   if (!d->tid2eid && !d->gate_bias && d->score_func == WZ_SCORE_SQRTSOFTPLUS) {
     // a score-routed layer without bias is legal (bias optional), nothing to check
   }
-  if (!ws && T > 0) return set_error(WZ_EINVAL, "%s: null workspace", what);
+  if (T == 0) return WZ_OK;  // nothing to do: no workspace needed
+  if (!ws) return set_error(WZ_EINVAL, "%s: null workspace", what);
   const size_t need = moe_ws_layout(d, T, nullptr).bytes;
   if (ws_bytes < need)
     return set_error(WZ_ESPACE, "%s: workspace %zu bytes < %zu needed for T=%lld", what, ws_bytes,

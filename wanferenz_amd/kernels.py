@@ -159,3 +159,13 @@ def install(mod) -> bool:
         setattr(mod, name, fn)
         took = True
     return took
+
+
+def uninstall(mod) -> bool:
+    """Restore the functions install() replaced on ``mod``."""
+    took = False
+    for name, fn in (("act_quant", act_quant), ("fp8_gemm", fp8_gemm), ("fp4_gemm", fp4_gemm)):
+        if getattr(mod, name, None) is fn and name in _REF:
+            setattr(mod, name, _REF.pop(name))
+            took = True
+    return took
