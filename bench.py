@@ -13,9 +13,11 @@ Printed JSON line (one):
               (U*13,369,344 + 25,167,360 + 2,098,176 + 4*T*D) bytes / time,
               U = distinct experts the step's routing selected
   ms_per_step layer latency (µs/layer = 1000 * ms_per_step)
-  roofline    the dominant kernel (moe_w13: routed w1/w3 + shared w1/w3),
-              algorithmic bytes per launch / its mean duration measured live
-              with HIP events on the launch stream
+  roofline    the dominant kernel (w13: routed w1/w3 + shared w1/w3 + SwiGLU),
+              algorithmic bytes per launch / its mean launch duration, measured
+              live: the stage replayed alone for all layers from a captured
+              graph, HIP events on the replay stream (stage_times)
+  stage_us    the same per-launch measurement for every stage of the layer
   cpu_baseline the oracle (numpy restatement of the reference CPU path) on one
               T-token layer, single thread
   per_T       the same layer measured at T = 1, 2, 4, 8
@@ -72,6 +74,9 @@ def parse():
     ap.add_argument("--prefill", default="128,512,2048",
                     help="comma-separated prefill T values ('' to skip)")
     ap.add_argument("--prefill-layers", type=int, default=3)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device-to-device copy 5 times (the reference kernel of "
+                         "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
 
 
@@ -152,31 +157,51 @@ def time_steps(graphs, steps, warmup):
     return start.elapsed_time(end) / 1000.0, wall
 
 
-def kernel_times(layers, xs, reps=2):
-    """Eager pass with every library launch bracketed by HIP events."""
+STAGES = (("route", 0), ("w13", 1), ("hquant", 2), ("w2", 3), ("combine", 4))  # WZ_STAGE_*
+
+
+def stage_times(layers, xs, outs, reps=20):
+    """Mean µs per launch of each stage of the layer.
+
+    Each stage alone (wz_moe_replay_stage: the same kernels on the state the
+    last forward left in the workspace) is captured for all layers into one
+    graph, so its launches run back to back with no launch gaps and no event
+    packets between kernels; HIP events on the replay stream bracket ``reps``
+    replays.  Rotating over all layers keeps the weights out of the caches as
+    in the timed run.
+    """
     import torch
 
-    from wanferenz_amd._native import KernelTimer
-
-    for (moe, _), (_, x) in zip(layers, xs):
-        moe.forward(x)
-    torch.cuda.synchronize()
-    with KernelTimer(64 * len(layers) * reps) as kt:
+    T = xs[0][1].size(0)
+    res = {}
+    for name, st in STAGES:
+        if name == "combine" and T <= 16:
+            continue  # fused into w2 on the decode path
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for (moe, _), (_, x), out in zip(layers, xs, outs):
+                moe.replay_stage(x, st, out)
+        g.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
         for _ in range(reps):
-            for (moe, _), (_, x) in zip(layers, xs):
-                moe.forward(x)
-    torch.cuda.synchronize()
-    return kt.mean_ms()
+            g.replay()
+        end.record()
+        torch.cuda.synchronize()
+        res[name] = start.elapsed_time(end) * 1000.0 / (reps * len(layers))
+        del g
+    return res
 
 
 def measure_T(layers, T, steps, warmup, dev, salt):
     xs = make_inputs(len(layers), T, dev, salt)
     Us = distinct_experts(layers, xs)
-    graphs, _ = capture(layers, xs)
+    graphs, outs = capture(layers, xs)
     secs, wall = time_steps(graphs, steps, warmup)
     L = len(layers)
     total_bytes = sum(layer_bytes(Us[i % L], T) for i in range(steps))
-    kt = kernel_times(layers, xs)
+    kt = stage_times(layers, xs, outs)
     return dict(T=T, secs=secs, wall=wall, Us=Us, total_bytes=total_bytes, kernels=kt, xs=xs)
 
 
@@ -201,10 +226,10 @@ def measure_prefill(layers, Ts, dev):
             _, idx, _, _, _ = moe.route(x)
             torch.cuda.synchronize()
             loads.append(np.bincount(idx.cpu().numpy().ravel(), minlength=E))
-        graphs, _ = capture(players, xs)
+        graphs, outs = capture(players, xs)
         steps = max(6, min(60, 24576 // T))
         secs, _ = time_steps(graphs, steps, max(2, steps // 4))
-        kt = kernel_times(players, xs, reps=1)
+        kt = stage_times(players, xs, outs, reps=max(2, steps // 3))
         L = len(players)
         nbytes = sum(layer_bytes(int((loads[i % L] > 0).sum()), T) for i in range(steps))
         us = secs / steps * 1e6
@@ -218,7 +243,7 @@ def measure_prefill(layers, Ts, dev):
                        "max_expert_rows": int(max(l.max() for l in loads)),
                        "mean_active_experts": round(float(np.mean([(l > 0).sum() for l in loads])), 1),
                        "steps": steps,
-                       "kernel_us": {k: round(v * 1000.0, 2) for k, v in sorted(kt.items())}}
+                       "stage_us": {k: round(v, 2) for k, v in kt.items()}}
     return res
 
 
@@ -269,6 +294,15 @@ def main():
 
     from wanferenz_amd import _native
 
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": 1 << 30, "launches": 5}), flush=True)
+        return
     _native.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -280,9 +314,9 @@ def main():
     ms = secs / args.steps * 1000.0
     Umean = float(np.mean(main_run["Us"]))
     kt = main_run["kernels"]
-    w13_ms = kt.get("moe_w13", float("nan"))
+    w13_us = kt["w13"]
     w13_b = float(np.mean([w13_bytes(u, T) for u in main_run["Us"]]))
-    achieved = w13_b / (w13_ms / 1000.0) / 1e9
+    achieved = w13_b / (w13_us * 1e-6) / 1e9
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
@@ -298,8 +332,8 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "moe_w13", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None, "bytes_per_launch": round(w13_b),
-                     "mean_us": round(w13_ms * 1000.0, 2)},
-        "kernel_us": {k: round(v * 1000.0, 2) for k, v in sorted(kt.items())},
+                     "mean_us": round(w13_us, 2)},
+        "stage_us": {k: round(v, 2) for k, v in kt.items()},
     }
     if not args.no_sweep:
         sweep = {}
@@ -310,7 +344,7 @@ def main():
             sweep[str(Ts)] = {"us_per_layer": round(r["secs"] / n * 1e6, 2), "GB_s": round(v, 1),
                               "hbm_frac": round(v / HBM_PEAK_GBS, 4),
                               "mean_U": round(float(np.mean(r["Us"])), 1),
-                              "kernel_us": {k: round(x * 1000.0, 2) for k, x in sorted(r["kernels"].items())}}
+                              "stage_us": {k: round(x, 2) for k, x in r["kernels"].items()}}
         out["per_T"] = sweep
     if args.prefill:
         Ts = [int(t) for t in args.prefill.split(",") if t]

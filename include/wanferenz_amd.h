@@ -142,6 +142,22 @@ int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const int64_t* inpu
                    void* y_bf16, float* weights_out, int64_t* indices_out, void* ws,
                    size_t ws_bytes, hipStream_t stream);
 
+/* Profiling replay: re-launch one kernel stage of the preceding wz_moe_forward call
+ * made with the same d, x, T, y and ws (the workspace still holds that call's
+ * routing tables and intermediates), so a stage can be timed on its own or
+ * captured alone in a graph.  Stages: WZ_STAGE_ROUTE (gate + top-k + permutation;
+ * prefill also its M-tiles and act_quant(x)), WZ_STAGE_W13 (w1|w3 + SwiGLU, routed
+ * and shared), WZ_STAGE_HQUANT (act_quant of h), WZ_STAGE_W2 (w2; for T <= 16 with
+ * the weighted combine into y), WZ_STAGE_COMBINE (T > 16: the combine into y).
+ * No counterpart in the reference (its benchmarks time whole calls). */
+#define WZ_STAGE_ROUTE 0
+#define WZ_STAGE_W13 1
+#define WZ_STAGE_HQUANT 2
+#define WZ_STAGE_W2 3
+#define WZ_STAGE_COMBINE 4
+int wz_moe_replay_stage(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids, int64_t T,
+                        int stage, void* y_bf16, void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* Routing only (Gate.forward + the canonical permutation of expert_batch.py:24-37):
  * weights fp32 [T,k], indices int64 [T,k], offsets int32 [E+1],
  * perm_token int32 [T*k], perm_slot int32 [T*k]. */

@@ -293,3 +293,23 @@ def test_v4_prefill_parity(v4_layer, T, bias):
     print(f"V4 prefill T={T} ({bias} bias, experts hit {int((counts > 0).sum())}, max rows "
           f"{int(counts.max())}): sampled rows vs oracle rel {rel:.2e} cos {cos:.8f}; vs decode "
           f"rel {rel_d:.2e} cos {cos_d:.8f} bit-equal {np.mean(got == dec):.4f}; near-ties {near}")
+
+
+@pytest.mark.parametrize("T", [4, 40])
+def test_replay_stages_reproduce_the_forward(gpu, T):
+    """wz_moe_replay_stage re-runs a stage of the last forward on its workspace state."""
+    import dataclasses
+    case = dataclasses.replace(CASES["top6_t8"], T=T)
+    inp = make_inputs(case)
+    moe = upload_case(case, inp, gpu)
+    x = bf16_tensor(inp.x, gpu)
+    y = moe.forward(x).clone()
+    out = torch.zeros_like(y)
+    for st in (N.WZ_STAGE_ROUTE, N.WZ_STAGE_W13, N.WZ_STAGE_HQUANT, N.WZ_STAGE_W2, N.WZ_STAGE_COMBINE):
+        moe.replay_stage(x, st, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, y)
+    out.zero_()
+    moe.replay_stage(x, N.WZ_STAGE_W2 if T <= 16 else N.WZ_STAGE_COMBINE, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, y)

@@ -30,6 +30,7 @@ SIGNATURES = {
     "wz_moe_workspace_init": (_I, [_P, ctypes.c_size_t, _P]),
     "wz_moe_forward": (_I, [_P, _P, _P, _I64, _P, _P, _P, _P, ctypes.c_size_t, _P]),
     "wz_moe_route": (_I, [_P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]),
+    "wz_moe_replay_stage": (_I, [_P, _P, _P, _I64, _I, _P, _P, ctypes.c_size_t, _P]),
     "wz_rmsnorm": (_I, [_P, _P, _P, _I64, _I64, _F, _P]),
     "wz_add_bf16": (_I, [_P, _P, _P, _I64, _P]),
     "wz_synth_fill": (_I, [_P, _I64, ctypes.c_uint64, _I64, _I, ctypes.c_double, ctypes.c_double, _P]),
@@ -47,6 +48,11 @@ WZ_WSCALE_E8M0 = 1
 WZ_SCORE_SOFTMAX = 0
 WZ_SCORE_SIGMOID = 1
 WZ_SCORE_SQRTSOFTPLUS = 2
+WZ_STAGE_ROUTE = 0
+WZ_STAGE_W13 = 1
+WZ_STAGE_HQUANT = 2
+WZ_STAGE_W2 = 3
+WZ_STAGE_COMBINE = 4
 
 _LIB = None
 _LOCK = threading.Lock()

@@ -5,6 +5,7 @@
 // e8m0 scale per 32 K-elements, bf16 activations and outputs.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -126,14 +127,21 @@ __device__ __forceinline__ v4i load16_nt(const void* p) {
 namespace wz {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
-int prof_pre(hipStream_t s);
-void prof_post(int slot, const char* name, hipStream_t s);
+int prof_pre(hipStream_t s, hipEvent_t* start, hipEvent_t* stop);
+void prof_post(int slot, const char* name);
 }  // namespace wz
 
-// Launch with optional event bracketing: WZ_LAUNCH("name", stream, kernel, grid, block, lds, args...)
-#define WZ_LAUNCH(NAME, STREAM, KERNEL, GRID, BLOCK, LDS, ...)                 \
-  do {                                                                         \
-    const int wz_prof_slot_ = ::wz::prof_pre(STREAM);                          \
-    hipLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, STREAM, __VA_ARGS__);         \
-    ::wz::prof_post(wz_prof_slot_, NAME, STREAM);                              \
+// Launch, timed when profiling is on: WZ_LAUNCH("name", stream, kernel, grid, block, lds, args...).
+// A timed launch goes through hipExtLaunchKernelGGL, whose start/stop events take the
+// dispatch's own begin and end timestamps (no marker packets around the kernel).
+#define WZ_LAUNCH(NAME, STREAM, KERNEL, GRID, BLOCK, LDS, ...)                                  \
+  do {                                                                                          \
+    hipEvent_t wz_ev_b_ = nullptr, wz_ev_e_ = nullptr;                                          \
+    const int wz_prof_slot_ = ::wz::prof_pre(STREAM, &wz_ev_b_, &wz_ev_e_);                      \
+    if (wz_prof_slot_ >= 0) {                                                                   \
+      hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, STREAM, wz_ev_b_, wz_ev_e_, 0, __VA_ARGS__); \
+      ::wz::prof_post(wz_prof_slot_, NAME);                                                     \
+    } else {                                                                                    \
+      hipLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, STREAM, __VA_ARGS__);                        \
+    }                                                                                           \
   } while (0)

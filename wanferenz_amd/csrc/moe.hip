@@ -337,8 +337,9 @@ __global__ void export_routing_kernel(const MoeWs ws, int P, float* __restrict__
 // ------------------------------------------------------------------ host ----
 
 int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* ids, int64_t T,
-                  void* y, hipStream_t stream);
-int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, int64_t T, hipStream_t stream);
+                  void* y, hipStream_t stream, int only);
+int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, int64_t T, hipStream_t stream,
+                           int only);
 int launch_prefill_gate(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* input_ids, int64_t T,
                         hipStream_t stream);
 
@@ -457,7 +458,7 @@ extern "C" int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const in
   const MoeWs w = moe_ws_layout(d, T, static_cast<uint8_t*>(ws));
   if (T <= kDecodeMaxT && d->n_experts <= kMaxExperts) {
     if (d->tid2eid && !input_ids) return set_error(WZ_EINVAL, "moe: hash-routed layer needs input_ids");
-    if (int rc = launch_decode(d, w, x_bf16, input_ids, T, y_bf16, stream)) return rc;
+    if (int rc = launch_decode(d, w, x_bf16, input_ids, T, y_bf16, stream, -1)) return rc;
     if (weights_out || indices_out) {
       const int P = int(T * d->topk);
       WZ_LAUNCH("moe_export", stream, export_routing_kernel, dim3(unsigned((P + 255) / 256)), dim3(256), 0, w,
@@ -469,7 +470,7 @@ extern "C" int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const in
   if (int rc = launch_routing(d, w, x_bf16, input_ids, T, stream)) return rc;
   const int k = d->topk, D = d->dim;
   const int64_t P = T * k;
-  if (int rc = launch_prefill_experts(d, w, x_bf16, T, stream)) return rc;
+  if (int rc = launch_prefill_experts(d, w, x_bf16, T, stream, -1)) return rc;
   WZ_LAUNCH("moe_combine", stream, combine_kernel, dim3(unsigned((D / 8 + 255) / 256), unsigned(T)), dim3(256),
                      0, w, k, D, static_cast<uint16_t*>(y_bf16));
   if (int rc = check_launch("moe combine")) return rc;
@@ -479,4 +480,29 @@ extern "C" int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const in
     if (int rc = check_launch("moe export")) return rc;
   }
   return WZ_OK;
+}
+
+extern "C" int wz_moe_replay_stage(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids, int64_t T,
+                                   int stage, void* y_bf16, void* ws, size_t ws_bytes, hipStream_t stream) {
+  using namespace wz;
+  if (int rc = validate(d, T, ws, ws_bytes, "moe_replay_stage")) return rc;
+  if (stage < WZ_STAGE_ROUTE || stage > WZ_STAGE_COMBINE)
+    return set_error(WZ_EINVAL, "moe_replay_stage: unknown stage %d", stage);
+  if (T == 0) return WZ_OK;
+  if (!x_bf16 || !y_bf16) return set_error(WZ_EINVAL, "moe_replay_stage: null x or y");
+  const MoeWs w = moe_ws_layout(d, T, static_cast<uint8_t*>(ws));
+  if (T <= kDecodeMaxT) {
+    if (stage == WZ_STAGE_COMBINE) return WZ_OK;  // fused into WZ_STAGE_W2
+    return launch_decode(d, w, x_bf16, input_ids, T, y_bf16, stream, stage);
+  }
+  if (stage == WZ_STAGE_ROUTE) {
+    if (int rc = launch_routing(d, w, x_bf16, input_ids, T, stream)) return rc;
+  }
+  if (stage == WZ_STAGE_COMBINE) {
+    const int k = d->topk, D = d->dim;
+    WZ_LAUNCH("moe_combine", stream, combine_kernel, dim3(unsigned((D / 8 + 255) / 256), unsigned(T)), dim3(256), 0,
+              w, k, D, static_cast<uint16_t*>(y_bf16));
+    return check_launch("moe combine");
+  }
+  return launch_prefill_experts(d, w, x_bf16, T, stream, stage);
 }

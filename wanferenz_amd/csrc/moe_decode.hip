@@ -605,8 +605,9 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
   }
 }
 
+// only < 0: the whole layer; otherwise the one stage WZ_STAGE_* (profiling replays).
 int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* ids, int64_t T,
-                  void* y, hipStream_t stream) {
+                  void* y, hipStream_t stream, int only) {
   const int E = d->n_experts, k = d->topk, D = d->dim, I = d->inter;
   const int n_gate = (E + kRouteWaves - 1) / kRouteWaves;
   const int64_t P = T * k;
@@ -614,18 +615,27 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
   if (P > kMaxDecPairs) return set_error(WZ_EINVAL, "moe decode: T*topk=%lld exceeds %d", (long long)P, kMaxDecPairs);
   if (!d->w13p || !d->w13p_s || !d->w2p || !d->w2p_s || !d->sh13p || !d->sh2p)
     return set_error(WZ_EINVAL, "moe decode: packed banks missing (wz_moe_pack)");
-  WZ_LAUNCH("moe_route", stream, route_decode_kernel, dim3(unsigned(n_gate * T + T)), dim3(kRouteThreads_), 0,
-            *d, w, static_cast<const uint16_t*>(x), ids, int(T), n_gate, u_max);
-  if (int rc = check_launch("moe route")) return rc;
-  WZ_LAUNCH("moe_w13", stream, w13_decode_kernel, dim3(unsigned((u_max + 1) * (I / 16))), dim3(kDecThreads), 0, *d,
-            w, int(T), u_max);
-  if (int rc = check_launch("moe w13")) return rc;
-  WZ_LAUNCH("moe_hquant", stream, hquant_kernel, dim3(unsigned(u_max * T + T)), dim3(kDecThreads), 0, w, int(T), I,
-            u_max, d->act_scale_kind != WZ_SCALE_F32);
-  if (int rc = check_launch("moe hquant")) return rc;
-  WZ_LAUNCH("moe_w2", stream, w2_combine_kernel, dim3(unsigned(D / 16)), dim3(kW2Threads), 0, *d, w, int(T), u_max,
-            static_cast<uint16_t*>(y));
-  return check_launch("moe w2");
+  if (only < 0 || only == WZ_STAGE_ROUTE) {
+    WZ_LAUNCH("moe_route", stream, route_decode_kernel, dim3(unsigned(n_gate * T + T)), dim3(kRouteThreads_), 0,
+              *d, w, static_cast<const uint16_t*>(x), ids, int(T), n_gate, u_max);
+    if (int rc = check_launch("moe route")) return rc;
+  }
+  if (only < 0 || only == WZ_STAGE_W13) {
+    WZ_LAUNCH("moe_w13", stream, w13_decode_kernel, dim3(unsigned((u_max + 1) * (I / 16))), dim3(kDecThreads), 0,
+              *d, w, int(T), u_max);
+    if (int rc = check_launch("moe w13")) return rc;
+  }
+  if (only < 0 || only == WZ_STAGE_HQUANT) {
+    WZ_LAUNCH("moe_hquant", stream, hquant_kernel, dim3(unsigned(u_max * T + T)), dim3(kDecThreads), 0, w, int(T),
+              I, u_max, d->act_scale_kind != WZ_SCALE_F32);
+    if (int rc = check_launch("moe hquant")) return rc;
+  }
+  if (only < 0 || only == WZ_STAGE_W2) {
+    WZ_LAUNCH("moe_w2", stream, w2_combine_kernel, dim3(unsigned(D / 16)), dim3(kW2Threads), 0, *d, w, int(T),
+              u_max, static_cast<uint16_t*>(y));
+    if (int rc = check_launch("moe w2")) return rc;
+  }
+  return WZ_OK;
 }
 
 }  // namespace wz

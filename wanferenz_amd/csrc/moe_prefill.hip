@@ -633,16 +633,20 @@ int launch_act_quant(const void* x, int64_t rows, int64_t K, uint8_t* q, void* s
 // M-tiles a grid must cover: sum over experts of ceil(c/128) <= P/128 + active experts.
 static inline int64_t prefill_mt_max(int64_t P, int E) { return P / kPM + (P < E ? P : E) + 1; }
 
-int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, int64_t T, hipStream_t stream) {
+// only < 0: every expert stage; otherwise the one stage WZ_STAGE_* (profiling replays).
+int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, int64_t T, hipStream_t stream,
+                           int only) {
   const int E = d->n_experts, k = d->topk, D = d->dim, I = d->inter;
   const int64_t P = T * k;
   if (!d->w13p || !d->w13p_s || !d->w2p || !d->w2p_s || !d->sh13p || !d->sh2p)
     return set_error(WZ_EINVAL, "moe prefill: packed banks missing (call wz_moe_pack)");
   const int qkind = d->act_scale_kind == WZ_SCALE_F32 ? WZ_SCALE_F32 : WZ_SCALE_UE8M0_F32;
   const int64_t mt_max = prefill_mt_max(P, E), mt_dense = (T + kPM - 1) / kPM;
-  WZ_LAUNCH("moe_mtile", stream, mtile_kernel, dim3(1), dim3(1024), 0, w, E, int(P), int(mt_max));
-  if (int rc = check_launch("moe mtile")) return rc;
-  if (int rc = launch_act_quant(x, T, D, w.xq, w.xs, qkind, stream)) return rc;
+  if (only < 0 || only == WZ_STAGE_ROUTE) {
+    WZ_LAUNCH("moe_mtile", stream, mtile_kernel, dim3(1), dim3(1024), 0, w, E, int(P), int(mt_max));
+    if (int rc = check_launch("moe mtile")) return rc;
+    if (int rc = launch_act_quant(x, T, D, w.xq, w.xs, qkind, stream)) return rc;
+  }
   // column tiles of 16 per WG: routed 4 waves x 4 weight tiles, shared 4 x 2
   const int nb13 = (I / 16 + 7) / 8, nb13d = (I / 16 + 3) / 4;
   const int nb2 = (D / 16 + 15) / 16, nb2d = (D / 16 + 7) / 8;
@@ -650,24 +654,32 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
   const bool cs = cr && d->shared_w_scale_kind == WZ_WSCALE_E8M0;
   const int Ti = int(T), dn13 = int(mt_dense * nb13d), dn2 = int(mt_dense * nb2d);
   const dim3 blk(kPThreads), g13(unsigned(dn13 + mt_max * nb13)), g2(unsigned(dn2 + mt_max * nb2));
-  if (cr && cs) {
-    WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, true, true>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13);
-  } else if (cr) {
-    WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, true, false>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13);
-  } else {
-    WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, false, false>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13);
+  if (only < 0 || only == WZ_STAGE_W13) {
+    if (cr && cs) {
+      WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, true, true>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13);
+    } else if (cr) {
+      WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, true, false>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13);
+    } else {
+      WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, false, false>), g13, blk, 0, *d, w, Ti, nb13, nb13d,
+                dn13);
+    }
+    if (int rc = check_launch("moe w13")) return rc;
   }
-  if (int rc = check_launch("moe w13")) return rc;
-  if (int rc = launch_act_quant(w.h, P, I, w.hq, w.hs, qkind, stream)) return rc;
-  if (int rc = launch_act_quant(w.sh_h, T, I, w.hq + P * I, w.hs + P * (I / 128), qkind, stream)) return rc;
-  if (cr && cs) {
-    WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, true, true>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
-  } else if (cr) {
-    WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, true, false>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
-  } else {
-    WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, false, false>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
+  if (only < 0 || only == WZ_STAGE_HQUANT) {
+    if (int rc = launch_act_quant(w.h, P, I, w.hq, w.hs, qkind, stream)) return rc;
+    if (int rc = launch_act_quant(w.sh_h, T, I, w.hq + P * I, w.hs + P * (I / 128), qkind, stream)) return rc;
   }
-  return check_launch("moe w2");
+  if (only < 0 || only == WZ_STAGE_W2) {
+    if (cr && cs) {
+      WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, true, true>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
+    } else if (cr) {
+      WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, true, false>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
+    } else {
+      WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, false, false>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
+    }
+    if (int rc = check_launch("moe w2")) return rc;
+  }
+  return WZ_OK;
 }
 
 }  // namespace wz

@@ -1,10 +1,11 @@
 // Optional per-launch timing with HIP events (bench.py's live kernel timing).
 //
-// When enabled, every kernel launch site of the library brackets its launch
-// with two events on the launch stream; wz_prof_get() returns each launch's
-// name and elapsed milliseconds.  Disabled (the default) it costs one branch
-// per launch.  Launches made while the stream is being captured into a graph
-// are never instrumented.
+// When enabled, every kernel launch of the library is dispatched with a
+// start/stop event pair (hipExtLaunchKernelGGL), which the runtime stamps
+// with that dispatch's own begin and end times; wz_prof_get() returns each
+// launch's name and elapsed milliseconds.  Disabled (the default) it costs
+// one branch per launch.  Launches made while the stream is being captured
+// into a graph are never instrumented.
 #include <vector>
 
 #include "common.h"
@@ -21,19 +22,17 @@ bool g_on = false;
 
 namespace wz {
 
-int prof_pre(hipStream_t s) {
+int prof_pre(hipStream_t s, hipEvent_t* start, hipEvent_t* stop) {
   if (!g_on || g_used >= int(g_slots.size())) return -1;
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return -1;
-  Slot& sl = g_slots[g_used];
-  if (hipEventRecord(sl.b, s) != hipSuccess) return -1;
+  *start = g_slots[g_used].b;
+  *stop = g_slots[g_used].e;
   return g_used++;
 }
 
-void prof_post(int slot, const char* name, hipStream_t s) {
-  if (slot < 0) return;
-  g_slots[slot].name = name;
-  hipEventRecord(g_slots[slot].e, s);
+void prof_post(int slot, const char* name) {
+  if (slot >= 0) g_slots[slot].name = name;
 }
 
 }  // namespace wz

@@ -249,6 +249,22 @@ class HipMoE:
 
     __call__ = forward
 
+    def replay_stage(self, x: torch.Tensor, stage: int, out: torch.Tensor,
+                     input_ids: Optional[torch.Tensor] = None) -> None:
+        """Re-launch one stage (N.WZ_STAGE_*) of the preceding forward(x, input_ids, out) call.
+
+        The workspace still holds that call's routing tables and intermediates;
+        this is for timing a stage alone (eagerly or captured in a graph).
+        """
+        xv = x.reshape(-1, self.cfg.dim)
+        T = xv.size(0)
+        if T > self._ws_tokens:
+            raise RuntimeError("HipMoE.replay_stage: no preceding forward with this many tokens")
+        ids = None if input_ids is None else input_ids.reshape(-1).to(torch.int64).contiguous()
+        N.call("wz_moe_replay_stage", ctypes.byref(self.desc), xv.data_ptr(),
+               None if ids is None else ids.data_ptr(), T, int(stage), out.data_ptr(),
+               self._ws.data_ptr(), self._ws.numel(), N.stream_handle(self.device))
+
     def route(self, x: torch.Tensor, input_ids: Optional[torch.Tensor] = None):
         """Gate.forward + canonical permutation: (weights, indices, offsets, perm_token, perm_slot)."""
         D, E, k = self.cfg.dim, self.cfg.n_experts, self.cfg.topk
