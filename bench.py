@@ -53,6 +53,18 @@ W13_ROUTED_BYTES = 2 * (I * D // 2) + 2 * (I * D // 32)             # 8,912,896
 W13_SHARED_BYTES = 2 * I * D + 2 * (I // 128) * (D // 128)          # 16,778,240
 
 
+def committed_traffic(T: int):
+    """HBM bytes per launch of the w13 stage at this T from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None when none was recorded."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(rf"traffic_bytes_per_launch w13 decode T={T} = (\d+)", open(path).read())
+    return int(m.group(1)) if m else None
+
+
 def layer_bytes(U: int, T: int) -> int:
     return U * ROUTED_EXPERT_BYTES + SHARED_BYTES + GATE_BYTES + 4 * T * D
 
