@@ -167,3 +167,16 @@ def test_act_quant_error_bound():
         step = 2.0 ** (ex - 3)
         assert (np.abs(dq - y) <= step / 2 + a * 2.0 ** -22).all()  # + the fp32 rounding of x / s
         assert (np.abs(dq) <= 448.0).all()
+
+
+def test_rmsnorm_matches_torch():
+    """oracle.rmsnorm (architecture.py:217-230) vs torch's own F.rms_norm in float32, then bf16."""
+    rng = np.random.default_rng(5)
+    x = bf16_round(rng.standard_normal((6, 4096)).astype(np.float32) * np.float32(2.0))
+    w = bf16_round(rng.uniform(0.5, 1.5, 4096).astype(np.float32))
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(x), (4096,), torch.from_numpy(w), eps=1e-6)
+    ref = ref.to(torch.bfloat16).float().numpy()
+    got = om.rmsnorm(x, w, 1e-6)
+    # fp32 reductions differ in order: equal up to one bf16 step at rounding boundaries
+    step = np.spacing(np.abs(ref).astype(np.float32)) * 65536
+    assert (np.abs(got - ref) <= step).all() and np.mean(got == ref) > 0.99
