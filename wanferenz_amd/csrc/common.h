@@ -127,6 +127,7 @@ __device__ __forceinline__ v4i load16_nt(const void* p) {
 namespace wz {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+int cu_count();
 int prof_pre(hipStream_t s, hipEvent_t* start, hipEvent_t* stop);
 void prof_post(int slot, const char* name);
 }  // namespace wz

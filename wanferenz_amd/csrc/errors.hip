@@ -28,6 +28,21 @@ int check_launch(const char* what) {
 
 extern "C" const char* wz_last_error(void) { return g_err; }
 
+namespace wz {
+// Compute units of the current device (cached per device; 256 on MI355X).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+}  // namespace wz
+
 extern "C" int wz_device_info(int* cu_count, int* xcd_count) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return wz::set_error(WZ_EINVAL, "wz_device_info: no device");

@@ -27,6 +27,8 @@
 // lookup (its expert id) before its weight stream starts, and no per-lane
 // token gather.  Weights come from the packed banks (pack.hip): every load
 // instruction reads 1 KB contiguous, non-temporal (read once).
+#include <algorithm>
+
 #include "moe_common.h"
 
 namespace wz {
@@ -392,6 +394,54 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
 
 // -------------------------------------------------------------------- w13 ---
 
+// Shared expert w1 / w3 (FP8, packed) for features 16 b .. 16 b + 15, all T
+// tokens; the four waves split K and meet in LDS (red: 4 x 2 x 4 x 64 floats).
+__device__ __forceinline__ void w13_shared_item(const wz_moe_desc& d, const MoeWs& ws, int T, int b, float* red) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nl = lane & 15, g = lane >> 4;
+  const int D = d.dim, I = d.inter;
+  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
+  const int a_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
+  const int KB = D / 128;
+  const int kb0 = (wave * KB) / 4, kb1 = ((wave + 1) * KB) / 4;
+  const uint8_t* arow = nl < T ? ws.xq + int64_t(nl) * D : nullptr;
+  const float* asrow = nl < T ? ws.xs + int64_t(nl) * (D / 128) : nullptr;
+  v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  // ---- shared expert w1 / w3 (FP8, packed) for features f0..f0+15 ----
+  const int f0 = b * 16;
+  const uint8_t* tiles = static_cast<const uint8_t*>(d.sh13p) + int64_t(b) * KB * 4096;
+  const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  const int64_t sbase = int64_t(f0 >> 7) * KB;
+  for (int kb = kb0; kb < kb1; kb += 8) {  // 8 K-blocks (32 KB per wave) in flight at once
+    v8i w[2][8];
+    int se[2][8];
+    float sf[2][8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (kb + q < kb1) {
+        w[0][q] = pk_fp8(tiles + int64_t(kb + q) * 4096, lane);
+        w[1][q] = pk_fp8(tiles + int64_t(kb + q) * 4096 + 2048, lane);
+        fp8_wscale(d.sh_w1_s, sbase + kb + q, d.shared_w_scale_kind, se[0][q], sf[0][q]);
+        fp8_wscale(d.sh_w3_s, sbase + kb + q, d.shared_w_scale_kind, se[1][q], sf[1][q]);
+      }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (kb + q < kb1) {
+        const AOp a = a_from_fp8(arow, asrow, kb + q, g, a_kind);
+        mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], a_pow2, bp, lane);
+        mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], a_pow2, bp, lane);
+      }
+  }
+  reduce_waves<2>(acc, red, wave, lane);
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = g * 4 + i;
+      if (t < T) ws.sh_h[int64_t(t) * I + f0 + nl] = f32_to_bf16(swiglu(acc[0][i], acc[1][i], d.swiglu_limit));
+    }
+  }
+}
+
 __global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, MoeWs ws, int T, int u_max) {
   __shared__ float red[4 * 2 * 4 * kWave];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -407,39 +457,7 @@ __global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, 
   v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
   int b = blockIdx.x;
   if (b < FT) {
-    // ---- shared expert w1 / w3 (FP8, packed) for features f0..f0+15 ----
-    const int f0 = b * 16;
-    const uint8_t* tiles = static_cast<const uint8_t*>(d.sh13p) + int64_t(b) * KB * 4096;
-    const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
-    const int64_t sbase = int64_t(f0 >> 7) * KB;
-    for (int kb = kb0; kb < kb1; kb += 4) {
-      v8i w[2][4];
-      int se[2][4];
-      float sf[2][4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (kb + q < kb1) {
-          w[0][q] = pk_fp8(tiles + int64_t(kb + q) * 4096, lane);
-          w[1][q] = pk_fp8(tiles + int64_t(kb + q) * 4096 + 2048, lane);
-          fp8_wscale(d.sh_w1_s, sbase + kb + q, d.shared_w_scale_kind, se[0][q], sf[0][q]);
-          fp8_wscale(d.sh_w3_s, sbase + kb + q, d.shared_w_scale_kind, se[1][q], sf[1][q]);
-        }
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (kb + q < kb1) {
-          const AOp a = a_from_fp8(arow, asrow, kb + q, g, a_kind);
-          mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], a_pow2, bp, lane);
-          mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], a_pow2, bp, lane);
-        }
-    }
-    reduce_waves<2>(acc, red, wave, lane);
-    if (wave == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = g * 4 + i;
-        if (t < T) ws.sh_h[int64_t(t) * I + f0 + nl] = f32_to_bf16(swiglu(acc[0][i], acc[1][i], d.swiglu_limit));
-      }
-    }
+    w13_shared_item(d, ws, T, b, red);
     return;
   }
   b -= FT;
@@ -503,6 +521,155 @@ __global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, 
 
 // Row r < u_max*T: h row (u, t), quantised only when routed; row u_max*T + t:
 // the shared expert's row t.
+// Routed experts' w1/w3 for the decode batch on persistent workgroups.
+//
+// Work item = (active expert u, 16 intermediate features ft): 64 KB of packed
+// MXFP4 tiles.  Items are numbered u * FT + ft, so a run of consecutive items
+// is one contiguous stretch of the packed bank; workgroup b takes items b,
+// b + G, b + 2G, ... of the N = n_active * FT items (grid stride), so the
+// resident workgroups always stream one contiguous window of the bank.  Per item the four
+// waves split K (at most 8 K-blocks each) and meet in LDS; while an item's
+// MFMAs, reduction and epilogue run, the next item's tiles are in flight (two
+// register buffers, steady-state loads unconditional so the counted waits
+// stay exact).  The A operand (the token batch's e4m3 rows for this wave's
+// K-blocks) is loaded once and kept in registers for every item; its block
+// scales must be powers of two (they ride in the MFMA), the other scale kinds
+// take w13_decode_kernel.
+
+template <int NKB>
+struct W13Buf {
+  v4i w1[NKB], w3[NKB];
+  uint32_t s1[2], s3[2];  // packed e8m0 dwords (4 K-blocks each)
+  int u, ft;
+};
+
+// NKB = K-blocks per wave = D / 512 (compile-time, so no load is conditional).
+template <int NKB>
+__global__ __launch_bounds__(kDecThreads) void w13_stream_kernel(wz_moe_desc d, MoeWs ws, int T, int u_max) {
+  __shared__ float red[2][4 * 2 * 4 * kWave];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nl = lane & 15, g = lane >> 4;
+  const int D = d.dim, I = d.inter, E = d.n_experts;
+  const int a_kind = WZ_SCALE_UE8M0_F32;  // power-of-two scales (host-checked)
+  const int KB = 4 * NKB, KG = (KB + 3) / 4, FT = I / 16;
+  const int kb0 = wave * NKB;
+  const int n_act = min(ws.n_active[0], u_max);
+  const int N = n_act * FT;
+  if (int(blockIdx.x) < FT) {  // the shared expert's items run beside the routed stream
+    w13_shared_item(d, ws, T, blockIdx.x, red[0]);
+    return;
+  }
+  // grid-stride over items: at any moment the resident workgroups read one
+  // contiguous window of the bank (G consecutive items)
+  const int G = gridDim.x - FT;
+  const int i0 = blockIdx.x - FT;
+  if (i0 >= N) return;
+  // active-expert ids in LDS, so a tile address never waits on a global load
+  __shared__ int s_act[kMaxExperts];
+  for (int j = tid; j < n_act; j += kDecThreads) s_act[j] = clampi(ws.active[j], 0, E - 1);
+  __syncthreads();
+
+  v8i av[NKB];
+  int ae[NKB];
+  {
+    const uint8_t* arow = nl < T ? ws.xq + int64_t(nl) * D : nullptr;
+    const float* asrow = nl < T ? ws.xs + int64_t(nl) * (D / 128) : nullptr;
+#pragma unroll
+    for (int q = 0; q < NKB; ++q) {
+      const AOp a = a_from_fp8(arow, asrow, kb0 + q, g, a_kind);
+      av[q] = a.v;
+      ae[q] = a.se8;
+    }
+  }
+  const int kg0 = kb0 >> 2;
+
+  auto fetch = [&](W13Buf<NKB>& b, int item) {
+    b.u = item / FT;
+    b.ft = item % FT;
+    const int e = s_act[b.u];
+    const int64_t tile = int64_t(e) * FT + b.ft;
+    const uint8_t* wt = static_cast<const uint8_t*>(d.w13p) + (tile * KB + kb0) * 2048 + lane * 16;
+#pragma unroll
+    for (int q = 0; q < NKB; ++q) {
+      b.w1[q] = load16_nt(wt + q * 2048);
+      b.w3[q] = load16_nt(wt + q * 2048 + 1024);
+    }
+    const uint32_t* st = static_cast<const uint32_t*>(d.w13p_s) + tile * KG * 2 * 64 + lane;
+#pragma unroll
+    for (int q = 0; q < (NKB + 3) / 4; ++q) {
+      const int kg = min(kg0 + q, KG - 1);
+      b.s1[q] = st[(kg * 2 + 0) * 64];
+      b.s3[q] = st[(kg * 2 + 1) * 64];
+    }
+  };
+
+  auto process = [&](const W13Buf<NKB>& b, int par) {
+    int qrow[4] = {-1, -1, -1, -1};
+    float wrow[4] = {0.f, 0.f, 0.f, 0.f};
+    if (wave == 0) {  // epilogue rows of this item, fetched ahead of the MFMAs
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = g * 4 + i;
+        qrow[i] = t < T ? ws.umap[b.u * T + t] : -1;
+        wrow[i] = t < T ? ws.uwt[b.u * T + t] : 0.0f;
+      }
+    }
+    v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int q = 0; q < NKB; ++q) {
+      const int kk = kb0 + q, qi = (kk >> 2) - kg0, sh = 8 * (kk & 3);
+      const int e1 = int(((qi ? b.s1[1] : b.s1[0]) >> sh) & 0xFFu);
+      const int e3 = int(((qi ? b.s3[1] : b.s3[0]) >> sh) & 0xFFu);
+      const v8i w1 = v8i{b.w1[q][0], b.w1[q][1], b.w1[q][2], b.w1[q][3], 0, 0, 0, 0};
+      const v8i w3 = v8i{b.w3[q][0], b.w3[q][1], b.w3[q][2], b.w3[q][3], 0, 0, 0, 0};
+      acc[0] = mfma_scaled<kFmtFp8, kFmtFp4>(av[q], w1, acc[0], ae[q], e1);
+      acc[1] = mfma_scaled<kFmtFp8, kFmtFp4>(av[q], w3, acc[1], ae[q], e3);
+    }
+    float* r = red[par];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[((wave * 2 + m) * 4 + i) * kWave + lane] = acc[m][i];
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float gs = r[((0 * 2 + 0) * 4 + i) * kWave + lane], us = r[((0 * 2 + 1) * 4 + i) * kWave + lane];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+          gs += r[((w * 2 + 0) * 4 + i) * kWave + lane];
+          us += r[((w * 2 + 1) * 4 + i) * kWave + lane];
+        }
+        if (qrow[i] >= 0) {
+          const int t = g * 4 + i;
+          ws.h[(int64_t(b.u) * T + t) * I + b.ft * 16 + nl] = f32_to_bf16(wrow[i] * swiglu(gs, us, d.swiglu_limit));
+        }
+      }
+    }
+  };
+
+  W13Buf<NKB> b0, b1;
+  fetch(b0, i0);
+  int i = i0;
+  // steady state: the next item's fetch is always valid
+  for (; i + 2 * G < N; i += 2 * G) {
+    fetch(b1, i + G);
+    process(b0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(b0, i + 2 * G);
+    process(b1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // last one or two items
+  if (i + G < N) {
+    fetch(b1, i + G);
+    process(b0, 0);
+    process(b1, 1);
+  } else {
+    process(b0, 0);
+  }
+}
+
 __global__ __launch_bounds__(kDecThreads) void hquant_kernel(MoeWs ws, int T, int I, int u_max, bool pow2) {
   const int r = blockIdx.x, UT = u_max * T;
   const uint16_t* src;
@@ -621,8 +788,25 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
     if (int rc = check_launch("moe route")) return rc;
   }
   if (only < 0 || only == WZ_STAGE_W13) {
-    WZ_LAUNCH("moe_w13", stream, w13_decode_kernel, dim3(unsigned((u_max + 1) * (I / 16))), dim3(kDecThreads), 0,
-              *d, w, int(T), u_max);
+    const int nkb = D / 512;
+    if (D % 512 == 0 && (nkb == 1 || nkb == 2 || nkb == 4 || nkb == 8) && d->act_scale_kind != WZ_SCALE_F32) {
+      // blocks [0, I/16): the shared expert's items; then the persistent routed WGs
+      // routed WGs: one per CU, up to two when there are >= 8 items per WG to pipeline
+      const int64_t items = int64_t(u_max) * (I / 16), cus = cu_count();
+      const dim3 grid(unsigned(I / 16 + std::min<int64_t>(items, std::max<int64_t>(cus, std::min<int64_t>(2 * cus, items / 8)))));
+      if (nkb == 8) {
+        WZ_LAUNCH("moe_w13", stream, w13_stream_kernel<8>, grid, dim3(kDecThreads), 0, *d, w, int(T), u_max);
+      } else if (nkb == 4) {
+        WZ_LAUNCH("moe_w13", stream, w13_stream_kernel<4>, grid, dim3(kDecThreads), 0, *d, w, int(T), u_max);
+      } else if (nkb == 2) {
+        WZ_LAUNCH("moe_w13", stream, w13_stream_kernel<2>, grid, dim3(kDecThreads), 0, *d, w, int(T), u_max);
+      } else {
+        WZ_LAUNCH("moe_w13", stream, w13_stream_kernel<1>, grid, dim3(kDecThreads), 0, *d, w, int(T), u_max);
+      }
+    } else {
+      WZ_LAUNCH("moe_w13", stream, w13_decode_kernel, dim3(unsigned((u_max + 1) * (I / 16))), dim3(kDecThreads), 0,
+                *d, w, int(T), u_max);
+    }
     if (int rc = check_launch("moe w13")) return rc;
   }
   if (only < 0 || only == WZ_STAGE_HQUANT) {
