@@ -187,8 +187,6 @@ def stage_times(layers, xs, outs, reps=20):
     T = xs[0][1].size(0)
     res = {}
     for name, st in STAGES:
-        if name == "combine" and T <= 16:
-            continue  # fused into w2 on the decode path
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for (moe, _), (_, x), out in zip(layers, xs, outs):

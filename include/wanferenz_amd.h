@@ -147,8 +147,8 @@ int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const int64_t* inpu
  * routing tables and intermediates), so a stage can be timed on its own or
  * captured alone in a graph.  Stages: WZ_STAGE_ROUTE (gate + top-k + permutation;
  * prefill also its M-tiles and act_quant(x)), WZ_STAGE_W13 (w1|w3 + SwiGLU, routed
- * and shared), WZ_STAGE_HQUANT (act_quant of h), WZ_STAGE_W2 (w2; for T <= 16 with
- * the weighted combine into y), WZ_STAGE_COMBINE (T > 16: the combine into y).
+ * and shared), WZ_STAGE_HQUANT (act_quant of h), WZ_STAGE_W2 (w2), WZ_STAGE_COMBINE
+ * (the weighted combine into y; a no-op where a decode shape fuses it into w2).
  * No counterpart in the reference (its benchmarks time whole calls). */
 #define WZ_STAGE_ROUTE 0
 #define WZ_STAGE_W13 1

@@ -295,11 +295,11 @@ def test_v4_prefill_parity(v4_layer, T, bias):
           f"rel {rel_d:.2e} cos {cos_d:.8f} bit-equal {np.mean(got == dec):.4f}; near-ties {near}")
 
 
-@pytest.mark.parametrize("T", [4, 40])
-def test_replay_stages_reproduce_the_forward(gpu, T):
+@pytest.mark.parametrize("name,T", [("top6_t8", 4), ("toy_t4", 4), ("toy_t4", 16), ("top6_t8", 40)])
+def test_replay_stages_reproduce_the_forward(gpu, name, T):
     """wz_moe_replay_stage re-runs a stage of the last forward on its workspace state."""
     import dataclasses
-    case = dataclasses.replace(CASES["top6_t8"], T=T)
+    case = dataclasses.replace(CASES[name], T=T)
     inp = make_inputs(case)
     moe = upload_case(case, inp, gpu)
     x = bf16_tensor(inp.x, gpu)
@@ -310,6 +310,7 @@ def test_replay_stages_reproduce_the_forward(gpu, T):
     torch.cuda.synchronize()
     assert torch.equal(out, y)
     out.zero_()
-    moe.replay_stage(x, N.WZ_STAGE_W2 if T <= 16 else N.WZ_STAGE_COMBINE, out)
+    moe.replay_stage(x, N.WZ_STAGE_W2, out)
+    moe.replay_stage(x, N.WZ_STAGE_COMBINE, out)
     torch.cuda.synchronize()
     assert torch.equal(out, y)

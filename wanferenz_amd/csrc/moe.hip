@@ -302,12 +302,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  int prev_e = -1;
   for (int j = 0; j < k; ++j) {
     const int p = ps[j];
-    const int pe = ws.idx[int64_t(clampi(ws.perm_token[p], 0, gridDim.y - 1)) * k + clampi(ws.perm_slot[p], 0, k - 1)];
-    if (pe == prev_e) continue;  // repeated expert of a hash-routed token: counted once
-    prev_e = pe;
+    // a repeated expert of a hash-routed token counts once: its last slot (the row
+    // a decode step computes; architecture.py:790 index_put keeps the last write)
+    if (j + 1 < k) {
+      const int pn = ps[j + 1];
+      const int pe = ws.idx[int64_t(clampi(ws.perm_token[p], 0, gridDim.y - 1)) * k + clampi(ws.perm_slot[p], 0, k - 1)];
+      const int ne = ws.idx[int64_t(clampi(ws.perm_token[pn], 0, gridDim.y - 1)) * k + clampi(ws.perm_slot[pn], 0, k - 1)];
+      if (pe == ne) continue;
+    }
     const v4i v = load16(ws.out2 + int64_t(p) * D + c * 8);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -324,6 +328,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int
     o[i] = uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
   }
   *reinterpret_cast<v4i*>(y + int64_t(t) * D + c * 8) = v4i{int(o[0]), int(o[1]), int(o[2]), int(o[3])};
+}
+
+// y = combine of the routed rows in out2 and the shared rows in sh_out.
+int launch_combine(const MoeWs& w, int64_t T, int k, int D, void* y, hipStream_t stream) {
+  WZ_LAUNCH("moe_combine", stream, combine_kernel, dim3(unsigned((D / 8 + 255) / 256), unsigned(T)), dim3(256), 0,
+            w, k, D, static_cast<uint16_t*>(y));
+  return check_launch("moe combine");
 }
 
 __global__ void export_routing_kernel(const MoeWs ws, int P, float* __restrict__ w_out,
@@ -471,9 +482,7 @@ extern "C" int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const in
   const int k = d->topk, D = d->dim;
   const int64_t P = T * k;
   if (int rc = launch_prefill_experts(d, w, x_bf16, T, stream, -1)) return rc;
-  WZ_LAUNCH("moe_combine", stream, combine_kernel, dim3(unsigned((D / 8 + 255) / 256), unsigned(T)), dim3(256),
-                     0, w, k, D, static_cast<uint16_t*>(y_bf16));
-  if (int rc = check_launch("moe combine")) return rc;
+  if (int rc = launch_combine(w, T, k, D, y_bf16, stream)) return rc;
   if (weights_out || indices_out) {
     WZ_LAUNCH("moe_export", stream, export_routing_kernel, dim3(unsigned((P + 255) / 256)), dim3(256), 0, w,
                        int(P), weights_out, indices_out);
@@ -491,18 +500,10 @@ extern "C" int wz_moe_replay_stage(const wz_moe_desc* d, const void* x_bf16, con
   if (T == 0) return WZ_OK;
   if (!x_bf16 || !y_bf16) return set_error(WZ_EINVAL, "moe_replay_stage: null x or y");
   const MoeWs w = moe_ws_layout(d, T, static_cast<uint8_t*>(ws));
-  if (T <= kDecodeMaxT) {
-    if (stage == WZ_STAGE_COMBINE) return WZ_OK;  // fused into WZ_STAGE_W2
-    return launch_decode(d, w, x_bf16, input_ids, T, y_bf16, stream, stage);
-  }
+  if (T <= kDecodeMaxT) return launch_decode(d, w, x_bf16, input_ids, T, y_bf16, stream, stage);
   if (stage == WZ_STAGE_ROUTE) {
     if (int rc = launch_routing(d, w, x_bf16, input_ids, T, stream)) return rc;
   }
-  if (stage == WZ_STAGE_COMBINE) {
-    const int k = d->topk, D = d->dim;
-    WZ_LAUNCH("moe_combine", stream, combine_kernel, dim3(unsigned((D / 8 + 255) / 256), unsigned(T)), dim3(256), 0,
-              w, k, D, static_cast<uint16_t*>(y_bf16));
-    return check_launch("moe combine");
-  }
+  if (stage == WZ_STAGE_COMBINE) return launch_combine(w, T, d->topk, d->dim, y_bf16, stream);
   return launch_prefill_experts(d, w, x_bf16, T, stream, stage);
 }
