@@ -174,6 +174,18 @@ __device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t n) {
 }
 
 __device__ __forceinline__ void release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+
+// Device-scope relaxed accesses: performed at the device coherence point, so a
+// value stored this way by one workgroup, with the storing wave's stores
+// drained (vm_drain) before it signals, is seen by another workgroup's
+// load_agent without an L2 writeback / invalidate.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0); }
 __device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
 
 }  // namespace wz

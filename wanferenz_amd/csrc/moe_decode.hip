@@ -34,7 +34,7 @@
 namespace wz {
 
 constexpr int kDecThreads = 256;
-constexpr int kRouteWaves = 16;                 // one wave per decode token in the routing phase
+constexpr int kRouteWaves = 8;                  // waves of a route-launch workgroup
 constexpr int kRouteThreads_ = kRouteWaves * 64;
 
 __device__ __forceinline__ v8i pk_fp4(const uint8_t* tile, int lane) {
@@ -104,17 +104,24 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
   for (int t = wave; t < T; t += kRouteWaves) {
     float sv[kSlots];
     uint32_t key[kSlots];
+    float raw[kSlots], rawb[kSlots];
+    const bool smax = d.score_func == WZ_SCORE_SOFTMAX;
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int e = lane + 64 * i;
+      raw[i] = e < E ? load_agent(ws.scores + int64_t(t) * E + e) : 0.0f;
+      rawb[i] = (e < E && !smax) ? load_agent(ws.biased + int64_t(t) * E + e) : 0.0f;
+    }
     double mx = -1e300, sum = 0.0;
-    if (d.score_func == WZ_SCORE_SOFTMAX) {
-      const float* a = ws.scores + int64_t(t) * E;
+    if (smax) {
 #pragma unroll
       for (int i = 0; i < kSlots; ++i)
-        if (lane + 64 * i < E) mx = fmax(mx, double(a[lane + 64 * i]));
+        if (lane + 64 * i < E) mx = fmax(mx, double(raw[i]));
 #pragma unroll
       for (int m = 32; m >= 1; m >>= 1) mx = fmax(mx, __shfl_xor(mx, m, kWave));
 #pragma unroll
       for (int i = 0; i < kSlots; ++i)
-        if (lane + 64 * i < E) sum += exp(double(a[lane + 64 * i]) - mx);
+        if (lane + 64 * i < E) sum += exp(double(raw[i]) - mx);
 #pragma unroll
       for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, kWave);
     }
@@ -124,12 +131,12 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       sv[i] = 0.0f;
       key[i] = 0u;
       if (e < E) {
-        if (d.score_func == WZ_SCORE_SOFTMAX) {
-          sv[i] = float(exp(double(ws.scores[int64_t(t) * E + e]) - mx) / sum);
+        if (smax) {
+          sv[i] = float(exp(double(raw[i]) - mx) / sum);
           key[i] = f32_key((d.tid2eid == nullptr && d.gate_bias != nullptr) ? sv[i] + d.gate_bias[e] : sv[i]);
         } else {
-          sv[i] = ws.scores[int64_t(t) * E + e];
-          key[i] = f32_key(ws.biased[int64_t(t) * E + e]);
+          sv[i] = raw[i];
+          key[i] = f32_key(rawb[i]);
         }
       }
     }
@@ -330,6 +337,68 @@ __device__ void quant_row(uint8_t* __restrict__ q, float* __restrict__ s, const 
   }
 }
 
+// Shared expert w1 / w3 for features 16 b .. 16 b + 15 with act_quant(x) fused
+// into the A-operand load (this runs in the route launch, before xq exists);
+// the four waves of `group` split K and meet in LDS.
+__device__ __forceinline__ void w13_shared_item_bf16(const wz_moe_desc& d, const MoeWs& ws,
+                                                     const uint16_t* __restrict__ x, int T, int b, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nl = lane & 15, g = lane >> 4;
+  const int D = d.dim, I = d.inter;
+  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
+  const int KB = D / 128;
+  const int kb0 = (wave * KB) / kRouteWaves, kb1 = ((wave + 1) * KB) / kRouteWaves;
+  const uint16_t* xrow = nl < T ? x + int64_t(nl) * D : nullptr;
+  const int f0 = b * 16;
+  const uint8_t* tiles = static_cast<const uint8_t*>(d.sh13p) + int64_t(b) * KB * 4096;
+  const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  const int64_t sbase = int64_t(f0 >> 7) * KB;
+  v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  for (int kb = kb0; kb < kb1; kb += 4) {
+    v8i w[2][4];
+    int se[2][4];
+    float sf[2][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (kb + q < kb1) {
+        w[0][q] = pk_fp8(tiles + int64_t(kb + q) * 4096, lane);
+        w[1][q] = pk_fp8(tiles + int64_t(kb + q) * 4096 + 2048, lane);
+        fp8_wscale(d.sh_w1_s, sbase + kb + q, d.shared_w_scale_kind, se[0][q], sf[0][q]);
+        fp8_wscale(d.sh_w3_s, sbase + kb + q, d.shared_w_scale_kind, se[1][q], sf[1][q]);
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (kb + q < kb1) {
+        const AOp a = a_from_bf16(xrow, kb + q, g, a_pow2);
+        mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], a_pow2, bp, lane);
+        mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], a_pow2, bp, lane);
+      }
+  }
+  // red: [kRouteWaves][2][4][64] floats; partials summed in wave order
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[((wave * 2 + m) * 4 + i) * kWave + lane] = acc[m][i];
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float gs = red[((0 * 2 + 0) * 4 + i) * kWave + lane], us = red[((0 * 2 + 1) * 4 + i) * kWave + lane];
+#pragma unroll
+      for (int w = 1; w < kRouteWaves; ++w) {
+        gs += red[((w * 2 + 0) * 4 + i) * kWave + lane];
+        us += red[((w * 2 + 1) * 4 + i) * kWave + lane];
+      }
+      const int t = g * 4 + i;
+      if (t < T) ws.sh_h[int64_t(t) * I + f0 + nl] = f32_to_bf16(swiglu(gs, us, d.swiglu_limit));
+    }
+  }
+}
+
+// Blocks [0, n_gate): gate waves, one expert each over all T tokens, then the
+// last to arrive routes.  [n_gate, n_gate + T): act_quant of x.  The rest:
+// the shared expert's w1 / w3 items, one per block (its waves split K), which
+// do not depend on the routing and so stream while it runs.
 __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_desc d, MoeWs ws,
                                                                    const uint16_t* __restrict__ x,
                                                                    const int64_t* __restrict__ ids, int T,
@@ -339,108 +408,89 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
   const int D = d.dim, E = d.n_experts;
   const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
   int b = blockIdx.x;
-  if (b < n_gate * T) {
-    // ---- gate logit of one (expert, token) per wave; lane 0 applies the score
+  if (b < n_gate) {
+    // ---- gate logits of one expert for every token; lane 0 applies the score
     // function and the bias (the selection key) ----
-    const int e = (b % n_gate) * kRouteWaves + wave, t = b / n_gate;
+    const int e = b * kRouteWaves + wave;
     if (e < E) {
       const uint16_t* wr = static_cast<const uint16_t*>(d.gate_w) + int64_t(e) * D;
-      const uint16_t* xr = x + int64_t(t) * D;
       const int nc = D / 8;
-      double acc = 0.0;
+      double acc[kDecodeMaxT];
+#pragma unroll
+      for (int t = 0; t < kDecodeMaxT; ++t) acc[t] = 0.0;
 #pragma unroll 1
       for (int c0 = 0; c0 < nc; c0 += 64 * 8) {
-        v4i wv[8], xv[8];
+        v4i wv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int c = c0 + lane + 64 * i;
           wv[i] = c < nc ? load16(wr + c * 8) : v4i{0, 0, 0, 0};
-          xv[i] = c < nc ? load16(xr + c * 8) : v4i{0, 0, 0, 0};
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int t0 = 0; t0 < kDecodeMaxT; t0 += 2) {
+          if (t0 < T) {
+            v4i xv[2][8];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc += double(bf16lo(uint32_t(xv[i][j])) * bf16lo(uint32_t(wv[i][j])));
-            acc += double(bf16hi(uint32_t(xv[i][j])) * bf16hi(uint32_t(wv[i][j])));
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                const int c = c0 + lane + 64 * i;
+                xv[j][i] = (t0 + j < T && c < nc) ? load16(x + int64_t(t0 + j) * D + c * 8) : v4i{0, 0, 0, 0};
+              }
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+              for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  acc[t0 + j] += double(bf16lo(uint32_t(xv[j][i][q])) * bf16lo(uint32_t(wv[i][q])));
+                  acc[t0 + j] += double(bf16hi(uint32_t(xv[j][i][q])) * bf16hi(uint32_t(wv[i][q])));
+                }
           }
+        }
       }
 #pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, kWave);
-      if (lane == 0) {
-        const int64_t o = int64_t(t) * E + e;
-        const float logit = float(acc);
-        if (d.score_func == WZ_SCORE_SOFTMAX) {
-          ws.scores[o] = logit;
-        } else {
-          const float sc = score_of(logit, d.score_func);
-          ws.scores[o] = sc;
-          ws.biased[o] = (d.tid2eid == nullptr && d.gate_bias != nullptr) ? sc + d.gate_bias[e] : sc;
+      for (int t = 0; t < kDecodeMaxT; ++t) {
+        if (t < T) {
+          double v = acc[t];
+#pragma unroll
+          for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+          if (lane == 0) {
+            const int64_t o = int64_t(t) * E + e;
+            const float logit = float(v);
+            if (d.score_func == WZ_SCORE_SOFTMAX) {
+              store_agent(ws.scores + o, logit);
+            } else {
+              const float sc = score_of(logit, d.score_func);
+              store_agent(ws.scores + o, sc);
+              store_agent(ws.biased + o,
+                          (d.tid2eid == nullptr && d.gate_bias != nullptr) ? sc + d.gate_bias[e] : sc);
+            }
+          }
         }
       }
     }
-    release_agent();
+    vm_drain();  // this wave's score stores are performed before the arrival below
     __syncthreads();
-    if (tid == 0) s_last = arrive_last(&ws.counters[0], uint32_t(n_gate * T)) ? 1 : 0;
+    if (tid == 0) s_last = arrive_last(&ws.counters[0], uint32_t(n_gate)) ? 1 : 0;
     __syncthreads();
     if (!s_last) return;
-    acquire_agent();
-    route_last(d, ws, ids, T, u_max);
+    route_last(d, ws, ids, T, u_max);  // reads the scores with load_agent
     return;
   }
-  b -= n_gate * T;
-  if (b < T) quant_row(ws.xq + int64_t(b) * D, ws.xs + int64_t(b) * (D / 128), x + int64_t(b) * D, D, a_pow2);
+  b -= n_gate;
+  if (b < T) {
+    quant_row(ws.xq + int64_t(b) * D, ws.xs + int64_t(b) * (D / 128), x + int64_t(b) * D, D, a_pow2);
+    return;
+  }
+  b -= T;
+  {
+    __shared__ float red[kRouteWaves * 2 * 4 * kWave];
+    w13_shared_item_bf16(d, ws, x, T, b, red);
+  }
 }
 
 // -------------------------------------------------------------------- w13 ---
-
-// Shared expert w1 / w3 (FP8, packed) for features 16 b .. 16 b + 15, all T
-// tokens; the four waves split K and meet in LDS (red: 4 x 2 x 4 x 64 floats).
-__device__ __forceinline__ void w13_shared_item(const wz_moe_desc& d, const MoeWs& ws, int T, int b, float* red) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nl = lane & 15, g = lane >> 4;
-  const int D = d.dim, I = d.inter;
-  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
-  const int a_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
-  const int KB = D / 128;
-  const int kb0 = (wave * KB) / 4, kb1 = ((wave + 1) * KB) / 4;
-  const uint8_t* arow = nl < T ? ws.xq + int64_t(nl) * D : nullptr;
-  const float* asrow = nl < T ? ws.xs + int64_t(nl) * (D / 128) : nullptr;
-  v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  // ---- shared expert w1 / w3 (FP8, packed) for features f0..f0+15 ----
-  const int f0 = b * 16;
-  const uint8_t* tiles = static_cast<const uint8_t*>(d.sh13p) + int64_t(b) * KB * 4096;
-  const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
-  const int64_t sbase = int64_t(f0 >> 7) * KB;
-  for (int kb = kb0; kb < kb1; kb += 8) {  // 8 K-blocks (32 KB per wave) in flight at once
-    v8i w[2][8];
-    int se[2][8];
-    float sf[2][8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-      if (kb + q < kb1) {
-        w[0][q] = pk_fp8(tiles + int64_t(kb + q) * 4096, lane);
-        w[1][q] = pk_fp8(tiles + int64_t(kb + q) * 4096 + 2048, lane);
-        fp8_wscale(d.sh_w1_s, sbase + kb + q, d.shared_w_scale_kind, se[0][q], sf[0][q]);
-        fp8_wscale(d.sh_w3_s, sbase + kb + q, d.shared_w_scale_kind, se[1][q], sf[1][q]);
-      }
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-      if (kb + q < kb1) {
-        const AOp a = a_from_fp8(arow, asrow, kb + q, g, a_kind);
-        mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], a_pow2, bp, lane);
-        mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], a_pow2, bp, lane);
-      }
-  }
-  reduce_waves<2>(acc, red, wave, lane);
-  if (wave == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = g * 4 + i;
-      if (t < T) ws.sh_h[int64_t(t) * I + f0 + nl] = f32_to_bf16(swiglu(acc[0][i], acc[1][i], d.swiglu_limit));
-    }
-  }
-}
 
 __global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, MoeWs ws, int T, int u_max) {
   __shared__ float red[4 * 2 * 4 * kWave];
@@ -455,12 +505,7 @@ __global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, 
   const uint8_t* arow = nl < T ? ws.xq + int64_t(nl) * D : nullptr;
   const float* asrow = nl < T ? ws.xs + int64_t(nl) * (D / 128) : nullptr;
   v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  int b = blockIdx.x;
-  if (b < FT) {
-    w13_shared_item(d, ws, T, b, red);
-    return;
-  }
-  b -= FT;
+  const int b = blockIdx.x;
   // ---- routed expert: MXFP4 w1 / w3 for features ft*16 .. +15 ----
   const int u = b / FT, ft = b % FT;
   if (u >= min(ws.n_active[0], u_max)) return;
@@ -555,14 +600,10 @@ __global__ __launch_bounds__(kDecThreads) void w13_stream_kernel(wz_moe_desc d, 
   const int kb0 = wave * NKB;
   const int n_act = min(ws.n_active[0], u_max);
   const int N = n_act * FT;
-  if (int(blockIdx.x) < FT) {  // the shared expert's items run beside the routed stream
-    w13_shared_item(d, ws, T, blockIdx.x, red[0]);
-    return;
-  }
   // grid-stride over items: at any moment the resident workgroups read one
   // contiguous window of the bank (G consecutive items)
-  const int G = gridDim.x - FT;
-  const int i0 = blockIdx.x - FT;
+  const int G = gridDim.x;
+  const int i0 = blockIdx.x;
   if (i0 >= N) return;
   // active-expert ids in LDS, so a tile address never waits on a global load
   __shared__ int s_act[kMaxExperts];
@@ -783,17 +824,17 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
   if (!d->w13p || !d->w13p_s || !d->w2p || !d->w2p_s || !d->sh13p || !d->sh2p)
     return set_error(WZ_EINVAL, "moe decode: packed banks missing (wz_moe_pack)");
   if (only < 0 || only == WZ_STAGE_ROUTE) {
-    WZ_LAUNCH("moe_route", stream, route_decode_kernel, dim3(unsigned(n_gate * T + T)), dim3(kRouteThreads_), 0,
-              *d, w, static_cast<const uint16_t*>(x), ids, int(T), n_gate, u_max);
+    WZ_LAUNCH("moe_route", stream, route_decode_kernel, dim3(unsigned(n_gate + T + I / 16)), dim3(kRouteThreads_),
+              0, *d, w, static_cast<const uint16_t*>(x), ids, int(T), n_gate, u_max);
     if (int rc = check_launch("moe route")) return rc;
   }
   if (only < 0 || only == WZ_STAGE_W13) {
     const int nkb = D / 512;
     if (D % 512 == 0 && (nkb == 1 || nkb == 2 || nkb == 4 || nkb == 8) && d->act_scale_kind != WZ_SCALE_F32) {
-      // blocks [0, I/16): the shared expert's items; then the persistent routed WGs
       // routed WGs: one per CU, up to two when there are >= 8 items per WG to pipeline
+      // (the shared expert's w1 / w3 ran in the route launch)
       const int64_t items = int64_t(u_max) * (I / 16), cus = cu_count();
-      const dim3 grid(unsigned(I / 16 + std::min<int64_t>(items, std::max<int64_t>(cus, std::min<int64_t>(2 * cus, items / 8)))));
+      const dim3 grid(unsigned(std::min<int64_t>(items, std::max<int64_t>(cus, std::min<int64_t>(2 * cus, items / 8)))));
       if (nkb == 8) {
         WZ_LAUNCH("moe_w13", stream, w13_stream_kernel<8>, grid, dim3(kDecThreads), 0, *d, w, int(T), u_max);
       } else if (nkb == 4) {
@@ -804,7 +845,7 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
         WZ_LAUNCH("moe_w13", stream, w13_stream_kernel<1>, grid, dim3(kDecThreads), 0, *d, w, int(T), u_max);
       }
     } else {
-      WZ_LAUNCH("moe_w13", stream, w13_decode_kernel, dim3(unsigned((u_max + 1) * (I / 16))), dim3(kDecThreads), 0,
+      WZ_LAUNCH("moe_w13", stream, w13_decode_kernel, dim3(unsigned(u_max * (I / 16))), dim3(kDecThreads), 0,
                 *d, w, int(T), u_max);
     }
     if (int rc = check_launch("moe w13")) return rc;
