@@ -50,7 +50,6 @@ ROUTED_EXPERT_BYTES = 3 * (I * D // 2) + 3 * (I * D // 32)          # 13,369,344
 SHARED_BYTES = 3 * I * D + 3 * (I // 128) * (D // 128)              # 25,167,360
 GATE_BYTES = E * D * 2 + E * 4                                       # 2,098,176
 W13_ROUTED_BYTES = 2 * (I * D // 2) + 2 * (I * D // 32)             # 8,912,896
-W13_SHARED_BYTES = 2 * I * D + 2 * (I // 128) * (D // 128)          # 16,778,240
 
 
 def committed_traffic(T: int):
@@ -70,8 +69,10 @@ def layer_bytes(U: int, T: int) -> int:
 
 
 def w13_bytes(U: int, T: int) -> int:
-    # weights + x read (bf16) + h written (bf16, routed pairs and shared rows)
-    return U * W13_ROUTED_BYTES + W13_SHARED_BYTES + 2 * T * D + 2 * (T * K_TOP + T) * I
+    # the w13 launch streams the routed experts' w1|w3 (the shared expert's run in the
+    # route launch): weights + the quantized x read (e4m3 + fp32 scales) + h written
+    # (bf16, one row per routed (token, expert) pair)
+    return U * W13_ROUTED_BYTES + T * D + 4 * T * (D // 128) + 2 * T * K_TOP * I
 
 
 def parse():
@@ -341,7 +342,10 @@ def main():
         "hbm_frac_layer": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "kernel": "moe_w13", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": round(w13_b),
+                     "traffic": committed_traffic(T),
+                     "traffic_source": "profiles/hbm_traffic_pmc.md: rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                                       "per launch of the w13 kernel, copy-calibrated",
+                     "bytes_per_launch": round(w13_b),
                      "mean_us": round(w13_us, 2)},
         "stage_us": {k: round(v, 2) for k, v in kt.items()},
     }

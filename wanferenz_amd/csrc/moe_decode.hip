@@ -395,52 +395,56 @@ __device__ __forceinline__ void w13_shared_item_bf16(const wz_moe_desc& d, const
   }
 }
 
-// Blocks [0, n_gate): gate waves, one expert each over all T tokens, then the
-// last to arrive routes.  [n_gate, n_gate + T): act_quant of x.  The rest:
-// the shared expert's w1 / w3 items, one per block (its waves split K), which
-// do not depend on the routing and so stream while it runs.
+// Blocks [0, n_gate): gate waves.  An expert's logits for all T tokens are
+// split over `split` consecutive waves of one block (a K range each, fp64
+// partials summed in wave order), so the gate's fp64 work spreads over
+// n_gate = E * split / 8 CUs; then the last block to arrive routes.
+// [n_gate, n_gate + T): act_quant of x.  The rest: the shared expert's w1 / w3
+// items, one per block (its waves split K), which do not depend on the routing
+// and so stream while it runs.
 __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_desc d, MoeWs ws,
                                                                    const uint16_t* __restrict__ x,
                                                                    const int64_t* __restrict__ ids, int T,
-                                                                   int n_gate, int u_max) {
+                                                                   int n_gate, int split, int u_max) {
   __shared__ int s_last;
+  __shared__ double part[kRouteWaves][kDecodeMaxT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int D = d.dim, E = d.n_experts;
   const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
   int b = blockIdx.x;
   if (b < n_gate) {
-    // ---- gate logits of one expert for every token; lane 0 applies the score
-    // function and the bias (the selection key) ----
-    const int e = b * kRouteWaves + wave;
+    // ---- partial gate logits: expert e, 16-byte chunks [c0, c1) of D ----
+    const int task = b * kRouteWaves + wave;
+    const int e = task / split, sp = task % split;
+    const int nc = D / 8, c0 = (sp * nc) / split, c1 = ((sp + 1) * nc) / split;
+    double acc[kDecodeMaxT];
+#pragma unroll
+    for (int t = 0; t < kDecodeMaxT; ++t) acc[t] = 0.0;
     if (e < E) {
       const uint16_t* wr = static_cast<const uint16_t*>(d.gate_w) + int64_t(e) * D;
-      const int nc = D / 8;
-      double acc[kDecodeMaxT];
-#pragma unroll
-      for (int t = 0; t < kDecodeMaxT; ++t) acc[t] = 0.0;
 #pragma unroll 1
-      for (int c0 = 0; c0 < nc; c0 += 64 * 8) {
-        v4i wv[8];
+      for (int cb = c0; cb < c1; cb += 64 * 4) {
+        v4i wv[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int c = c0 + lane + 64 * i;
-          wv[i] = c < nc ? load16(wr + c * 8) : v4i{0, 0, 0, 0};
+        for (int i = 0; i < 4; ++i) {
+          const int c = cb + lane + 64 * i;
+          wv[i] = c < c1 ? load16(wr + c * 8) : v4i{0, 0, 0, 0};
         }
 #pragma unroll
         for (int t0 = 0; t0 < kDecodeMaxT; t0 += 2) {
           if (t0 < T) {
-            v4i xv[2][8];
+            v4i xv[2][4];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
-              for (int i = 0; i < 8; ++i) {
-                const int c = c0 + lane + 64 * i;
-                xv[j][i] = (t0 + j < T && c < nc) ? load16(x + int64_t(t0 + j) * D + c * 8) : v4i{0, 0, 0, 0};
+              for (int i = 0; i < 4; ++i) {
+                const int c = cb + lane + 64 * i;
+                xv[j][i] = (t0 + j < T && c < c1) ? load16(x + int64_t(t0 + j) * D + c * 8) : v4i{0, 0, 0, 0};
               }
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
-              for (int i = 0; i < 8; ++i)
+              for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                   acc[t0 + j] += double(bf16lo(uint32_t(xv[j][i][q])) * bf16lo(uint32_t(wv[i][q])));
@@ -449,24 +453,33 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
           }
         }
       }
+    }
 #pragma unroll
-      for (int t = 0; t < kDecodeMaxT; ++t) {
-        if (t < T) {
-          double v = acc[t];
+    for (int t = 0; t < kDecodeMaxT; ++t) {
+      if (t < T) {
+        double v = acc[t];
 #pragma unroll
-          for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-          if (lane == 0) {
-            const int64_t o = int64_t(t) * E + e;
-            const float logit = float(v);
-            if (d.score_func == WZ_SCORE_SOFTMAX) {
-              store_agent(ws.scores + o, logit);
-            } else {
-              const float sc = score_of(logit, d.score_func);
-              store_agent(ws.scores + o, sc);
-              store_agent(ws.biased + o,
-                          (d.tid2eid == nullptr && d.gate_bias != nullptr) ? sc + d.gate_bias[e] : sc);
-            }
-          }
+        for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+        if (lane == 0) part[wave][t] = v;
+      }
+    }
+    __syncthreads();
+    // ---- one thread per (expert of this block, token): partials in wave
+    // order, then the score function and the bias (the selection key) ----
+    const int epb = kRouteWaves / split;
+    if (tid < epb * T) {
+      const int es = tid / T, t = tid % T, e2 = b * epb + es;
+      if (e2 < E) {
+        double v = 0.0;
+        for (int s2 = 0; s2 < split; ++s2) v += part[es * split + s2][t];
+        const int64_t o = int64_t(t) * E + e2;
+        const float logit = float(v);
+        if (d.score_func == WZ_SCORE_SOFTMAX) {
+          store_agent(ws.scores + o, logit);
+        } else {
+          const float sc = score_of(logit, d.score_func);
+          store_agent(ws.scores + o, sc);
+          store_agent(ws.biased + o, (d.tid2eid == nullptr && d.gate_bias != nullptr) ? sc + d.gate_bias[e2] : sc);
         }
       }
     }
@@ -813,11 +826,203 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
   }
 }
 
+// ------------------------------------------------------- w2 (streamed) ---
+//
+// Routed experts' w2 on persistent workgroups, then combine_decode.
+// Work item = (active expert u, 64 output columns): four 16-column tiles over
+// the full K = I, 64 KB of packed MXFP4, contiguous in the packed bank.  A
+// workgroup takes a contiguous run of items, so consecutive items share the
+// expert and its A operand (the expert's e4m3 h rows for this wave's quarter
+// of K) stays in registers until the expert changes.  Each wave computes its
+// K quarter of all four tiles; the quarters meet in LDS; the bf16 expert
+// output goes to its pair row out2[q].  The next item's tiles are in flight
+// while the current one computes.  The shared expert's 64-column groups
+// (FP8) are the first D/64 workgroups and write sh_out.
+template <int NKB>
+struct W2Buf {
+  v4i w[4][NKB];
+  uint32_t s[4];  // packed e8m0 dword of each column tile (this wave's K quarter)
+  int u, g64;
+};
+
+__device__ __forceinline__ void w2_shared_group(const wz_moe_desc& d, const MoeWs& ws, int T, int u_max,
+                                                int grp) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nl = lane & 15, g = lane >> 4;
+  const int D = d.dim, I = d.inter, KB = I / 128;
+  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
+  const int a_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
+  const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  const int UT = u_max * T;
+  const uint8_t* arow = nl < T ? ws.hq + int64_t(UT + nl) * I : nullptr;
+  const float* asrow = nl < T ? ws.hs + int64_t(UT + nl) * (I / 128) : nullptr;
+  const int dt = grp * 4 + wave, n0 = dt * 16;  // wave w: column tile 4 grp + w, full K
+  const uint8_t* tiles = static_cast<const uint8_t*>(d.sh2p) + int64_t(dt) * KB * 2048;
+  const int64_t sbase = int64_t(n0 >> 7) * KB;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < KB; kb += 8) {
+    v8i w[8];
+    int se[8];
+    float sf[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (kb + q < KB) {
+        w[q] = pk_fp8(tiles + int64_t(kb + q) * 2048, lane);
+        fp8_wscale(d.sh_w2_s, sbase + kb + q, d.shared_w_scale_kind, se[q], sf[q]);
+      }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (kb + q < KB) {
+        const AOp a = a_from_fp8(arow, asrow, kb + q, g, a_kind);
+        mma_step<kFmtFp8, kFmtFp8>(acc, a, w[q], se[q], sf[q], a_pow2, bp, lane);
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = g * 4 + i;
+    if (t < T) ws.sh_out[int64_t(t) * D + n0 + nl] = f32_to_bf16(acc[i]);
+  }
+}
+
+// NKB = K-blocks per wave = I / 512 (compile time: no conditional loads).
+template <int NKB>
+__global__ __launch_bounds__(kDecThreads) void w2_stream_kernel(wz_moe_desc d, MoeWs ws, int T, int u_max) {
+  __shared__ float red[2][4 * 4 * 4 * kWave];
+  __shared__ int s_act[kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nl = lane & 15, g = lane >> 4;
+  const int D = d.dim, I = d.inter, E = d.n_experts, P = T * d.topk;
+  const int KB = 4 * NKB, KG = (KB + 3) / 4, DT = D / 16, NG = D / 64;
+  const int kb0 = wave * NKB, kg0 = kb0 >> 2;
+  if (int(blockIdx.x) < NG) {
+    w2_shared_group(d, ws, T, u_max, blockIdx.x);
+    return;
+  }
+  const int n_act = min(ws.n_active[0], u_max);
+  const int N = n_act * NG;
+  const int G = gridDim.x - NG, b = blockIdx.x - NG;
+  const int i0 = int((int64_t(b) * N) / G), i1 = int((int64_t(b + 1) * N) / G);
+  if (i0 >= i1) return;
+  for (int j = tid; j < n_act; j += kDecThreads) s_act[j] = clampi(ws.active[j], 0, E - 1);
+  __syncthreads();
+
+  auto fetch = [&](W2Buf<NKB>& bf, int item) {
+    bf.u = item / NG;
+    bf.g64 = item % NG;
+    const int e = s_act[bf.u];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int64_t tile = int64_t(e) * DT + bf.g64 * 4 + c;
+      const uint8_t* wt = static_cast<const uint8_t*>(d.w2p) + (tile * KB + kb0) * 1024 + lane * 16;
+#pragma unroll
+      for (int q = 0; q < NKB; ++q) bf.w[c][q] = load16_nt(wt + q * 1024);
+      bf.s[c] = static_cast<const uint32_t*>(d.w2p_s)[(tile * KG + kg0) * 64 + lane];
+    }
+  };
+
+  v8i av[NKB];
+  int ae[NKB];
+  int cur_u = -1;
+  auto load_a = [&](int u) {
+    const uint8_t* arow = nl < T ? ws.hq + int64_t(u * T + nl) * I : nullptr;
+    const float* asrow = nl < T ? ws.hs + int64_t(u * T + nl) * (I / 128) : nullptr;
+#pragma unroll
+    for (int q = 0; q < NKB; ++q) {
+      const AOp a = a_from_fp8(arow, asrow, kb0 + q, g, WZ_SCALE_UE8M0_F32);
+      av[q] = a.v;
+      ae[q] = a.se8;
+    }
+    cur_u = u;
+  };
+
+  auto process = [&](const W2Buf<NKB>& bf, int par) {
+    if (bf.u != cur_u) load_a(bf.u);
+    v4f acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int q = 0; q < NKB; ++q) {
+      const int sh = 8 * ((kb0 + q) & 3);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const v8i w = v8i{bf.w[c][q][0], bf.w[c][q][1], bf.w[c][q][2], bf.w[c][q][3], 0, 0, 0, 0};
+        acc[c] = mfma_scaled<kFmtFp8, kFmtFp4>(av[q], w, acc[c], ae[q], int((bf.s[c] >> sh) & 0xFFu));
+      }
+    }
+    float* r = red[par];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[((wave * 4 + c) * 4 + i) * kWave + lane] = acc[c][i];
+    __syncthreads();
+    // wave c finishes column tile c: K quarters summed in wave order, bf16 to the pair row
+    const int c = wave;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = g * 4 + i;
+      const int q = t < T ? ws.umap[bf.u * T + t] : -1;
+      float v = r[((0 * 4 + c) * 4 + i) * kWave + lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) v += r[((w * 4 + c) * 4 + i) * kWave + lane];
+      if (q >= 0 && q < P) ws.out2[int64_t(q) * D + (bf.g64 * 4 + c) * 16 + nl] = f32_to_bf16(v);
+    }
+  };
+
+  W2Buf<NKB> b0, b1;
+  fetch(b0, i0);
+  int i = i0;
+  for (; i + 2 < i1; i += 2) {
+    fetch(b1, i + 1);
+    process(b0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(b0, i + 2);
+    process(b1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (i + 1 < i1) {
+    fetch(b1, i + 1);
+    process(b0, 0);
+    process(b1, 1);
+  } else {
+    process(b0, 0);
+  }
+}
+
+// y[t] = bf16(sum over the token's distinct experts, ascending id, of out2 rows
+// + the shared row); tok_pos / tok_n come from the decode routing.
+__global__ __launch_bounds__(256) void combine_decode_kernel(MoeWs ws, int T, int k, int D,
+                                                             uint16_t* __restrict__ y) {
+  const int i = blockIdx.x * 256 + threadIdx.x;  // one 8-column chunk of one token
+  const int t = i / (D / 8), c = i % (D / 8);
+  if (t >= T) return;
+  const int P = T * k;
+  const int n = clampi(ws.tok_n[t], 0, k);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < n; ++j) {
+    const int q = clampi(ws.tok_pos[t * k + j], 0, P - 1);
+    const v4i v = load16(ws.out2 + int64_t(q) * D + c * 8);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      acc[2 * m] += bf16lo(uint32_t(v[m]));
+      acc[2 * m + 1] += bf16hi(uint32_t(v[m]));
+    }
+  }
+  const v4i sv = load16(ws.sh_out + int64_t(t) * D + c * 8);
+  uint32_t o[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    o[m] = uint32_t(f32_to_bf16(acc[2 * m] + bf16lo(uint32_t(sv[m])))) |
+           (uint32_t(f32_to_bf16(acc[2 * m + 1] + bf16hi(uint32_t(sv[m])))) << 16);
+  *reinterpret_cast<v4i*>(y + int64_t(t) * D + c * 8) = v4i{int(o[0]), int(o[1]), int(o[2]), int(o[3])};
+}
+
 // only < 0: the whole layer; otherwise the one stage WZ_STAGE_* (profiling replays).
 int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* ids, int64_t T,
                   void* y, hipStream_t stream, int only) {
   const int E = d->n_experts, k = d->topk, D = d->dim, I = d->inter;
-  const int n_gate = (E + kRouteWaves - 1) / kRouteWaves;
+  // K-split of the gate: the largest of 8, 4, 2, 1 waves per expert that keeps
+  // the gate within 128 workgroups (of 8 waves)
+  int split = 8;
+  while (split > 1 && int64_t(E) * split > 128 * kRouteWaves) split >>= 1;
+  const int n_gate = int((int64_t(E) * split + kRouteWaves - 1) / kRouteWaves);
   const int64_t P = T * k;
   const int u_max = int(P < E ? P : E);
   if (P > kMaxDecPairs) return set_error(WZ_EINVAL, "moe decode: T*topk=%lld exceeds %d", (long long)P, kMaxDecPairs);
@@ -825,7 +1030,7 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
     return set_error(WZ_EINVAL, "moe decode: packed banks missing (wz_moe_pack)");
   if (only < 0 || only == WZ_STAGE_ROUTE) {
     WZ_LAUNCH("moe_route", stream, route_decode_kernel, dim3(unsigned(n_gate + T + I / 16)), dim3(kRouteThreads_),
-              0, *d, w, static_cast<const uint16_t*>(x), ids, int(T), n_gate, u_max);
+              0, *d, w, static_cast<const uint16_t*>(x), ids, int(T), n_gate, split, u_max);
     if (int rc = check_launch("moe route")) return rc;
   }
   if (only < 0 || only == WZ_STAGE_W13) {
@@ -855,10 +1060,34 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
               I, u_max, d->act_scale_kind != WZ_SCALE_F32);
     if (int rc = check_launch("moe hquant")) return rc;
   }
+  // The streamed w2 plus its combine launch measured faster than
+  // w2_combine_kernel at T = 8 (45 vs 54 us at the V4 shape) and slower at
+  // T <= 4 (30 vs 29.5 us at T = 4, 21 vs 11 us at T = 1).
+  const int nkb2 = I / 512;
+  const bool w2s = T >= 6 && I % 512 == 0 && (nkb2 == 1 || nkb2 == 2 || nkb2 == 4) && D % 64 == 0 &&
+                   d->act_scale_kind != WZ_SCALE_F32;
   if (only < 0 || only == WZ_STAGE_W2) {
-    WZ_LAUNCH("moe_w2", stream, w2_combine_kernel, dim3(unsigned(D / 16)), dim3(kW2Threads), 0, *d, w, int(T),
-              u_max, static_cast<uint16_t*>(y));
+    if (w2s) {
+      const int64_t items = int64_t(u_max) * (D / 64), cus = cu_count();
+      const dim3 grid(unsigned(D / 64 + std::min<int64_t>(items, std::max<int64_t>(cus, std::min<int64_t>(2 * cus, items / 8)))));
+      if (nkb2 == 4) {
+        WZ_LAUNCH("moe_w2", stream, w2_stream_kernel<4>, grid, dim3(kDecThreads), 0, *d, w, int(T), u_max);
+      } else if (nkb2 == 2) {
+        WZ_LAUNCH("moe_w2", stream, w2_stream_kernel<2>, grid, dim3(kDecThreads), 0, *d, w, int(T), u_max);
+      } else {
+        WZ_LAUNCH("moe_w2", stream, w2_stream_kernel<1>, grid, dim3(kDecThreads), 0, *d, w, int(T), u_max);
+      }
+    } else {
+      WZ_LAUNCH("moe_w2", stream, w2_combine_kernel, dim3(unsigned(D / 16)), dim3(kW2Threads), 0, *d, w, int(T),
+                u_max, static_cast<uint16_t*>(y));
+    }
     if (int rc = check_launch("moe w2")) return rc;
+  }
+  if (w2s && (only < 0 || only == WZ_STAGE_COMBINE)) {
+    const int64_t n = T * (D / 8);
+    WZ_LAUNCH("moe_combine", stream, combine_decode_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, w,
+              int(T), k, D, static_cast<uint16_t*>(y));
+    if (int rc = check_launch("moe combine")) return rc;
   }
   return WZ_OK;
 }
