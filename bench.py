@@ -84,6 +84,10 @@ def parse():
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-stage", action="store_true",
+                    help="skip the decode stage (MoE + FP8 projections + norms, one graph per step)")
+    ap.add_argument("--no-gemv", action="store_true",
+                    help="skip the FP8 linear (dense projection shapes) measurement")
     ap.add_argument("--prefill", default="128,512,2048",
                     help="comma-separated prefill T values ('' to skip)")
     ap.add_argument("--prefill-layers", type=int, default=3)
@@ -214,6 +218,157 @@ def measure_T(layers, T, steps, warmup, dev, salt):
     total_bytes = sum(layer_bytes(Us[i % L], T) for i in range(steps))
     kt = stage_times(layers, xs, outs)
     return dict(T=T, secs=secs, wall=wall, Us=Us, total_bytes=total_bytes, kernels=kt, xs=xs)
+
+
+GEMV_SHAPES = ((4096, 1024), (1024, 4096), (4096, 4096), (16384, 4096))  # (N, K)
+GEMV_TS = (1, 4, 8, 128)
+GEMV_ROTATE_BYTES = 640 << 20   # weight copies per shape: more than the 256 MB Infinity Cache
+
+
+def gemv_bytes(N: int, K: int, T: int) -> int:
+    # e4m3 weight + fp32 128x128 block scales + bf16 x read + bf16 y written
+    return N * K + 4 * ((N + 127) // 128) * ((K + 127) // 128) + 2 * T * K + 2 * T * N
+
+
+def measure_gemv(dev, reps=5):
+    """FP8 block-scaled linear (act_quant fused) at the dense-projection shapes.
+
+    Weights: e4m3 codes with NaN codes replaced, fp32 128x128 block scales
+    U[0.5, 1.5) (the probe recipe of fp8_vector.py:185-232); per-token ue8m0
+    activation quantisation.  "packed": the weight relaid once into MFMA tiles
+    (kernels.PackedFp8Linear: GEMV at T <= 16, act_quant + tile GEMM above);
+    "rowmajor": the reference layout as fp8_gemm receives it (wz_fp8_linear).
+    Each shape rotates over enough weight copies (>= 640 MB) that every launch
+    streams its weight from HBM; one graph holds one launch per copy, HIP
+    events bracket ``reps`` replays.
+    """
+    import torch
+
+    from wanferenz_amd import _native as N
+    from wanferenz_amd import kernels, synth
+
+    def timed(launches):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            launches()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            launches()
+        g.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            g.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1000.0 / reps
+
+    res = {}
+    for Nn, K in GEMV_SHAPES:
+        R = max(2, -(-GEMV_ROTATE_BYTES // (Nn * K)))
+        pool = torch.empty(R, Nn, K, dtype=torch.uint8, device=dev)
+        synth.device_fill(pool, synth.stream_key(0, synth.S_FP8_W), synth.FILL_E4M3)
+        sc = torch.empty(R, (Nn + 127) // 128, (K + 127) // 128, dtype=torch.float32, device=dev)
+        synth.device_fill(sc, synth.stream_key(0, synth.S_FP8_W_S), synth.FILL_F32_UNIFORM, 0.5, 1.5)
+        lins = [kernels.PackedFp8Linear(pool[r].view(torch.float8_e4m3fn), sc[r], "ue8m0") for r in range(R)]
+        entry = {"weight_copies": R}
+        for layout in ("packed", "rowmajor"):
+            row = {}
+            for T in GEMV_TS:
+                xb = synth.normal_bf16(synth.stream_key(T, synth.S_FP8_X), (T, K), 1.0)
+                x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
+                y = torch.empty(T, Nn, dtype=torch.bfloat16, device=dev)
+                if layout == "packed":
+                    for lin in lins:
+                        lin.reserve(T)
+
+                    def launches():
+                        for lin in lins:
+                            lin(x, out=y)
+                else:
+                    def launches():
+                        st = N.stream_handle(dev)
+                        for r in range(R):
+                            N.call("wz_fp8_linear", N.ptr(x), N.ptr(pool[r]), N.ptr(sc[r]), N.ptr(y), T, Nn, K,
+                                   N.WZ_SCALE_UE8M0_F32, N.WZ_WSCALE_F32, st)
+                us = timed(launches) / R
+                gbs = gemv_bytes(Nn, K, T) / (us * 1e-6) / 1e9
+                row[str(T)] = {"us": round(us, 2), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                               "TFLOP_s": round(2.0 * T * Nn * K / (us * 1e-6) / 1e12, 2)}
+            entry[layout] = row
+        res[f"{Nn}x{K}"] = entry
+        del pool, sc, lins
+        torch.cuda.empty_cache()
+    return res
+
+
+STAGE_Q, STAGE_WIDE = 1024, 16384
+
+
+def stage_proj_bytes(T: int) -> int:
+    """FP8 projection bytes of one stage block: e4m3 weights + e8m0 128x128 scales +
+    bf16 activations in and out."""
+    tot = 0
+    for Nn, K in ((STAGE_Q, D), (D, STAGE_Q), (D, D), (STAGE_WIDE, D)):
+        tot += Nn * K + ((Nn + 127) // 128) * ((K + 127) // 128) + 2 * T * (K + Nn)
+    return tot
+
+
+def measure_stage(layers, dev, T=4, steps=256, warmup=16):
+    """The decode stage: every MoE layer as one block with its FP8 projections,
+    RMSNorms and residual adds, one hipGraph per step (wanferenz_amd/stage.py).
+
+    A fresh x ~ N(0, 1) per step (seed = step), staged into the graph's input
+    buffer by a device copy inside the timed region.  Bytes per step: each
+    block's projections + its MoE layer with the distinct experts U_b of that
+    block's routing, counted on eager steps over the same inputs.
+    """
+    import torch
+
+    from wanferenz_amd import stage, synth
+
+    blocks = [stage.synthetic_block(moe, D, STAGE_Q, STAGE_WIDE, seed=100 + l, device=dev)
+              for l, (moe, _) in enumerate(layers)]
+    st = stage.DecodeStage(blocks, T)
+    xs = np.stack([synth.normal_bf16(synth.stream_key(s, synth.S_X), (T, D), 1.0) for s in range(steps)])
+    xg = torch.from_numpy(xs.view(np.int16)).view(torch.bfloat16).to(dev)
+    # routing of every block on a sample of the steps' inputs (eager, outside the timing)
+    rts = [(torch.empty(T, K_TOP, dtype=torch.float32, device=dev),
+            torch.empty(T, K_TOP, dtype=torch.int64, device=dev)) for _ in blocks]
+    Us = []
+    for s in range(0, steps, max(1, steps // 16)):
+        st.step(xg[s], routing=rts)
+        torch.cuda.synchronize()
+        Us.append([len(set(ri.cpu().numpy().ravel().tolist())) for _, ri in rts])
+    U_mean = float(np.mean(Us))
+    st.capture()
+    for s in range(warmup):
+        st.replay(xg[s % steps])
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for s in range(steps):
+        st.replay(xg[s])
+    end.record()
+    torch.cuda.synchronize()
+    secs = start.elapsed_time(end) / 1000.0
+    nb = len(blocks)
+    step_bytes = nb * (stage_proj_bytes(T) + layer_bytes(1, T)) + (U_mean - 1) * nb * ROUTED_EXPERT_BYTES
+    us = secs / steps * 1e6
+    gbs = step_bytes / (us * 1e-6) / 1e9
+    del st, blocks
+    torch.cuda.empty_cache()
+    return {"workload": f"decode stage: {nb} blocks x (RMSNorm, FP8 projections {STAGE_Q}x{D}, {D}x{STAGE_Q}, "
+                        f"{D}x{D}, {STAGE_WIDE}x{D}, residual, RMSNorm, MoE layer, residual), T={T}, one hipGraph "
+                        f"per step, fresh x per step",
+            "T": T, "blocks": nb, "steps": steps, "us_per_step": round(us, 1),
+            "us_per_block": round(us / nb, 2), "tokens_per_s": round(T * steps / secs, 1),
+            "mean_distinct_experts": round(U_mean, 2), "bytes_per_step": int(step_bytes),
+            "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def prefill_flops(T: int) -> float:
@@ -363,6 +518,10 @@ def main():
     if args.prefill:
         Ts = [int(t) for t in args.prefill.split(",") if t]
         out["prefill"] = measure_prefill(layers[:max(1, args.prefill_layers)], Ts, dev)
+    if not args.no_gemv:
+        out["fp8_gemv"] = measure_gemv(dev)
+    if not args.no_stage:
+        out["decode_stage"] = measure_stage(layers, dev, T=args.T)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(layers, cfg, T, dev)
     print(json.dumps(out), flush=True)

@@ -74,6 +74,22 @@ int wz_fp8_linear(const void* x_bf16, const void* w_e4m3, const void* w_s, void*
                   int64_t M, int64_t N, int64_t K, int act_scale_kind, int w_scale_kind,
                   hipStream_t stream);
 
+/* FP8 linear on a packed weight.  wz_fp8_pack relays W e4m3 [N, K] (N % 16 == 0,
+ * K % 128 == 0) once into MFMA-ready 16-row x 128-K tiles, [N/16][K/128][2][1 KB]
+ * (N*K bytes), the load-time relayout the reference does for its FP8 decode GEMV
+ * (fp8_vector.py:316-351 _lay_shared).  wz_fp8_linear_packed then computes
+ * y[M,N] bf16 = linear(x, w) with act_quant fused — architecture.py:121-132
+ * (act_quant + fp8_gemm, reference.py:117-146, 292-311); w_s [ceil(N/128), K/128]
+ * float32 or e8m0 (w_scale_kind); act_scale_kind selects the activation scale rule
+ * (WZ_SCALE_F32: amax/448, otherwise the power-of-two ue8m0 rule).  M <= 16 with
+ * K in {1024, 2048, 4096} needs no workspace; otherwise ws must hold
+ * wz_fp8_linear_workspace_bytes(M, K) bytes (the quantised x). */
+int wz_fp8_pack(const void* w_e4m3, int64_t N, int64_t K, void* packed, hipStream_t stream);
+size_t wz_fp8_linear_workspace_bytes(int64_t M, int64_t K);
+int wz_fp8_linear_packed(const void* x_bf16, const void* w_packed, const void* w_s, void* y_bf16,
+                         int64_t M, int64_t N, int64_t K, int act_scale_kind, int w_scale_kind,
+                         void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* fp4_gemm: C[M,N] bf16 = (a * a_s) @ (e2m1(w) * w_s)^T, weight scale e8m0 per 32 K.
  * Replaces fp4_gemm(a, a_s, b, b_s, scale_dtype) — reference.py:572-591 / torch_ops.py:102-108.
  * a_e4m3 [M,K], a_s [M,K/128], w_fp4x2 [N,K/2], w_s_e8m0 [N,K/32]. */

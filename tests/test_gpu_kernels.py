@@ -223,3 +223,116 @@ def test_fp4_gemm_k_mapping(gpu):
         if cols != [5] or kk != k:
             bad.append((k, kk, cols))
     assert not bad, f"k -> (k', cols): {bad}"
+
+
+@pytest.mark.parametrize("T,D", [(1, 4096), (4, 4096), (37, 1024), (3, 7168)])
+def test_rms_norm_matches_oracle(gpu, T, D):
+    """RMSNorm (architecture.py:217-230) vs the oracle: the fp32 sum of squares runs in
+    a different order, so outputs may differ by one bf16 ulp where the fp32 product
+    lands next to a rounding boundary; nearly all elements are bit-equal."""
+    xb = _x(11 + T, T, D, 3.0)
+    wgt = synth.fill_f32_uniform(synth.stream_key(12, synth.S_FP8_X), 0, D, 0.5, 1.5)
+    y = kernels.rms_norm(bf16_tensor(xb, gpu).view(T, D), f32_tensor(wgt, gpu), 1e-6)
+    torch.cuda.synchronize()
+    got = f32_of_bf16(y)
+    ref = om.rmsnorm(from_bf16_bits(xb).reshape(T, D), wgt, 1e-6)
+    rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert rel.max() <= 2.0 ** -7, rel.max()          # at most one bf16 ulp
+    assert (got == ref).mean() >= 0.99
+
+
+def test_rms_norm_closed_forms(gpu):
+    """An all-zero row gives zeros (rsqrt(eps) * 0); a constant row of +-c with unit
+    weight gives c / sqrt(c^2 + eps) = 1 - O(1e-7), which rounds to exactly +-1 in bf16."""
+    from oracle.numerics import bf16_bits
+
+    D = 2048
+    xf = np.zeros((4, D), np.float32)
+    xf[1] = 0.5
+    xf[2] = -3.0
+    xf[3, : D // 2] = 2.0
+    xf[3, D // 2:] = -2.0
+    y = kernels.rms_norm(bf16_tensor(bf16_bits(xf), gpu), f32_tensor(np.ones(D, np.float32), gpu))
+    torch.cuda.synchronize()
+    got = f32_of_bf16(y)
+    assert not got[0].any()
+    assert np.all(got[1] == 1.0) and np.all(got[2] == -1.0)
+    assert np.all(got[3, : D // 2] == 1.0) and np.all(got[3, D // 2:] == -1.0)
+
+
+def test_add_bf16_is_one_rounding(gpu):
+    """a + b as one IEEE fp32 add (round to nearest even) and one bf16 rounding, the
+    same two steps numpy's float32 add and the oracle's bf16_round take: bit-equal."""
+    n = 4096 * 5
+    a = _x(31, 1, n)
+    b = _x(32, 1, n)
+    out = kernels.add(bf16_tensor(a, gpu), bf16_tensor(b, gpu))
+    torch.cuda.synchronize()
+    from oracle.numerics import bf16_round
+
+    ref = bf16_round((from_bf16_bits(a) + from_bf16_bits(b)).astype(np.float32))
+    assert np.array_equal(f32_of_bf16(out).ravel(), ref.ravel())
+
+
+@pytest.mark.parametrize("w_fp32", [True, False])
+@pytest.mark.parametrize("N,K", [(4096, 1024), (1024, 4096), (4096, 4096), (16384, 4096)])
+@pytest.mark.parametrize("M", [1, 8, 128])
+def test_fp8_linear_projection_shapes(gpu, w_fp32, N, K, M):
+    """fp8_linear (act_quant fused) at the dense projection shapes, weights generated on
+    the device by the same hash stream as the host generator; the oracle checks three
+    128-row weight blocks (first, middle, last) of every output."""
+    w = torch.empty(N, K, dtype=torch.uint8, device=gpu)
+    synth.device_fill(w, synth.stream_key(N + K, synth.S_FP8_W), synth.FILL_E4M3)
+    nb, kb = N // 128, K // 128
+    if w_fp32:
+        ws = torch.empty(nb, kb, dtype=torch.float32, device=gpu)
+        synth.device_fill(ws, synth.stream_key(N + K, synth.S_FP8_W_S), synth.FILL_F32_UNIFORM, 0.5, 1.5)
+    else:
+        ws = torch.empty(nb, kb, dtype=torch.uint8, device=gpu)
+        synth.device_fill(ws, synth.stream_key(N + K, synth.S_FP8_W_S), synth.FILL_E8M0, 112, 116)
+        ws = ws.view(torch.float8_e8m0fnu)
+    xb = _x(M * 7 + K, M, K)
+    y = kernels.fp8_linear(bf16_tensor(xb, gpu), w.view(torch.float8_e4m3fn), ws, "ue8m0", torch.float32)
+    torch.cuda.synchronize()
+    got = f32_of_bf16(y)
+    blocks = sorted({0, nb // 2, nb - 1})
+    rows = np.concatenate([np.arange(b * 128, b * 128 + 128) for b in blocks])
+    w_sub = bytes8(w[torch.from_numpy(rows).to(gpu)])
+    ws_sub = ws[blocks].cpu()
+    ws_sub = ws_sub.numpy() if w_fp32 else e8m0_decode(ws_sub.view(torch.uint8).numpy())
+    rq, rs = om.act_quant(from_bf16_bits(xb), 128, True)
+    ref = om.fp8_gemm(rq, rs, w_sub, ws_sub)
+    rel, cos = _close(got[:, rows], ref)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    # the packed-weight path (GEMV at M <= 16, act_quant + tile GEMM above)
+    lin = kernels.PackedFp8Linear(w.view(torch.float8_e4m3fn), ws, "ue8m0")
+    y2 = lin(bf16_tensor(xb, gpu))
+    torch.cuda.synchronize()
+    rel2, cos2 = _close(f32_of_bf16(y2)[:, rows], ref)
+    assert rel2 <= TOL_REL and cos2 >= TOL_COS, (rel2, cos2)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 4096), (5, 512, 1024), (16, 128, 2048), (40, 256, 4096),
+                                   (3, 128, 1536)])
+def test_fp8_linear_packed_exact(gpu, M, N, K):
+    """x in {0, +-0.5, +-1, +-1.5} with one 2.0 per 128-block quantises exactly (ue8m0
+    scale 2^-7), weight codes of the same values with unit scales: every partial sum
+    is exact in fp32, so the packed linear must equal the oracle bit for bit, on the
+    GEMV path (M <= 16) and the quantise + tile GEMM path (M = 40, K = 1536)."""
+    from oracle.numerics import bf16_bits
+
+    vals = np.array([0.0, 0.5, -0.5, 1.0, -1.0, 1.5, -1.5], np.float32)
+    d = synth.draws(synth.stream_key(M * N + K, 98), 0, M * K)
+    xf = vals[(d % np.uint64(len(vals))).astype(np.int64)].reshape(M, K)
+    xf[:, ::128] = 2.0
+    codes = [0x00, 0x30, 0xB0, 0x38, 0xB8, 0x3C, 0xBC, 0x40, 0xC0]
+    w = _exact_codes(N * K + 3, N * K, codes).reshape(N, K)
+    ws = np.full(((N + 127) // 128, K // 128), 127, np.uint8)
+    wt = u8_tensor(w, gpu, torch.float8_e4m3fn)
+    wst = u8_tensor(ws, gpu, torch.float8_e8m0fnu)
+    lin = kernels.PackedFp8Linear(wt, wst, "ue8m0")
+    y = lin(bf16_tensor(bf16_bits(xf), gpu))
+    torch.cuda.synchronize()
+    rq, rs = om.act_quant(xf, 128, True)
+    ref = om.fp8_gemm(rq, rs, w, e8m0_decode(ws))
+    assert np.array_equal(bits16(y), bf16_bits(ref))

@@ -682,4 +682,40 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
   return WZ_OK;
 }
 
+// Dense FP8 GEMM y[M, N] (bf16) = xq[M, K] . W^T for a linear whose weight is
+// in the packed tile format (launch_pack_fp8): the shared-expert w2 tile path
+// (MODE 3) with the linear's dimensions, M-tiles of up to 128 rows staged in
+// LDS, 8 column tiles per workgroup.
+int launch_dense_fp8(const uint8_t* wp, const void* w_s, int w_kind, const uint8_t* xq, const float* xs,
+                     bool a_pow2, uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  wz_moe_desc d = {};
+  d.dim = int(N);
+  d.inter = int(K);
+  d.n_experts = 1;
+  d.topk = 0;
+  d.act_scale_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
+  d.shared_w_scale_kind = w_kind;
+  d.sh2p = wp;
+  d.sh_w2_s = w_s;
+  MoeWs w = {};
+  w.hq = const_cast<uint8_t*>(xq);
+  w.hs = const_cast<float*>(xs);
+  w.sh_out = y;
+  const int nb2d = int((N / 16 + 7) / 8);
+  const int dense = int((M + kPM - 1) / kPM) * nb2d;
+  const bool cs = a_pow2 && w_kind == WZ_WSCALE_E8M0;
+  const dim3 grid{unsigned(dense)}, blk{unsigned(kPThreads)};
+  if (cs) {
+    WZ_LAUNCH("fp8_linear", stream, (prefill_gemm_kernel<false, true, true>), grid, blk, 0, d, w, int(M), 1, nb2d,
+              dense);
+  } else if (a_pow2) {
+    WZ_LAUNCH("fp8_linear", stream, (prefill_gemm_kernel<false, true, false>), grid, blk, 0, d, w, int(M), 1, nb2d,
+              dense);
+  } else {
+    WZ_LAUNCH("fp8_linear", stream, (prefill_gemm_kernel<false, false, false>), grid, blk, 0, d, w, int(M), 1,
+              nb2d, dense);
+  }
+  return check_launch("fp8_linear dense");
+}
+
 }  // namespace wz

@@ -121,6 +121,19 @@ extern "C" size_t wz_moe_packed_bytes(const wz_moe_desc* d, int which) {
   return b < 0 ? 0 : size_t(b);
 }
 
+namespace wz {
+
+// A dense FP8 weight [N, K] in the shared-expert w2 tile format:
+// [N/16][K/128][2 halves][1 KB].
+int launch_pack_fp8(const void* w, int64_t N, int64_t K, void* dst, hipStream_t stream) {
+  const int64_t n16 = N * K / 16;
+  WZ_LAUNCH("fp8_pack", stream, pack_weights_kernel, dim3(unsigned((n16 + 255) / 256)), dim3(256), 0,
+            static_cast<const uint8_t*>(w), nullptr, static_cast<uint8_t*>(dst), n16, 3, 1, int(N), int(K));
+  return check_launch("fp8_pack");
+}
+
+}  // namespace wz
+
 extern "C" int wz_moe_pack(const wz_moe_desc* d, void* w13p, void* w13p_s, void* w2p, void* w2p_s,
                            void* sh13p, void* sh2p, hipStream_t stream) {
   using namespace wz;

@@ -136,6 +136,85 @@ def fp8_linear(x, weight, weight_scale, scale_fmt="ue8m0", scale_dtype=_E8M0):
     return _finish(y)
 
 
+class PackedFp8Linear:
+    """An FP8 linear whose weight is relaid once into MFMA-ready tiles (wz_fp8_pack).
+
+    ``__call__(x)`` is linear(x, weight) for the FP8 weight (architecture.py:121-132:
+    act_quant with the module's scale rule, then fp8_gemm) -> bf16 [..., N].  The
+    packed copy holds the same N*K bytes as the weight; the scale tensor is used as
+    given (float32 or e8m0 [ceil(N/128), K/128]).  ``reserve(M)`` sizes the workspace
+    for row counts above the GEMV range before a graph capture.
+    """
+
+    def __init__(self, weight, weight_scale, scale_fmt="ue8m0"):
+        assert weight.is_contiguous() and weight_scale.is_contiguous()
+        _require_cuda(weight, weight_scale)
+        if weight.dtype not in (_E4M3, torch.uint8):
+            raise TypeError(f"PackedFp8Linear: e4m3 weight expected, got {weight.dtype}")
+        self.N, self.K = weight.shape
+        self.w_kind = _wscale_kind_of(weight_scale)
+        self.act_kind = N.WZ_SCALE_F32 if scale_fmt is None else N.WZ_SCALE_UE8M0_F32
+        self.scale = weight_scale
+        self.packed = torch.empty(self.N * self.K, dtype=torch.uint8, device=weight.device)
+        N.call("wz_fp8_pack", N.ptr(weight), self.N, self.K, N.ptr(self.packed), N.stream_handle(weight.device))
+        self._ws = None
+
+    def workspace_bytes(self, M: int) -> int:
+        return int(N.lib().wz_fp8_linear_workspace_bytes(M, self.K))
+
+    def reserve(self, M: int):
+        need = self.workspace_bytes(M)
+        if need and (self._ws is None or self._ws.numel() < need):
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(f"PackedFp8Linear: reserve({M}) before capturing a graph")
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.packed.device)
+        return self
+
+    def __call__(self, x, out=None):
+        assert x.is_contiguous() and x.size(-1) == self.K
+        _require_cuda(x)
+        if x.dtype != torch.bfloat16:
+            raise TypeError(f"PackedFp8Linear: bf16 input expected, got {x.dtype}")
+        M = x.numel() // self.K
+        self.reserve(M)
+        y = torch.empty(*x.size()[:-1], self.N, dtype=torch.bfloat16, device=x.device) if out is None else out
+        ws = self._ws
+        N.call("wz_fp8_linear_packed", N.ptr(x), N.ptr(self.packed), N.ptr(self.scale), N.ptr(y), M, self.N,
+               self.K, self.act_kind, self.w_kind, N.ptr(ws), 0 if ws is None else ws.numel(),
+               N.stream_handle(x.device))
+        return y
+
+
+def rms_norm(x, weight, eps=1e-6, out=None):
+    """RMSNorm.forward (architecture.py:217-230): bf16(weight * (x * rsqrt(mean(x^2) + eps))),
+    fp32 math, one row per token; weight is the module's fp32 parameter."""
+    assert x.is_contiguous() and weight.is_contiguous()
+    _require_cuda(x, weight)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.float32:
+        raise TypeError(f"rms_norm: x must be bf16 and weight float32 (got {x.dtype}, {weight.dtype})")
+    D = x.size(-1)
+    if weight.numel() != D:
+        raise ValueError(f"rms_norm: weight has {weight.numel()} elements for rows of {D}")
+    y = torch.empty_like(x) if out is None else out
+    N.call("wz_rmsnorm", N.ptr(x), N.ptr(weight), N.ptr(y), x.numel() // D, D, float(eps),
+           N.stream_handle(x.device))
+    return y
+
+
+def add(a, b, out=None):
+    """Elementwise a + b of two bf16 tensors of one shape, fp32 sum rounded once to bf16:
+    the plain residual step (x + f(x)) of a decoder stage.  The model's own blocks mix
+    the residual through hyper-connections (Block.hc_post, architecture.py:839-850),
+    which this function does not implement."""
+    assert a.is_contiguous() and b.is_contiguous() and a.shape == b.shape
+    _require_cuda(a, b)
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise TypeError(f"add: bf16 operands expected (got {a.dtype}, {b.dtype})")
+    out = torch.empty_like(a) if out is None else out
+    N.call("wz_add_bf16", N.ptr(a), N.ptr(b), N.ptr(out), a.numel(), N.stream_handle(a.device))
+    return out
+
+
 _fp8_gemm_marker = "_v4_hip_fp8_gemm"
 fp8_gemm._v4_hip_fp8_gemm = True
 fp4_gemm._v4_hip_fp4_gemm = True
