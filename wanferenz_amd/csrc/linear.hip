@@ -72,9 +72,10 @@ __global__ __launch_bounds__(kGvThreads) void fp8_gemv_kernel(const uint16_t* __
     for (int q = 0; q < NKB; ++q) fp8_wscale(w_s, int64_t(item >> 3) * KB + kb0 + q, w_kind, b.se[q], b.sf[q]);
   };
 
-  // this wave's K slice of the (<= 16) token rows, quantised once (issuing the
-  // first weight tile ahead of it measured slower: the x wait then also waits
-  // for that tile, and the second tile's request goes out later)
+  // this wave's K slice of the (<= 16) token rows, quantised once.  The
+  // weights are requested after the quantisation: issuing them first (weights
+  // then x, or x then weights with the quantisation in between) measured
+  // 0.3-1.3 us slower per launch.
   const uint16_t* xrow = nl < M ? x + int64_t(nl) * K : nullptr;
   AOp a[NKB];
 #pragma unroll

@@ -57,16 +57,29 @@ __device__ __forceinline__ AOp a_from_fp8(const uint8_t* row, const void* srow, 
 // that share a row (l, l^16, l^32, l^48) together hold the whole 128-block
 // (two 16-element runs each), so the block amax is two xor-shuffles.  Every lane of the
 // wave must call this (rows may be null -> zeros).
-__device__ __forceinline__ AOp a_from_bf16(const uint16_t* row, int kb, int g, bool pow2) {
-  AOp a = a_zero();
-  v4i w[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+struct ARaw {
+  v4i w[4];
+};
+
+// The load half of a_from_bf16: issue it early, quantise (a_quant_bf16) once
+// other loads are in flight.
+__device__ __forceinline__ ARaw a_load_bf16(const uint16_t* row, int kb, int g) {
+  ARaw r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.w[i] = v4i{0, 0, 0, 0};
   if (row != nullptr) {
     const uint16_t* p = row + kb * 128 + g * 16;
-    w[0] = load16(p);
-    w[1] = load16(p + 8);
-    w[2] = load16(p + 64);
-    w[3] = load16(p + 72);
+    r.w[0] = load16(p);
+    r.w[1] = load16(p + 8);
+    r.w[2] = load16(p + 64);
+    r.w[3] = load16(p + 72);
   }
+  return r;
+}
+
+__device__ __forceinline__ AOp a_quant_bf16(const ARaw& r, bool pow2) {
+  AOp a = a_zero();
+  const v4i* w = r.w;
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -89,6 +102,10 @@ __device__ __forceinline__ AOp a_from_bf16(const uint16_t* row, int kb, int g, b
                        quant_div(bf16lo(w3), sc, pow2), quant_div(bf16hi(w3), sc, pow2)));
   }
   return a;
+}
+
+__device__ __forceinline__ AOp a_from_bf16(const uint16_t* row, int kb, int g, bool pow2) {
+  return a_quant_bf16(a_load_bf16(row, kb, g), pow2);
 }
 
 // MXFP4 weight row (packed e2m1 [K/2], e8m0 scales [K/32]) -> B operand of K-block kb.

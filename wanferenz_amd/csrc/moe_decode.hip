@@ -358,6 +358,10 @@ __device__ __forceinline__ void w13_shared_item_bf16(const wz_moe_desc& d, const
     v8i w[2][4];
     int se[2][4];
     float sf[2][4];
+    ARaw xr[4];  // x first: its quantisation then overlaps the weight loads
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (kb + q < kb1) xr[q] = a_load_bf16(xrow, kb + q, g);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       if (kb + q < kb1) {
@@ -369,7 +373,7 @@ __device__ __forceinline__ void w13_shared_item_bf16(const wz_moe_desc& d, const
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       if (kb + q < kb1) {
-        const AOp a = a_from_bf16(xrow, kb + q, g, a_pow2);
+        const AOp a = a_quant_bf16(xr[q], a_pow2);
         mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], a_pow2, bp, lane);
         mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], a_pow2, bp, lane);
       }
