@@ -602,6 +602,8 @@ template <int NKB>
 struct W13Buf {
   v4i w1[NKB], w3[NKB];
   uint32_t s1[2], s3[2];  // packed e8m0 dwords (4 K-blocks each)
+  int q[4];               // epilogue: pair rows of this lane's four token rows (-1: unrouted)
+  float wt[4];            //           and their routing weights
   int u, ft;
 };
 
@@ -659,19 +661,17 @@ __global__ __launch_bounds__(kDecThreads) void w13_stream_kernel(wz_moe_desc d, 
       b.s1[q] = st[(kg * 2 + 0) * 64];
       b.s3[q] = st[(kg * 2 + 1) * 64];
     }
+    // the epilogue's row map travels with the tiles: loaded inside process it
+    // would be issued after the next item's tiles and its wait would include them
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = min(g * 4 + i, T - 1);
+      b.q[i] = ws.umap[b.u * T + t];
+      b.wt[i] = ws.uwt[b.u * T + t];
+    }
   };
 
   auto process = [&](const W13Buf<NKB>& b, int par) {
-    int qrow[4] = {-1, -1, -1, -1};
-    float wrow[4] = {0.f, 0.f, 0.f, 0.f};
-    if (wave == 0) {  // epilogue rows of this item, fetched ahead of the MFMAs
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = g * 4 + i;
-        qrow[i] = t < T ? ws.umap[b.u * T + t] : -1;
-        wrow[i] = t < T ? ws.uwt[b.u * T + t] : 0.0f;
-      }
-    }
     v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int q = 0; q < NKB; ++q) {
@@ -698,10 +698,9 @@ __global__ __launch_bounds__(kDecThreads) void w13_stream_kernel(wz_moe_desc d, 
           gs += r[((w * 2 + 0) * 4 + i) * kWave + lane];
           us += r[((w * 2 + 1) * 4 + i) * kWave + lane];
         }
-        if (qrow[i] >= 0) {
-          const int t = g * 4 + i;
-          ws.h[(int64_t(b.u) * T + t) * I + b.ft * 16 + nl] = f32_to_bf16(wrow[i] * swiglu(gs, us, d.swiglu_limit));
-        }
+        const int t = g * 4 + i;
+        if (t < T && b.q[i] >= 0)
+          ws.h[(int64_t(b.u) * T + t) * I + b.ft * 16 + nl] = f32_to_bf16(b.wt[i] * swiglu(gs, us, d.swiglu_limit));
       }
     }
   };
@@ -846,6 +845,7 @@ template <int NKB>
 struct W2Buf {
   v4i w[4][NKB];
   uint32_t s[4];  // packed e8m0 dword of each column tile (this wave's K quarter)
+  int q[4];       // pair rows of this lane's four token rows (-1: unrouted), fetched with the tiles
   int u, g64;
 };
 
@@ -922,6 +922,8 @@ __global__ __launch_bounds__(kDecThreads) void w2_stream_kernel(wz_moe_desc d, M
       for (int q = 0; q < NKB; ++q) bf.w[c][q] = load16_nt(wt + q * 1024);
       bf.s[c] = static_cast<const uint32_t*>(d.w2p_s)[(tile * KG + kg0) * 64 + lane];
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bf.q[i] = ws.umap[bf.u * T + min(g * 4 + i, T - 1)];
   };
 
   v8i av[NKB];
@@ -962,7 +964,7 @@ __global__ __launch_bounds__(kDecThreads) void w2_stream_kernel(wz_moe_desc d, M
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = g * 4 + i;
-      const int q = t < T ? ws.umap[bf.u * T + t] : -1;
+      const int q = t < T ? bf.q[i] : -1;
       float v = r[((0 * 4 + c) * 4 + i) * kWave + lane];
 #pragma unroll
       for (int w = 1; w < 4; ++w) v += r[((w * 4 + c) * 4 + i) * kWave + lane];
