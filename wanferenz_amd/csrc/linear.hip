@@ -15,7 +15,7 @@
 //   b, b+G, ... with the next tile's weights in flight during the current
 //   tile's MFMAs; the eight K partials meet in LDS, summed in wave order.
 // Otherwise: act_quant into the caller's workspace, then the dense tile GEMM
-//   (launch_dense_fp8: M-tiles of <= 128 rows staged in LDS).
+//   (launch_dense_fp8: M-tiles of <= 64 rows staged in LDS).
 #include "mfma_ops.h"
 
 #include <algorithm>

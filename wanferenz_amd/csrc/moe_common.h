@@ -10,6 +10,7 @@ constexpr int kMaxExperts = 512;
 constexpr int kMaxPairs = 16384;
 constexpr int kGateTok = 8;
 constexpr int kDecodeMaxT = 16;       // tokens served by the decode kernels
+constexpr int kPrefillTileRows = 64;  // pair rows per M-tile of the prefill / dense GEMMs
 constexpr int kCounterWords = 4096;   // arrival counters at the start of the workspace
 
 // Scratch of one MoE layer call, carved from the caller's workspace.  The
@@ -83,7 +84,7 @@ static inline MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base
   const int64_t HQ = (T <= kDecodeMaxT ? UT : P) + T;  // decode rows (u, t) / prefill pairs, then shared rows
   w.hq = take(size_t(HQ) * I);
   w.hs = reinterpret_cast<float*>(take(sizeof(float) * HQ * (I / 128)));
-  const int64_t MT = P / 128 + (P < E ? P : E) + 1;     // M-tiles of 128 pair rows (prefill)
+  const int64_t MT = P / kPrefillTileRows + (P < E ? P : E) + 1;  // M-tiles of pair rows (prefill)
   w.mt_u = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * MT));
   w.mt_row0 = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * MT));
   w.mt_n = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * MT));

@@ -1,7 +1,7 @@
 // MoE prefill path (T > 16 tokens): expert-grouped MFMA GEMMs over the
 // canonical (expert, token, slot) pair order produced by the routing kernels.
 //
-//   mtile     each active expert's pair rows cut into tiles of 128 rows.
+//   mtile     each active expert's pair rows cut into tiles of 64 rows.
 //   xquant    act_quant(x) once for all experts (quant.hip).
 //   w13       per (M-tile, 64 intermediate features): the gathered 128 fp8
 //             activation rows of one 128-wide K-block are staged in LDS; each
@@ -22,7 +22,8 @@
 
 namespace wz {
 
-constexpr int kPM = 128;          // pair rows per M-tile
+constexpr int kPM = kPrefillTileRows;  // pair rows per M-tile (64: the tile bodies then fit two
+                                       // workgroups per CU, twice the weight bytes in flight)
 constexpr int kPThreads = 256;    // 4 waves
 constexpr int kARow = 144;        // LDS row stride of the staged A tile (bytes)
 
@@ -356,7 +357,7 @@ struct BTiles {
   float f[NT];
 };
 
-// Expert-grouped tile GEMM over one M-tile (<= 128 rows) and one N-block.
+// Expert-grouped tile GEMM over one M-tile (<= 64 rows) and one N-block.
 //   MODE 0: routed w1/w3 (packed MXFP4) over gathered x rows -> SwiGLU -> h
 //   MODE 1: shared w1/w3 (packed FP8) over token rows        -> SwiGLU -> sh_h
 //   MODE 2: routed w2 (packed MXFP4) over h rows             -> out2
@@ -404,26 +405,26 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
   }
 
   // A staging: thread -> (row, half of the 128-byte K-block)
-  const int sr = tid >> 1, sh = tid & 1;
+  const int sr = tid >> 2, sq = tid & 3;  // 4 threads per row, 32 bytes each
   const int rr = min(sr, nrows - 1);
   int src;
   if (MODE == 0) src = clampi(ws.perm_token[row0 + rr], 0, T - 1);
   else if (MODE == 1) src = row0 + rr;
   else if (MODE == 2) src = row0 + rr;
   else src = P + row0 + rr;
-  const uint8_t* arow = (W13 ? ws.xq : ws.hq) + int64_t(src) * K + sh * 64;
+  const uint8_t* arow = (W13 ? ws.xq : ws.hq) + int64_t(src) * K + sq * 32;
   const float* asrow = (W13 ? ws.xs : ws.hs) + int64_t(src) * KB;
-  v4i av[4];
+  v4i av[2];
   float asv;
   auto a_fetch = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) av[i] = load16(arow + kb * 128 + 16 * i);
+    for (int i = 0; i < 2; ++i) av[i] = load16(arow + kb * 128 + 16 * i);
     asv = asrow[kb];
   };
   auto a_put = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(&a_s[buf][sr * kARow + sh * 64 + 16 * i]) = av[i];
-    as_s[buf][sr] = asv;  // both halves of the row store the same scale: no divergent branch
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<v4i*>(&a_s[buf][sr * kARow + sq * 32 + 16 * i]) = av[i];
+    as_s[buf][sr] = asv;  // the row's four threads store the same scale: no divergent branch
   };
 
   auto b_fetch = [&](BTiles<NTW>& b, int kb) {
@@ -596,28 +597,27 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
   }
 }
 
-// Tile dispatch on its height: the body is compiled for 1, 2, 4 or 8 row
+// Tile dispatch on its height: the body is compiled for 1, 2 or 4 row
 // tiles of 16, so its MFMA loops carry no row branches.
 template <int MODE, bool CHAIN>
 __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws, int T, int mt, int nt,
                                           uint8_t (*a_s)[kPM * kARow], float (*as_s)[kPM]) {
   TileRows tr;
   if (!tile_of(ws, mt, (MODE & 1) != 0, T, T * d.topk, d.n_experts, tr)) return;
+  static_assert(kPM == 64, "tile heights up to 4 row tiles");
   if (tr.nrows <= 16)
     gemm_tile_body<MODE, CHAIN, 1>(d, ws, T, tr, nt, a_s, as_s);
   else if (tr.nrows <= 32)
     gemm_tile_body<MODE, CHAIN, 2>(d, ws, T, tr, nt, a_s, as_s);
-  else if (tr.nrows <= 64)
-    gemm_tile_body<MODE, CHAIN, 4>(d, ws, T, tr, nt, a_s, as_s);
   else
-    gemm_tile_body<MODE, CHAIN, 8>(d, ws, T, tr, nt, a_s, as_s);
+    gemm_tile_body<MODE, CHAIN, 4>(d, ws, T, tr, nt, a_s, as_s);
 }
 
 // One launch serves the shared expert's dense tiles (block ids first, so the
 // few long-running shared tiles start early) and the routed experts' M-tiles.
 // W13 selects w1/w3 + SwiGLU or w2; CR / CS: scale chaining of routed / shared.
 template <bool W13, bool CR, bool CS>
-__global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_gemm_kernel(
     wz_moe_desc d, MoeWs ws, int T, int nblk, int nblk_dense, int dense_blocks) {
   __shared__ __align__(16) uint8_t a_s[3][kPM * kARow];
   __shared__ float as_s[3][kPM];
@@ -684,7 +684,7 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
 
 // Dense FP8 GEMM y[M, N] (bf16) = xq[M, K] . W^T for a linear whose weight is
 // in the packed tile format (launch_pack_fp8): the shared-expert w2 tile path
-// (MODE 3) with the linear's dimensions, M-tiles of up to 128 rows staged in
+// (MODE 3) with the linear's dimensions, M-tiles of up to 64 rows staged in
 // LDS, 8 column tiles per workgroup.
 int launch_dense_fp8(const uint8_t* wp, const void* w_s, int w_kind, const uint8_t* xq, const float* xs,
                      bool a_pow2, uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
