@@ -424,36 +424,41 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     double acc[kDecodeMaxT];
 #pragma unroll
     for (int t = 0; t < kDecodeMaxT; ++t) acc[t] = 0.0;
-    if (e < E) {
+    if (e < E && c0 < c1) {
       const uint16_t* wr = static_cast<const uint16_t*>(d.gate_w) + int64_t(e) * D;
 #pragma unroll 1
-      for (int cb = c0; cb < c1; cb += 64 * 4) {
-        v4i wv[4];
+      for (int cb = c0; cb < c1; cb += 64 * 2) {
+        // two 16-byte chunks per lane; a chunk past c1 gets w = 0 and a clamped,
+        // valid x address, so every load below is unconditional
+        v4i wv[2];
+        int cx[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2; ++i) {
           const int c = cb + lane + 64 * i;
           wv[i] = c < c1 ? load16(wr + c * 8) : v4i{0, 0, 0, 0};
+          cx[i] = min(c, c1 - 1);
         }
+        // tokens in groups of 8: a group's x chunks are all requested before any
+        // is used (one round trip per group; token indices past T are clamped)
 #pragma unroll
-        for (int t0 = 0; t0 < kDecodeMaxT; t0 += 2) {
-          if (t0 < T) {
-            v4i xv[2][4];
+        for (int tg = 0; tg < kDecodeMaxT; tg += 8) {
+          if (tg < T) {
+            v4i xv[8][2];
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 8; ++j)
 #pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                const int c = cb + lane + 64 * i;
-                xv[j][i] = (t0 + j < T && c < c1) ? load16(x + int64_t(t0 + j) * D + c * 8) : v4i{0, 0, 0, 0};
+              for (int i = 0; i < 2; ++i) xv[j][i] = load16(x + int64_t(min(tg + j, T - 1)) * D + cx[i] * 8);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              if (tg + j < T) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                  for (int q = 0; q < 4; ++q) {
+                    acc[tg + j] += double(bf16lo(uint32_t(xv[j][i][q])) * bf16lo(uint32_t(wv[i][q])));
+                    acc[tg + j] += double(bf16hi(uint32_t(xv[j][i][q])) * bf16hi(uint32_t(wv[i][q])));
+                  }
               }
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                  acc[t0 + j] += double(bf16lo(uint32_t(xv[j][i][q])) * bf16lo(uint32_t(wv[i][q])));
-                  acc[t0 + j] += double(bf16hi(uint32_t(xv[j][i][q])) * bf16hi(uint32_t(wv[i][q])));
-                }
           }
         }
       }
