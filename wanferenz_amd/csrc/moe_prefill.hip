@@ -34,8 +34,8 @@ constexpr int kARow = 144;        // LDS row stride of the staged A tile (bytes)
 // decode path use the correctly rounded dot product).  Two passes:
 //
 //  gate_mfma   approximate logits a~[t,e] with V_MFMA_F32_16X16X16_BF16: each
-//              32-wide K chunk is summed by two MFMAs from zero and added to
-//              an fp64 accumulator, so |a~ - a| <= 33 * 2^-23 * S + (fp64
+//              64-wide K chunk is summed by four MFMAs from zero and added to
+//              an fp64 accumulator, so |a~ - a| <= 65 * 2^-23 * S + (fp64
 //              terms), S = sum_d |x_d w_d|, whatever order or rounding mode
 //              the MFMA uses inside a chunk (bf16 x bf16 products are exact
 //              in fp32).  S itself comes from the same MFMA on |x|, |w|.
@@ -52,6 +52,8 @@ constexpr int kARow = 144;        // LDS row stride of the staged A tile (bytes)
 
 typedef short v4s __attribute__((ext_vector_type(4)));
 
+constexpr int kGateChunk = 64;  // K elements summed in fp32 (four MFMAs from zero) per fp64 add
+
 __device__ __forceinline__ v4s v4s_lo(v4i a) {
   return v4s{short(a[0] & 0xFFFF), short(uint32_t(a[0]) >> 16), short(a[1] & 0xFFFF), short(uint32_t(a[1]) >> 16)};
 }
@@ -66,7 +68,68 @@ __device__ __forceinline__ v4i abs_bf16x8(v4i a) {
 // meet in LDS.  A lane loads 8 consecutive bf16 of its row for two 16x16x16
 // MFMAs; A and B use the same lane -> K assignment, so each K element's two
 // factors meet in one product.
+// One workgroup: 32 tokens x 64 experts; wave w owns expert tile w (16 experts)
+// for both 16-token tiles, over the full K, so a loaded W fragment feeds two
+// MFMAs and the token fragments are shared by the four waves through L1.
 __global__ __launch_bounds__(256) void gate_mfma_kernel(const uint16_t* __restrict__ x,
+                                                        const uint16_t* __restrict__ W,
+                                                        float* __restrict__ approx, float* __restrict__ absdot,
+                                                        int T, int E, int D) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int egs = (E + 63) / 64;
+  const int tg = blockIdx.x / egs, eg = blockIdx.x % egs;
+  const int nl = lane & 15, g = lane >> 4;
+  const int ex = eg * 64 + wave * 16 + nl;
+  // clamped rows: every load is unconditional; rows past T / E are never stored
+  const uint16_t* wr = W + int64_t(min(ex, E - 1)) * D;
+  const uint16_t* xr0 = x + int64_t(min(tg * 32 + nl, T - 1)) * D;
+  const uint16_t* xr1 = x + int64_t(min(tg * 32 + 16 + nl, T - 1)) * D;
+  double acc[2][4] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
+  v4f sabs[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  const v4f z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int k0 = 0; k0 < D; k0 += kGateChunk) {
+    v4i a0[2], a1[2], b[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      a0[h] = load16(xr0 + k0 + 32 * h + 8 * g);
+      a1[h] = load16(xr1 + k0 + 32 * h + 8 * g);
+      b[h] = load16(wr + k0 + 32 * h + 8 * g);
+    }
+    v4f p0 = z, p1 = z;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      p0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a0[h]), v4s_lo(b[h]), p0, 0, 0, 0);
+      p0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a0[h]), v4s_hi(b[h]), p0, 0, 0, 0);
+      p1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a1[h]), v4s_lo(b[h]), p1, 0, 0, 0);
+      p1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a1[h]), v4s_hi(b[h]), p1, 0, 0, 0);
+      const v4i a0a = abs_bf16x8(a0[h]), a1a = abs_bf16x8(a1[h]), ba = abs_bf16x8(b[h]);
+      sabs[0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a0a), v4s_lo(ba), sabs[0], 0, 0, 0);
+      sabs[0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a0a), v4s_hi(ba), sabs[0], 0, 0, 0);
+      sabs[1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a1a), v4s_lo(ba), sabs[1], 0, 0, 0);
+      sabs[1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a1a), v4s_hi(ba), sabs[1], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[0][i] += double(p0[i]);
+      acc[1][i] += double(p1[i]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = tg * 32 + m * 16 + g * 4 + i;
+      if (t < T && ex < E) {
+        approx[int64_t(t) * E + ex] = float(acc[m][i]);
+        absdot[int64_t(t) * E + ex] = sabs[m][i];
+      }
+    }
+}
+
+// Small T: one workgroup per 16 tokens x 16 experts, the four waves split K
+// (32-wide chunks; its error stays within the 64-chunk bound used below).
+__global__ __launch_bounds__(256) void gate_mfma_ksplit_kernel(const uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ W,
                                                         float* __restrict__ approx, float* __restrict__ absdot,
                                                         int T, int E, int D) {
@@ -149,7 +212,7 @@ __device__ __forceinline__ float exact_logit(const v4i (&xv)[kXC], const uint16_
 }
 
 constexpr int kRSlots = kMaxExperts / 64;
-constexpr float kChunkErr = 33.0f / 8388608.0f;  // 33 * 2^-23
+constexpr float kChunkErr = float(kGateChunk + 1) / 8388608.0f;  // (chunk + 1) * 2^-23
 
 __global__ __launch_bounds__(256) void topk_refine_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ W,
@@ -273,10 +336,19 @@ int launch_prefill_gate(const wz_moe_desc* d, const MoeWs& w, const void* x, con
   const uint16_t* xb = static_cast<const uint16_t*>(x);
   const uint16_t* gw = static_cast<const uint16_t*>(d->gate_w);
   if (!d->tid2eid) {
-    const int64_t tiles = ((T + 15) / 16) * ((E + 15) / 16);
-    WZ_LAUNCH("moe_gate", stream, gate_mfma_kernel, dim3(unsigned(tiles)), dim3(256), 0, xb, gw, w.scores,
-              w.biased, int(T), E, D);
-    if (int rc = check_launch("moe gate")) return rc;
+    // the 32 x 64 tiles need T >= 1024 to give every CU a workgroup; below,
+    // the 16 x 16 tiles with K split over the waves
+    if (T < 1024) {
+      const int64_t tiles = ((T + 15) / 16) * ((E + 15) / 16);
+      WZ_LAUNCH("moe_gate", stream, gate_mfma_ksplit_kernel, dim3(unsigned(tiles)), dim3(256), 0, xb, gw, w.scores,
+                w.biased, int(T), E, D);
+      if (int rc = check_launch("moe gate")) return rc;
+    } else {
+      const int64_t tiles = ((T + 31) / 32) * ((E + 63) / 64);
+      WZ_LAUNCH("moe_gate", stream, gate_mfma_kernel, dim3(unsigned(tiles)), dim3(256), 0, xb, gw, w.scores,
+                w.biased, int(T), E, D);
+      if (int rc = check_launch("moe gate")) return rc;
+    }
   }
   WZ_LAUNCH("moe_topk", stream, topk_refine_kernel, dim3(unsigned((T + 3) / 4)), dim3(256), 0, xb, gw, w.scores,
             w.biased, d->tid2eid ? nullptr : d->gate_bias, d->tid2eid, input_ids, d->vocab, int(T), E, D, d->topk,
