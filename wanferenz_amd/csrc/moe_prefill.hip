@@ -434,9 +434,9 @@ struct BTiles {
 //   MODE 1: shared w1/w3 (packed FP8) over token rows        -> SwiGLU -> sh_h
 //   MODE 2: routed w2 (packed MXFP4) over h rows             -> out2
 //   MODE 3: shared w2 (packed FP8) over shared h rows        -> sh_out
-// A wave owns NTW weight tiles of 16 output columns (routed: 4, i.e. w13: 2
-// feature tiles x {w1, w3}, w2: 4 column tiles; shared FP8 tiles are twice
-// the bytes, so 2), and one A operand read from LDS feeds NTW MFMAs.
+// A wave owns NTW weight tiles of 16 output columns (routed w13: 4, i.e. 2
+// feature tiles x {w1, w3}; routed w2: 2 column tiles; shared FP8 tiles are
+// twice the bytes, so 2), and one A operand read from LDS feeds NTW MFMAs.
 // The K loop is software-pipelined: the B tiles of K-steps kb+1 and kb+2 are
 // in flight while kb computes, and the A block of kb+1 sits in registers on
 // its way to LDS; A goes through three LDS buffers with one barrier per step.
@@ -449,7 +449,10 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
                                                int nt, uint8_t (*a_s)[kPM * kARow], float (*as_s)[kPM]) {
   constexpr bool W13 = MODE < 2, DENSE = (MODE & 1) != 0;
   constexpr int WF = DENSE ? kFmtFp8 : kFmtFp4;
-  constexpr int NTW = DENSE ? 2 : 4;          // weight tiles per wave
+  // weight tiles per wave: routed w1/w3 4 (2 feature tiles x {w1, w3}); routed
+  // w2 2 (4 spilled registers at two workgroups per CU and measured 7 % slower);
+  // FP8 shared tiles, twice the bytes, 2
+  constexpr int NTW = (DENSE || MODE == 2) ? 2 : 4;
   constexpr int CPW = W13 ? NTW / 2 : NTW;    // 16-column output tiles per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nl = lane & 15, g = lane >> 4;
@@ -719,9 +722,10 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
     if (int rc = check_launch("moe mtile")) return rc;
     if (int rc = launch_act_quant(x, T, D, w.xq, w.xs, qkind, stream)) return rc;
   }
-  // column tiles of 16 per WG: routed 4 waves x 4 weight tiles, shared 4 x 2
+  // column tiles of 16 per WG: routed w1/w3 4 waves x 2 feature tiles, routed w2
+  // and the shared tiles 4 waves x 2
   const int nb13 = (I / 16 + 7) / 8, nb13d = (I / 16 + 3) / 4;
-  const int nb2 = (D / 16 + 15) / 16, nb2d = (D / 16 + 7) / 8;
+  const int nb2 = (D / 16 + 7) / 8, nb2d = (D / 16 + 7) / 8;
   const bool cr = d->act_scale_kind != WZ_SCALE_F32;
   const bool cs = cr && d->shared_w_scale_kind == WZ_WSCALE_E8M0;
   const int Ti = int(T), dn13 = int(mt_dense * nb13d), dn2 = int(mt_dense * nb2d);
