@@ -189,6 +189,23 @@ int wz_rmsnorm(const void* x_bf16, const float* weight, void* y_bf16, int64_t T,
 /* bf16 elementwise add (residual): out = bf16(float(a) + float(b)). */
 int wz_add_bf16(const void* a, const void* b, void* out, int64_t n, hipStream_t stream);
 
+/* RMSNorm fused with the FP8 act_quant of its output — RMSNorm.forward
+ * (architecture.py:217-230) followed by act_quant (reference.py:117-146,
+ * torch_ops.py:33-49) as the producer of an FP8 linear's input, without the
+ * bf16 row in memory.  x [T, D] bf16 (D % 128 == 0, D <= 8192), weight fp32 [D]
+ * -> q e4m3 [T, D], s [T, D/128] (scale_kind as wz_act_quant_fp8). */
+int wz_rmsnorm_quant(const void* x_bf16, const float* weight, void* q_e4m3, void* s, int64_t T,
+                     int64_t D, float eps, int scale_kind, hipStream_t stream);
+
+/* The FP8 wire format of a pipeline-stage boundary — _pack_t / _unpack_t
+ * (serving/chain.py:208-222): per row scale = bf16(clamp(amax/448, 1e-8, bf16 max)),
+ * q = e4m3(clamp(x/scale, +-448)); unpack y = bf16(q * scale).  x, y [M, D] bf16,
+ * q [M, D] e4m3, scale [M] bf16. */
+int wz_fp8_wire_pack(const void* x_bf16, void* q_e4m3, void* scale_bf16, int64_t M, int64_t D,
+                     hipStream_t stream);
+int wz_fp8_wire_unpack(const void* q_e4m3, const void* scale_bf16, void* y_bf16, int64_t M, int64_t D,
+                       hipStream_t stream);
+
 /* Synthetic-input generator (no reference counterpart: fills benchmark and test inputs
  * with the portable counter-based hash of wanferenz_amd/synth.py).
  * mode 0: u8 = low byte of draw; 1: e8m0 = lo + draw % (hi-lo+1);

@@ -74,6 +74,29 @@ def act_quant(x: np.ndarray, block: int = 128, round_pow2: bool = True):
     return codes, s[..., 0].astype(np.float32)
 
 
+BF16_MAX = np.float32(3.3895313892515355e38)
+
+
+def wire_pack(x: np.ndarray):
+    """The FP8 wire format of a stage boundary (_pack_t, serving/chain.py:208-217).
+
+    Per row (last dim): scale = bf16(clamp(amax / 448, 1e-8, bf16 max)) in fp32
+    arithmetic, q = e4m3(clamp(x / scale, +-448)).  Returns (q uint8 codes, scale
+    float32 holding bf16 values [...]).
+    """
+    f = np.asarray(x, dtype=np.float32)
+    amax = np.abs(f).max(axis=-1, keepdims=True)
+    scale = bf16_round(np.clip(amax / np.float32(448.0), np.float32(1e-8), BF16_MAX).astype(np.float32))
+    q = np.clip(f / scale, np.float32(-FP8_MAX), np.float32(FP8_MAX)).astype(np.float32)
+    return e4m3_encode(q), scale[..., 0]
+
+
+def wire_unpack(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """_unpack_t (chain.py:220-222): bf16(q) * scale in bf16 -> bf16 values as float32."""
+    v = e4m3_decode(q).astype(np.float32)
+    return bf16_round((v * np.asarray(scale, np.float32)[..., None]).astype(np.float32))
+
+
 def dequant_act(q: np.ndarray, s: np.ndarray, block: int = 128) -> np.ndarray:
     v = e4m3_decode(q).astype(np.float64)
     return v * np.repeat(np.asarray(s, dtype=np.float64), block, axis=-1)[..., : v.shape[-1]]

@@ -336,3 +336,49 @@ def test_fp8_linear_packed_exact(gpu, M, N, K):
     rq, rs = om.act_quant(xf, 128, True)
     ref = om.fp8_gemm(rq, rs, w, e8m0_decode(ws))
     assert np.array_equal(bits16(y), bf16_bits(ref))
+
+
+def _wire_rows(seed, M, D):
+    from oracle.numerics import bf16_bits
+
+    x = from_bf16_bits(_x(seed, M, D, 2.0)).reshape(M, D)
+    if M >= 4:
+        x[0] = 0.0
+        x[1] *= np.float32(1e-33)   # scales near the 1e-8 floor
+        x[2] = np.float32(448.0 * 2.0 ** 7) * np.sign(x[2])
+        x[3, 7] = np.float32(3.0e38)
+    return bf16_bits(x.astype(np.float32))
+
+
+@pytest.mark.parametrize("M,D", [(1, 4096), (5, 1024), (33, 7168), (8, 520)])
+def test_wire_pack_unpack_bit_exact(gpu, M, D):
+    """The FP8 stage-boundary format (serving/chain.py:208-222) vs the oracle: codes,
+    bf16 scales and the unpacked bf16 values bit for bit."""
+    xb = _wire_rows(41 + M, M, D)
+    q, s = kernels.wire_pack(bf16_tensor(xb, gpu).view(M, D))
+    y = kernels.wire_unpack(q, s)
+    torch.cuda.synchronize()
+    rq, rs = om.wire_pack(from_bf16_bits(xb).reshape(M, D))
+    assert np.array_equal(bytes8(q), rq)
+    assert np.array_equal(f32_of_bf16(s), rs)
+    assert np.array_equal(f32_of_bf16(y).reshape(M, D), om.wire_unpack(rq, rs))
+
+
+@pytest.mark.parametrize("scale_fmt,scale_dtype", [("ue8m0", torch.float8_e8m0fnu), (None, torch.float32)])
+@pytest.mark.parametrize("T,D", [(1, 4096), (4, 7168), (37, 1024)])
+def test_rms_norm_quant_is_norm_then_act_quant(gpu, scale_fmt, scale_dtype, T, D):
+    """The fused producer equals rms_norm followed by act_quant bit for bit (same
+    arithmetic), and the oracle's act_quant of that normalised row."""
+    xb = _x(51 + T, T, D, 2.0)
+    wgt = synth.fill_f32_uniform(synth.stream_key(52, synth.S_NORM), 0, D, 0.5, 1.5)
+    x, w = bf16_tensor(xb, gpu).view(T, D), f32_tensor(wgt, gpu)
+    q, s = kernels.rms_norm_quant(x, w, 1e-6, scale_fmt, scale_dtype)
+    y = kernels.rms_norm(x, w, 1e-6)
+    q2, s2 = kernels.act_quant(y, 128, scale_fmt, scale_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8))
+    assert torch.equal(s.view(torch.uint8), s2.view(torch.uint8))
+    rq, rs = om.act_quant(f32_of_bf16(y).reshape(T, D), 128, scale_fmt is not None)
+    assert np.array_equal(bytes8(q).reshape(T, D), rq)
+    got_s = e8m0_decode(bytes8(s)) if scale_fmt else s.cpu().numpy()
+    assert np.array_equal(got_s.reshape(rs.shape), rs)

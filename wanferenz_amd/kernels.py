@@ -201,6 +201,46 @@ def rms_norm(x, weight, eps=1e-6, out=None):
     return y
 
 
+def rms_norm_quant(x, weight, eps=1e-6, scale_fmt="ue8m0", scale_dtype=_E8M0):
+    """act_quant(rms_norm(x, weight, eps)) in one pass (architecture.py:217-230 then
+    reference.py:117-146): -> (e4m3 [..., D], scales [..., D/128])."""
+    assert x.is_contiguous() and weight.is_contiguous()
+    _require_cuda(x, weight)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.float32:
+        raise TypeError(f"rms_norm_quant: x must be bf16 and weight float32 (got {x.dtype}, {weight.dtype})")
+    D = x.size(-1)
+    kind = _act_kind(scale_fmt, scale_dtype)
+    q = torch.empty(x.shape, dtype=_E4M3, device=x.device)
+    s = torch.empty(*x.shape[:-1], D // 128, dtype=_E8M0 if kind == N.WZ_SCALE_UE8M0 else torch.float32,
+                    device=x.device)
+    N.call("wz_rmsnorm_quant", N.ptr(x), N.ptr(weight), N.ptr(q), N.ptr(s), x.numel() // D, D, float(eps), kind,
+           N.stream_handle(x.device))
+    return q, s
+
+
+def wire_pack(t):
+    """_pack_t (serving/chain.py:208-217): bf16 [..., D] -> (e4m3 [..., D], bf16 scale [...])."""
+    assert t.is_contiguous()
+    _require_cuda(t)
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"wire_pack: bf16 input expected, got {t.dtype}")
+    D = t.size(-1)
+    q = torch.empty(t.shape, dtype=_E4M3, device=t.device)
+    scale = torch.empty(t.shape[:-1], dtype=torch.bfloat16, device=t.device)
+    N.call("wz_fp8_wire_pack", N.ptr(t), N.ptr(q), N.ptr(scale), t.numel() // D, D, N.stream_handle(t.device))
+    return q, scale
+
+
+def wire_unpack(q, scale):
+    """_unpack_t (serving/chain.py:220-222): bf16(q) * scale -> bf16 [..., D]."""
+    assert q.is_contiguous() and scale.is_contiguous()
+    _require_cuda(q, scale)
+    D = q.size(-1)
+    y = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    N.call("wz_fp8_wire_unpack", N.ptr(q), N.ptr(scale), N.ptr(y), q.numel() // D, D, N.stream_handle(q.device))
+    return y
+
+
 def add(a, b, out=None):
     """Elementwise a + b of two bf16 tensors of one shape, fp32 sum rounded once to bf16:
     the plain residual step (x + f(x)) of a decoder stage.  The model's own blocks mix
