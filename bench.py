@@ -26,6 +26,11 @@ Printed JSON line (one):
               GB/s, and MFMA utilisation = 6*D*I*(T*k + T) flops / time against
               the dense FP8 (5.0 PFLOP/s, the rate of an e4m3 x e2m1 scaled
               MFMA) and FP4 (10.1 PFLOP/s) peaks
+  fp8_gemv    the FP8 linear at the dense projection shapes (packed and row-major)
+  sparse_attn sparse attention at 64 heads of 512, topk 640: decode B = 1, 4, 8
+              (µs, gathered-row GB/s) and prefill S = 512, 2048 (bf16 MFMA
+              utilisation)
+  decode_stage 12 blocks of norms, projections and MoE in one graph per step
 """
 
 from __future__ import annotations
@@ -45,6 +50,7 @@ METRIC = "MoE layer µs + HBM GB/s (decode T=1-8); FP4 MFMA util (prefill T=2048
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 FP4_PEAK_TFLOPS = 10100.0
+BF16_PEAK_TFLOPS = 2500.0
 D, I, E, K_TOP = 4096, 2048, 256, 6
 ROUTED_EXPERT_BYTES = 3 * (I * D // 2) + 3 * (I * D // 32)          # 13,369,344
 SHARED_BYTES = 3 * I * D + 3 * (I // 128) * (D // 128)              # 25,167,360
@@ -88,6 +94,8 @@ def parse():
                     help="skip the decode stage (MoE + FP8 projections + norms, one graph per step)")
     ap.add_argument("--no-gemv", action="store_true",
                     help="skip the FP8 linear (dense projection shapes) measurement")
+    ap.add_argument("--no-attn", action="store_true",
+                    help="skip the sparse attention measurement")
     ap.add_argument("--prefill", default="128,512,2048",
                     help="comma-separated prefill T values ('' to skip)")
     ap.add_argument("--prefill-layers", type=int, default=3)
@@ -225,6 +233,31 @@ GEMV_TS = (1, 4, 8, 128)
 GEMV_ROTATE_BYTES = 640 << 20   # weight copies per shape: more than the 256 MB Infinity Cache
 
 
+def graph_timed(launches, reps):
+    """Mean µs of one replay of a graph holding ``launches()`` (warmed eagerly on a
+    side stream, captured, replayed once), HIP events around ``reps`` replays."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        launches()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launches()
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / reps
+
+
 def gemv_bytes(N: int, K: int, T: int) -> int:
     # e4m3 weight + fp32 128x128 block scales + bf16 x read + bf16 y written
     return N * K + 4 * ((N + 127) // 128) * ((K + 127) // 128) + 2 * T * K + 2 * T * N
@@ -246,26 +279,6 @@ def measure_gemv(dev, reps=5):
 
     from wanferenz_amd import _native as N
     from wanferenz_amd import kernels, synth
-
-    def timed(launches):
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            launches()
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            launches()
-        g.replay()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(reps):
-            g.replay()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) * 1000.0 / reps
 
     res = {}
     for Nn, K in GEMV_SHAPES:
@@ -295,7 +308,7 @@ def measure_gemv(dev, reps=5):
                         for r in range(R):
                             N.call("wz_fp8_linear", N.ptr(x), N.ptr(pool[r]), N.ptr(sc[r]), N.ptr(y), T, Nn, K,
                                    N.WZ_SCALE_UE8M0_F32, N.WZ_WSCALE_F32, st)
-                us = timed(launches) / R
+                us = graph_timed(launches, reps) / R
                 gbs = gemv_bytes(Nn, K, T) / (us * 1e-6) / 1e9
                 row[str(T)] = {"us": round(us, 2), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                                "TFLOP_s": round(2.0 * T * Nn * K / (us * 1e-6) / 1e12, 2)}
@@ -369,6 +382,73 @@ def measure_stage(layers, dev, T=4, steps=256, warmup=16):
             "us_per_block": round(us / nb, 2), "tokens_per_s": round(T * steps / secs, 1),
             "mean_distinct_experts": round(U_mean, 2), "bytes_per_step": int(step_bytes),
             "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+ATTN_H, ATTN_D, ATTN_TOPK, ATTN_WIN = 64, 512, 640, 128
+ATTN_CACHE = ATTN_WIN + 65536 // 4   # window + compressed rows of a 64K context at ratio 4
+
+
+def measure_attn(dev, reps=10):
+    """sparse_attn at the V4-Flash attention shape: 64 heads of 512, 640 gathered
+    rows per query (the 128-row window + 512 selected compressed rows).
+
+    decode: B sequences x 1 query over a cache of 128 + 16384 rows; the window
+    indices are the 128 window rows, the selected ones 512 distinct random rows
+    of the compressed part.  Enough (kv, index) copies rotate that their caches
+    total >= 640 MB.  Algorithmic bytes per query: the 640 gathered rows + q + o
+    + the indices.  prefill: one sequence of S queries over S + S/4 rows, every
+    query with 640 valid random indices (no causal -1 entries: the full work).
+    FLOPs per query: 4 * H * D * topk (S = QK^T and O = PV).
+    """
+    import torch
+
+    from wanferenz_amd import _native as N
+    from wanferenz_amd import kernels
+
+    g = torch.Generator().manual_seed(7)
+    H, Dh, K, W = ATTN_H, ATTN_D, ATTN_TOPK, ATTN_WIN
+
+    def case(B, S, n, R, prefill):
+        q = (torch.randn(B, S, H, Dh, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+        sink = torch.randn(H, generator=g).to(dev)
+        o = torch.empty_like(q)
+        kvs, idxs = [], []
+        for _ in range(R):
+            kvs.append((torch.randn(B, n, Dh, generator=g)).to(torch.bfloat16).to(dev))
+            if prefill:
+                ix = torch.stack([torch.randperm(n, generator=g)[:K] for _ in range(B * S)])
+            else:
+                ix = torch.stack([torch.cat([torch.arange(W), W + torch.randperm(n - W, generator=g)[:K - W]])
+                                  for _ in range(B * S)])
+            idxs.append(ix.view(B, S, K).to(torch.int32).to(dev))
+
+        wsb = kernels.sparse_attn_workspace_bytes(B, S, H, Dh, K)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+
+        def launches():
+            st = N.stream_handle(dev)
+            for kv, ix in zip(kvs, idxs):
+                N.call("wz_sparse_attn", N.ptr(q), N.ptr(kv), N.ptr(sink), N.ptr(ix), N.ptr(o), B, S, H, Dh, n, K,
+                       Dh ** -0.5, N.ptr(ws) if wsb else None, wsb, st)
+
+        us = graph_timed(launches, reps) / R
+        nq = B * S
+        byts = (n * B * Dh * 2 if prefill else nq * K * Dh * 2) + nq * (4 * H * Dh + 4 * K)
+        fl = 4.0 * H * Dh * K * nq
+        return {"us": round(us, 2), "workgroups_per_query": max(1, wsb // max(1, B * S * (H // 64) * (128 + 64 * Dh) * 4)),
+                "GB_s": round(byts / (us * 1e-6) / 1e9, 1),
+                "hbm_frac": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "TFLOP_s": round(fl / (us * 1e-6) / 1e12, 2),
+                "mfma_frac_bf16": round(fl / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+
+    res = {"shape": f"H={H} D={Dh} topk={K} (window {W} + {K - W} selected)"}
+    for B in (1, 4, 8):
+        per = B * ATTN_CACHE * Dh * 2
+        res[f"decode_B{B}"] = case(B, 1, ATTN_CACHE, max(2, -(-GEMV_ROTATE_BYTES // per)), False)
+    for S in (512, 2048):
+        res[f"prefill_S{S}"] = case(1, S, S + S // 4, 2, True)
+    torch.cuda.empty_cache()
+    return res
 
 
 def prefill_flops(T: int) -> float:
@@ -520,6 +600,8 @@ def main():
         out["prefill"] = measure_prefill(layers[:max(1, args.prefill_layers)], Ts, dev)
     if not args.no_gemv:
         out["fp8_gemv"] = measure_gemv(dev)
+    if not args.no_attn:
+        out["sparse_attn"] = measure_attn(dev)
     if not args.no_stage:
         out["decode_stage"] = measure_stage(layers, dev, T=args.T)
     if not args.no_cpu:

@@ -197,6 +197,22 @@ int wz_add_bf16(const void* a, const void* b, void* out, int64_t n, hipStream_t 
 int wz_rmsnorm_quant(const void* x_bf16, const float* weight, void* q_e4m3, void* s, int64_t T,
                      int64_t D, float eps, int scale_kind, hipStream_t stream);
 
+/* Sparse attention over gathered KV rows — sparse_attn(q, kv, attn_sink, topk_idxs,
+ * softmax_scale), torch_ops.py:114-146 / reference.py:314-418: blockwise online
+ * softmax with a per-head sink logit in the denominator, K = V = kv (one KV head).
+ * q [B, S, H, D] bf16 (H % 16 == 0, D in {128, 256, 512}), kv [B, N, D] bf16,
+ * attn_sink [H] fp32, topk_idxs [B, S, topk] int32 (-1 or >= N: unused) ->
+ * o [B, S, H, D] bf16; q, kv, o 16-byte aligned.  A query whose first 64 indices
+ * are all unused gets NaN, as in the reference.  With H % 64 == 0 and few queries
+ * the 64-index blocks of a query are split over workgroups whose partial results
+ * go to `workspace` (wz_sparse_attn_workspace_bytes; 0 = no split at this shape):
+ * pass NULL to compute every query in one workgroup instead (topk <= 2048). */
+int64_t wz_sparse_attn_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t D, int64_t topk);
+int wz_sparse_attn(const void* q_bf16, const void* kv_bf16, const float* attn_sink,
+                   const int32_t* topk_idxs, void* o_bf16, int64_t B, int64_t S, int64_t H,
+                   int64_t D, int64_t N, int64_t topk, float softmax_scale, void* workspace,
+                   int64_t workspace_bytes, hipStream_t stream);
+
 /* The FP8 wire format of a pipeline-stage boundary — _pack_t / _unpack_t
  * (serving/chain.py:208-222): per row scale = bf16(clamp(amax/448, 1e-8, bf16 max)),
  * q = e4m3(clamp(x/scale, +-448)); unpack y = bf16(q * scale).  x, y [M, D] bf16,

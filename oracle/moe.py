@@ -366,3 +366,41 @@ def max_rel_err(got: np.ndarray, ref: np.ndarray) -> float:
 
 
 __all__ = [n for n in dir() if not n.startswith("_") and n not in ("annotations", "math")]
+
+
+def sparse_attn(q: np.ndarray, kv: np.ndarray, attn_sink: np.ndarray, topk_idxs: np.ndarray,
+                softmax_scale: float, block: int = 64) -> np.ndarray:
+    """Sparse attention over gathered rows (torch_ops.py:114-146), float32 as the
+    reference's CPU path: blockwise online softmax with the sink term in the
+    denominator, K = V = kv.  q [b, s, h, d], kv [b, n, d] (float32 holding bf16
+    values), attn_sink [h], topk_idxs [b, s, topk] (-1 = unused).  Returns bf16
+    values as float32 [b, s, h, d]."""
+    q = np.asarray(q, np.float32)
+    kv = np.asarray(kv, np.float32)
+    b, s, h, d = q.shape
+    topk = topk_idxs.shape[-1]
+    acc = np.zeros((b, s, h, d), np.float32)
+    sum_exp = np.zeros((b, s, h), np.float32)
+    m = np.full((b, s, h), -np.inf, np.float32)
+    bi = np.arange(b)[:, None, None]
+    with np.errstate(invalid="ignore", over="ignore"):
+        for t in range(0, max(topk, 1), block):
+            n = min(block, topk - t)
+            idx = np.full((b, s, block), -1, np.int64)
+            if n > 0:
+                idx[..., :n] = topk_idxs[..., t:t + n]
+            valid = idx >= 0
+            g = kv[bi, np.maximum(idx, 0)]
+            g = np.where(valid[..., None], g, np.float32(0))
+            sc = (np.einsum("bshd,bstd->bsht", q, g).astype(np.float32) * np.float32(softmax_scale))
+            sc = np.where(valid[:, :, None, :], sc, -np.inf).astype(np.float32)
+            m_prev = m
+            m = np.maximum(m, sc.max(-1))
+            resc = np.exp(m_prev - m).astype(np.float32)
+            resc = np.where(np.isnan(resc), np.float32(1), resc)
+            p = np.exp(sc - m[..., None]).astype(np.float32)
+            sum_exp = (sum_exp * resc + p.sum(-1)).astype(np.float32)
+            acc = (acc * resc[..., None] + np.einsum("bsht,bstd->bshd", p, g)).astype(np.float32)
+        sum_exp = (sum_exp + np.exp(np.asarray(attn_sink, np.float32).reshape(1, 1, h) - m)).astype(np.float32)
+        return bf16_round((acc / sum_exp[..., None]).astype(np.float32))
+

@@ -65,11 +65,12 @@ def test_unservable_layers_decline_to_the_kept_forward(mod, why):
 
 def test_kernel_install_rebinds_module_globals():
     m = types.ModuleType("kernels_host")
-    orig = {n: (lambda *a, **k: None) for n in ("act_quant", "fp8_gemm", "fp4_gemm")}
+    orig = {n: (lambda *a, **k: None) for n in ("act_quant", "fp8_gemm", "fp4_gemm", "sparse_attn")}
     for n, f in orig.items():
         setattr(m, n, f)
     assert kernels.install(m) is True
     assert m.act_quant is kernels.act_quant and m.fp8_gemm is kernels.fp8_gemm and m.fp4_gemm is kernels.fp4_gemm
+    assert m.sparse_attn is kernels.sparse_attn
     assert kernels.install(m) is False
     assert kernels.uninstall(m) is True
     assert all(getattr(m, n) is f for n, f in orig.items())

@@ -38,6 +38,8 @@ SIGNATURES = {
     "wz_add_bf16": (_I, [_P, _P, _P, _I64, _P]),
     "wz_rmsnorm_quant": (_I, [_P, _P, _P, _P, _I64, _I64, _F, _I, _P]),
     "wz_fp8_wire_pack": (_I, [_P, _P, _P, _I64, _I64, _P]),
+    "wz_sparse_attn_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "wz_sparse_attn": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P]),
     "wz_fp8_wire_unpack": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "wz_synth_fill": (_I, [_P, _I64, ctypes.c_uint64, _I64, _I, ctypes.c_double, ctypes.c_double, _P]),
     "wz_prof_begin": (_I, [_I]),

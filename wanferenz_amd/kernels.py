@@ -5,7 +5,8 @@ sparse_attn, hc_split_sinkhorn`` from ``wanferenz.kernels.reference``
 (wanferenz/model/architecture.py:12-19) and resolves them as module globals
 at call time, so rebinding them on the loaded model module redirects every
 FP8 / FP4 linear (the precedent is wanferenz/kernels/fp8_vector.py:476-485).
-:func:`install` does that for the three functions on this path.
+:func:`install` does that for the four functions on this path (all but
+hc_split_sinkhorn).
 
 Signatures, argument meaning and error behaviour follow
 wanferenz/kernels/reference.py:117-146 (act_quant), :292-311 (fp8_gemm) and
@@ -218,6 +219,42 @@ def rms_norm_quant(x, weight, eps=1e-6, scale_fmt="ue8m0", scale_dtype=_E8M0):
     return q, s
 
 
+def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale, workspace=None):
+    """sparse_attn (torch_ops.py:114-146, reference.py:397-418): q [b, s, h, d] bf16,
+    kv [b, n, d] bf16, attn_sink [h] fp32, topk_idxs [b, s, topk] int32 -> [b, s, h, d]
+    in q's dtype.  Head counts that are not a multiple of 16 are padded with zero
+    heads, as the reference's GPU wrapper does (reference.py:406-416).  With few
+    queries the index blocks are split over workgroups whose partials need
+    ``sparse_attn_workspace_bytes`` of device memory: ``workspace`` (a uint8 tensor
+    at least that large) is used when given, else one is allocated."""
+    _require_cuda(q, kv, attn_sink, topk_idxs)
+    b, s, h, d = q.shape
+    if q.dtype != torch.bfloat16 or kv.dtype != torch.bfloat16:
+        raise TypeError(f"sparse_attn: bf16 q and kv expected (got {q.dtype}, {kv.dtype})")
+    hp = (h + 15) // 16 * 16
+    if hp != h:
+        q = torch.cat([q, q.new_zeros(b, s, hp - h, d)], dim=2)
+        attn_sink = torch.cat([attn_sink, attn_sink.new_zeros(hp - h)])
+    q = q.contiguous()
+    kv = kv.contiguous()
+    sink = attn_sink.float().contiguous()
+    idx = topk_idxs.to(torch.int32).contiguous()
+    topk = idx.size(-1)
+    o = torch.empty_like(q)
+    need = sparse_attn_workspace_bytes(b, s, hp, d, topk)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws, wsb = (N.ptr(workspace), workspace.numel()) if need else (None, 0)
+    N.call("wz_sparse_attn", N.ptr(q), N.ptr(kv), N.ptr(sink), N.ptr(idx), N.ptr(o), b, s, hp, d, kv.size(1),
+           topk, float(softmax_scale), ws, wsb, N.stream_handle(q.device))
+    return o if hp == h else o.narrow(2, 0, h).contiguous()
+
+
+def sparse_attn_workspace_bytes(b, s, h, d, topk) -> int:
+    """Device bytes of the split partials of a sparse_attn call (0: not split)."""
+    return int(N.lib().wz_sparse_attn_workspace_bytes(b, s, h, d, topk))
+
+
 def wire_pack(t):
     """_pack_t (serving/chain.py:208-217): bf16 [..., D] -> (e4m3 [..., D], bf16 scale [...])."""
     assert t.is_contiguous()
@@ -263,15 +300,22 @@ act_quant._v4_hip_act_quant = True
 _REF = {}
 
 
+def _installed():
+    return (("act_quant", act_quant), ("fp8_gemm", fp8_gemm), ("fp4_gemm", fp4_gemm), ("sparse_attn", sparse_attn))
+
+
 def install(mod) -> bool:
-    """Rebind act_quant / fp8_gemm / fp4_gemm on a loaded reference model module.
+    """Rebind act_quant / fp8_gemm / fp4_gemm / sparse_attn on a loaded reference
+    model module (each one the module has).
 
     Idempotent via the marker attributes; the replaced functions are kept in
     ``_REF`` (the reference's _REF_FP8_GEMM pattern, fp8_vector.py:472-491).
     """
     took = False
-    for name, fn in (("act_quant", act_quant), ("fp8_gemm", fp8_gemm), ("fp4_gemm", fp4_gemm)):
-        cur = getattr(mod, name, None)
+    for name, fn in _installed():
+        if not hasattr(mod, name):
+            continue
+        cur = getattr(mod, name)
         if cur is fn:
             continue
         _REF.setdefault(name, cur)
@@ -283,7 +327,7 @@ def install(mod) -> bool:
 def uninstall(mod) -> bool:
     """Restore the functions install() replaced on ``mod``."""
     took = False
-    for name, fn in (("act_quant", act_quant), ("fp8_gemm", fp8_gemm), ("fp4_gemm", fp4_gemm)):
+    for name, fn in _installed():
         if getattr(mod, name, None) is fn and name in _REF:
             setattr(mod, name, _REF.pop(name))
             took = True
