@@ -106,3 +106,19 @@ def test_bad_shapes_raise(gpu):
     with pytest.raises(N.WzError, match="head dim"):
         kernels.sparse_attn(q, kv, torch.zeros(64, device=gpu), torch.zeros(1, 1, 4, dtype=torch.int32, device=gpu),
                             1.0)
+
+
+@pytest.mark.parametrize("h,d,s", [(64, 512, 1), (64, 128, 600), (16, 256, 3)])
+def test_running_max_moves(gpu, h, d, s):
+    """Rows grow block by block (row r scaled by 1 + 5 (r // 64)), so the running
+    maximum moves by more than 8 at later blocks and the accumulated output is
+    rescaled on the way; split (few queries) and unsplit (600 queries) paths."""
+    topk = 320
+    q, kv, sink, idx = _inputs(21 + h + d, 1, s, h, d, topk, topk, invalid=0.0)
+    grow = (1.0 + 5.0 * (np.arange(topk) // 64)).astype(np.float32)
+    kv = om.bf16_round((kv * grow[None, :, None]).astype(np.float32))
+    idx[:] = np.arange(topk, dtype=np.int32)
+    idx[..., 70] = -1  # an unused slot inside a later block as well
+    scale = d ** -0.5
+    ref = om.sparse_attn(q, kv, sink, idx, scale)
+    _check(_run(gpu, q, kv, sink, idx, scale), ref)

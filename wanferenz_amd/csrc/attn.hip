@@ -19,7 +19,6 @@ typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
 constexpr int kAttnBlock = 64;     // indices per block (the reference's SPARSE_ATTN_BLOCK)
 constexpr int kAttnIdxCap = 2048;  // indices one workgroup covers (32 blocks)
 constexpr int kAttnMaxSplit = 64;  // workgroups one query's blocks are split over
-constexpr int kKsPadB = 16;        // LDS bytes of padding after each 1 KB of KV rows
 constexpr float kLazyMax = 8.0f;   // the running max moves when a block exceeds it by more
 
 __device__ __forceinline__ v4f mfma_bf16_32(v8s_t a, v8s_t b, v4f c) {
@@ -30,16 +29,22 @@ __device__ __forceinline__ v4f mfma_bf16_32(v8s_t a, v8s_t b, v4f c) {
 // Floats of one (query, 64 heads, split) partial: m[64], l[64], O[64][D].
 __host__ __device__ constexpr int64_t attn_part_floats(int d) { return 128 + 64 * int64_t(d); }
 
-// LDS image of one block of 64 KV rows: each 1 KB that one wave's buffer load
-// fills (1024 / (2D) rows), followed by kKsPadB bytes.
+// LDS image of one block of 64 KV rows, row-major, no padding.  The 16-byte
+// chunks of row r sit XOR-swizzled (chunk c at slot c ^ swz(r)), so that both
+// read patterns are free of bank conflicts: 16 rows reading one chunk (the K
+// operand of S^T) land on 16 distinct 4-bank groups, and 8 rows reading two
+// adjacent chunks (the transpose reads of V) on 16 distinct groups as well.
 template <int D>
 struct KsLayout {
-  static constexpr int RB = 2 * D;            // bytes per row
-  static constexpr int RPI = 1024 / RB;       // rows per 1 KB load
-  static constexpr int GB = 1024 + kKsPadB;   // LDS bytes per load
-  static constexpr int NG = kAttnBlock / RPI; // loads per block
-  static constexpr int BYTES = NG * GB;
-  static __device__ __forceinline__ int off(int row) { return (row / RPI) * GB + (row % RPI) * RB; }
+  static constexpr int RB = 2 * D;             // bytes per row
+  static constexpr int RPI = 1024 / RB;        // rows per 1 KB load
+  static constexpr int NG = kAttnBlock / RPI;  // loads per block
+  static constexpr int BYTES = kAttnBlock * RB;
+  static __device__ __forceinline__ int swz(int row) { return ((row & 7) << 1) ^ ((row >> 3) & 1); }
+  // byte address of element `col` (a multiple of 4) of `row`
+  static __device__ __forceinline__ int at(int row, int col) {
+    return row * RB + (((col >> 3) ^ swz(row)) << 4) + ((col & 7) << 1);
+  }
 };
 
 // One 16-byte-per-lane buffer load straight into LDS at lds_base + 16 * lane.
@@ -56,6 +61,14 @@ __device__ __forceinline__ void load_lds_16(__amdgpu_buffer_rsrc_t rsrc, uint32_
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return uint32_t(f32_to_bf16(a)) | (uint32_t(f32_to_bf16(b)) << 16);
+}
+
+// Two floats -> packed bf16 pair with the hardware converter (round to nearest
+// even, as f32_to_bf16; a NaN stays a NaN).
+__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
 // One workgroup per (query, 64 heads, range of 64-index blocks), 4 waves;
@@ -92,6 +105,7 @@ __global__ __launch_bounds__(256, 1) void sparse_attn_kernel(const uint16_t* __r
   constexpr int KC = D / 32;  // 32-wide d chunks of S
   constexpr int NT = D / 16;  // 16-column tiles of O
   static_assert(L::NG % 4 == 0, "a block's loads must split evenly over the 4 waves");
+  static_assert(L::RB / 16 >= 16, "the swizzle permutes 16 chunks of a row");
   __shared__ __align__(16) uint8_t ksb[2][L::BYTES];
   __shared__ int s_idx[kAttnIdxCap];
   __shared__ int s_any;
@@ -107,6 +121,12 @@ __global__ __launch_bounds__(256, 1) void sparse_attn_kernel(const uint16_t* __r
   const int hg0 = hq * 64 + 16 * wave;
   const bool active = hg0 < H;  // H % 16 == 0: the whole head group exists
 
+  // Q fragments first (they do not wait for the indices; B operand of S^T): lane (head nl, group g) holds d 32cc + 8g .. +8
+  v8s_t qb[KC];
+  const uint16_t* qrow = q + (int64_t(bs) * H + (active ? hg0 : 0) + nl) * D;
+#pragma unroll
+  for (int cc = 0; cc < KC; ++cc) qb[cc] = *reinterpret_cast<const v8s_t*>(qrow + 32 * cc + 8 * g);
+
   const int32_t* ib = idx + int64_t(bs) * topk + int64_t(blk0) * kAttnBlock;
   if (tid == 0) s_any = 0;
   for (int j = tid; j < nb * kAttnBlock; j += 256) {
@@ -121,23 +141,21 @@ __global__ __launch_bounds__(256, 1) void sparse_attn_kernel(const uint16_t* __r
   const __amdgpu_buffer_rsrc_t kv_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(kv + int64_t(b) * N * D), short(0), int(int64_t(N) * L::RB), 0x00020000);
   const uint32_t ks_lds = uint32_t(uintptr_t((__attribute__((address_space(3))) uint8_t*)&ksb[0][0]));
+  // Load gi of a block fills rows gi * RPI .. +RPI; lane i writes slot i & (RB/16 - 1)
+  // of row gi * RPI + i / (RB/16), so it fetches that row's chunk slot ^ swz(row).
   auto issue = [&](int t) {
-    const int rin = lane / (L::RB / 16), ch = lane % (L::RB / 16);
+    const int rin = lane / (L::RB / 16), slot = lane % (L::RB / 16);
+    int ri[L::NG / 4];  // every row index first: the asm loads below order memory accesses
+#pragma unroll
+    for (int j = 0; j < L::NG / 4; ++j) ri[j] = s_idx[t * kAttnBlock + (j * 4 + wave) * L::RPI + rin];
 #pragma unroll
     for (int j = 0; j < L::NG / 4; ++j) {
-      const int gi = j * 4 + wave;
-      const int ri = s_idx[t * kAttnBlock + gi * L::RPI + rin];
-      const uint32_t vo = ri < 0 ? 0x80000000u : uint32_t(ri) * L::RB + ch * 16;
-      load_lds_16(kv_rsrc, __builtin_amdgcn_readfirstlane(ks_lds + (t & 1) * L::BYTES + gi * L::GB), vo);
+      const int gi = j * 4 + wave, row = gi * L::RPI + rin;
+      const uint32_t vo = ri[j] < 0 ? 0x80000000u : uint32_t(ri[j]) * L::RB + ((slot ^ L::swz(row)) << 4);
+      load_lds_16(kv_rsrc, __builtin_amdgcn_readfirstlane(ks_lds + (t & 1) * L::BYTES + gi * 1024), vo);
     }
   };
   issue(0);
-
-  // Q fragments (B operand of S^T): lane (head nl, group g) holds d 32cc + 8g .. +8
-  v8s_t qb[KC];
-  const uint16_t* qrow = q + (int64_t(bs) * H + (active ? hg0 : 0) + nl) * D;
-#pragma unroll
-  for (int cc = 0; cc < KC; ++cc) qb[cc] = *reinterpret_cast<const v8s_t*>(qrow + 32 * cc + 8 * g);
 
   v4f acc[NT];  // acc[nt][i] = O[head 4g + i][16nt + nl]
 #pragma unroll
@@ -153,17 +171,25 @@ __global__ __launch_bounds__(256, 1) void sparse_attn_kernel(const uint16_t* __r
     if (!active) continue;
 
     // ---- S^T[rows, 16 heads]: sacc[rt][i] = S[row 16rt + 4g + i][head nl] ----
+    // K fragments are read two d chunks ahead of their MFMAs (three buffers)
     v4f sacc[4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) sacc[rt] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int cc = 0; cc < KC; ++cc) {
-      v8s_t ka[4];
+    v8s_t kf[3][4];
+    auto kload = [&](int cc, v8s_t* dst) {
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt)
-        ka[rt] = *reinterpret_cast<const v8s_t*>(ks + L::off(16 * rt + nl) + 2 * (32 * cc + 8 * g));
+        dst[rt] = *reinterpret_cast<const v8s_t*>(ks + L::at(16 * rt + nl, 32 * cc + 8 * g));
+    };
+    kload(0, kf[0]);
+    kload(1, kf[1]);
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) sacc[rt] = mfma_bf16_32(ka[rt], qb[cc], sacc[rt]);
+    for (int cc = 0; cc < KC; ++cc) {
+      if (cc + 2 < KC) kload(cc + 2, kf[(cc + 2) % 3]);
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads two chunks ahead of their use
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) sacc[rt] = mfma_bf16_32(kf[cc % 3][rt], qb[cc], sacc[rt]);
+      __builtin_amdgcn_sched_barrier(0);
     }
     float bmax = -INFINITY;
 #pragma unroll
@@ -179,14 +205,24 @@ __global__ __launch_bounds__(256, 1) void sparse_attn_kernel(const uint16_t* __r
     const bool bump = bmax > m_use + kLazyMax;
     if (__ballot(bump)) {
       const float m_new = bump ? bmax : m_use;
-      const float resc = !bump ? 1.0f : (m_use == -INFINITY ? 0.0f : __expf(m_use - m_new));
+      const bool fresh = m_use == -INFINITY;  // nothing accumulated yet for this head
+      const float resc = !bump ? 1.0f : (fresh ? 0.0f : __expf(m_use - m_new));
       l_run *= resc;
       m_use = m_new;
+      // O[h, :] *= resc(h) on the matrix core, so the accumulators stay where the
+      // P V products keep them: O += A_i B_i (V_MFMA_F32_16X16X4_F32, k = lane
+      // group g) with B_i[g][n] = O[4g + i][n] (component i of each lane) and
+      // A_i[m][g] = resc(m) - 1 where m = 4g + i, else 0; step i only changes
+      // rows = i (mod 4), which later steps do not read.  Skipped while every
+      // bumped head is fresh (its accumulators are still zero).
+      if (__ballot(bump && !fresh)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float ri = __shfl(resc, 4 * g + i, kWave);  // factor of head 4g + i
+        for (int i = 0; i < 4; ++i) {
+          const float ai = nl == 4 * g + i ? resc - 1.0f : 0.0f;
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[nt][i] *= ri;
+          for (int nt = 0; nt < NT; ++nt)
+            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(ai, acc[nt][i], acc[nt], 0, 0, 0);
+        }
       }
     }
     v8s_t pa[2];
@@ -199,22 +235,33 @@ __global__ __launch_bounds__(256, 1) void sparse_attn_kernel(const uint16_t* __r
         pv[4 + i] = sacc[2 * kc + 1][i] == -INFINITY ? 0.0f : __expf(sacc[2 * kc + 1][i] - m_use);
         l_run += pv[i] + pv[4 + i];
       }
-      const uint4 u = make_uint4(pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
-                                 pack_bf16x2(pv[6], pv[7]));
+      const uint4 u = make_uint4(cvt_bf16x2(pv[0], pv[1]), cvt_bf16x2(pv[2], pv[3]), cvt_bf16x2(pv[4], pv[5]),
+                                 cvt_bf16x2(pv[6], pv[7]));
       pa[kc] = __builtin_bit_cast(v8s_t, u);
     }
 
     // ---- O[16 heads, D] += P[16 heads, 64 rows] V[64 rows, D] ----
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int col2 = 2 * (16 * nt + 4 * (nl & 3));
+    // V fragments are read two column tiles ahead of their MFMAs (three buffers)
+    v8s_t vf[3][2];
+    auto vload = [&](int nt, v8s_t* dst) {
+      const int col = 16 * nt + 4 * (nl & 3);
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
         const int row = 32 * kc + 4 * g + (nl >> 2);
-        const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t*)(ks + L::off(row) + col2));
-        const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t*)(ks + L::off(row + 16) + col2));
-        acc[nt] = mfma_bf16_32(pa[kc], __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), acc[nt]);
+        const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t*)(ks + L::at(row, col)));
+        const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t*)(ks + L::at(row + 16, col)));
+        dst[kc] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
+    };
+    vload(0, vf[0]);
+    vload(1, vf[1]);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (nt + 2 < NT) vload(nt + 2, vf[(nt + 2) % 3]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) acc[nt] = mfma_bf16_32(pa[kc], vf[nt % 3][kc], acc[nt]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   if (!active) return;
@@ -223,14 +270,20 @@ __global__ __launch_bounds__(256, 1) void sparse_attn_kernel(const uint16_t* __r
   l_run += __shfl_xor(l_run, 32, kWave);
   const bool poisoned = blk0 == 0 && s_any == 0;
   if (!SPLIT) {
+    // normalise by the sum (sink term included): one reciprocal per head, then
+    // products (within 1 fp32 ulp of the quotient, before the bf16 rounding)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int hd = hg0 + 4 * g + i;
       const float lh = __shfl(l_run, 4 * g + i, kWave), mh = __shfl(m_use, 4 * g + i, kWave);
-      const float tot = poisoned ? __builtin_nanf("") : lh + __expf(sink[hd] - mh);
+      const float inv = poisoned ? __builtin_nanf("") : 1.0f / (lh + __expf(sink[hd] - mh));
       uint16_t* orow = o + (int64_t(bs) * H + hd) * D;
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) orow[16 * nt + nl] = f32_to_bf16(acc[nt][i] / tot);
+      for (int nt = 0; nt < NT; nt += 2) {
+        const uint32_t pr = cvt_bf16x2(acc[nt][i] * inv, acc[nt + 1][i] * inv);
+        orow[16 * nt + nl] = uint16_t(pr & 0xFFFFu);
+        orow[16 * nt + 16 + nl] = uint16_t(pr >> 16);
+      }
     }
   } else {
     float* pp = part + int64_t(blockIdx.x) * attn_part_floats(D);
@@ -249,11 +302,15 @@ __global__ __launch_bounds__(256, 1) void sparse_attn_kernel(const uint16_t* __r
 
 // Merge the (m, l, O) partials of 4 heads of one (query, 64 heads):
 // o = sum_c e^(m_c - M) O_c / (sum_c e^(m_c - M) l_c + e^(sink - M)), M = max_c m_c.
+// Every partial's (m, l) is loaded at once, then the O partials in batches of
+// 16 splits, so each phase costs one memory round trip.
 template <int D>
 __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const float* __restrict__ part,
                                                                   const float* __restrict__ sink,
                                                                   uint16_t* __restrict__ o, int H, int nsplit) {
   constexpr int64_t PF = attn_part_floats(D);
+  constexpr int kBatch = 16;
+  __shared__ float s_m[4][kAttnMaxSplit], s_l[4][kAttnMaxSplit];
   __shared__ float wts[4][kAttnMaxSplit];
   __shared__ float inv[4];
   const int tid = threadIdx.x, HQ = (H + 63) / 64;
@@ -262,15 +319,20 @@ __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const float* _
   const int hl0 = 4 * k;
   if (hq * 64 + hl0 >= H) return;  // heads come in groups of 16 (whole workgroup)
   const float* pb = part + int64_t(qh) * nsplit * PF;
+  for (int j = tid; j < 4 * nsplit; j += 256) {
+    const int h4 = j & 3, cs = j >> 2;
+    s_m[h4][cs] = pb[cs * PF + hl0 + h4];
+    s_l[h4][cs] = pb[cs * PF + 64 + hl0 + h4];
+  }
+  __syncthreads();
   if (tid < 4) {
-    const int hl = hl0 + tid;
     float M = -INFINITY;
-    for (int cs = 0; cs < nsplit; ++cs) M = fmaxf(M, pb[cs * PF + hl]);
-    float den = __expf(sink[hq * 64 + hl] - M);
+    for (int cs = 0; cs < nsplit; ++cs) M = fmaxf(M, s_m[tid][cs]);
+    float den = __expf(sink[hq * 64 + hl0 + tid] - M);
     for (int cs = 0; cs < nsplit; ++cs) {
-      const float w = __expf(pb[cs * PF + hl] - M);
+      const float w = __expf(s_m[tid][cs] - M);
       wts[tid][cs] = w;
-      den += w * pb[cs * PF + 64 + hl];
+      den += w * s_l[tid][cs];
     }
     inv[tid] = 1.0f / den;
   }
@@ -279,27 +341,19 @@ __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const float* _
     const int h4 = e / D, d = e % D;
     const float* src = pb + 128 + int64_t(hl0 + h4) * D + d;
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    int cs = 0;
-    for (; cs + 8 <= nsplit; cs += 8) {
-      float4 v[8];
+    for (int c0 = 0; c0 < nsplit; c0 += kBatch) {
+      float4 v[kBatch];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4*>(src + (cs + u) * PF);
+      for (int u = 0; u < kBatch; ++u)
+        v[u] = c0 + u < nsplit ? *reinterpret_cast<const float4*>(src + (c0 + u) * PF) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = wts[h4][cs + u];
+      for (int u = 0; u < kBatch; ++u) {
+        const float w = c0 + u < nsplit ? wts[h4][c0 + u] : 0.0f;
         a.x += w * v[u].x;
         a.y += w * v[u].y;
         a.z += w * v[u].z;
         a.w += w * v[u].w;
       }
-    }
-    for (; cs < nsplit; ++cs) {
-      const float4 v = *reinterpret_cast<const float4*>(src + cs * PF);
-      const float w = wts[h4][cs];
-      a.x += w * v.x;
-      a.y += w * v.y;
-      a.z += w * v.z;
-      a.w += w * v.w;
     }
     const float s = inv[h4];
     uint16_t* orow = o + (int64_t(bs) * H + hq * 64 + hl0 + h4) * D + d;
