@@ -688,6 +688,25 @@ __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws,
     gemm_tile_body<MODE, CHAIN, 4>(d, ws, T, tr, nt, a_s, as_s);
 }
 
+// Workgroups are dispatched to the XCDs round-robin (block b to XCD b % 8),
+// each XCD with its own L2.  The routed blocks [d0, d0 + n) are renumbered so
+// that each XCD takes one contiguous run of (M-tile, N-block) pairs: the
+// N-blocks of an M-tile then share its gathered activation rows in one L2, and
+// consecutive M-tiles of an expert (which read the same weight tiles) run on
+// the same XCD at about the same time.  A bijection on [d0, d0 + n) for any
+// XCD count, so only locality depends on the dispatch order.
+__device__ __forceinline__ int xcd_contiguous(int b, int d0, int n) {
+  constexpr int kXcds = 8;
+  const int x = b % kXcds;
+  int before = 0;  // routed blocks on the XCDs ahead of x
+  for (int y = 0; y < x; ++y) {
+    const int fy = d0 + ((y - d0) & (kXcds - 1));  // first routed block on XCD y
+    before += fy < d0 + n ? (d0 + n - fy + kXcds - 1) / kXcds : 0;
+  }
+  const int fx = d0 + ((x - d0) & (kXcds - 1));
+  return before + (b - fx) / kXcds;
+}
+
 // One launch serves the shared expert's dense tiles (block ids first, so the
 // few long-running shared tiles start early) and the routed experts' M-tiles.
 // W13 selects w1/w3 + SwiGLU or w2; CR / CS: scale chaining of routed / shared.
@@ -697,10 +716,14 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   __shared__ __align__(16) uint8_t a_s[3][kPM * kARow];
   __shared__ float as_s[3][kPM];
   const int b = blockIdx.x;
-  if (b < dense_blocks)
+  if (b < dense_blocks) {
     gemm_tile<W13 ? 1 : 3, CS>(d, ws, T, b / nblk_dense, b % nblk_dense, a_s, as_s);
-  else
-    gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, (b - dense_blocks) / nblk, (b - dense_blocks) % nblk, a_s, as_s);
+  } else {
+    const int n = ws.n_mt[0] * nblk;  // routed blocks with work
+    if (b - dense_blocks >= n) return;
+    const int r = xcd_contiguous(b, dense_blocks, n);
+    gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, r / nblk, r % nblk, a_s, as_s);
+  }
 }
 
 int launch_act_quant(const void* x, int64_t rows, int64_t K, uint8_t* q, void* s, int kind, hipStream_t stream);
