@@ -126,3 +126,26 @@ def test_last_error_is_per_thread():
     t.start()
     t.join()
     assert "scale kind" in seen[0] and _err() == mine
+
+
+def test_sparse_attn_workspace_and_argument_errors():
+    """wz_sparse_attn sizes its split partials on the host and rejects bad
+    arguments before any launch (the pointers below are never dereferenced)."""
+    L = N.lib()
+    # decode (one query, 64 heads of 512, 640 indices): 10 blocks, one workgroup each,
+    # partial = m[64] + l[64] + O[64][512] floats
+    assert L.wz_sparse_attn_workspace_bytes(1, 1, 64, 512, 640) == 10 * (128 + 64 * 512) * 4
+    assert L.wz_sparse_attn_workspace_bytes(1, 512, 64, 512, 640) == 0  # enough queries: no split
+    assert L.wz_sparse_attn_workspace_bytes(1, 1, 48, 512, 640) == 10 * (128 + 64 * 512) * 4  # 48 heads: one group
+    q, kv, sink, idx, o = 16, 32, 48, 64, 80  # aligned stand-ins
+
+    def call(B=1, S=1, H=64, D=512, Nn=100, topk=640, ws=None, wsb=0, qq=q):
+        return L.wz_sparse_attn(qq, kv, sink, idx, o, B, S, H, D, Nn, topk, 0.1, ws, wsb, None)
+
+    assert call(H=40) == -1 and "multiple of 16" in _err()
+    assert call(D=96) == -1 and "head dim" in _err()
+    assert call(qq=17) == -1 and "16-byte aligned" in _err()
+    assert call(ws=96, wsb=64) == -1 and "workspace of 64 bytes" in _err()
+    assert call(topk=4096) == -1 and "needs a workspace" in _err()
+    assert call(Nn=1 << 22) == -1 and "2 GiB" in _err()
+    assert call(B=0) == 0 and call(S=0) == 0  # no queries: nothing to do
