@@ -27,6 +27,7 @@ Printed JSON line (one):
               the dense FP8 (5.0 PFLOP/s, the rate of an e4m3 x e2m1 scaled
               MFMA) and FP4 (10.1 PFLOP/s) peaks
   fp8_gemv    the FP8 linear at the dense projection shapes (packed and row-major)
+  grouped_fp4 the grouped MXFP4 GEMM of the banked decode path (6 experts' w1|w3, w2)
   sparse_attn sparse attention at 64 heads of 512, topk 640: decode B = 1, 4, 8
               (µs, gathered-row GB/s) and prefill S = 512, 2048 (bf16 MFMA
               utilisation)
@@ -319,6 +320,43 @@ def measure_gemv(dev, reps=5):
     return res
 
 
+def measure_grouped_fp4(dev, reps=10):
+    """grouped_fp4_gemm at the banked decode shapes (fp4_grouped.py:297, 312):
+    G = 6 experts' w1|w3 (N = 2I, K = D) and w2 (N = D, K = I), one e4m3 row each,
+    rotating over >= 640 MB of weight copies.  Bytes: the G weight slices with
+    their e8m0 scales + the rows in and out."""
+    import torch
+
+    from wanferenz_amd import _native as N
+    from wanferenz_amd import synth
+
+    res = {}
+    G = K_TOP
+    for name, Nn, K in (("w13", 2 * I, D), ("w2", D, I)):
+        per = G * (Nn * K // 2 + Nn * K // 32)
+        R = max(2, -(-GEMV_ROTATE_BYTES // per))
+        w = torch.empty(R, G, Nn, K // 2, dtype=torch.uint8, device=dev)
+        synth.device_fill(w, synth.stream_key(1, synth.S_W13), synth.FILL_U8)
+        ws = torch.full((R, G, Nn, K // 32), 121, dtype=torch.uint8, device=dev)
+        a = torch.full((G, K), 0x38, dtype=torch.uint8, device=dev)  # e4m3 1.0
+        a_s = torch.ones(G, K // 128, dtype=torch.float32, device=dev)
+        c = torch.empty(G, Nn, dtype=torch.bfloat16, device=dev)
+
+        def launches():
+            st = N.stream_handle(dev)
+            for r in range(R):
+                N.call("wz_grouped_fp4_gemm", N.ptr(a), N.ptr(a_s), N.ptr(w[r]), N.ptr(ws[r]), N.ptr(c), G, Nn, K,
+                       N.WZ_SCALE_F32, st)
+
+        us = graph_timed(launches, reps) / R
+        byts = per + G * K + 4 * G * (K // 128) + 2 * G * Nn
+        res[name] = {"G": G, "N": Nn, "K": K, "us": round(us, 2), "GB_s": round(byts / (us * 1e-6) / 1e9, 1),
+                     "hbm_frac": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del w, ws
+        torch.cuda.empty_cache()
+    return res
+
+
 STAGE_Q, STAGE_WIDE = 1024, 16384
 
 
@@ -600,6 +638,7 @@ def main():
         out["prefill"] = measure_prefill(layers[:max(1, args.prefill_layers)], Ts, dev)
     if not args.no_gemv:
         out["fp8_gemv"] = measure_gemv(dev)
+        out["grouped_fp4"] = measure_grouped_fp4(dev)
     if not args.no_attn:
         out["sparse_attn"] = measure_attn(dev)
     if not args.no_stage:

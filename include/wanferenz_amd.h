@@ -97,6 +97,16 @@ int wz_fp4_gemm(const void* a_e4m3, const void* a_s, const void* w_fp4x2, const 
                 void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
                 hipStream_t stream);
 
+/* Grouped MXFP4 GEMM — grouped_fp4_gemm(a, a_s, w, w_s, scale_dtype),
+ * fp4_grouped.py:96-128: row g of a against its own weight, C[g, :] =
+ * dequant(a[g]) @ (e2m1(w[g]) * w_s[g])^T, i.e. fp4_gemm of one row per expert
+ * (the reference's CPU path loops fp4_gemm the same way, :112-121).
+ * a [G, K] e4m3 + a_s [G, K/128] (act_scale_kind as wz_fp4_gemm), w [G, N, K/2]
+ * e2m1x2 + w_s [G, N, K/32] e8m0 -> c [G, N] bf16; N % 16 == 0, K % 128 == 0. */
+int wz_grouped_fp4_gemm(const void* a_e4m3, const void* a_s, const void* w_fp4x2, const void* w_s_e8m0,
+                        void* c_bf16, int64_t G, int64_t N, int64_t K, int act_scale_kind,
+                        hipStream_t stream);
+
 /* One MoE layer (Gate + routed MXFP4 experts + FP8 shared expert + combine).
  * Mirrors MoE.forward — architecture.py:744-794, Gate.forward :696-718, Expert.forward :729-741,
  * on the expert-bank layout of fp4_grouped._relayout_moe (fp4_grouped.py:142-188). */

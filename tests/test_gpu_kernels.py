@@ -382,3 +382,27 @@ def test_rms_norm_quant_is_norm_then_act_quant(gpu, scale_fmt, scale_dtype, T, D
     assert np.array_equal(bytes8(q).reshape(T, D), rq)
     got_s = e8m0_decode(bytes8(s)) if scale_fmt else s.cpu().numpy()
     assert np.array_equal(got_s.reshape(rs.shape), rs)
+
+
+@pytest.mark.parametrize("act_fmt", ["ue8m0", None])
+@pytest.mark.parametrize("G,N,K", [(6, 4096, 4096), (6, 4096, 2048), (1, 256, 1024), (40, 128, 512)])
+def test_grouped_fp4_gemm(gpu, act_fmt, G, N, K):
+    """grouped_fp4_gemm (fp4_grouped.py:96-128): row g against its own expert weight.
+    Bit-equal to fp4_gemm of that row (the reference's CPU path computes it that way,
+    fp4_grouped.py:112-121) and to the oracle's fp4_gemm within the bf16 bar."""
+    xb = _x(G * 13 + N + K, G, K)
+    sd = torch.float8_e8m0fnu if act_fmt else torch.float32
+    q, s = kernels.act_quant(bf16_tensor(xb, gpu), 128, act_fmt, sd)
+    ws_ = [_fp4_weight(N * 5 + K + g, N, K) for g in range(G)]
+    w = np.stack([a for a, _ in ws_])
+    wsc = np.stack([b for _, b in ws_])
+    wt, wst = u8_tensor(w, gpu, torch.float4_e2m1fn_x2), u8_tensor(wsc, gpu, torch.float8_e8m0fnu)
+    c = kernels.grouped_fp4_gemm(q, s, wt, wst, sd)
+    got = f32_of_bf16(c)
+    rows = torch.cat([kernels.fp4_gemm(q[g:g + 1].contiguous(), s[g:g + 1].contiguous(), wt[g], wst[g], sd)
+                      for g in range(G)])
+    assert np.array_equal(bits16(c), bits16(rows))
+    rq, rs = om.act_quant(from_bf16_bits(xb), 128, act_fmt is not None)
+    ref = np.concatenate([om.fp4_gemm(rq[g:g + 1], rs[g:g + 1], w[g], e8m0_decode(wsc[g])) for g in range(G)])
+    rel, cos = _close(got, ref)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)

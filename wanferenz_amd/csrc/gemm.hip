@@ -21,16 +21,14 @@ namespace wz {
 constexpr int kGemmThreads = 256;
 constexpr int kUnroll = 8;
 
+// One workgroup's 16 output columns [n0, n0 + 16) for rows m_base .. m_base + 16 MT.
 template <int WF, bool A_BF16, int MT>
-__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(
-    const void* __restrict__ A, const void* __restrict__ As, int act_kind,
-    const uint8_t* __restrict__ W, const void* __restrict__ Ws, int w_kind,
-    uint16_t* __restrict__ C, int M, int N, int K) {
+__device__ __forceinline__ void skinny_body(const void* __restrict__ A, const void* __restrict__ As, int act_kind,
+                                            const uint8_t* __restrict__ W, const void* __restrict__ Ws, int w_kind,
+                                            uint16_t* __restrict__ C, int M, int N, int K, int m_base, int n0) {
   __shared__ float red[4][MT][kWave][4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nl = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16;
-  const int m_base = blockIdx.y * (16 * MT);
   const int nkb = K / 128;
   const int kb0 = (wave * nkb) / 4, kb1 = ((wave + 1) * nkb) / 4;
   const int ldw = WF == kFmtFp4 ? K / 2 : K;
@@ -104,6 +102,30 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(
       if (m < M) C[int64_t(m) * N + n0 + nl] = f32_to_bf16(v);
     }
   }
+}
+
+template <int WF, bool A_BF16, int MT>
+__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(
+    const void* __restrict__ A, const void* __restrict__ As, int act_kind,
+    const uint8_t* __restrict__ W, const void* __restrict__ Ws, int w_kind,
+    uint16_t* __restrict__ C, int M, int N, int K) {
+  skinny_body<WF, A_BF16, MT>(A, As, act_kind, W, Ws, w_kind, C, M, N, K, blockIdx.y * (16 * MT), blockIdx.x * 16);
+}
+
+// Row g of A against its own MXFP4 weight W[g] (the per-expert GEMV of the
+// banked decode path): blockIdx.y = g, each row one M=1 skinny product.
+__global__ __launch_bounds__(kGemmThreads) void grouped_fp4_kernel(const uint8_t* __restrict__ A,
+                                                                   const void* __restrict__ As, int act_kind,
+                                                                   const uint8_t* __restrict__ W,
+                                                                   const uint8_t* __restrict__ Ws,
+                                                                   uint16_t* __restrict__ C, int N, int K) {
+  const int64_t g = blockIdx.y;
+  const int nkb = K / 128;
+  const void* as_g = act_kind == WZ_SCALE_UE8M0
+                         ? static_cast<const void*>(static_cast<const uint8_t*>(As) + g * nkb)
+                         : static_cast<const void*>(static_cast<const float*>(As) + g * nkb);
+  skinny_body<kFmtFp4, false, 1>(A + g * K, as_g, act_kind, W + g * N * (K / 2), Ws + g * N * (K / 32),
+                                 WZ_WSCALE_E8M0, C + g * N, 1, N, K, 0, blockIdx.x * 16);
 }
 
 template <int WF, bool A_BF16>
@@ -181,4 +203,21 @@ extern "C" int wz_fp4_gemm(const void* a_e4m3, const void* a_s, const void* w_fp
     return set_error(WZ_EINVAL, "fp4_gemm: null pointer");
   return launch_skinny<kFmtFp4, false>(a_e4m3, a_s, act_scale_kind, w_fp4x2, w_s_e8m0,
                                        WZ_WSCALE_E8M0, c_bf16, M, N, K, stream, "fp4_gemm");
+}
+
+extern "C" int wz_grouped_fp4_gemm(const void* a_e4m3, const void* a_s, const void* w_fp4x2,
+                                   const void* w_s_e8m0, void* c_bf16, int64_t G, int64_t N, int64_t K,
+                                   int act_scale_kind, hipStream_t stream) {
+  using namespace wz;
+  if (int rc = check_dims("grouped_fp4_gemm", G, N, K)) return rc;
+  if (G > 65535) return set_error(WZ_EINVAL, "grouped_fp4_gemm: G=%lld rows exceed 65535", (long long)G);
+  if (act_scale_kind < 0 || act_scale_kind > 2)
+    return set_error(WZ_EINVAL, "grouped_fp4_gemm: bad scale kind %d", act_scale_kind);
+  if (G == 0) return WZ_OK;
+  if (!a_e4m3 || !a_s || !w_fp4x2 || !w_s_e8m0 || !c_bf16)
+    return set_error(WZ_EINVAL, "grouped_fp4_gemm: null pointer");
+  WZ_LAUNCH("grouped_fp4_gemm", stream, grouped_fp4_kernel, dim3(unsigned(N / 16), unsigned(G)), dim3(kGemmThreads), 0,
+            static_cast<const uint8_t*>(a_e4m3), a_s, act_scale_kind, static_cast<const uint8_t*>(w_fp4x2),
+            static_cast<const uint8_t*>(w_s_e8m0), static_cast<uint16_t*>(c_bf16), int(N), int(K));
+  return check_launch("grouped_fp4_gemm");
 }

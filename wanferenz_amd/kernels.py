@@ -124,6 +124,29 @@ def fp4_gemm(a, a_s, b, b_s, scale_dtype=torch.float32):
     return _finish(c)
 
 
+def grouped_fp4_gemm(a, a_s, w, w_s, scale_dtype=torch.float32):
+    """C[g, :] = dequant(a[g]) @ (e2m1(w[g]) * w_s[g])^T in bf16; fp4_grouped.py:96-128.
+
+    a [G, K] e4m3 with a_s [G, K/128], w [G, N, K/2] e2m1x2 with w_s [G, N, K/32]
+    e8m0 (the gathered bank slices of the banked decode path).  The contiguity
+    and N-tile assertions are the reference's; the reference's G <= 32 bound
+    (its A tile) does not apply here."""
+    assert a.is_contiguous() and w.is_contiguous(), "grouped fp4: a and w must be contiguous"
+    assert a_s.is_contiguous() and w_s.is_contiguous(), "grouped fp4: scales must be contiguous"
+    assert w.size(1) % 128 == 0, f"grouped fp4: N={w.size(1)} is not a whole number of 128-wide tiles"
+    _require_cuda(a, a_s, w, w_s)
+    if w_s.dtype != _E8M0:
+        raise TypeError(f"grouped_fp4_gemm: MXFP4 weight scales are e8m0, got {w_s.dtype}")
+    G, K = a.shape
+    Nn = w.size(1)
+    if w.size(0) != G or w.size(2) * 2 != K:
+        raise ValueError(f"grouped_fp4_gemm: a [{G}, {K}] against w {tuple(w.shape)}")
+    c = torch.empty(G, Nn, dtype=torch.bfloat16, device=a.device)
+    N.call("wz_grouped_fp4_gemm", N.ptr(a), N.ptr(a_s), N.ptr(w), N.ptr(w_s), N.ptr(c), G, Nn, K,
+           _scale_kind_of(a_s), N.stream_handle(a.device))
+    return _finish(c)
+
+
 def fp8_linear(x, weight, weight_scale, scale_fmt="ue8m0", scale_dtype=_E8M0):
     """linear() for an FP8 weight with act_quant fused into the GEMM (architecture.py:121-132)."""
     assert x.is_contiguous() and weight.is_contiguous() and weight_scale.is_contiguous()
