@@ -34,6 +34,26 @@ __device__ __forceinline__ AOp a_zero() {
 
 // Pre-quantised activation row (e4m3 [K]) with its block scales.
 // scale_kind: WZ_SCALE_F32 -> float scales; UE8M0 -> e8m0 bytes; UE8M0_F32 -> pow2 floats.
+// A operand of K-block kb from a row that exists: no null test, so a batch of
+// these loads can be issued together with the weight loads.
+__device__ __forceinline__ AOp a_from_fp8_row(const uint8_t* row, const void* srow, int kb, int g,
+                                              int scale_kind) {
+  AOp a = a_zero();
+  const uint8_t* p = row + kb * 128 + g * 16;
+  v4i lo = load16(p), hi = load16(p + 64);
+  a.v = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  if (scale_kind == WZ_SCALE_UE8M0) {
+    a.se8 = reinterpret_cast<const uint8_t*>(srow)[kb];
+  } else {
+    float s = reinterpret_cast<const float*>(srow)[kb];
+    if (scale_kind == WZ_SCALE_UE8M0_F32)
+      a.se8 = int((__float_as_uint(s) >> 23) & 0xFFu);
+    else
+      a.sf = s;
+  }
+  return a;
+}
+
 __device__ __forceinline__ AOp a_from_fp8(const uint8_t* row, const void* srow, int kb, int g,
                                           int scale_kind) {
   AOp a = a_zero();

@@ -749,10 +749,20 @@ __global__ __launch_bounds__(kDecThreads) void hquant_kernel(MoeWs ws, int T, in
 constexpr int kW2Waves = 16;
 constexpr int kW2Threads = kW2Waves * 64;
 
+// One workgroup per 16 output columns; jobs go to waves round-robin: the
+// shared expert (FP8, twice the bytes of a routed expert per column) as two K
+// halves first, then every active routed expert over the full K.  Every load
+// of a batch (weight tiles, their scales, the batch's A blocks) is issued
+// before the first wait: token rows past T read row T - 1 (their MFMA output
+// rows are dropped) and K-blocks past the end re-read the last one (their
+// MFMAs are skipped), so no load sits behind a branch.  Each job's 16-column
+// result for the batch's token rows lands in LDS; the workgroup then sums each
+// token's experts in ascending id, adds the shared expert and writes bf16 y.
 __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, MoeWs ws, int T, int u_max,
                                                                 uint16_t* __restrict__ y) {
+  constexpr int kShParts = 2;
   __shared__ float out_s[kMaxDecPairs][16];  // routed pair (permuted position) x 16 columns
-  __shared__ float sh_s[kDecodeMaxT][16];
+  __shared__ float sh_s[kShParts][kDecodeMaxT][16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nl = lane & 15, g = lane >> 4;
   const int D = d.dim, I = d.inter, k = d.topk;
@@ -762,60 +772,62 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
   const int KB = I / 128, KG = (KB + 3) / 4, DT = D / 16, UT = u_max * T;
   const int P = T * k;
   const int n_act = min(ws.n_active[0], u_max);
-  for (int job = wave; job <= n_act; job += kW2Waves) {
-    const bool shared = job == n_act;
-    const int arow0 = shared ? UT : job * T;
-    const uint8_t* arow = nl < T ? ws.hq + int64_t(arow0 + nl) * I : nullptr;
-    const float* asrow = nl < T ? ws.hs + int64_t(arow0 + nl) * (I / 128) : nullptr;
+  const int nrow = min(nl, T - 1);
+  for (int job = wave; job < kShParts + n_act; job += kW2Waves) {
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-    if (shared) {
+    if (job < kShParts) {
+      const uint8_t* arow = ws.hq + int64_t(UT + nrow) * I;
+      const float* asrow = ws.hs + int64_t(UT + nrow) * (I / 128);
       const uint8_t* tiles = static_cast<const uint8_t*>(d.sh2p) + int64_t(dt) * KB * 2048;
       const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
       const int64_t sbase = int64_t(n0 >> 7) * KB;
-      for (int kb = 0; kb < KB; kb += 4) {
+      const int kb0 = job * KB / kShParts, kb1 = (job + 1) * KB / kShParts;
+      for (int kb = kb0; kb < kb1; kb += 4) {
         v8i w[4];
         int se[4];
         float sf[4];
+        AOp a[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int kk = min(kb + q, kb1 - 1);
+          w[q] = pk_fp8(tiles + int64_t(kk) * 2048, lane);
+          fp8_wscale(d.sh_w2_s, sbase + kk, d.shared_w_scale_kind, se[q], sf[q]);
+          a[q] = a_from_fp8_row(arow, asrow, kk, g, a_kind);
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          if (kb + q < KB) {
-            w[q] = pk_fp8(tiles + int64_t(kb + q) * 2048, lane);
-            fp8_wscale(d.sh_w2_s, sbase + kb + q, d.shared_w_scale_kind, se[q], sf[q]);
-          }
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (kb + q < KB) {
-            const AOp a = a_from_fp8(arow, asrow, kb + q, g, a_kind);
-            mma_step<kFmtFp8, kFmtFp8>(acc, a, w[q], se[q], sf[q], a_pow2, bp, lane);
-          }
+          if (kb + q < kb1) mma_step<kFmtFp8, kFmtFp8>(acc, a[q], w[q], se[q], sf[q], a_pow2, bp, lane);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (g * 4 + i < T) sh_s[g * 4 + i][nl] = bf16_round(acc[i]);
+        if (g * 4 + i < T) sh_s[job][g * 4 + i][nl] = acc[i];
     } else {
-      const int e = clampi(ws.active[job], 0, d.n_experts - 1);
-      const uint8_t* wt = static_cast<const uint8_t*>(d.w2p) + (int64_t(e) * DT + dt) * KB * 1024;
+      const int u = job - kShParts;
+      const uint8_t* arow = ws.hq + int64_t(u * T + nrow) * I;
+      const float* asrow = ws.hs + int64_t(u * T + nrow) * (I / 128);
+      const int e = clampi(ws.active[u], 0, d.n_experts - 1);
+      const uint8_t* wt = static_cast<const uint8_t*>(d.w2p) + (int64_t(e) * DT + dt) * KB * 1024 + lane * 16;
       const uint32_t* st = static_cast<const uint32_t*>(d.w2p_s) + (int64_t(e) * DT + dt) * KG * 64 + lane;
       int qrow[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qrow[i] = g * 4 + i < T ? ws.umap[job * T + g * 4 + i] : -1;
-      for (int kb = 0; kb < KB; kb += 8) {
-        v8i w[8];
-        uint32_t sc[3];
+      for (int i = 0; i < 4; ++i) qrow[i] = g * 4 + i < T ? ws.umap[u * T + g * 4 + i] : -1;
+      for (int kb = 0; kb < KB; kb += 4) {  // one scale dword per batch of 4 K-blocks
+        v4i w[4];
+        AOp a[4];
+        const uint32_t sc = st[(kb >> 2) * 64];
 #pragma unroll
-        for (int q = 0; q < 3; ++q) sc[q] = (kb >> 2) + q < KG ? st[((kb >> 2) + q) * 64] : 0u;
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          if (kb + q < KB) w[q] = pk_fp4(wt + int64_t(kb + q) * 1024, lane);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int kk = kb + q;
-          if (kk < KB) {
-            const AOp a = a_from_fp8(arow, asrow, kk, g, a_kind);
-            const int es = int((sc[(kk >> 2) - (kb >> 2)] >> (8 * (kk & 3))) & 0xFFu);
-            mma_step<kFmtFp8, kFmtFp4>(acc, a, w[q], es, 1.0f, a_pow2, true, lane);
-          }
+        for (int q = 0; q < 4; ++q) {
+          const int kk = min(kb + q, KB - 1);
+          w[q] = load16_nt(wt + int64_t(kk) * 1024);
+          a[q] = a_from_fp8_row(arow, asrow, kk, g, a_kind);
         }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (kb + q < KB) {
+            const int es = int((sc >> (8 * q)) & 0xFFu);
+            const v8i wb = v8i{w[q][0], w[q][1], w[q][2], w[q][3], 0, 0, 0, 0};
+            mma_step<kFmtFp8, kFmtFp4>(acc, a[q], wb, es, 1.0f, a_pow2, true, lane);
+          }
       }
       // each linear's output is bf16 (architecture.py:741)
 #pragma unroll
@@ -829,7 +841,7 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
     const int n = clampi(ws.tok_n[t], 0, k);
     float acc = 0.0f;
     for (int j = 0; j < n; ++j) acc += out_s[clampi(ws.tok_pos[t * k + j], 0, P - 1)][col];
-    acc += sh_s[t][col];
+    acc += bf16_round(sh_s[0][t][col] + sh_s[1][t][col]);
     y[int64_t(t) * D + n0 + col] = f32_to_bf16(acc);
   }
 }
