@@ -19,10 +19,10 @@
 namespace wz {
 
 constexpr int kGemmThreads = 256;
-constexpr int kUnroll = 8;
 
 // One workgroup's 16 output columns [n0, n0 + 16) for rows m_base .. m_base + 16 MT.
-template <int WF, bool A_BF16, int MT>
+// kUnroll = K-blocks per load batch (a wave owns about nkb / 4 of them).
+template <int WF, bool A_BF16, int MT, int kUnroll>
 __device__ __forceinline__ void skinny_body(const void* __restrict__ A, const void* __restrict__ As, int act_kind,
                                             const uint8_t* __restrict__ W, const void* __restrict__ Ws, int w_kind,
                                             uint16_t* __restrict__ C, int M, int N, int K, int m_base, int n0) {
@@ -48,39 +48,45 @@ __device__ __forceinline__ void skinny_body(const void* __restrict__ A, const vo
     float sbf[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int k = kb + u;
-      if (k < kb1) {
-        if (WF == kFmtFp4) {
-          bb[u] = b_fp4(wrow, k, g);
-          sbe[u] = b_fp4_scale(wsrow, k, g);
-          sbf[u] = 1.0f;
-        } else {
-          bb[u] = b_fp8(wrow, k, g);
-          fp8_wscale(Ws, int64_t(n0 >> 7) * nkb + k, w_kind, sbe[u], sbf[u]);
-        }
+      const int k = min(kb + u, kb1 - 1);  // past kb1: a valid re-read whose MFMA is skipped
+      if (WF == kFmtFp4) {
+        bb[u] = b_fp4(wrow, k, g);
+        sbe[u] = b_fp4_scale(wsrow, k, g);
+        sbf[u] = 1.0f;
+      } else {
+        bb[u] = b_fp8(wrow, k, g);
+        fp8_wscale(Ws, int64_t(n0 >> 7) * nkb + k, w_kind, sbe[u], sbf[u]);
       }
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       const int m = m_base + t * 16 + nl;
-      const bool live = m < M;
+      if (A_BF16) {
+        const bool live = m < M;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int k = kb + u;
-        if (k < kb1) {
-          AOp a;
-          if (A_BF16)
-            a = a_from_bf16(live ? reinterpret_cast<const uint16_t*>(A) + int64_t(m) * K : nullptr, k, g,
-                            a_pow2);
-          else
-            a = a_from_fp8(live ? reinterpret_cast<const uint8_t*>(A) + int64_t(m) * K : nullptr,
-                           live ? (act_kind == WZ_SCALE_UE8M0
-                                       ? static_cast<const void*>(reinterpret_cast<const uint8_t*>(As) + int64_t(m) * nkb)
-                                       : static_cast<const void*>(reinterpret_cast<const float*>(As) + int64_t(m) * nkb))
-                                : nullptr,
-                           k, g, act_kind);
-          mma_step<kFmtFp8, WF>(acc[t], a, bb[u], sbe[u], sbf[u], a_pow2, b_pow2, lane);
+        for (int u = 0; u < kUnroll; ++u) {
+          const int k = kb + u;
+          if (k < kb1) {
+            const AOp a = a_from_bf16(live ? reinterpret_cast<const uint16_t*>(A) + int64_t(m) * K : nullptr, k, g,
+                                      a_pow2);
+            mma_step<kFmtFp8, WF>(acc[t], a, bb[u], sbe[u], sbf[u], a_pow2, b_pow2, lane);
+          }
         }
+      } else {
+        // the tile's A blocks of this batch are all requested before the first
+        // MFMA: rows past M read row M - 1 (their outputs are not stored) and
+        // K-blocks past kb1 re-read the last one (their MFMAs are skipped)
+        const int mr = min(m, M - 1);
+        const uint8_t* arow = reinterpret_cast<const uint8_t*>(A) + int64_t(mr) * K;
+        const void* asrow = act_kind == WZ_SCALE_UE8M0
+                                ? static_cast<const void*>(reinterpret_cast<const uint8_t*>(As) + int64_t(mr) * nkb)
+                                : static_cast<const void*>(reinterpret_cast<const float*>(As) + int64_t(mr) * nkb);
+        AOp a[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) a[u] = a_from_fp8_row(arow, asrow, min(kb + u, kb1 - 1), g, act_kind);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+          if (kb + u < kb1) mma_step<kFmtFp8, WF>(acc[t], a[u], bb[u], sbe[u], sbf[u], a_pow2, b_pow2, lane);
       }
     }
   }
@@ -104,16 +110,23 @@ __device__ __forceinline__ void skinny_body(const void* __restrict__ A, const vo
   }
 }
 
-template <int WF, bool A_BF16, int MT>
+template <int WF, bool A_BF16, int MT, int U>
 __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(
     const void* __restrict__ A, const void* __restrict__ As, int act_kind,
     const uint8_t* __restrict__ W, const void* __restrict__ Ws, int w_kind,
     uint16_t* __restrict__ C, int M, int N, int K) {
-  skinny_body<WF, A_BF16, MT>(A, As, act_kind, W, Ws, w_kind, C, M, N, K, blockIdx.y * (16 * MT), blockIdx.x * 16);
+  skinny_body<WF, A_BF16, MT, U>(A, As, act_kind, W, Ws, w_kind, C, M, N, K, blockIdx.y * (16 * MT), blockIdx.x * 16);
+}
+
+// K-blocks per load batch for a wave that owns ceil(nkb / 4) of them.
+static inline int skinny_unroll(int64_t K) {
+  const int64_t per_wave = (K / 128 + 3) / 4;
+  return per_wave >= 8 ? 8 : per_wave >= 4 ? 4 : 2;
 }
 
 // Row g of A against its own MXFP4 weight W[g] (the per-expert GEMV of the
 // banked decode path): blockIdx.y = g, each row one M=1 skinny product.
+template <int U>
 __global__ __launch_bounds__(kGemmThreads) void grouped_fp4_kernel(const uint8_t* __restrict__ A,
                                                                    const void* __restrict__ As, int act_kind,
                                                                    const uint8_t* __restrict__ W,
@@ -124,7 +137,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_fp4_kernel(const uint8_t
   const void* as_g = act_kind == WZ_SCALE_UE8M0
                          ? static_cast<const void*>(static_cast<const uint8_t*>(As) + g * nkb)
                          : static_cast<const void*>(static_cast<const float*>(As) + g * nkb);
-  skinny_body<kFmtFp4, false, 1>(A + g * K, as_g, act_kind, W + g * N * (K / 2), Ws + g * N * (K / 32),
+  skinny_body<kFmtFp4, false, 1, U>(A + g * K, as_g, act_kind, W + g * N * (K / 2), Ws + g * N * (K / 32),
                                  WZ_WSCALE_E8M0, C + g * N, 1, N, K, 0, blockIdx.x * 16);
 }
 
@@ -138,15 +151,25 @@ static int launch_skinny(const void* A, const void* As, int act_kind, const void
   dim3 grid(unsigned(N / 16), unsigned((M + rows_per_block - 1) / rows_per_block));
   const uint8_t* w = static_cast<const uint8_t*>(W);
   uint16_t* c = static_cast<uint16_t*>(C);
-#define WZ_SKINNY(MTV)                                                                           \
-  WZ_LAUNCH(what, stream, (skinny_gemm_kernel<WF, A_BF16, MTV>), grid, dim3(kGemmThreads), 0, A, As, \
+  const int u = skinny_unroll(K);
+#define WZ_SKINNY(MTV, UV)                                                                            \
+  WZ_LAUNCH(what, stream, (skinny_gemm_kernel<WF, A_BF16, MTV, UV>), grid, dim3(kGemmThreads), 0, A, As, \
             act_kind, w, Ws, w_kind, c, int(M), int(N), int(K))
-  switch (mt) {
-    case 1: WZ_SKINNY(1); break;
-    case 2: WZ_SKINNY(2); break;
-    case 4: WZ_SKINNY(4); break;
-    default: WZ_SKINNY(8); break;
+#define WZ_SKINNY_U(MTV)            \
+  if (u == 8) {                     \
+    WZ_SKINNY(MTV, 8);              \
+  } else if (u == 4) {              \
+    WZ_SKINNY(MTV, 4);              \
+  } else {                          \
+    WZ_SKINNY(MTV, 2);              \
   }
+  switch (mt) {
+    case 1: WZ_SKINNY_U(1); break;
+    case 2: WZ_SKINNY_U(2); break;
+    case 4: WZ_SKINNY_U(4); break;
+    default: WZ_SKINNY_U(8); break;
+  }
+#undef WZ_SKINNY_U
 #undef WZ_SKINNY
   return check_launch(what);
 }
@@ -216,8 +239,21 @@ extern "C" int wz_grouped_fp4_gemm(const void* a_e4m3, const void* a_s, const vo
   if (G == 0) return WZ_OK;
   if (!a_e4m3 || !a_s || !w_fp4x2 || !w_s_e8m0 || !c_bf16)
     return set_error(WZ_EINVAL, "grouped_fp4_gemm: null pointer");
-  WZ_LAUNCH("grouped_fp4_gemm", stream, grouped_fp4_kernel, dim3(unsigned(N / 16), unsigned(G)), dim3(kGemmThreads), 0,
-            static_cast<const uint8_t*>(a_e4m3), a_s, act_scale_kind, static_cast<const uint8_t*>(w_fp4x2),
-            static_cast<const uint8_t*>(w_s_e8m0), static_cast<uint16_t*>(c_bf16), int(N), int(K));
+  const dim3 grid(unsigned(N / 16), unsigned(G));
+  const uint8_t* a = static_cast<const uint8_t*>(a_e4m3);
+  const uint8_t* w = static_cast<const uint8_t*>(w_fp4x2);
+  const uint8_t* ws = static_cast<const uint8_t*>(w_s_e8m0);
+  uint16_t* c = static_cast<uint16_t*>(c_bf16);
+  const int u = skinny_unroll(K);
+  if (u == 8) {
+    WZ_LAUNCH("grouped_fp4_gemm", stream, grouped_fp4_kernel<8>, grid, dim3(kGemmThreads), 0, a, a_s, act_scale_kind,
+              w, ws, c, int(N), int(K));
+  } else if (u == 4) {
+    WZ_LAUNCH("grouped_fp4_gemm", stream, grouped_fp4_kernel<4>, grid, dim3(kGemmThreads), 0, a, a_s, act_scale_kind,
+              w, ws, c, int(N), int(K));
+  } else {
+    WZ_LAUNCH("grouped_fp4_gemm", stream, grouped_fp4_kernel<2>, grid, dim3(kGemmThreads), 0, a, a_s, act_scale_kind,
+              w, ws, c, int(N), int(K));
+  }
   return check_launch("grouped_fp4_gemm");
 }
