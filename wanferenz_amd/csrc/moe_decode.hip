@@ -875,28 +875,30 @@ __device__ __forceinline__ void w2_shared_group(const wz_moe_desc& d, const MoeW
   const int a_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
   const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
   const int UT = u_max * T;
-  const uint8_t* arow = nl < T ? ws.hq + int64_t(UT + nl) * I : nullptr;
-  const float* asrow = nl < T ? ws.hs + int64_t(UT + nl) * (I / 128) : nullptr;
+  // rows past T read row T - 1 (their outputs are not stored), so every load of
+  // a batch is issued before the first wait
+  const int nrow = min(nl, T - 1);
+  const uint8_t* arow = ws.hq + int64_t(UT + nrow) * I;
+  const float* asrow = ws.hs + int64_t(UT + nrow) * (I / 128);
   const int dt = grp * 4 + wave, n0 = dt * 16;  // wave w: column tile 4 grp + w, full K
   const uint8_t* tiles = static_cast<const uint8_t*>(d.sh2p) + int64_t(dt) * KB * 2048;
   const int64_t sbase = int64_t(n0 >> 7) * KB;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
-  for (int kb = 0; kb < KB; kb += 8) {
-    v8i w[8];
-    int se[8];
-    float sf[8];
+  for (int kb = 0; kb < KB; kb += 4) {
+    v8i w[4];
+    int se[4];
+    float sf[4];
+    AOp a[4];
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
-      if (kb + q < KB) {
-        w[q] = pk_fp8(tiles + int64_t(kb + q) * 2048, lane);
-        fp8_wscale(d.sh_w2_s, sbase + kb + q, d.shared_w_scale_kind, se[q], sf[q]);
-      }
+    for (int q = 0; q < 4; ++q) {
+      const int kk = min(kb + q, KB - 1);
+      w[q] = pk_fp8(tiles + int64_t(kk) * 2048, lane);
+      fp8_wscale(d.sh_w2_s, sbase + kk, d.shared_w_scale_kind, se[q], sf[q]);
+      a[q] = a_from_fp8_row(arow, asrow, kk, g, a_kind);
+    }
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
-      if (kb + q < KB) {
-        const AOp a = a_from_fp8(arow, asrow, kb + q, g, a_kind);
-        mma_step<kFmtFp8, kFmtFp8>(acc, a, w[q], se[q], sf[q], a_pow2, bp, lane);
-      }
+    for (int q = 0; q < 4; ++q)
+      if (kb + q < KB) mma_step<kFmtFp8, kFmtFp8>(acc, a[q], w[q], se[q], sf[q], a_pow2, bp, lane);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -946,12 +948,13 @@ __global__ __launch_bounds__(kDecThreads) void w2_stream_kernel(wz_moe_desc d, M
   v8i av[NKB];
   int ae[NKB];
   int cur_u = -1;
-  auto load_a = [&](int u) {
-    const uint8_t* arow = nl < T ? ws.hq + int64_t(u * T + nl) * I : nullptr;
-    const float* asrow = nl < T ? ws.hs + int64_t(u * T + nl) * (I / 128) : nullptr;
+  auto load_a = [&](int u) {  // rows past T read row T - 1 (their outputs are not stored)
+    const int nrow = min(nl, T - 1);
+    const uint8_t* arow = ws.hq + int64_t(u * T + nrow) * I;
+    const float* asrow = ws.hs + int64_t(u * T + nrow) * (I / 128);
 #pragma unroll
     for (int q = 0; q < NKB; ++q) {
-      const AOp a = a_from_fp8(arow, asrow, kb0 + q, g, WZ_SCALE_UE8M0_F32);
+      const AOp a = a_from_fp8_row(arow, asrow, kb0 + q, g, WZ_SCALE_UE8M0_F32);
       av[q] = a.v;
       ae[q] = a.se8;
     }
@@ -1018,17 +1021,23 @@ __global__ __launch_bounds__(256) void combine_decode_kernel(MoeWs ws, int T, in
   if (t >= T) return;
   const int P = T * k;
   const int n = clampi(ws.tok_n[t], 0, k);
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < n; ++j) {
-    const int q = clampi(ws.tok_pos[t * k + j], 0, P - 1);
-    const v4i v = load16(ws.out2 + int64_t(q) * D + c * 8);
+  // every row is requested before the first sum: slots past n re-read the
+  // token's first row and are not added
+  v4i v[kDecodeMaxT];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      acc[2 * m] += bf16lo(uint32_t(v[m]));
-      acc[2 * m + 1] += bf16hi(uint32_t(v[m]));
-    }
-  }
+  for (int j = 0; j < kDecodeMaxT; ++j)
+    if (j < k) v[j] = load16(ws.out2 + int64_t(clampi(ws.tok_pos[t * k + (j < n ? j : 0)], 0, P - 1)) * D + c * 8);
   const v4i sv = load16(ws.sh_out + int64_t(t) * D + c * 8);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < kDecodeMaxT; ++j)
+    if (j < n) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        acc[2 * m] += bf16lo(uint32_t(v[j][m]));
+        acc[2 * m + 1] += bf16hi(uint32_t(v[j][m]));
+      }
+    }
   uint32_t o[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m)
