@@ -106,7 +106,7 @@ def v4_layer(gpu):
     return cfg, w, host, moe
 
 
-def _oracle_params_from_device(cfg, w, host, experts, bias=None):
+def _oracle_params_from_device(cfg, w, host, experts, bias=None, round_pow2=True):
     """Oracle parameters for the experts a routing touched, copied back from HBM."""
     I = cfg.inter
     ex = [None] * cfg.n_experts
@@ -121,7 +121,7 @@ def _oracle_params_from_device(cfg, w, host, experts, bias=None):
     return om.MoEParams(cfg.dim, I, cfg.n_experts, cfg.topk, from_bf16_bits(host["gate_w"]),
                         host.get("gate_bias") if bias is None else bias, ex, shared, cfg.score_func,
                         cfg.route_scale,
-                        cfg.swiglu_limit, True, None)
+                        cfg.swiglu_limit, round_pow2, None)
 
 
 def test_v4_device_fill_matches_host_generator(v4_layer):
@@ -137,14 +137,12 @@ def test_v4_device_fill_matches_host_generator(v4_layer):
     assert np.array_equal(w.w2_s[e].cpu().numpy().ravel(), ref)
 
 
-@pytest.mark.parametrize("T", [1, 4, 8])
-def test_v4_decode_parity(v4_layer, T):
-    cfg, w, host, moe = v4_layer
+def _v4_decode_check(cfg, w, host, moe, T, round_pow2=True):
     xb = synth.normal_bf16(synth.stream_key(100 + T, synth.S_X), (T, cfg.dim), 1.0)
     x = bf16_tensor(xb, "cuda")
     g = om.gate(from_bf16_bits(xb), from_bf16_bits(host["gate_w"]), host["gate_bias"], cfg.topk,
                 cfg.score_func, cfg.route_scale)
-    p = _oracle_params_from_device(cfg, w, host, sorted(set(g.indices.ravel().tolist())))
+    p = _oracle_params_from_device(cfg, w, host, sorted(set(g.indices.ravel().tolist())), round_pow2=round_pow2)
     ref = om.moe_forward(p, from_bf16_bits(xb))
     near = check_routing(moe, x, None, ref.gate, cfg.n_experts)
     # the decode kernels route on their own (route_decode_kernel): check what they export
@@ -158,7 +156,25 @@ def test_v4_decode_parity(v4_layer, T):
     got = f32_of_bf16(y)
     rel, cos = om.max_rel_err(got, ref.y), om.cosine(got, ref.y)
     assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
-    print(f"V4 T={T}: rel {rel:.2e} cos {cos:.8f} bit-equal {np.mean(got == ref.y):.4f} near-ties {near}")
+    print(f"V4 T={T} pow2 {round_pow2}: rel {rel:.2e} cos {cos:.8f} bit-equal {np.mean(got == ref.y):.4f} "
+          f"near-ties {near}")
+
+
+@pytest.mark.parametrize("T", [1, 4, 5, 8])
+def test_v4_decode_parity(v4_layer, T):
+    cfg, w, host, moe = v4_layer
+    _v4_decode_check(cfg, w, host, moe, T)
+
+
+def test_v4_decode_parity_fp32_act_scales(v4_layer):
+    """Float (non power-of-two) activation scales at the V4 shape: the decode
+    w2 then runs w2_combine_kernel (the LDS-staged kernel serves K-blocks of 16
+    only with power-of-two scales)."""
+    cfg, w, host, _ = v4_layer
+    cfg32 = MoEConfig(V4["dim"], V4["inter"], V4["n_experts"], V4["topk"], "sqrtsoftplus", 1.5, 10.0,
+                      N.WZ_SCALE_F32, N.WZ_WSCALE_E8M0)
+    moe32 = HipMoE(cfg32, w, max_tokens=8)
+    _v4_decode_check(cfg32, w, host, moe32, 3, round_pow2=False)
 
 
 def test_v4_decode_graph_replay(v4_layer):

@@ -47,18 +47,6 @@ struct KsLayout {
   }
 };
 
-// One 16-byte-per-lane buffer load straight into LDS at lds_base + 16 * lane.
-// Written as asm so the compiler does not treat it as an LDS store it must
-// wait for before every LDS read: the kernel waits for it itself (vmcnt 0 and
-// a barrier before the block is read), which lets the next block's rows land
-// while the current one is computed.
-__device__ __forceinline__ void load_lds_16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint32_t voffset) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(lds_base), "v"(voffset), "s"(rsrc)
-               : "memory", "m0");
-}
-
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return uint32_t(f32_to_bf16(a)) | (uint32_t(f32_to_bf16(b)) << 16);
 }

@@ -121,6 +121,36 @@ __device__ __forceinline__ v4i load16_nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
 }
 
+// One 16-byte-per-lane buffer load straight into LDS at lds_base + 16 * lane.
+// Written as asm so the compiler does not treat it as an LDS store it must
+// wait for before every LDS read: the kernel waits for it itself (a vmcnt
+// wait and a barrier before the rows are read), which lets later loads stay
+// in flight meanwhile.
+__device__ __forceinline__ void load_lds_16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_base), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// The same, 4 bytes per lane, to lds_base + 4 * lane.
+__device__ __forceinline__ void load_lds_4(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds_base), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n only (n < 64; gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// LDS byte address of a __shared__ object (the m0 operand of load_lds_16).
+template <typename X>
+__device__ __forceinline__ uint32_t lds_addr(X* p) {
+  return uint32_t(uintptr_t((__attribute__((address_space(3))) X*)p));
+}
+
 }  // namespace wz
 
 // Error reporting (errors.hip) and optional launch timing (prof.hip).

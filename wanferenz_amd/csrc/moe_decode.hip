@@ -15,11 +15,13 @@
 //           tiles streamed once, SwiGLU + clamp + routing weight, bf16 h;
 //           the shared expert's FP8 w1/w3 tiles run first in the same grid.
 //   hquant  act_quant of the h rows that are routed, and of the shared rows.
-//   w2      one WG per 16 output columns; each wave computes one expert's
-//           16-column tile over the full K (MXFP4, or FP8 for the shared
-//           expert) into LDS, then the WG sums each token's experts in
-//           ascending id, adds the shared expert and writes bf16 y
-//           (architecture.py:781-794, fp4_grouped.py:318-324).
+//   w2      one WG per 16 output columns (w2_lds_kernel): the WG copies the
+//           e4m3 h rows of every routed pair and the shared rows into LDS,
+//           then each wave computes one expert's 16-column tile over the full
+//           K (MXFP4, or FP8 for the shared expert's K halves) with the next
+//           job's tiles streaming into the registers it frees, and the WG
+//           sums each token's experts in ascending id, adds the shared expert
+//           and writes bf16 y (architecture.py:781-794, fp4_grouped.py:318-324).
 //
 // Tokens ride on the MFMA's 16-row side: the A operand of every expert is
 // the whole (<= 16 token) batch, row t = token t, and only the rows of the
@@ -28,6 +30,7 @@
 // token gather.  Weights come from the packed banks (pack.hip): every load
 // instruction reads 1 KB contiguous, non-temporal (read once).
 #include <algorithm>
+#include <type_traits>
 
 #include "moe_common.h"
 
@@ -846,6 +849,232 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
   }
 }
 
+// ------------------------------------------------- w2 (A rows in LDS) ---
+//
+// The jobs of w2_combine_kernel (shared expert as two K halves, then each
+// active routed expert over the full K; one workgroup per 16 output columns),
+// with the A operand read from LDS instead of registers.  The workgroup first
+// copies into LDS, with buffer loads straight to LDS, every e4m3 h row it can
+// need: one per routed (expert, token) pair, at its permuted position q < P,
+// then the T shared rows.  A wave's registers then hold only weight tiles: the
+// NS = I / 128 one-KB tile slots of its job are all in flight at once, and
+// while it computes job j the tiles of its next job (j + 16) are requested
+// slot by slot into the registers just consumed.
+constexpr int kW2LdsBytes = 152 * 1024;
+
+// LDS bytes of w2_lds_kernel: A rows, their scales, umap, row sources, active
+// ids, the per-token combine lists, the pair outputs and the shared halves.
+__host__ __device__ inline int64_t w2_lds_bytes(int64_t T, int64_t k, int64_t I, int64_t u_max) {
+  const int64_t P = T * k, R = P + T, KB = I / 128;
+  return ((R * I + 1023) & ~int64_t(1023)) + ((R * KB * 4 + 255) & ~int64_t(255)) +
+         4 * (u_max * T + P + 2 * u_max + P + T + P * 16 + 2 * T * 16);
+}
+
+// POW2: activation scales are powers of two (they ride in the MFMA).
+template <int NS, bool POW2>
+__global__ __launch_bounds__(kW2Threads) void w2_lds_kernel(wz_moe_desc d, MoeWs ws, int T, int u_max,
+                                                            uint16_t* __restrict__ y) {
+  __shared__ __align__(1024) uint8_t smem[kW2LdsBytes];
+  constexpr int KB = NS, I = NS * 128, KG = (KB + 3) / 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nl = lane & 15, g = lane >> 4;
+  const int D = d.dim, k = d.topk, E = d.n_experts;
+  const int dt = blockIdx.x, n0 = dt * 16, DT = D / 16;
+  const int P = T * k, R = P + T, UT = u_max * T;
+  const int a_bytes = (R * I + 1023) & ~1023, as_bytes = (R * KB * 4 + 255) & ~255;
+  float* as_s = reinterpret_cast<float*>(smem + a_bytes);           // [R][KB] scales of the A rows
+  int* um_s = reinterpret_cast<int*>(smem + a_bytes + as_bytes);    // [UT] umap
+  int* src_s = um_s + UT;                                   // [P] hq row of pair q, -1: none
+  int* act_s = src_s + P;                                   // [u_max] active expert ids
+  int* uf_s = act_s + u_max;                                // [u_max] first routed pair of expert u
+  int* tp_s = uf_s + u_max;                                 // [P] tok_pos
+  int* tn_s = tp_s + P;                                     // [T] tok_n
+  float* out_s = reinterpret_cast<float*>(tn_s + T);        // [P][16] routed pair outputs
+  float* sh_s = out_s + P * 16;                             // [2][T][16] shared K halves
+
+  // ---- routing tables into LDS, and the inverse of umap (pair -> hq row) ----
+  const int n_act = min(ws.n_active[0], u_max);
+  for (int i = tid; i < UT; i += kW2Threads) um_s[i] = ws.umap[i];
+  for (int i = tid; i < u_max; i += kW2Threads) {
+    act_s[i] = clampi(ws.active[i], 0, E - 1);
+    uf_s[i] = P;
+  }
+  for (int i = tid; i < P; i += kW2Threads) {
+    src_s[i] = -1;
+    tp_s[i] = clampi(ws.tok_pos[i], 0, P - 1);
+  }
+  for (int i = tid; i < T; i += kW2Threads) tn_s[i] = clampi(ws.tok_n[i], 0, k);
+  __syncthreads();
+  for (int i = tid; i < UT; i += kW2Threads) {
+    const int q = um_s[i];
+    if (q >= 0 && q < P) {
+      src_s[q] = i;
+      atomicMin(&uf_s[i / T], q);
+    }
+  }
+  __syncthreads();
+
+  // ---- jobs: 0 .. n_act - 1 routed expert u = job, then the shared expert's
+  // two K halves (so a shared half is always a wave's last job).  Slot s of
+  // any job is at tiles_of(job) + s KB: a shared K half is KB / 2 FP8 tiles of
+  // 2 KB, the same NS one-KB slots.  The shared halves' scales are read per
+  // K-block; scales_of gives them a harmless in-range address. ----
+  const int nj = n_act + 2;
+  auto tiles_of = [&](int job) {
+    return job < n_act
+               ? static_cast<const uint8_t*>(d.w2p) + (int64_t(act_s[job]) * DT + dt) * KB * 1024 + lane * 16
+               : static_cast<const uint8_t*>(d.sh2p) + (int64_t(dt) * KB + (job - n_act) * (KB / 2)) * 2048 +
+                     lane * 16;
+  };
+  auto scales_of = [&](int job) {
+    return static_cast<const uint32_t*>(d.w2p_s) +
+           (job < n_act ? (int64_t(act_s[job]) * DT + dt) * KG * 64 : int64_t(0)) + lane;
+  };
+  v4i w[NS];
+  uint32_t sc[KG];
+  int j = wave;
+  // ---- A rows and their scales -> LDS, straight from the buffers (no
+  // registers held; an unused row reads past the end: zeros) ----
+  {
+    const __amdgpu_buffer_rsrc_t hq_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(ws.hq, short(0), int(int64_t(UT + T) * I), 0x00020000);
+    const __amdgpu_buffer_rsrc_t hs_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(ws.hs, short(0), int(int64_t(UT + T) * KB * 4), 0x00020000);
+    const uint32_t a_lds = lds_addr(smem);
+    for (int i = wave; i < a_bytes / 1024; i += kW2Waves) {
+      const int b = i * 1024 + lane * 16, row = b / I, off = b % I;
+      const int src = row < P ? src_s[row] : (row < R ? UT + row - P : -1);
+      const uint32_t vo = src < 0 ? 0x80000000u : uint32_t(src * I + off);
+      load_lds_16(hq_rsrc, __builtin_amdgcn_readfirstlane(a_lds + i * 1024), vo);
+    }
+    for (int i = wave; i < as_bytes / 256; i += kW2Waves) {
+      const int e = i * 64 + lane, row = e / KB, kk = e % KB;
+      const int src = row < P ? src_s[row] : (row < R ? UT + row - P : -1);
+      const uint32_t vo = src < 0 ? 0x80000000u : uint32_t((src * KB + kk) * 4);
+      load_lds_4(hs_rsrc, __builtin_amdgcn_readfirstlane(a_lds + a_bytes + i * 256), vo);
+    }
+  }
+  // then this wave's first job (the same order as a refill: scales, tiles);
+  // only the LDS loads above are waited for before the barrier, so the MFMAs
+  // start as the tiles land.  The barrier first puts every wave's LDS loads
+  // ahead of all tile loads in the CU's memory queue (otherwise a wave's
+  // rows return behind other waves' 16 KB of tiles).
+  asm volatile("s_barrier" : : : "memory");
+  if (j < nj) {
+    const uint32_t* st = scales_of(j);
+#pragma unroll
+    for (int c = 0; c < KG; ++c) sc[c] = st[c * 64];
+    const uint8_t* base = tiles_of(j);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) w[s] = load16_nt(base + s * 1024);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(NS + KG));
+  } else {
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+  }
+  // every wave's LDS loads have landed (a bare barrier: __syncthreads' fence
+  // would also wait for the tiles)
+  asm volatile("s_barrier" : : : "memory");
+
+  // A operand of K-block kk from LDS row `row`
+  auto a_lds = [&](int row, int kk) {
+    AOp a = a_zero();
+    const uint8_t* p = smem + row * I + kk * 128 + g * 16;
+    const v4i lo = *reinterpret_cast<const v4i*>(p), hi = *reinterpret_cast<const v4i*>(p + 64);
+    a.v = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    const float s = as_s[row * KB + kk];
+    if constexpr (POW2)
+      a.se8 = int((__float_as_uint(s) >> 23) & 0xFFu);
+    else
+      a.sf = s;
+    return a;
+  };
+
+  // Keeps slot s's MFMA ahead of the load that refills slot s: without it the
+  // MFMAs (pure) sink to the end of the job and every old tile stays live.
+  auto pin = [](v4f& acc) { asm volatile("" : "+v"(acc) : : "memory"); };
+  const int trow = min(nl, T - 1);
+  // shared expert, K half h = job - n_act (FP8: one MFMA per two slots); a
+  // wave's last job, so nothing is refilled.  bpw: e8m0 weight scales (else float)
+  auto shared_half = [&](auto bpw) {
+    constexpr bool kBp = decltype(bpw)::value;
+    const int h = j - n_act;
+    const int kb0 = h * (KB / 2), lrow = P + trow;
+    const int64_t sbase = int64_t(n0 >> 7) * KB;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; s += 2) {
+      const int kk = kb0 + s / 2;
+      int se;
+      float sf;
+      fp8_wscale(d.sh_w2_s, sbase + kk, kBp ? WZ_WSCALE_E8M0 : WZ_WSCALE_F32, se, sf);
+      const AOp a = a_lds(lrow, kk);
+      const v8i wb = v8i{w[s][0], w[s][1], w[s][2], w[s][3], w[s + 1][0], w[s + 1][1], w[s + 1][2], w[s + 1][3]};
+      mma_step<kFmtFp8, kFmtFp8>(acc, a, wb, se, sf, POW2, kBp, lane);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (g * 4 + i < T) sh_s[(h * T + g * 4 + i) * 16 + nl] = acc[i];
+  };
+  // routed job j (expert u = j, full K); refill: request job j + 16's scales
+  // and tiles, slot s right after slot s's MFMA
+  auto routed = [&](auto refill) {
+    const int u = j;
+    const int q = um_s[u * T + trow], qf = uf_s[u];
+    // a token not routed to u reads u's first routed row (its output row is
+    // dropped below), so the wave reads few distinct LDS rows
+    const int lrow = (q >= 0 && q < P) ? q : (qf < P ? qf : P + trow);
+    const uint8_t* nb = nullptr;
+    uint32_t scn[KG];
+    if constexpr (decltype(refill)::value) {
+      const uint32_t* st = scales_of(j + kW2Waves);
+#pragma unroll
+      for (int c = 0; c < KG; ++c) scn[c] = st[c * 64];
+      nb = tiles_of(j + kW2Waves);
+    }
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const AOp a = a_lds(lrow, s);
+      const int es = int((sc[s >> 2] >> (8 * (s & 3))) & 0xFFu);
+      const v8i wb = v8i{w[s][0], w[s][1], w[s][2], w[s][3], 0, 0, 0, 0};
+      mma_step<kFmtFp8, kFmtFp4>(acc, a, wb, es, 1.0f, POW2, true, lane);
+      pin(acc);
+      if constexpr (decltype(refill)::value) w[s] = load16_nt(nb + s * 1024);
+    }
+    if constexpr (decltype(refill)::value) {
+#pragma unroll
+      for (int c = 0; c < KG; ++c) sc[c] = scn[c];
+    }
+    // each linear's output is bf16 (architecture.py:741)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = g * 4 + i;
+      const int qo = t < T ? um_s[u * T + t] : -1;
+      if (qo >= 0 && qo < P) out_s[qo * 16 + nl] = bf16_round(acc[i]);
+    }
+  };
+
+  // every job with a successor is routed (the shared halves come last)
+  for (; j + kW2Waves < nj; j += kW2Waves) routed(std::true_type{});
+  if (j < n_act) {
+    routed(std::false_type{});
+  } else if (j < nj) {
+    if (d.shared_w_scale_kind == WZ_WSCALE_E8M0)
+      shared_half(std::true_type{});
+    else
+      shared_half(std::false_type{});
+  }
+  __syncthreads();
+  if (tid < 16 * T) {
+    const int t = tid >> 4, col = tid & 15;
+    const int n = tn_s[t];
+    float acc = 0.0f;
+    for (int jj = 0; jj < n; ++jj) acc += out_s[tp_s[t * k + jj] * 16 + col];
+    acc += bf16_round(sh_s[t * 16 + col] + sh_s[(T + t) * 16 + col]);
+    y[int64_t(t) * D + n0 + col] = f32_to_bf16(acc);
+  }
+}
+
 // ------------------------------------------------------- w2 (streamed) ---
 //
 // Routed experts' w2 on persistent workgroups, then combine_decode.
@@ -1092,14 +1321,40 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
               I, u_max, d->act_scale_kind != WZ_SCALE_F32);
     if (int rc = check_launch("moe hquant")) return rc;
   }
-  // The streamed w2 plus its combine launch measured faster than
-  // w2_combine_kernel at T = 8 (45 vs 54 us at the V4 shape) and slower at
-  // T <= 4 (30 vs 29.5 us at T = 4, 21 vs 11 us at T = 1).
-  const int nkb2 = I / 512;
-  const bool w2s = T >= 6 && I % 512 == 0 && (nkb2 == 1 || nkb2 == 2 || nkb2 == 4) && D % 64 == 0 &&
+  // w2_lds_kernel wherever its LDS image fits (V4: T <= 8; 21.5 / 35.4 us at
+  // T = 4 / 8 against 25.1 us for w2_combine_kernel and 41.9 us for the
+  // streamed w2 plus its combine launch).  Otherwise the streamed pair at
+  // T >= 6 and w2_combine_kernel below.
+  const int nkb2 = I / 512, kb2 = I / 128;
+  // w2_lds_kernel: I / 128 K-blocks of 2 .. 16 (16 only with power-of-two
+  // activation scales: the float-scale variant spills there) and the LDS image fits
+  const bool p2 = d->act_scale_kind != WZ_SCALE_F32;
+  const bool w2l = I % 128 == 0 && (kb2 == 2 || kb2 == 4 || kb2 == 8 || (kb2 == 16 && p2)) &&
+                   w2_lds_bytes(T, k, I, u_max) <= kW2LdsBytes;
+  const bool w2s = !w2l && T >= 6 && I % 512 == 0 && (nkb2 == 1 || nkb2 == 2 || nkb2 == 4) && D % 64 == 0 &&
                    d->act_scale_kind != WZ_SCALE_F32;
   if (only < 0 || only == WZ_STAGE_W2) {
-    if (w2s) {
+    if (w2l) {
+      const dim3 grid{unsigned(D / 16)};
+      uint16_t* yo = static_cast<uint16_t*>(y);
+#define WZ_W2L(NS)                                                                                            \
+  do {                                                                                                        \
+    if (p2)                                                                                                   \
+      WZ_LAUNCH("moe_w2", stream, (w2_lds_kernel<NS, true>), grid, dim3(kW2Threads), 0, *d, w, int(T), u_max, yo); \
+    else                                                                                                      \
+      WZ_LAUNCH("moe_w2", stream, (w2_lds_kernel<NS, false>), grid, dim3(kW2Threads), 0, *d, w, int(T), u_max, yo); \
+  } while (0)
+      if (kb2 == 16) {
+        WZ_LAUNCH("moe_w2", stream, (w2_lds_kernel<16, true>), grid, dim3(kW2Threads), 0, *d, w, int(T), u_max, yo);
+      } else if (kb2 == 8) {
+        WZ_W2L(8);
+      } else if (kb2 == 4) {
+        WZ_W2L(4);
+      } else {
+        WZ_W2L(2);
+      }
+#undef WZ_W2L
+    } else if (w2s) {
       const int64_t items = int64_t(u_max) * (D / 64), cus = cu_count();
       const dim3 grid(unsigned(D / 64 + std::min<int64_t>(items, std::max<int64_t>(cus, std::min<int64_t>(2 * cus, items / 8)))));
       if (nkb2 == 4) {
