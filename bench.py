@@ -3,10 +3,13 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--T 4] [--layers 12] [--no-cpu]
 
 A step is one MoE layer forward (gate + top-6 routing + permute + MXFP4 routed
-experts + FP8 shared expert + combine) over T synthetic tokens, replayed from
-a HIP graph captured per layer.  Steps rotate over ``--layers`` independent
-layers (12 x 3.45 GB of expert banks resident in HBM) with a different input
-per layer, so the 256 MB Infinity Cache cannot serve repeated expert reads.
+experts + FP8 shared expert + combine) over T synthetic tokens.  Steps rotate
+over ``--layers`` independent layers (12 x 3.45 GB of expert banks resident in
+HBM) with a different input per layer, so the 256 MB Infinity Cache cannot
+serve repeated expert reads.  The layers are captured in rotation order as
+one HIP graph, as a decode step captures its layers (no graph-launch gap
+between layers); K steps replay it K // L times, then a graph of the first
+K % L layers.
 
 Printed JSON line (one):
   value       algorithmic HBM GB/s of the layer = sum over steps of
@@ -142,10 +145,13 @@ def distinct_experts(layers, xs):
     return Us
 
 
-def capture(layers, xs):
+def capture(layers, xs, steps):
+    """One graph of every layer in rotation order (as a decode step captures
+    its layers: no graph-launch gap between layers), plus a graph of the first
+    steps % L layers, so that exactly `steps` layer forwards can be timed."""
     import torch
 
-    graphs, outs = [], []
+    outs = []
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -156,27 +162,37 @@ def capture(layers, xs):
             outs.append(out)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    for (moe, _), (_, x), out in zip(layers, xs, outs):
+
+    def graph_of(n):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            moe.forward(x, out=out)
-        graphs.append(g)
+            for (moe, _), (_, x), out in list(zip(layers, xs, outs))[:n]:
+                moe.forward(x, out=out)
+        return g
+
+    L = len(layers)
+    full = graph_of(L)
+    tail = graph_of(steps % L) if steps % L else None
     torch.cuda.synchronize()
-    return graphs, outs
+    return (full, tail), outs
 
 
-def time_steps(graphs, steps, warmup):
+def time_steps(graphs, steps, warmup, L):
+    """Seconds for exactly `steps` layer forwards in rotation order
+    (steps // L replays of the all-layer graph, then the tail graph)."""
     import torch
 
-    L = len(graphs)
-    for i in range(warmup):
-        graphs[i % L].replay()
+    full, tail = graphs
+    for _ in range(-(-warmup // L)):
+        full.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
-    for i in range(steps):
-        graphs[i % L].replay()
+    for _ in range(steps // L):
+        full.replay()
+    if tail is not None:
+        tail.replay()
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -221,9 +237,9 @@ def stage_times(layers, xs, outs, reps=20):
 def measure_T(layers, T, steps, warmup, dev, salt):
     xs = make_inputs(len(layers), T, dev, salt)
     Us = distinct_experts(layers, xs)
-    graphs, outs = capture(layers, xs)
-    secs, wall = time_steps(graphs, steps, warmup)
+    graphs, outs = capture(layers, xs, steps)
     L = len(layers)
+    secs, wall = time_steps(graphs, steps, warmup, L)
     total_bytes = sum(layer_bytes(Us[i % L], T) for i in range(steps))
     kt = stage_times(layers, xs, outs)
     return dict(T=T, secs=secs, wall=wall, Us=Us, total_bytes=total_bytes, kernels=kt, xs=xs)
@@ -510,9 +526,9 @@ def measure_prefill(layers, Ts, dev):
             _, idx, _, _, _ = moe.route(x)
             torch.cuda.synchronize()
             loads.append(np.bincount(idx.cpu().numpy().ravel(), minlength=E))
-        graphs, outs = capture(players, xs)
         steps = max(6, min(60, 24576 // T))
-        secs, _ = time_steps(graphs, steps, max(2, steps // 4))
+        graphs, outs = capture(players, xs, steps)
+        secs, _ = time_steps(graphs, steps, max(2, steps // 4), len(players))
         kt = stage_times(players, xs, outs, reps=max(2, steps // 3))
         L = len(players)
         nbytes = sum(layer_bytes(int((loads[i % L] > 0).sum()), T) for i in range(steps))
@@ -608,7 +624,7 @@ def main():
         "dtype": "mxfp4(e2m1)*fp8(e4m3)->fp32", "data": "synthetic",
         "config": {"workload": f"DeepSeek-V4-Flash MoE layer decode, T={T} tokens: hidden 4096, "
                                f"256 routed MXFP4 experts + 1 FP8 shared, top-6, intermediate 2048; "
-                               f"{args.layers} layers rotated, hipGraph per layer",
+                               f"{args.layers} layers rotated in one hipGraph",
                    "T": T, "layers": args.layers, "mean_distinct_experts": Umean},
         "us_per_layer": round(ms * 1000.0, 2),
         "tokens_per_s": round(T * args.steps / secs, 1),
