@@ -144,6 +144,8 @@ __device__ __forceinline__ void load_lds_4(__amdgpu_buffer_rsrc_t rsrc, uint32_t
 // s_waitcnt immediate that waits for vmcnt <= n only (n < 64; gfx9 encoding:
 // vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// ... and one that waits for lgkmcnt <= n only (n < 16).
+constexpr int lgkmcnt_only(int n) { return 15 | (3 << 14) | (7 << 4) | (n << 8); }
 
 // LDS byte address of a __shared__ object (the m0 operand of load_lds_16).
 template <typename X>

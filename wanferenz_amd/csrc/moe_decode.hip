@@ -933,46 +933,82 @@ __global__ __launch_bounds__(kW2Threads) void w2_lds_kernel(wz_moe_desc d, MoeWs
   v4i w[NS];
   uint32_t sc[KG];
   int j = wave;
-  // ---- A rows and their scales -> LDS, straight from the buffers (no
-  // registers held; an unused row reads past the end: zeros) ----
+  // ---- A rows: act_quant (torch_ops.py:33-49, the arithmetic of quant_row)
+  // of the bf16 h row of every routed pair and of the T shared rows, into LDS
+  // as e4m3 codes and block scales.  A 16-lane group takes one 128-block (8
+  // elements per lane), kQ 16-byte chunks per thread in the first pass and 4
+  // in later ones.  The first pass's loads go out before this wave's first
+  // tiles, so its quantisation waits for them alone; later passes (T > 4 at
+  // the V4 shape) queue behind the tiles.  Then the first job's scales and tiles, and the
+  // MFMAs start as the tiles land. ----
+  constexpr int kQ = 8;
+  constexpr int CPR = I / 8;  // 16-byte chunks per row
+  const int nch = R * CPR;
+  auto h_chunk = [&](int c) {  // a pair with no row (a repeated expert) reads shared row 0
+    const int cc = min(c, nch - 1), row = cc / CPR, off = (cc % CPR) * 8;
+    const int src = row < P ? src_s[row] : -1;
+    const uint16_t* base = row < P ? (src >= 0 ? ws.h + int64_t(src) * I : ws.sh_h) : ws.sh_h + int64_t(row - P) * I;
+    return load16(base + off);
+  };
+  auto quant_pass = [&](int c0, const auto& hv) {
+    constexpr int n = sizeof(hv) / sizeof(hv[0]);
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+      const int c = c0 + i * kW2Threads + tid;  // a 16-lane group: one 128-block of one row
+      float f[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f[2 * q] = bf16lo(uint32_t(hv[i][q]));
+        f[2 * q + 1] = bf16hi(uint32_t(hv[i][q]));
+      }
+      float amax = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
+      amax = wave_max_xor(amax, 1);
+      amax = wave_max_xor(amax, 2);
+      amax = wave_max_xor(amax, 4);
+      amax = wave_max_xor(amax, 8);
+      const ActScale sc = act_scale(amax, POW2);
+      if (c < nch) {
+        const int row = c / CPR, off = (c % CPR) * 8;
+        const uint32_t lo = pack_fp8x4(quant_div(f[0], sc, POW2), quant_div(f[1], sc, POW2),
+                                       quant_div(f[2], sc, POW2), quant_div(f[3], sc, POW2));
+        const uint32_t hi = pack_fp8x4(quant_div(f[4], sc, POW2), quant_div(f[5], sc, POW2),
+                                       quant_div(f[6], sc, POW2), quant_div(f[7], sc, POW2));
+        *reinterpret_cast<uint2*>(smem + row * I + off) = make_uint2(lo, hi);
+        if ((lane & 15) == 0) as_s[row * KB + off / 128] = sc.s;
+      }
+    }
+  };
   {
-    const __amdgpu_buffer_rsrc_t hq_rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(ws.hq, short(0), int(int64_t(UT + T) * I), 0x00020000);
-    const __amdgpu_buffer_rsrc_t hs_rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(ws.hs, short(0), int(int64_t(UT + T) * KB * 4), 0x00020000);
-    const uint32_t a_lds = lds_addr(smem);
-    for (int i = wave; i < a_bytes / 1024; i += kW2Waves) {
-      const int b = i * 1024 + lane * 16, row = b / I, off = b % I;
-      const int src = row < P ? src_s[row] : (row < R ? UT + row - P : -1);
-      const uint32_t vo = src < 0 ? 0x80000000u : uint32_t(src * I + off);
-      load_lds_16(hq_rsrc, __builtin_amdgcn_readfirstlane(a_lds + i * 1024), vo);
+    v4i hv[kQ];
+#pragma unroll
+    for (int i = 0; i < kQ; ++i) hv[i] = h_chunk(i * kW2Threads + tid);
+    // the first job's tiles in two halves around the first pass (registers)
+    const uint8_t* base = j < nj ? tiles_of(j) : nullptr;
+    if (j < nj) {
+      const uint32_t* st = scales_of(j);
+#pragma unroll
+      for (int c = 0; c < KG; ++c) sc[c] = st[c * 64];
+#pragma unroll
+      for (int s = 0; s < NS / 2; ++s) w[s] = load16_nt(base + s * 1024);
     }
-    for (int i = wave; i < as_bytes / 256; i += kW2Waves) {
-      const int e = i * 64 + lane, row = e / KB, kk = e % KB;
-      const int src = row < P ? src_s[row] : (row < R ? UT + row - P : -1);
-      const uint32_t vo = src < 0 ? 0x80000000u : uint32_t((src * KB + kk) * 4);
-      load_lds_4(hs_rsrc, __builtin_amdgcn_readfirstlane(a_lds + a_bytes + i * 256), vo);
+    quant_pass(0, hv);
+    if (j < nj) {
+#pragma unroll
+      for (int s = NS / 2; s < NS; ++s) w[s] = load16_nt(base + s * 1024);
+    }
+    // later passes run with every tile slot live: 4 chunks per thread
+    for (int c0 = kQ * kW2Threads; c0 < nch; c0 += 4 * kW2Threads) {
+      v4i h4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) h4[i] = h_chunk(c0 + i * kW2Threads + tid);
+      quant_pass(c0, h4);
     }
   }
-  // then this wave's first job (the same order as a refill: scales, tiles);
-  // only the LDS loads above are waited for before the barrier, so the MFMAs
-  // start as the tiles land.  The barrier first puts every wave's LDS loads
-  // ahead of all tile loads in the CU's memory queue (otherwise a wave's
-  // rows return behind other waves' 16 KB of tiles).
-  asm volatile("s_barrier" : : : "memory");
-  if (j < nj) {
-    const uint32_t* st = scales_of(j);
-#pragma unroll
-    for (int c = 0; c < KG; ++c) sc[c] = st[c * 64];
-    const uint8_t* base = tiles_of(j);
-#pragma unroll
-    for (int s = 0; s < NS; ++s) w[s] = load16_nt(base + s * 1024);
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(NS + KG));
-  } else {
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-  }
-  // every wave's LDS loads have landed (a bare barrier: __syncthreads' fence
+  // every thread's LDS writes are done (a bare barrier: __syncthreads' fence
   // would also wait for the tiles)
+  __builtin_amdgcn_s_waitcnt(lgkmcnt_only(0));
   asm volatile("s_barrier" : : : "memory");
 
   // A operand of K-block kk from LDS row `row`
@@ -1316,21 +1352,21 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
     }
     if (int rc = check_launch("moe w13")) return rc;
   }
-  if (only < 0 || only == WZ_STAGE_HQUANT) {
+  // w2_lds_kernel wherever its LDS image fits (V4: T <= 8; 21.5 / 35.4 us at
+  // T = 4 / 8 against 25.1 us for w2_combine_kernel and 41.9 us for the
+  // streamed w2 plus its combine launch).  Otherwise the streamed pair at
+  // T >= 6 and w2_combine_kernel below.  w2_lds_kernel quantises h itself.
+  const int nkb2 = I / 512, kb2 = I / 128;
+  // K-blocks of 2 .. 16 (16 only with power-of-two activation scales: the
+  // float-scale variant spills there) and the LDS image fits
+  const bool p2 = d->act_scale_kind != WZ_SCALE_F32;
+  const bool w2l = I % 128 == 0 && (kb2 == 2 || kb2 == 4 || kb2 == 8 || (kb2 == 16 && p2)) &&
+                   w2_lds_bytes(T, k, I, u_max) <= kW2LdsBytes;
+  if (!w2l && (only < 0 || only == WZ_STAGE_HQUANT)) {
     WZ_LAUNCH("moe_hquant", stream, hquant_kernel, dim3(unsigned(u_max * T + T)), dim3(kDecThreads), 0, w, int(T),
               I, u_max, d->act_scale_kind != WZ_SCALE_F32);
     if (int rc = check_launch("moe hquant")) return rc;
   }
-  // w2_lds_kernel wherever its LDS image fits (V4: T <= 8; 21.5 / 35.4 us at
-  // T = 4 / 8 against 25.1 us for w2_combine_kernel and 41.9 us for the
-  // streamed w2 plus its combine launch).  Otherwise the streamed pair at
-  // T >= 6 and w2_combine_kernel below.
-  const int nkb2 = I / 512, kb2 = I / 128;
-  // w2_lds_kernel: I / 128 K-blocks of 2 .. 16 (16 only with power-of-two
-  // activation scales: the float-scale variant spills there) and the LDS image fits
-  const bool p2 = d->act_scale_kind != WZ_SCALE_F32;
-  const bool w2l = I % 128 == 0 && (kb2 == 2 || kb2 == 4 || kb2 == 8 || (kb2 == 16 && p2)) &&
-                   w2_lds_bytes(T, k, I, u_max) <= kW2LdsBytes;
   const bool w2s = !w2l && T >= 6 && I % 512 == 0 && (nkb2 == 1 || nkb2 == 2 || nkb2 == 4) && D % 64 == 0 &&
                    d->act_scale_kind != WZ_SCALE_F32;
   if (only < 0 || only == WZ_STAGE_W2) {
