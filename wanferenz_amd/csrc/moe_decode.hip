@@ -625,31 +625,21 @@ __global__ __launch_bounds__(kDecThreads) void w13_stream_kernel(wz_moe_desc d, 
   const int a_kind = WZ_SCALE_UE8M0_F32;  // power-of-two scales (host-checked)
   const int KB = 4 * NKB, KG = (KB + 3) / 4, FT = I / 16;
   const int kb0 = wave * NKB;
+  // active-expert ids in LDS, so a tile address never waits on a global load
+  // (all u_max entries, read together with n_active: one round trip)
+  __shared__ int s_act[kMaxExperts];
   const int n_act = min(ws.n_active[0], u_max);
+  for (int j = tid; j < u_max; j += kDecThreads) s_act[j] = clampi(ws.active[j], 0, E - 1);
+  __syncthreads();
   const int N = n_act * FT;
   // grid-stride over items: at any moment the resident workgroups read one
   // contiguous window of the bank (G consecutive items)
   const int G = gridDim.x;
   const int i0 = blockIdx.x;
   if (i0 >= N) return;
-  // active-expert ids in LDS, so a tile address never waits on a global load
-  __shared__ int s_act[kMaxExperts];
-  for (int j = tid; j < n_act; j += kDecThreads) s_act[j] = clampi(ws.active[j], 0, E - 1);
-  __syncthreads();
-
-  v8i av[NKB];
-  int ae[NKB];
-  {
-    const uint8_t* arow = nl < T ? ws.xq + int64_t(nl) * D : nullptr;
-    const float* asrow = nl < T ? ws.xs + int64_t(nl) * (D / 128) : nullptr;
-#pragma unroll
-    for (int q = 0; q < NKB; ++q) {
-      const AOp a = a_from_fp8(arow, asrow, kb0 + q, g, a_kind);
-      av[q] = a.v;
-      ae[q] = a.se8;
-    }
-  }
   const int kg0 = kb0 >> 2;
+  v8i av[NKB];  // the A operand (this wave's K-blocks), loaded after the first tiles
+  int ae[NKB];
 
   auto fetch = [&](W13Buf<NKB>& b, int item) {
     b.u = item / FT;
@@ -715,6 +705,18 @@ __global__ __launch_bounds__(kDecThreads) void w13_stream_kernel(wz_moe_desc d, 
 
   W13Buf<NKB> b0, b1;
   fetch(b0, i0);
+  // the A operand after the first item's tiles: token rows past T read row
+  // T - 1 (their outputs are dropped), so its loads go out as one batch
+  {
+    const uint8_t* arow = ws.xq + int64_t(min(nl, T - 1)) * D;
+    const float* asrow = ws.xs + int64_t(min(nl, T - 1)) * (D / 128);
+#pragma unroll
+    for (int q = 0; q < NKB; ++q) {
+      const AOp a = a_from_fp8_row(arow, asrow, kb0 + q, g, a_kind);
+      av[q] = a.v;
+      ae[q] = a.se8;
+    }
+  }
   int i = i0;
   // steady state: the next item's fetch is always valid
   for (; i + 2 * G < N; i += 2 * G) {
