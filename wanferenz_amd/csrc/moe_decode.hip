@@ -415,6 +415,9 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
                                                                    int n_gate, int split, int u_max) {
   __shared__ int s_last;
   __shared__ double part[kRouteWaves][kDecodeMaxT];
+  // 16 KB: a gate block's per-lane partials (double [8][4][64]) or a shared
+  // item's cross-wave sums (float [8][2][4][64])
+  __shared__ __align__(16) float rbuf[kRouteWaves * 2 * 4 * kWave];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int D = d.dim, E = d.n_experts;
   const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
@@ -466,13 +469,23 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
         }
       }
     }
+    // ---- each token's sum over the wave's 64 lanes, 4 tokens at a time: the
+    // lanes' partials go through this wave's LDS rows, then 16 lanes per token
+    // each add 4 of them and 4 shuffle levels finish (fixed order) ----
+    double(*gsum)[4][kWave] = reinterpret_cast<double(*)[4][kWave]>(rbuf);
 #pragma unroll
-    for (int t = 0; t < kDecodeMaxT; ++t) {
-      if (t < T) {
-        double v = acc[t];
+    for (int t0 = 0; t0 < kDecodeMaxT; t0 += 4) {
+      if (t0 < T) {
 #pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-        if (lane == 0) part[wave][t] = v;
+        for (int c = 0; c < 4; ++c) gsum[wave][c][lane] = acc[t0 + c];
+        const int c = lane >> 4, j = lane & 15;
+        double v = gsum[wave][c][4 * j];
+        v += gsum[wave][c][4 * j + 1];
+        v += gsum[wave][c][4 * j + 2];
+        v += gsum[wave][c][4 * j + 3];
+#pragma unroll
+        for (int m = 8; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+        if (j == 0 && t0 + c < T) part[wave][t0 + c] = v;
       }
     }
     __syncthreads();
@@ -509,10 +522,7 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     return;
   }
   b -= T;
-  {
-    __shared__ float red[kRouteWaves * 2 * 4 * kWave];
-    w13_shared_item_bf16(d, ws, x, T, b, red);
-  }
+  w13_shared_item_bf16(d, ws, x, T, b, rbuf);
 }
 
 // -------------------------------------------------------------------- w13 ---
