@@ -86,6 +86,8 @@ __device__ __forceinline__ float swiglu(float gs, float us, float limit) {
 constexpr int kMaxDecPairs = kDecodeMaxT * 16;
 constexpr int kMaxUT = kDecodeMaxT * kMaxDecPairs;
 
+// KS: 64-expert slots per lane (E <= 64 KS); 4 serve V4's 256 experts.
+template <int KS>
 __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t* ids, int T, int u_max) {
   __shared__ int s_e[kMaxDecPairs];
   __shared__ int s_q[kMaxDecPairs];
@@ -98,7 +100,7 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
   __shared__ float s_uwt[kMaxUT];
   const int E = d.n_experts, k = d.topk, P = T * k, UT = u_max * T;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  constexpr int kSlots = kMaxExperts / 64;
+  constexpr int kSlots = KS;
   // ---- top-k, one wave per token.  The gate waves already wrote each
   // expert's score and biased score; softmax needs the whole row here.
   // (Loops in this single-workgroup phase stay rolled: it runs once per
@@ -259,7 +261,7 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
     }
     const int rank = __popcll(mask & lt);
     const bool leader = (mask & lt) == 0ull;
-    for (int i = tid; i < kRouteWaves * kMaxExperts; i += kRouteThreads_) (&wc[0][0])[i] = 0;
+    for (int i = tid; i < kRouteWaves * E; i += kRouteThreads_) wc[i / E][i % E] = 0;
     __syncthreads();
     if (valid && leader) wc[wave][e] = __popcll(mask);
     __syncthreads();
@@ -409,6 +411,7 @@ __device__ __forceinline__ void w13_shared_item_bf16(const wz_moe_desc& d, const
 // [n_gate, n_gate + T): act_quant of x.  The rest: the shared expert's w1 / w3
 // items, one per block (its waves split K), which do not depend on the routing
 // and so stream while it runs.
+template <int KS>
 __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_desc d, MoeWs ws,
                                                                    const uint16_t* __restrict__ x,
                                                                    const int64_t* __restrict__ ids, int T,
@@ -513,7 +516,7 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     if (tid == 0) s_last = arrive_last(&ws.counters[0], uint32_t(n_gate)) ? 1 : 0;
     __syncthreads();
     if (!s_last) return;
-    route_last(d, ws, ids, T, u_max);  // reads the scores with load_agent
+    route_last<KS>(d, ws, ids, T, u_max);  // reads the scores with load_agent
     return;
   }
   b -= n_gate;
@@ -1338,8 +1341,16 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
   if (!d->w13p || !d->w13p_s || !d->w2p || !d->w2p_s || !d->sh13p || !d->sh2p)
     return set_error(WZ_EINVAL, "moe decode: packed banks missing (wz_moe_pack)");
   if (only < 0 || only == WZ_STAGE_ROUTE) {
-    WZ_LAUNCH("moe_route", stream, route_decode_kernel, dim3(unsigned(n_gate + T + I / 16)), dim3(kRouteThreads_),
-              0, *d, w, static_cast<const uint16_t*>(x), ids, int(T), n_gate, split, u_max);
+    // top-k lanes walk E / 64 slots: 4 for up to 256 experts, else 8
+    const dim3 rgrid{unsigned(n_gate + T + I / 16)};
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    if (E <= 256) {
+      WZ_LAUNCH("moe_route", stream, route_decode_kernel<4>, rgrid, dim3(kRouteThreads_), 0, *d, w, xb, ids, int(T),
+                n_gate, split, u_max);
+    } else {
+      WZ_LAUNCH("moe_route", stream, route_decode_kernel<8>, rgrid, dim3(kRouteThreads_), 0, *d, w, xb, ids, int(T),
+                n_gate, split, u_max);
+    }
     if (int rc = check_launch("moe route")) return rc;
   }
   if (only < 0 || only == WZ_STAGE_W13) {
