@@ -1,6 +1,8 @@
 // MoE decode path (T <= 16 tokens: the decode step and the DSpark verify widths).
 //
-// Four stream-ordered launches, no host sync, no allocation (graph-capturable):
+// Three stream-ordered launches while w2's LDS image fits (at the V4 shape
+// T <= 8), four or five otherwise; no host sync, no allocation
+// (graph-capturable):
 //
 //   route   WGs of 16 gate experts x one token: logits x.W^T (exact bf16 products, fp64
 //           sums); the last gate WG to arrive (agent-scope counter) does score
@@ -14,7 +16,9 @@
 //   w13     per (active expert, 16 intermediate features): MXFP4 w1 and w3
 //           tiles streamed once, SwiGLU + clamp + routing weight, bf16 h;
 //           the shared expert's FP8 w1/w3 tiles run first in the same grid.
-//   hquant  act_quant of the h rows that are routed, and of the shared rows.
+//   hquant  act_quant of the h rows that are routed, and of the shared rows
+//           (only when w2_lds_kernel does not serve: that kernel quantises h
+//           into LDS itself).
 //   w2      one WG per 16 output columns (w2_lds_kernel): the WG copies the
 //           e4m3 h rows of every routed pair and the shared rows into LDS,
 //           then each wave computes one expert's 16-column tile over the full
