@@ -34,7 +34,7 @@ class MoECase:
 
 
 CASES = {
-    # toy layer on the reference CPU path (hidden 1024, 16 routed + 1 shared,
+    # The toy layer the reference's CPU path runs (hidden 1024, 16 routed + 1 shared,
     # top-2, intermediate 512, T=4).
     "toy_t4": MoECase("toy_t4", 1024, 512, 16, 2, 4),
     "toy_t1": MoECase("toy_t1", 1024, 512, 16, 2, 1, seed=1),
