@@ -90,6 +90,18 @@ int wz_fp8_linear_packed(const void* x_bf16, const void* w_packed, const void* w
                          int64_t M, int64_t N, int64_t K, int act_scale_kind, int w_scale_kind,
                          void* ws, size_t ws_bytes, hipStream_t stream);
 
+/* fp8_gemm on a packed weight (wz_fp8_pack): the same product as wz_fp8_gemm from
+ * pre-quantised activations a_e4m3 [M, K] with a_s [M, K/128] (act_scale_kind) —
+ * fp8_gemm(a, a_s, b, b_s), reference.py:292-311, served the way the reference's
+ * decode retile serves it (_fp8_gemm_fast, fp8_vector.py:289-297): M <= 16 with
+ * K in {1024, 2048, 4096} runs the GEMV, otherwise the dense tile GEMM.  ws must
+ * hold wz_fp8_gemm_packed_workspace_bytes(M, K, act_scale_kind) bytes (nonzero
+ * only for e8m0 activation scales outside the GEMV). */
+size_t wz_fp8_gemm_packed_workspace_bytes(int64_t M, int64_t K, int act_scale_kind);
+int wz_fp8_gemm_packed(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
+                       void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind, int w_scale_kind,
+                       void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* fp4_gemm: C[M,N] bf16 = (a * a_s) @ (e2m1(w) * w_s)^T, weight scale e8m0 per 32 K.
  * Replaces fp4_gemm(a, a_s, b, b_s, scale_dtype) — reference.py:572-591 / torch_ops.py:102-108.
  * a_e4m3 [M,K], a_s [M,K/128], w_fp4x2 [N,K/2], w_s_e8m0 [N,K/32]. */
@@ -124,12 +136,15 @@ typedef struct wz_moe_desc {
   const void* gate_w;     /* bf16 [E, D] */
   const float* gate_bias; /* fp32 [E]; NULL for hash-routed layers */
   const int32_t* tid2eid; /* int32 [vocab, k] for hash-routed layers, else NULL */
+  /* Reference-layout weights: read only by wz_moe_pack; wz_moe_forward and
+   * wz_moe_route accept NULL for these seven (w13, w13_s, w2, w2_s, sh_w1, sh_w3,
+   * sh_w2), so a caller that packs expert by expert never holds them. */
   const void* w13;        /* fp4x2 [E, 2I, D/2]: rows [0,I) = w1, [I,2I) = w3 */
   const void* w13_s;      /* e8m0  [E, 2I, D/32] */
   const void* w2;         /* fp4x2 [E, D, I/2] */
   const void* w2_s;       /* e8m0  [E, D, I/32] */
   const void* sh_w1;      /* e4m3 [I, D] */
-  const void* sh_w1_s;    /* [I/128, D/128] */
+  const void* sh_w1_s;    /* [I/128, D/128]; the three shared scales are always required */
   const void* sh_w3;      /* e4m3 [I, D] */
   const void* sh_w3_s;
   const void* sh_w2;      /* e4m3 [D, I] */
@@ -154,8 +169,26 @@ size_t wz_moe_packed_bytes(const wz_moe_desc* d, int which);
 int wz_moe_pack(const wz_moe_desc* d, void* w13p, void* w13p_s, void* w2p, void* w2p_s, void* sh13p,
                 void* sh2p, hipStream_t stream);
 
+/* Pack one routed expert straight from its own tensors into slot e of the packed
+ * banks that d points at (d->w13p, w13p_s, w2p, w2p_s must be set; the other
+ * pointers of d are not read): w1, w3 e2m1x2 [I, D/2] with e8m0 scales [I, D/32],
+ * w2 e2m1x2 [D, I/2] with e8m0 [D, I/32].  Loading expert by expert this way
+ * never materialises the reference-layout bank: the packed banks are the only
+ * copy, the role of _relayout_moe(preserve=False) — fp4_grouped.py:142-188,
+ * serving/partition.py:398-405, where the checkpoint is loaded into the bank. */
+int wz_moe_pack_expert(const wz_moe_desc* d, int64_t e, const void* w1, const void* w1_s, const void* w3,
+                       const void* w3_s, const void* w2, const void* w2_s, hipStream_t stream);
+
+/* Pack the shared expert's FP8 weights (sh_w1, sh_w3 e4m3 [I, D], sh_w2 [D, I])
+ * into d->sh13p and d->sh2p — the shared w1|w3 bank of fp8_vector._lay_shared
+ * (fp8_vector.py:316-351) in the MFMA tile format. */
+int wz_moe_pack_shared(const wz_moe_desc* d, const void* sh_w1, const void* sh_w3, const void* sh_w2,
+                       hipStream_t stream);
+
 /* Bytes of scratch that serve every wz_moe_forward / wz_moe_route call of 1..T
- * tokens (the decode tables of T <= 16 can outgrow a small prefill's needs). */
+ * tokens (the decode tables of T <= 16 can outgrow a small prefill's needs).
+ * T is capped at the chunk that wz_moe_forward runs at once (16384 / k tokens),
+ * so the workspace of a long prompt stays that of one chunk. */
 size_t wz_moe_workspace_bytes(const wz_moe_desc* d, int64_t T);
 
 /* Zero the parts of a fresh workspace that must start at zero (arrival
@@ -163,7 +196,12 @@ size_t wz_moe_workspace_bytes(const wz_moe_desc* d, int64_t T);
 int wz_moe_workspace_init(void* ws, size_t ws_bytes, hipStream_t stream);
 
 /* Full layer: x_bf16 [T, D], input_ids int64 [T] (read only by hash layers) -> y_bf16 [T, D].
- * Optional routing outputs (may be NULL): weights fp32 [T,k], indices int64 [T,k]. */
+ * Optional routing outputs (may be NULL): weights fp32 [T,k], indices int64 [T,k].
+ * Any T: the tokens run in successive chunks of 16384 / k on one workspace
+ * (MoE.forward takes any number of tokens, architecture.py:777-794).  A hash id
+ * outside [0, vocab), or a tid2eid entry outside [0, E), gives that token NaN
+ * routing weights and a NaN output row (the reference's tid2eid[input_ids]
+ * raises); reads stay in bounds. */
 int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids, int64_t T,
                    void* y_bf16, float* weights_out, int64_t* indices_out, void* ws,
                    size_t ws_bytes, hipStream_t stream);
@@ -186,7 +224,7 @@ int wz_moe_replay_stage(const wz_moe_desc* d, const void* x_bf16, const int64_t*
 
 /* Routing only (Gate.forward + the canonical permutation of expert_batch.py:24-37):
  * weights fp32 [T,k], indices int64 [T,k], offsets int32 [E+1],
- * perm_token int32 [T*k], perm_slot int32 [T*k]. */
+ * perm_token int32 [T*k], perm_slot int32 [T*k]; T * k <= 16384. */
 int wz_moe_route(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids, int64_t T,
                  float* weights, int64_t* indices, int32_t* offsets, int32_t* perm_token,
                  int32_t* perm_slot, void* ws, size_t ws_bytes, hipStream_t stream);

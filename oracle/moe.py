@@ -52,6 +52,9 @@ def round_scale(x: np.ndarray) -> np.ndarray:
     x = np.asarray(x, dtype=np.float32)
     m, e = np.frexp(x)
     e = np.where(m == 0.5, e - 1, e)
+    # frexp of NaN / inf: torch returns exponent 0, so the scale is 1 (numpy's
+    # exponent for them is platform-defined; fix it here)
+    e = np.where(np.isfinite(x), e, 0)
     return np.ldexp(np.float32(1.0), e).astype(np.float32)
 
 
@@ -67,7 +70,7 @@ def act_quant(x: np.ndarray, block: int = 128, round_pow2: bool = True):
     if K % block:
         raise ValueError(f"act_quant: last dim {K} not a multiple of {block}")
     z = x.reshape(x.shape[:-1] + (K // block, block))
-    amax = np.maximum(np.abs(z).max(axis=-1, keepdims=True), np.float32(1e-4))
+    amax = np.maximum(np.abs(z).max(axis=-1, keepdims=True), np.float32(1e-4))  # both keep NaN, as torch
     s = round_scale(amax * F32_INV448) if round_pow2 else (amax * F32_INV448).astype(np.float32)
     q = np.clip(z / s, np.float32(-FP8_MAX), np.float32(FP8_MAX)).astype(np.float32)
     codes = e4m3_encode(q).reshape(x.shape)

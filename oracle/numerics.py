@@ -60,17 +60,20 @@ def e4m3_encode(v: np.ndarray) -> np.ndarray:
     """float32 -> e4m3fn byte, round-to-nearest-even on the magnitude.
 
     Inputs must already be clamped to [-448, 448] (the reference clamps before
-    the cast, torch_ops.py:44).  The sign bit is taken from the float's sign,
-    so -0.0 and negative values that round to zero give 0x80.
+    the cast, torch_ops.py:44); NaN encodes as the e4m3fn NaN 0x7F with the
+    float's sign (torch's cast does the same).  The sign bit is taken from the
+    float's sign, so -0.0 and negative values that round to zero give 0x80.
     """
     v = np.asarray(v, dtype=np.float32)
     a = np.abs(v).astype(np.float64)
-    if np.any(a > FP8_MAX) or np.any(np.isnan(a)):
-        raise ValueError("e4m3_encode: input outside [-448, 448] or NaN")
+    nan = np.isnan(a)
+    if np.any(a[~nan] > FP8_MAX):
+        raise ValueError("e4m3_encode: input outside [-448, 448]")
+    a = np.where(nan, 0.0, a)
     lo = np.searchsorted(_E4M3_MID, a, side="left")
     hi = np.searchsorted(_E4M3_MID, a, side="right")
     code = lo + ((hi != lo) & (lo % 2 == 1))
-    code = code.astype(np.uint8)
+    code = np.where(nan, 0x7F, code).astype(np.uint8)
     return code | (np.signbit(v).astype(np.uint8) << 7)
 
 

@@ -1,11 +1,16 @@
-"""GPU parity through the drop-in boundary: MoE.forward replaced by install().
+"""GPU parity through the drop-in boundary: MoE.forward and the FP8 linears
+replaced by install().
 
 A mirror of the reference's MoE module (tests/mirror_model.py: same
 attributes, dtypes and shapes as wanferenz/model/architecture.py:674-794)
 holds a golden case's weights on the GPU.  After install(), MoE.forward runs
-the HIP layer: the per-expert parameters become views into one bank (the
-relayout of fp4_grouped._relayout_moe, fp4_grouped.py:142-188), and the
-output must match the reference's own golden vectors to the bf16 tolerance.
+the HIP layer: each expert's parameters are packed straight into the packed
+banks and then released (one copy in HBM, the reference's bank layout with
+preserve=False, serving/partition.py:398-405), and the output must match the
+reference's own golden vectors to the bf16 tolerance.  The FP8 linears go
+through the packed GEMV once kernels.install() has rebound linear / fp8_gemm
+(the reference's fp8_vector.install, fp8_vector.py:472-491), at the real V4
+projection shapes (fp8_vector.py:505-513).
 """
 
 import types
@@ -19,6 +24,9 @@ from oracle.numerics import from_bf16_bits
 from tests import mirror_model as mm
 from tests.golden.cases import CASES, make_inputs
 from tests.helpers import bf16_tensor, f32_of_bf16
+from oracle.numerics import e8m0_decode
+from tests.golden.cases import oracle_params
+from wanferenz_amd import kernels, synth
 from wanferenz_amd import moe as wm
 
 pytestmark = pytest.mark.gpu
@@ -40,7 +48,9 @@ def mod():
 
 
 @pytest.mark.parametrize("name", ["toy_t4", "toy_t37", "hash_t3", "top6_t8"])
-def test_installed_moe_forward_matches_golden(gpu, mod, name):
+@pytest.mark.parametrize("release", [True, False])
+def test_installed_moe_forward_matches_golden(gpu, mod, name, release, monkeypatch):
+    monkeypatch.setattr(wm, "RELEASE_EXPERTS", release)
     case = CASES[name]
     inp = make_inputs(case)
     moe = mm.moe_from_case(case, inp, gpu)
@@ -55,10 +65,169 @@ def test_installed_moe_forward_matches_golden(gpu, mod, name):
     gold = from_bf16_bits(np.load(f"tests/golden/{name}.npz")["y_bf16"])
     rel, cos = om.max_rel_err(got, gold), om.cosine(got, gold)
     assert rel <= 1e-2 and cos >= 0.9999, (rel, cos)
-    # the experts' parameters now live in the bank (views, no second copy)
-    bank = moe._grouped_bank
+    h = moe._hip_moe
+    assert h.weights is None  # the layer keeps only the packed banks
     w1 = moe.experts[3].w1.weight
-    assert w1.untyped_storage().data_ptr() == bank["w13"].untyped_storage().data_ptr()
+    if release:
+        # one copy of the experts: the module's expert weights are emptied
+        assert w1.numel() == 0 and moe.experts[0].w2.scale.numel() == 0
+        assert moe.shared_experts.w1.weight.numel() == 0 and moe.shared_experts.w1.scale.numel() > 0
+    else:
+        assert w1.numel() == case.inter * case.dim // 2
     # a second call reuses the cached layer
     y2 = mod.MoE.forward(moe, x, ids)
     assert torch.equal(y, y2) and moe._hip_steps == 2
+
+
+def test_installed_moe_serves_any_prompt_length(gpu, mod):
+    """MoE.forward takes any T (architecture.py:777-794).  At top-2, T = 8193 is
+    one token past a single call's 16384 routed pairs: the layer runs it as a
+    chunk of 8192 tokens and one of 1.  Rows are checked against the oracle
+    (sampled), against the same tokens in shorter calls (the layer is
+    token-local, and both calls of a row run the same kernels, so bit-equal),
+    and the lone last token against a one-token call."""
+    import dataclasses
+
+    case = dataclasses.replace(CASES["toy_t4"], name="toy_t8193", T=8193)
+    inp = make_inputs(case)
+    moe = mm.moe_from_case(case, inp, gpu)
+    wm.install(mod)
+    x = bf16_tensor(inp.x, gpu)
+    ids = torch.from_numpy(inp.input_ids).to(gpu)
+    y = mod.MoE.forward(moe, x.view(1, -1, case.dim), ids.view(1, -1)).view(case.T, case.dim)
+    h = moe._hip_moe
+    part = torch.cat([h.forward(x[:3000]), h.forward(x[3000:8192])])
+    last = h.forward(x[8192:])
+    torch.cuda.synchronize()
+    assert torch.equal(y[:8192], part)
+    assert torch.equal(y[8192:], last)
+    rows = [0, 1, 4095, 8191, 8192]
+    p = oracle_params(case, inp)
+    ref = om.moe_forward(p, from_bf16_bits(inp.x[rows]), inp.input_ids[rows])
+    got = f32_of_bf16(y[rows])
+    rel, cos = om.max_rel_err(got, ref.y), om.cosine(got, ref.y)
+    assert rel <= 1e-2 and cos >= 0.9999, (rel, cos)
+
+
+def test_hash_ids_outside_the_table(gpu):
+    """tid2eid[input_ids] raises for an id outside the table (architecture.py:710-711).
+    Host ids are checked before launch (IndexError); device ids are not read back:
+    that token's row comes out NaN, the other tokens' rows are unchanged."""
+    case = CASES["hash_t3"]
+    inp = make_inputs(case)
+    from tests.test_gpu_moe import upload_case
+
+    moe = upload_case(case, inp, gpu)
+    x = bf16_tensor(inp.x, gpu)
+    good = moe.forward(x, torch.from_numpy(inp.input_ids).to(gpu))
+    bad = inp.input_ids.copy()
+    bad[1] = case.vocab + 5
+    with pytest.raises(IndexError):
+        moe.forward(x, torch.from_numpy(bad))
+    for T, xs in ((case.T, x), (40, x.repeat(14, 1)[:40])):
+        ids = np.resize(bad, T)
+        y = moe.forward(xs, torch.from_numpy(ids).to(gpu))
+        ref = moe.forward(xs, torch.from_numpy(np.resize(inp.input_ids, T)).to(gpu))
+        torch.cuda.synchronize()
+        hit = ids >= case.vocab
+        yf = y.float().cpu().numpy()
+        assert np.isnan(yf[hit]).all()
+        assert torch.equal(y[torch.from_numpy(~hit).to(gpu)], ref[torch.from_numpy(~hit).to(gpu)])
+    assert torch.equal(moe.forward(x, torch.from_numpy(inp.input_ids).to(gpu)), good)
+
+
+# ------------------------------------------------------------- FP8 linears ---
+
+# The decode projections the reference's GEMV serves (fp8_vector.py:505-513), N x K.
+V4_PROJECTIONS = {"attn.wq_a": (1024, 4096), "attn.wkv": (512, 4096), "attn.wq_b": (32768, 1024),
+                  "attn.wo_b": (4096, 8192), "idx.wq_b": (8192, 1024), "shared.w13": (4096, 4096),
+                  "shared.w2": (4096, 2048)}
+
+
+@pytest.fixture
+def lin_mod():
+    """A model module exposing the linear-path globals (architecture.py:12-19, 121-134)."""
+    m = types.ModuleType("mirror_linear")
+    m.block_size, m.scale_fmt, m.scale_dtype = 128, "ue8m0", torch.float8_e8m0fnu
+
+    def unused(*a, **k):
+        raise AssertionError("the replaced binding was called")
+
+    m.act_quant = m.fp8_gemm = m.fp4_gemm = m.linear = unused
+    kernels.install(m)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    yield m
+    torch.set_default_dtype(prev)
+    kernels.uninstall(m)
+
+
+def _fp8_param(N, K, gpu, seed):
+    w = torch.empty(N, K, dtype=torch.uint8, device=gpu)
+    synth.device_fill(w, synth.stream_key(seed, synth.S_FP8_W), synth.FILL_E4M3)
+    s = torch.empty((N + 127) // 128, (K + 127) // 128, dtype=torch.uint8, device=gpu)
+    synth.device_fill(s, synth.stream_key(seed, synth.S_FP8_W_S), synth.FILL_E8M0, 112, 116)
+    p = torch.nn.Parameter(w.view(torch.float8_e4m3fn), requires_grad=False)
+    p.scale = torch.nn.Parameter(s.view(torch.float8_e8m0fnu), requires_grad=False)
+    return p
+
+
+@pytest.mark.parametrize("name", list(V4_PROJECTIONS))
+@pytest.mark.parametrize("M", [1, 4, 40])
+def test_installed_linear_runs_the_packed_path(gpu, lin_mod, name, M):
+    """linear(x, W) and act_quant + fp8_gemm through the installed bindings, on a
+    weight Parameter: both run on the packed copy made at first use, agree bit
+    for bit (same codes, same product), and match the oracle on three 128-row
+    blocks of the output."""
+    N, K = V4_PROJECTIONS[name]
+    w = _fp8_param(N, K, gpu, N + 3 * K)
+    xb = synth.normal_bf16(synth.stream_key(M + N, synth.S_FP8_X), (M, K), 1.0)
+    x = bf16_tensor(xb, gpu)
+    y = lin_mod.linear(x, w)
+    assert getattr(w, "_wz_packed", None) is not None
+    q, s = lin_mod.act_quant(x, 128, lin_mod.scale_fmt, lin_mod.scale_dtype)
+    y2 = lin_mod.fp8_gemm(q, s, w, w.scale, lin_mod.scale_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    nb = N // 128
+    blocks = sorted({0, nb // 2, nb - 1})
+    rows = np.concatenate([np.arange(b * 128, b * 128 + 128) for b in blocks])
+    wsub = w.detach().view(torch.uint8)[torch.from_numpy(rows).to(gpu)].cpu().numpy()
+    ssub = e8m0_decode(w.scale.detach().view(torch.uint8)[blocks].cpu().numpy())
+    rq, rs = om.act_quant(from_bf16_bits(xb), 128, True)
+    ref = om.fp8_gemm(rq, rs, wsub, ssub)
+    got = f32_of_bf16(y)[:, rows]
+    rel, cos = om.max_rel_err(got, ref), om.cosine(got, ref)
+    assert rel <= 1e-2 and cos >= 0.9999, (rel, cos)
+
+
+def test_packed_copy_follows_the_weight(gpu, lin_mod):
+    """Writing the weight in place (a checkpoint load after install) makes the next
+    call repack; a graph captured after a first call runs the packed GEMV."""
+    N, K = 1024, 4096
+    w = _fp8_param(N, K, gpu, 11)
+    x = bf16_tensor(synth.normal_bf16(synth.stream_key(5, synth.S_FP8_X), (2, K), 1.0), gpu)
+    y0 = lin_mod.linear(x, w)
+    w2 = _fp8_param(N, K, gpu, 12)
+    with torch.no_grad():
+        w.copy_(w2)
+        w.scale.copy_(w2.scale)
+    y1 = lin_mod.linear(x, w)
+    y_ref = lin_mod.linear(x, w2)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y_ref) and not torch.equal(y0, y1)
+    out = torch.empty_like(y1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            out.copy_(lin_mod.linear(x, w))
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out.copy_(lin_mod.linear(x, w))
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y1)

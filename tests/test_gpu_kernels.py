@@ -406,3 +406,70 @@ def test_grouped_fp4_gemm(gpu, act_fmt, G, N, K):
     ref = np.concatenate([om.fp4_gemm(rq[g:g + 1], rs[g:g + 1], w[g], e8m0_decode(wsc[g])) for g in range(G)])
     rel, cos = _close(got, ref)
     assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+
+
+def _nonfinite_rows(K):
+    """bf16 rows whose 128-blocks hold NaN, +-inf, both, all-NaN, or ordinary values."""
+    from oracle.numerics import bf16_bits
+
+    base = np.linspace(-3.0, 3.0, K, dtype=np.float32)
+    rows = []
+    for spec in ([], [(5, np.nan)], [(0, np.inf)], [(K - 1, -np.inf)], [(3, np.nan), (9, np.inf)],
+                 [(i, np.nan) for i in range(128)]):
+        r = base.copy()
+        for i, v in spec:
+            r[i] = v
+        rows.append(r)
+    return bf16_bits(np.stack(rows))
+
+
+def _same_codes(a, b):
+    a, b = np.asarray(a, np.uint8), np.asarray(b, np.uint8)
+    nan_a, nan_b = (a & 0x7F) == 0x7F, (b & 0x7F) == 0x7F
+    return np.array_equal(nan_a, nan_b) and np.array_equal(a[~nan_a], b[~nan_b])
+
+
+@pytest.mark.parametrize("scale_fmt,scale_dtype", [
+    ("ue8m0", torch.float8_e8m0fnu), ("ue8m0", torch.float32), (None, torch.float32)])
+def test_act_quant_non_finite_blocks(gpu, scale_fmt, scale_dtype):
+    """NaN / inf in a block quantise as the reference's torch act_quant does
+    (torch_ops.py:33-49): NaN survives the amax and the clamp, the fp32 scale
+    is NaN or inf, the ue8m0 scale is 1; other blocks are untouched."""
+    xb = _nonfinite_rows(512)
+    q, s = kernels.act_quant(bf16_tensor(xb, gpu), 128, scale_fmt, scale_dtype)
+    torch.cuda.synchronize()
+    rq, rs = om.act_quant(from_bf16_bits(xb), 128, scale_fmt is not None)
+    assert _same_codes(bytes8(q), rq)
+    got_s = e8m0_decode(bytes8(s)) if scale_dtype == torch.float8_e8m0fnu else s.cpu().numpy()
+    assert np.array_equal(got_s, rs, equal_nan=True)
+
+
+def test_nan_in_x_gives_nan_rows_through_the_fused_linear(gpu):
+    """A NaN activation makes its output row NaN on the packed GEMV (act_quant fused)
+    and the other rows are unchanged."""
+    from oracle.numerics import bf16_bits
+
+    N, K, M = 256, 1024, 4
+    w, ws = _fp8_weight(3, N, K, False)
+    lin = kernels.PackedFp8Linear(u8_tensor(w, gpu, torch.float8_e4m3fn), u8_tensor(ws, gpu, torch.float8_e8m0fnu))
+    xb = _x(77, M, K)
+    y0 = lin(bf16_tensor(xb, gpu))
+    xb2 = xb.copy()
+    xb2[2, 700] = bf16_bits(np.float32(np.nan))
+    y1 = lin(bf16_tensor(xb2, gpu))
+    torch.cuda.synchronize()
+    f1 = f32_of_bf16(y1)
+    assert np.isnan(f1[2]).all()
+    keep = [0, 1, 3]
+    assert np.array_equal(bits16(y1)[keep], bits16(y0)[keep])
+
+
+def test_wire_pack_non_finite_rows(gpu):
+    """_pack_t (serving/chain.py:208-217) on NaN / inf rows: NaN rows give a NaN scale
+    and NaN codes, an inf row the bf16-max scale, as torch computes them."""
+    xb = _nonfinite_rows(1024)
+    q, sc = kernels.wire_pack(bf16_tensor(xb, gpu))
+    torch.cuda.synchronize()
+    rq, rs = om.wire_pack(from_bf16_bits(xb))
+    assert _same_codes(bytes8(q), rq)
+    assert np.array_equal(f32_of_bf16(sc), rs, equal_nan=True)

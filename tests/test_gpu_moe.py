@@ -160,7 +160,7 @@ def _v4_decode_check(cfg, w, host, moe, T, round_pow2=True):
           f"near-ties {near}")
 
 
-@pytest.mark.parametrize("T", [1, 4, 5, 8])
+@pytest.mark.parametrize("T", [1, 2, 4, 5, 8])
 def test_v4_decode_parity(v4_layer, T):
     cfg, w, host, moe = v4_layer
     _v4_decode_check(cfg, w, host, moe, T)
@@ -276,15 +276,21 @@ def _decode_chunks(moe, x, chunk=16):
     return torch.cat([moe.forward(x[i:i + chunk]) for i in range(0, x.size(0), chunk)])
 
 
-@pytest.mark.parametrize("T,bias", [(64, "normal"), (300, "normal"), (2048, "zipf")])
+@pytest.mark.parametrize("T,bias", [(64, "normal"), (128, "normal"), (128, "zipf"), (300, "normal"),
+                                    (512, "normal"), (512, "zipf"), (2048, "zipf")])
 def test_v4_prefill_parity(v4_layer, T, bias):
+    """Prefill at the V4 shape; "zipf" is the calibrated Zipf(1.1) gate bias of the
+    prefill workload (wanferenz_amd/zipf_v4.json).  All routing is checked in full;
+    the outputs of 16 sampled rows (including rows of the most loaded expert)
+    against the oracle, and every row against the decode path run over 16-token
+    chunks."""
     import dataclasses
     cfg, w, host, moe = v4_layer
     b = host["gate_bias"]
     if bias == "zipf":
-        b = synth.zipf_bias(cfg.n_experts)
+        b = synth.zipf_bias(cfg.n_experts, beta=synth.zipf_v4_beta())
         w = dataclasses.replace(w, gate_bias=torch.from_numpy(b).to("cuda"))
-        moe = HipMoE(cfg, w, max_tokens=T)
+        moe = moe.with_gate_bias(w.gate_bias, max_tokens=T)
     xb = synth.normal_bf16(synth.stream_key(500 + T, synth.S_X), (T, cfg.dim), 1.0)
     x = bf16_tensor(xb, "cuda")
     g = om.gate(from_bf16_bits(xb), from_bf16_bits(host["gate_w"]), b, cfg.topk, cfg.score_func,
@@ -293,8 +299,12 @@ def test_v4_prefill_parity(v4_layer, T, bias):
     near = check_routing(moe, x, None, g, cfg.n_experts)
     y = moe.forward(x)
     got = f32_of_bf16(y)
-    # oracle on sampled rows
-    rows = sorted({0, 1, T // 2, T - 1})
+    # oracle on sampled rows: spread over the batch plus tokens of the most loaded expert
+    hot = int(counts.argmax())
+    hot_rows = np.nonzero((g.indices == hot).any(1))[0]
+    rng = np.random.default_rng(T)
+    rows = sorted(set(rng.choice(T, size=min(T, 10), replace=False).tolist()) | {0, T - 1}
+                  | set(hot_rows[:4].tolist()))
     xs = xb[rows]
     gs = om.gate(from_bf16_bits(xs), from_bf16_bits(host["gate_w"]), b, cfg.topk, cfg.score_func,
                  cfg.route_scale)
@@ -307,8 +317,64 @@ def test_v4_prefill_parity(v4_layer, T, bias):
     rel_d, cos_d = om.max_rel_err(got, dec), om.cosine(got, dec)
     assert rel_d <= TOL_REL and cos_d >= TOL_COS, (rel_d, cos_d)
     print(f"V4 prefill T={T} ({bias} bias, experts hit {int((counts > 0).sum())}, max rows "
-          f"{int(counts.max())}): sampled rows vs oracle rel {rel:.2e} cos {cos:.8f}; vs decode "
+          f"{int(counts.max())}): {len(rows)} sampled rows vs oracle rel {rel:.2e} cos {cos:.8f}; vs decode "
           f"rel {rel_d:.2e} cos {cos_d:.8f} bit-equal {np.mean(got == dec):.4f}; near-ties {near}")
+
+
+# Gate score functions other than the V4 sqrt-softplus (Gate.forward, architecture.py:700-705):
+# softmax (weights not renormalised) and sigmoid, on the decode (T <= 16) and prefill paths.
+SCORE_CASES = [(case, sf, T) for sf in ("softmax", "sigmoid")
+               for case, T in (("toy_t4", 4), ("top6_t8", 8), ("top6_t8", 100), ("toy_t37", 37))]
+
+
+@pytest.mark.parametrize("name,score_func,T", SCORE_CASES)
+def test_score_functions(gpu, name, score_func, T):
+    import dataclasses
+
+    case = dataclasses.replace(CASES[name], name=f"{name}_{score_func}", T=T, score_func=score_func)
+    inp = make_inputs(case)
+    moe = upload_case(case, inp, gpu)
+    x = bf16_tensor(inp.x, gpu)
+    ref = om.moe_forward(oracle_params(case, inp), from_bf16_bits(inp.x))
+    near = check_routing(moe, x, None, ref.gate, case.n_experts)
+    rw = torch.empty(T, case.topk, dtype=torch.float32, device=gpu)
+    ri = torch.empty(T, case.topk, dtype=torch.int64, device=gpu)
+    y = moe.forward(x, routing_out=(rw, ri))
+    if not near:
+        assert np.array_equal(ri.cpu().numpy(), ref.gate.indices)
+        wd = np.abs(rw.cpu().numpy() - ref.gate.weights)
+        assert (wd <= 4 * np.spacing(np.abs(ref.gate.weights).astype(np.float32))).all(), wd.max()
+    got = f32_of_bf16(y)
+    rel, cos = om.max_rel_err(got, ref.y), om.cosine(got, ref.y)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    print(f"{case.name} T={T}: rel {rel:.2e} cos {cos:.8f} near-ties {near}")
+
+
+@pytest.mark.parametrize("score_func,T", [("sigmoid", 4), ("sigmoid", 128), ("softmax", 4), ("softmax", 128)])
+def test_v4_score_functions(v4_layer, score_func, T):
+    """The V4 shape with the other score functions: decode (route_decode_kernel) and
+    prefill (MFMA gate with exact refinement for sigmoid; the fp64 dot gate for
+    softmax)."""
+    cfg, w, host, _ = v4_layer
+    cfg2 = MoEConfig(V4["dim"], V4["inter"], V4["n_experts"], V4["topk"], score_func, 1.5, 10.0,
+                     N.WZ_SCALE_UE8M0, N.WZ_WSCALE_E8M0)
+    moe = HipMoE(cfg2, w, max_tokens=T)
+    xb = synth.normal_bf16(synth.stream_key(900 + T, synth.S_X), (T, cfg.dim), 1.0)
+    x = bf16_tensor(xb, "cuda")
+    g = om.gate(from_bf16_bits(xb), from_bf16_bits(host["gate_w"]), host["gate_bias"], cfg.topk, score_func,
+                cfg.route_scale)
+    near = check_routing(moe, x, None, g, cfg.n_experts)
+    y = moe.forward(x)
+    rows = sorted({0, 1, T // 2, T - 1})
+    xs = xb[rows]
+    gs = om.gate(from_bf16_bits(xs), from_bf16_bits(host["gate_w"]), host["gate_bias"], cfg.topk, score_func,
+                 cfg.route_scale)
+    p = _oracle_params_from_device(cfg2, w, host, sorted(set(gs.indices.ravel().tolist())))
+    ref = om.moe_forward(p, from_bf16_bits(xs))
+    got = f32_of_bf16(y)[rows]
+    rel, cos = om.max_rel_err(got, ref.y), om.cosine(got, ref.y)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    print(f"V4 {score_func} T={T}: rel {rel:.2e} cos {cos:.8f} near-ties {near}")
 
 
 @pytest.mark.parametrize("name,T", [("top6_t8", 4), ("toy_t4", 4), ("toy_t4", 16), ("top6_t8", 40)])

@@ -35,15 +35,56 @@ def mod():
 
 def test_moe_install_is_idempotent_and_reversible(mod):
     ref = mod.MoE.forward
-    assert wm.moe_chain(mod) == "ref"
+    assert wm.moe_chain(mod) == ["ref"]
     assert wm.install(mod) is True
     assert getattr(mod.MoE.forward, "_v4_hip_moe", False)
     assert wm.install(mod) is False  # marker seen: no double wrap
     assert wm._REF_FORWARD is ref
-    assert wm.moe_chain(mod) == "hip>ref"
+    assert wm.moe_chain(mod) == ["hip", "ref"]
     assert wm.uninstall(mod) is True
-    assert mod.MoE.forward is ref and wm.moe_chain(mod) == "ref"
+    assert mod.MoE.forward is ref and wm.moe_chain(mod) == ["ref"]
     assert wm.uninstall(mod) is False
+
+
+def _marked_layer(name, marker, kept):
+    """A module shaped like one of the reference's MoE replacements
+    (expert_batch / fp4_grouped / expert_dispatch): a forward carrying the
+    install marker and a module-level _REF_FORWARD."""
+    import sys
+
+    m = types.ModuleType(name)
+
+    def fwd(self, x, input_ids):
+        return m._REF_FORWARD(self, x, input_ids)
+
+    fwd.__module__ = name
+    setattr(fwd, marker, True)
+    m.forward, m._REF_FORWARD = fwd, kept
+    sys.modules[name] = m
+    return m
+
+
+def test_moe_chain_walks_every_kept_forward(mod):
+    """moe_chain follows each marked forward to the one it kept, as the reference's
+    controls.moe_chain does (serving/controls.py:45-68)."""
+    import sys
+
+    ref = mod.MoE.forward
+    grouped = _marked_layer("fake_fp4_grouped", "_v4_grouped", ref)
+    multi = _marked_layer("fake_expert_batch", "_v4_multi", grouped.forward)
+    try:
+        mod.MoE.forward = multi.forward
+        assert wm.moe_chain(mod) == ["multi", "grouped", "ref"]
+        wm.install(mod)
+        assert wm.moe_chain(mod) == ["hip", "multi", "grouped", "ref"]
+        wm.uninstall(mod)
+        grouped._REF_FORWARD = multi.forward  # a loop
+        assert wm.moe_chain(mod) == ["multi", "grouped", "CYCLE"]
+        del sys.modules["fake_fp4_grouped"]
+        assert wm.moe_chain(mod) == ["multi", "grouped", "ORPHAN"]
+    finally:
+        sys.modules.pop("fake_fp4_grouped", None)
+        sys.modules.pop("fake_expert_batch", None)
 
 
 @pytest.mark.parametrize("why", ["world_size>1", "partial-experts", "not-mxfp4-bank"])
@@ -65,15 +106,64 @@ def test_unservable_layers_decline_to_the_kept_forward(mod, why):
 
 def test_kernel_install_rebinds_module_globals():
     m = types.ModuleType("kernels_host")
-    orig = {n: (lambda *a, **k: None) for n in ("act_quant", "fp8_gemm", "fp4_gemm", "sparse_attn")}
+    orig = {n: (lambda *a, **k: None) for n in ("act_quant", "fp8_gemm", "fp4_gemm", "sparse_attn", "linear")}
     for n, f in orig.items():
         setattr(m, n, f)
     assert kernels.install(m) is True
     assert m.act_quant is kernels.act_quant and m.fp8_gemm is kernels.fp8_gemm and m.fp4_gemm is kernels.fp4_gemm
-    assert m.sparse_attn is kernels.sparse_attn
+    assert m.sparse_attn is kernels.sparse_attn and m.linear is kernels.linear
     assert kernels.install(m) is False
     assert kernels.uninstall(m) is True
     assert all(getattr(m, n) is f for n, f in orig.items())
+
+
+def _torch_act_quant(x, block_size=128, scale_fmt=None, scale_dtype=torch.float32, inplace=False):
+    """The reference's CPU act_quant statement (torch_ops.py:33-49), written out
+    here as the binding install() replaces."""
+    z = x.float().unflatten(-1, (-1, block_size))
+    amax = z.abs().amax(-1, keepdim=True).clamp_min(1e-4)
+    s = amax / 448.0
+    if scale_fmt is not None:
+        s = torch.exp2(torch.ceil(torch.log2(s)))
+    q = (z / s).clamp(-448, 448).to(torch.float8_e4m3fn)
+    if inplace:
+        x.copy_((q.float() * s).flatten(-2).to(x.dtype))
+        return x
+    return q.flatten(-2), s.squeeze(-1).to(scale_dtype)
+
+
+def test_act_quant_outside_the_path_goes_to_the_replaced_binding():
+    """The attention calls act_quant(kv, 64, ..., True) (architecture.py:470, 632):
+    after install() that call must reach the replaced act_quant, not fail."""
+    m = types.ModuleType("model_host")
+    m.act_quant = _torch_act_quant
+    kernels.install(m)
+    try:
+        x = torch.randn(3, 256).to(torch.bfloat16)
+        want = _torch_act_quant(x.clone(), 64, "ue8m0", torch.float32, True)
+        got = m.act_quant(x.clone(), 64, "ue8m0", torch.float32, True)
+        assert torch.equal(got, want)
+        q1, s1 = m.act_quant(x, 64, None, torch.float32)
+        q0, s0 = _torch_act_quant(x, 64, None, torch.float32)
+        assert torch.equal(q1.view(torch.uint8), q0.view(torch.uint8)) and torch.equal(s1, s0)
+    finally:
+        kernels.uninstall(m)
+    with pytest.raises(NotImplementedError):
+        kernels.act_quant(torch.zeros(2, 128, dtype=torch.bfloat16), 64)
+
+
+def test_installed_linear_passes_non_fp8_weights_through():
+    """linear() for a bf16 weight is the replaced linear's result (F.linear)."""
+    import torch.nn.functional as F
+
+    m = types.ModuleType("model_linear")
+    m.linear = lambda x, w, bias=None: F.linear(x, w)
+    kernels.install(m)
+    try:
+        x, w = torch.randn(2, 64), torch.randn(8, 64)
+        assert torch.equal(m.linear(x, w), F.linear(x, w))
+    finally:
+        kernels.uninstall(m)
 
 
 def test_kernels_refuse_cpu_tensors():

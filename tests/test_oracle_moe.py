@@ -117,3 +117,31 @@ def test_hash_routing_reads_table_and_keeps_repeats_once():
     s1, s3, s2 = p.shared
     acc = (acc + om.expert_forward(x0, s1, s3, s2, None, p.swiglu_limit, p.round_pow2)).astype(np.float32)
     assert np.array_equal(om.bf16_round(acc), r.y[t:t + 1])
+
+
+def test_gate_scores_match_torch_for_every_score_function():
+    """Gate.forward (architecture.py:699-705) in torch fp32 against the oracle: the
+    oracle rounds each score once from float64 (so do the HIP kernels); torch's
+    fp32 sigmoid / softplus land within 2 ulp of that, its fp32 softmax within 8
+    (6 measured here: an fp32 sum of fp32 exponentials).  The selection agrees
+    wherever the k-th vs (k+1)-th margin is not within that noise."""
+    import torch
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(11)
+    T, D, E, k = 64, 512, 64, 6
+    x = from_bf16_bits((rng.standard_normal((T, D)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+    W = from_bf16_bits(((rng.standard_normal((E, D)) * 0.05).astype(np.float32).view(np.uint32) >> 16)
+                       .astype(np.uint16))
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    logits = torch.from_numpy(x).double() @ torch.from_numpy(W).double().T
+    logits = logits.float()
+    for sf, fn, ulps in (("softmax", lambda a: a.softmax(dim=-1), 8), ("sigmoid", torch.sigmoid, 2),
+                         ("sqrtsoftplus", lambda a: F.softplus(a).sqrt(), 2)):
+        g = om.gate(x, W, bias, k, sf, 1.5)
+        ts = fn(logits).numpy()
+        assert np.all(np.abs(g.scores - ts) <= ulps * np.spacing(np.abs(ts))), sf
+        tb = torch.from_numpy(ts) + torch.from_numpy(bias)
+        tidx = tb.topk(k, dim=-1)[1].numpy()
+        close = g.margin <= 2 * ulps * np.spacing(np.abs(g.biased).max(1))
+        assert np.array_equal(g.indices[~close], tidx[~close]), sf

@@ -81,8 +81,13 @@ def test_e4m3_encode_matches_torch_dense_sweep():
 def test_e4m3_encode_rejects_out_of_range():
     with pytest.raises(ValueError):
         e4m3_encode(np.float32([448.5]))
-    with pytest.raises(ValueError):
-        e4m3_encode(np.float32([np.nan]))
+
+
+def test_e4m3_encode_nan_is_torchs_nan_code():
+    v = np.float32([np.nan, -np.nan, 1.0])
+    got = e4m3_encode(v)
+    want = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert got.tolist() == want.tolist() == [0x7F, 0xFF, 0x38]
 
 
 def test_e2m1_from_definition_and_nibble_order():
@@ -180,3 +185,66 @@ def test_rmsnorm_matches_torch():
     # fp32 reductions differ in order: equal up to one bf16 step at rounding boundaries
     step = np.spacing(np.abs(ref).astype(np.float32)) * 65536
     assert (np.abs(got - ref) <= step).all() and np.mean(got == ref) > 0.99
+
+
+def _torch_act_quant(x, scale_fmt):
+    """The reference's CPU act_quant (torch_ops.py:15-49) evaluated by torch itself."""
+    import torch
+
+    def round_scale(amax, max_inv):
+        mant, exp = torch.frexp(amax * max_inv)
+        return torch.ldexp(torch.ones_like(amax), torch.where(mant == 0.5, exp - 1, exp))
+
+    z = torch.from_numpy(x).float().unflatten(-1, (-1, 128))
+    amax = z.abs().amax(-1, keepdim=True).clamp_min(1e-4)
+    s = round_scale(amax, 1.0 / 448.0) if scale_fmt is not None else amax * (1.0 / 448.0)
+    q = (z / s).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).flatten(-2)
+    return q.view(torch.uint8).numpy(), s.squeeze(-1).numpy()
+
+
+def _special_blocks():
+    """Rows of 128-blocks holding NaN, +inf, -inf, all of them, and ordinary values."""
+    base = np.linspace(-3.0, 3.0, 128, dtype=np.float32)
+    rows = []
+    for spec in ([], [(5, np.nan)], [(0, np.inf)], [(127, -np.inf)], [(3, np.nan), (9, np.inf)],
+                 [(i, np.nan) for i in range(128)]):
+        r = base.copy()
+        for i, v in spec:
+            r[i] = v
+        rows.append(r)
+    return np.stack(rows)
+
+
+def _same_codes(a, b):
+    """e4m3 codes equal, with any two NaN codes (0x7F / 0xFF) counted equal."""
+    a, b = np.asarray(a, np.uint8), np.asarray(b, np.uint8)
+    nan_a, nan_b = (a & 0x7F) == 0x7F, (b & 0x7F) == 0x7F
+    return np.array_equal(nan_a, nan_b) and np.array_equal(a[~nan_a], b[~nan_b])
+
+
+@pytest.mark.parametrize("round_pow2", [True, False])
+def test_act_quant_non_finite_blocks_follow_torch(round_pow2):
+    """NaN / inf inside a block: torch's amax and clamp keep NaN, the fp32 scale is
+    NaN or inf, and the ue8m0 rule gives scale 1 (frexp's exponent for a
+    non-finite value is 0); the oracle must do the same."""
+    x = _special_blocks()
+    q, s = om.act_quant(x, 128, round_pow2)
+    tq, ts = _torch_act_quant(x, "ue8m0" if round_pow2 else None)
+    assert _same_codes(q, tq)
+    assert np.array_equal(s, ts, equal_nan=True)
+    if round_pow2:
+        assert (s[1:] == 1.0).all()
+
+
+def test_wire_pack_non_finite_rows_follow_torch():
+    """_pack_t (serving/chain.py:208-217) on NaN / inf rows, evaluated by torch."""
+    import torch
+
+    x = _special_blocks()
+    q, scale = om.wire_pack(x)
+    f = torch.from_numpy(x)
+    ts = (f.abs().amax(-1, keepdim=True) / 448.0).clamp(min=1e-8, max=torch.finfo(torch.bfloat16).max)
+    ts = ts.to(torch.bfloat16)
+    tq = (f / ts.float()).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    assert _same_codes(q, tq.view(torch.uint8).numpy())
+    assert np.array_equal(scale, ts.float().squeeze(-1).numpy(), equal_nan=True)

@@ -42,3 +42,32 @@ def test_zipf_bias_orders_popularity():
     srt = np.sort(b)[::-1]
     r = np.arange(1, 256)
     assert np.allclose(srt[:-1] - srt[1:], 0.05 * 1.1 * np.log((r + 1) / r), rtol=1e-4, atol=1e-7)
+
+
+def test_zipf_exponent_recovers_known_laws():
+    """The MLE of a finite Zipf law returns s for expected counts proportional to r^-s
+    (the stationary point is exact there), in any order, and grows with the skew."""
+    r = np.arange(1, 257, dtype=np.float64)
+    for s in (0.5, 1.1, 2.0):
+        c = 1e6 * r ** -s
+        assert abs(synth.zipf_exponent(c) - s) < 1e-9
+        assert abs(synth.zipf_exponent(c[::-1].copy()) - s) < 1e-9
+    assert abs(synth.zipf_exponent(np.ones(256))) < 1e-9
+
+
+def test_committed_zipf_calibration_reproduces():
+    """wanferenz_amd/zipf_v4.json: the committed beta routes the calibration batch to
+    the committed histogram, whose fitted exponent is the Zipf(1.1) target."""
+    import json
+
+    with open(synth.ZIPF_V4_FILE) as f:
+        cal = json.load(f)
+    x, gw = synth.zipf_v4_calibration_batch(cal["T"])
+    counts = synth.route_counts(x, gw, synth.zipf_bias(256, cal["s"], cal["beta"]), cal["k"])
+    assert counts.tolist() == cal["counts_per_expert"]
+    assert counts.sum() == cal["T"] * cal["k"] and counts.max() <= cal["T"]
+    assert abs(synth.zipf_exponent(counts) - 1.1) < 2e-3
+    # the strength found by bisection is where the fit crosses s: either side falls short / overshoots
+    lo = synth.route_counts(x, gw, synth.zipf_bias(256, 1.1, cal["beta"] * 0.9), 6)
+    hi = synth.route_counts(x, gw, synth.zipf_bias(256, 1.1, cal["beta"] * 1.1), 6)
+    assert synth.zipf_exponent(lo) < 1.1 < synth.zipf_exponent(hi)

@@ -28,9 +28,13 @@ SIGNATURES = {
     "wz_fp8_pack": (_I, [_P, _I64, _I64, _P, _P]),
     "wz_fp8_linear_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "wz_fp8_linear_packed": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t, _P]),
+    "wz_fp8_gemm_packed_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I]),
+    "wz_fp8_gemm_packed": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t, _P]),
     "wz_moe_workspace_bytes": (ctypes.c_size_t, [_P, _I64]),
     "wz_moe_packed_bytes": (ctypes.c_size_t, [_P, _I]),
     "wz_moe_pack": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),
+    "wz_moe_pack_expert": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _P]),
+    "wz_moe_pack_shared": (_I, [_P, _P, _P, _P, _P]),
     "wz_moe_workspace_init": (_I, [_P, ctypes.c_size_t, _P]),
     "wz_moe_forward": (_I, [_P, _P, _P, _I64, _P, _P, _P, _P, ctypes.c_size_t, _P]),
     "wz_moe_route": (_I, [_P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]),

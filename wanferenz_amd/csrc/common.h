@@ -59,8 +59,28 @@ __device__ __forceinline__ int pow2_ceil_e8m0(float t) {
 
 __device__ __forceinline__ float e8m0_to_f32(int e) { return __uint_as_float(uint32_t(e) << 23); }
 
+// |x| folded into a running block amax the way torch's amax reduces: a NaN
+// anywhere makes the result NaN.  The magnitude bits of a float order as
+// unsigned integers like the magnitudes themselves, and every NaN sorts above
+// +inf, so an integer max of the sign-cleared bits is that reduction.
+__device__ __forceinline__ float absmax(float m, float x) {
+  return __uint_as_float(max(__float_as_uint(m) & 0x7FFFFFFFu, __float_as_uint(x) & 0x7FFFFFFFu));
+}
+
+__device__ __forceinline__ bool is_finite_f32(float x) {
+  return (__float_as_uint(x) & 0x7F800000u) != 0x7F800000u;
+}
+
+// clamp(x, lo, hi) as torch's clamp: NaN passes through.
+__device__ __forceinline__ float clamp_keep_nan(float x, float lo, float hi) {
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
 // Activation block scale from the block's amax (torch_ops.py:38-43):
 // amax floored at 1e-4, then amax/448 (fp32) or its power-of-two ceiling.
+// Non-finite blocks follow the reference's torch arithmetic: the floor keeps
+// NaN, the fp32 scale is NaN or inf, and the power-of-two rule gives 1 (frexp
+// returns exponent 0 for a non-finite value, torch_ops.py:17-21).
 struct ActScale {
   float s;       // the scale the reference stores
   float inv;     // exact reciprocal when pow2 (multiply == divide)
@@ -68,11 +88,11 @@ struct ActScale {
 };
 
 __device__ __forceinline__ ActScale act_scale(float amax, bool pow2) {
-  amax = fmaxf(amax, 1e-4f);
+  amax = amax < 1e-4f ? 1e-4f : amax;
   float t = amax * (1.0f / 448.0f);
   ActScale r;
   if (pow2) {
-    int e = pow2_ceil_e8m0(t);
+    int e = is_finite_f32(t) ? pow2_ceil_e8m0(t) : kE8m0One;
     r.e8m0 = e;
     r.s = e8m0_to_f32(e);
     r.inv = e8m0_to_f32(254 - e);
@@ -84,11 +104,12 @@ __device__ __forceinline__ ActScale act_scale(float amax, bool pow2) {
   return r;
 }
 
-// x / s, clamped to the e4m3 range (torch_ops.py:44).  For a power-of-two
-// scale the reciprocal multiply is exact, so it equals the IEEE quotient.
+// x / s, clamped to the e4m3 range (torch_ops.py:44; NaN stays NaN).  For a
+// power-of-two scale the reciprocal multiply is exact, so it equals the IEEE
+// quotient.
 __device__ __forceinline__ float quant_div(float x, const ActScale& sc, bool pow2) {
-  float q = pow2 ? x * sc.inv : x / sc.s;
-  return fminf(fmaxf(q, -kFp8Max), kFp8Max);
+  const float q = pow2 ? x * sc.inv : x / sc.s;
+  return clamp_keep_nan(q, -kFp8Max, kFp8Max);
 }
 
 // Two floats (already within +-448) -> two e4m3fn bytes, RNE, via the
@@ -100,8 +121,9 @@ __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float 
 
 // ---------------------------------------------------------------- wave ops ---
 
-__device__ __forceinline__ float wave_max_xor(float v, int mask) {
-  return fmaxf(v, __shfl_xor(v, mask, kWave));
+// Block amax across lanes (see absmax: NaN wins).
+__device__ __forceinline__ float wave_absmax_xor(float v, int mask) {
+  return absmax(v, __shfl_xor(v, mask, kWave));
 }
 
 // ---------------------------------------------------------------- MFMA -------

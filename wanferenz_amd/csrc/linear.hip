@@ -47,8 +47,11 @@ struct GvBuf {
   float sf[NKB];
 };
 
-template <int NKB>
-__global__ __launch_bounds__(kGvThreads) void fp8_gemv_kernel(const uint16_t* __restrict__ x,
+// QA: x is pre-quantised e4m3 [M, K] with block scales xs [M, K/128] of kind
+// a_kind (fp8_gemm's a, a_s); otherwise x is bf16 and act_quant is fused.
+template <int NKB, bool QA>
+__global__ __launch_bounds__(kGvThreads) void fp8_gemv_kernel(const void* __restrict__ x,
+                                                              const void* __restrict__ xs, int a_kind,
                                                               const uint8_t* __restrict__ wp,
                                                               const void* __restrict__ w_s, int w_kind,
                                                               uint16_t* __restrict__ y, int M, int N, int K,
@@ -76,10 +79,19 @@ __global__ __launch_bounds__(kGvThreads) void fp8_gemv_kernel(const uint16_t* __
   // weights are requested after the quantisation: issuing them first (weights
   // then x, or x then weights with the quantisation in between) measured
   // 0.3-1.3 us slower per launch.
-  const uint16_t* xrow = nl < M ? x + int64_t(nl) * K : nullptr;
   AOp a[NKB];
+  if constexpr (QA) {
+    const uint8_t* xrow = nl < M ? static_cast<const uint8_t*>(x) + int64_t(nl) * K : nullptr;
+    const void* srow = a_kind == WZ_SCALE_UE8M0
+                           ? static_cast<const void*>(static_cast<const uint8_t*>(xs) + int64_t(nl) * KB)
+                           : static_cast<const void*>(static_cast<const float*>(xs) + int64_t(nl) * KB);
 #pragma unroll
-  for (int q = 0; q < NKB; ++q) a[q] = a_from_bf16(xrow, kb0 + q, g, a_pow2);
+    for (int q = 0; q < NKB; ++q) a[q] = a_from_fp8(xrow, srow, kb0 + q, g, a_kind);
+  } else {
+    const uint16_t* xrow = nl < M ? static_cast<const uint16_t*>(x) + int64_t(nl) * K : nullptr;
+#pragma unroll
+    for (int q = 0; q < NKB; ++q) a[q] = a_from_bf16(xrow, kb0 + q, g, a_pow2);
+  }
   GvBuf<NKB> b0, b1;
   fetch(b0, first);
   auto process = [&](const GvBuf<NKB>& b, int item, int par) {
@@ -120,6 +132,8 @@ __global__ __launch_bounds__(kGvThreads) void fp8_gemv_kernel(const uint16_t* __
   }
 }
 
+static int gemv_grid(int64_t N, int nkb);
+
 static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 }  // namespace wz
@@ -157,15 +171,12 @@ extern "C" int wz_fp8_linear_packed(const void* x_bf16, const void* w_packed, co
   const bool pow2 = act_scale_kind != WZ_SCALE_F32;
   const int nkb = gemv_nkb(K);
   if (M <= kGvMaxM && nkb) {
-    // resident workgroups: one per CU at NKB = 4 (193 VGPRs), two below
-    const int64_t items = N / 16, per_cu = nkb == 4 ? 1 : 2;
-    const dim3 grid(unsigned(std::min<int64_t>(items, per_cu * int64_t(cu_count()))));
-    const uint16_t* x = static_cast<const uint16_t*>(x_bf16);
+    const dim3 grid(unsigned(gemv_grid(N, nkb)));
     const uint8_t* w = static_cast<const uint8_t*>(w_packed);
     uint16_t* y = static_cast<uint16_t*>(y_bf16);
-#define WZ_GEMV(NKBV)                                                                                    \
-  WZ_LAUNCH("fp8_gemv", stream, fp8_gemv_kernel<NKBV>, grid, dim3(kGvThreads), 0, x, w, w_s, w_scale_kind, y, \
-            int(M), int(N), int(K), pow2 ? 1 : 0)
+#define WZ_GEMV(NKBV)                                                                                   \
+  WZ_LAUNCH("fp8_gemv", stream, (fp8_gemv_kernel<NKBV, false>), grid, dim3(kGvThreads), 0, x_bf16,         \
+            static_cast<const void*>(nullptr), 0, w, w_s, w_scale_kind, y, int(M), int(N), int(K), pow2 ? 1 : 0)
     switch (nkb) {
       case 1: WZ_GEMV(1); break;
       case 2: WZ_GEMV(2); break;
@@ -184,4 +195,72 @@ extern "C" int wz_fp8_linear_packed(const void* x_bf16, const void* w_packed, co
   if (int rc = launch_act_quant(x_bf16, M, K, xq, xs, qkind, stream)) return rc;
   return launch_dense_fp8(static_cast<const uint8_t*>(w_packed), w_s, w_scale_kind, xq, xs, pow2,
                           static_cast<uint16_t*>(y_bf16), M, N, K, stream);
+}
+
+namespace wz {
+
+__global__ void e8m0_to_f32_kernel(const uint8_t* __restrict__ src, float* __restrict__ dst, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = e8m0_to_f32(src[i]);
+}
+
+static int gemv_grid(int64_t N, int nkb) {
+  // resident workgroups: one per CU at NKB = 4 (193 VGPRs), two below
+  const int64_t items = N / 16, per_cu = nkb == 4 ? 1 : 2;
+  return int(std::min<int64_t>(items, per_cu * int64_t(cu_count())));
+}
+
+}  // namespace wz
+
+extern "C" size_t wz_fp8_gemm_packed_workspace_bytes(int64_t M, int64_t K, int act_scale_kind) {
+  using namespace wz;
+  if (M <= 0 || K <= 0) return 0;
+  if (M <= kGvMaxM && gemv_nkb(K)) return 0;
+  return act_scale_kind == WZ_SCALE_UE8M0 ? size_t(M) * size_t(K / 128) * 4 : 0;
+}
+
+extern "C" int wz_fp8_gemm_packed(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
+                                  void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
+                                  int w_scale_kind, void* ws, size_t ws_bytes, hipStream_t stream) {
+  using namespace wz;
+  if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 128)
+    return set_error(WZ_EINVAL, "fp8_gemm_packed: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
+                     (long long)K);
+  if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
+    return set_error(WZ_EINVAL, "fp8_gemm_packed: dimension too large");
+  if (act_scale_kind < WZ_SCALE_F32 || act_scale_kind > WZ_SCALE_UE8M0_F32 ||
+      (w_scale_kind != WZ_WSCALE_F32 && w_scale_kind != WZ_WSCALE_E8M0))
+    return set_error(WZ_EINVAL, "fp8_gemm_packed: bad scale kinds %d/%d", act_scale_kind, w_scale_kind);
+  if (M == 0) return WZ_OK;
+  if (!a_e4m3 || !a_s || !w_packed || !w_s || !c_bf16) return set_error(WZ_EINVAL, "fp8_gemm_packed: null pointer");
+  const bool pow2 = act_scale_kind != WZ_SCALE_F32;
+  const int nkb = gemv_nkb(K);
+  const uint8_t* w = static_cast<const uint8_t*>(w_packed);
+  uint16_t* c = static_cast<uint16_t*>(c_bf16);
+  if (M <= kGvMaxM && nkb) {
+    const dim3 grid(unsigned(gemv_grid(N, nkb)));
+#define WZ_GEMV(NKBV)                                                                                            \
+  WZ_LAUNCH("fp8_gemv", stream, (fp8_gemv_kernel<NKBV, true>), grid, dim3(kGvThreads), 0, a_e4m3, a_s,           \
+            act_scale_kind, w, w_s, w_scale_kind, c, int(M), int(N), int(K), pow2 ? 1 : 0)
+    switch (nkb) {
+      case 1: WZ_GEMV(1); break;
+      case 2: WZ_GEMV(2); break;
+      default: WZ_GEMV(4); break;
+    }
+#undef WZ_GEMV
+    return check_launch("fp8_gemv");
+  }
+  const float* xs = static_cast<const float*>(a_s);
+  if (act_scale_kind == WZ_SCALE_UE8M0) {
+    const size_t need = wz_fp8_gemm_packed_workspace_bytes(M, K, act_scale_kind);
+    if (!ws || ws_bytes < need)
+      return set_error(WZ_ESPACE, "fp8_gemm_packed: workspace of %zu bytes needed for M=%lld K=%lld, got %zu", need,
+                       (long long)M, (long long)K, ws_bytes);
+    const int64_t n = M * (K / 128);
+    WZ_LAUNCH("e8m0_to_f32", stream, e8m0_to_f32_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+              static_cast<const uint8_t*>(a_s), static_cast<float*>(ws), n);
+    if (int rc = check_launch("fp8_gemm_packed scales")) return rc;
+    xs = static_cast<const float*>(ws);
+  }
+  return launch_dense_fp8(w, w_s, w_scale_kind, static_cast<const uint8_t*>(a_e4m3), xs, pow2, c, M, N, K, stream);
 }

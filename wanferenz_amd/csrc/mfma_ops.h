@@ -105,9 +105,9 @@ __device__ __forceinline__ AOp a_quant_bf16(const ARaw& r, bool pow2) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      amax = fmaxf(amax, fmaxf(fabsf(bf16lo(uint32_t(w[i][j]))), fabsf(bf16hi(uint32_t(w[i][j])))));
-  amax = wave_max_xor(amax, 16);
-  amax = wave_max_xor(amax, 32);
+      amax = absmax(absmax(amax, bf16lo(uint32_t(w[i][j]))), bf16hi(uint32_t(w[i][j])));
+  amax = wave_absmax_xor(amax, 16);
+  amax = wave_absmax_xor(amax, 32);
   const ActScale sc = act_scale(amax, pow2);
   a.se8 = pow2 ? sc.e8m0 : kE8m0One;
   a.sf = sc.s;

@@ -126,13 +126,18 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ sco
   }
   // lane j < k ends up holding the j-th selected expert
   int my_sel = 0;
+  bool poison = false;  // hash id or table entry out of range: NaN weights, in-range reads
   if (tid2eid != nullptr) {
     int64_t id = input_ids[t];
-    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+    const bool bad_id = id < 0 || id >= vocab;
+    id = bad_id ? 0 : id;
+    bool bad_e = false;
     if (lane < k) {
       const int e = tid2eid[id * k + lane];
-      my_sel = e < 0 ? 0 : (e >= E ? E - 1 : e);
+      bad_e = e < 0 || e >= E;
+      my_sel = bad_e ? 0 : e;
     }
+    poison = bad_id || __ballot(bad_e) != 0ull;
   } else {
     unsigned taken = 0u;
     for (int j = 0; j < k; ++j) {
@@ -159,6 +164,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ sco
   float v = mine;
   if (score_func != WZ_SCORE_SOFTMAX) v = v / tot;
   v = v * route_scale;
+  if (poison) v = __builtin_nanf("");
   if (lane < k) {
     weights[int64_t(t) * k + lane] = v;
     idx[int64_t(t) * k + lane] = my_sel;
@@ -354,8 +360,13 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
 int launch_prefill_gate(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* input_ids, int64_t T,
                         hipStream_t stream);
 
+// Tokens per call of the kernel sequence: the routed pairs of one call (T * k)
+// fit the kMaxPairs-row tables.  wz_moe_forward serves larger T as successive
+// chunks of this many tokens on the same workspace (the layer is token-local).
+static int64_t chunk_tokens(const wz_moe_desc* d) { return kMaxPairs / d->topk; }
+
 static int validate(const wz_moe_desc* d, int64_t T, const void* ws, size_t ws_bytes,
-                    const char* what) {
+                    const char* what, bool chunked = false) {
   if (!d) return set_error(WZ_EINVAL, "%s: null descriptor", what);
   if (d->dim <= 0 || d->dim % 128 || d->inter <= 0 || d->inter % 128)
     return set_error(WZ_EINVAL, "%s: dim=%d and inter=%d must be positive multiples of 128", what,
@@ -364,7 +375,7 @@ static int validate(const wz_moe_desc* d, int64_t T, const void* ws, size_t ws_b
     return set_error(WZ_EINVAL, "%s: n_experts=%d outside 1..%d", what, d->n_experts, kMaxExperts);
   if (d->topk <= 0 || d->topk > 16 || d->topk > d->n_experts)
     return set_error(WZ_EINVAL, "%s: topk=%d outside 1..min(16, n_experts)", what, d->topk);
-  if (T < 0 || T * d->topk > kMaxPairs)
+  if (T < 0 || T > (int64_t(1) << 40) || (!chunked && T * d->topk > kMaxPairs))
     return set_error(WZ_EINVAL, "%s: T=%lld x topk=%d exceeds %d routed pairs", what, (long long)T,
                      d->topk, kMaxPairs);
   if (d->score_func < 0 || d->score_func > 2)
@@ -378,7 +389,7 @@ static int validate(const wz_moe_desc* d, int64_t T, const void* ws, size_t ws_b
   }
   if (T == 0) return WZ_OK;  // nothing to do: no workspace needed
   if (!ws) return set_error(WZ_EINVAL, "%s: null workspace", what);
-  const size_t need = moe_ws_layout(d, T, nullptr).bytes;
+  const size_t need = wz_moe_workspace_bytes(d, T);
   if (ws_bytes < need)
     return set_error(WZ_ESPACE, "%s: workspace %zu bytes < %zu needed for T=%lld", what, ws_bytes,
                      need, (long long)T);
@@ -410,7 +421,8 @@ static int launch_routing(const wz_moe_desc* d, const MoeWs& w, const void* x,
 }  // namespace wz
 
 extern "C" size_t wz_moe_workspace_bytes(const wz_moe_desc* d, int64_t T) {
-  if (!d || T < 0) return 0;
+  if (!d || T < 0 || d->topk <= 0) return 0;
+  if (T > wz::chunk_tokens(d)) T = wz::chunk_tokens(d);
   const size_t big = wz::moe_ws_layout(d, T, nullptr).bytes;
   const size_t dec = wz::moe_ws_layout(d, T < wz::kDecodeMaxT ? T : wz::kDecodeMaxT, nullptr).bytes;
   return big > dec ? big : dec;
@@ -456,37 +468,49 @@ extern "C" int wz_moe_route(const wz_moe_desc* d, const void* x_bf16, const int6
   return WZ_OK;
 }
 
+namespace wz {
+
+static int forward_chunk(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids, int64_t T, void* y_bf16,
+                         float* weights_out, int64_t* indices_out, void* ws, hipStream_t stream) {
+  const MoeWs w = moe_ws_layout(d, T, static_cast<uint8_t*>(ws));
+  const int k = d->topk, D = d->dim;
+  const int64_t P = T * k;
+  if (T <= kDecodeMaxT) {
+    if (int rc = launch_decode(d, w, x_bf16, input_ids, T, y_bf16, stream, -1)) return rc;
+  } else {
+    if (int rc = launch_routing(d, w, x_bf16, input_ids, T, stream)) return rc;
+    if (int rc = launch_prefill_experts(d, w, x_bf16, T, stream, -1)) return rc;
+    if (int rc = launch_combine(w, T, k, D, y_bf16, stream)) return rc;
+  }
+  if (weights_out || indices_out) {
+    WZ_LAUNCH("moe_export", stream, export_routing_kernel, dim3(unsigned((P + 255) / 256)), dim3(256), 0, w,
+              int(P), weights_out, indices_out);
+    if (int rc = check_launch("moe export")) return rc;
+  }
+  return WZ_OK;
+}
+
+}  // namespace wz
+
 extern "C" int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids,
                               int64_t T, void* y_bf16, float* weights_out, int64_t* indices_out,
                               void* ws, size_t ws_bytes, hipStream_t stream) {
   using namespace wz;
-  if (int rc = validate(d, T, ws, ws_bytes, "moe_forward")) return rc;
+  if (int rc = validate(d, T, ws, ws_bytes, "moe_forward", true)) return rc;
   if (T == 0) return WZ_OK;
   if (!x_bf16 || !y_bf16) return set_error(WZ_EINVAL, "moe_forward: null x or y");
-  if (!d->w13 || !d->w13_s || !d->w2 || !d->w2_s || !d->sh_w1 || !d->sh_w1_s || !d->sh_w3 ||
-      !d->sh_w3_s || !d->sh_w2 || !d->sh_w2_s)
-    return set_error(WZ_EINVAL, "moe_forward: expert weights missing");
-  const MoeWs w = moe_ws_layout(d, T, static_cast<uint8_t*>(ws));
-  if (T <= kDecodeMaxT && d->n_experts <= kMaxExperts) {
-    if (d->tid2eid && !input_ids) return set_error(WZ_EINVAL, "moe: hash-routed layer needs input_ids");
-    if (int rc = launch_decode(d, w, x_bf16, input_ids, T, y_bf16, stream, -1)) return rc;
-    if (weights_out || indices_out) {
-      const int P = int(T * d->topk);
-      WZ_LAUNCH("moe_export", stream, export_routing_kernel, dim3(unsigned((P + 255) / 256)), dim3(256), 0, w,
-                P, weights_out, indices_out);
-      if (int rc = check_launch("moe export")) return rc;
-    }
-    return WZ_OK;
-  }
-  if (int rc = launch_routing(d, w, x_bf16, input_ids, T, stream)) return rc;
-  const int k = d->topk, D = d->dim;
-  const int64_t P = T * k;
-  if (int rc = launch_prefill_experts(d, w, x_bf16, T, stream, -1)) return rc;
-  if (int rc = launch_combine(w, T, k, D, y_bf16, stream)) return rc;
-  if (weights_out || indices_out) {
-    WZ_LAUNCH("moe_export", stream, export_routing_kernel, dim3(unsigned((P + 255) / 256)), dim3(256), 0, w,
-                       int(P), weights_out, indices_out);
-    if (int rc = check_launch("moe export")) return rc;
+  if (!d->w13p || !d->w13p_s || !d->w2p || !d->w2p_s || !d->sh13p || !d->sh2p)
+    return set_error(WZ_EINVAL, "moe_forward: packed expert banks missing (build them with wz_moe_pack)");
+  if (!d->sh_w1_s || !d->sh_w3_s || !d->sh_w2_s)
+    return set_error(WZ_EINVAL, "moe_forward: shared-expert block scales missing");
+  if (d->tid2eid && !input_ids) return set_error(WZ_EINVAL, "moe: hash-routed layer needs input_ids");
+  const int64_t C = chunk_tokens(d), k = d->topk, D = d->dim;
+  for (int64_t t0 = 0; t0 < T; t0 += C) {
+    const int64_t n = T - t0 < C ? T - t0 : C;
+    if (int rc = forward_chunk(d, static_cast<const uint16_t*>(x_bf16) + t0 * D, input_ids ? input_ids + t0 : nullptr,
+                               n, static_cast<uint16_t*>(y_bf16) + t0 * D, weights_out ? weights_out + t0 * k : nullptr,
+                               indices_out ? indices_out + t0 * k : nullptr, ws, stream))
+      return rc;
   }
   return WZ_OK;
 }

@@ -79,8 +79,8 @@ __device__ __forceinline__ void reduce_waves(v4f (&acc)[NB], float* red, int wav
 __device__ __forceinline__ float swiglu(float gs, float us, float limit) {
   float gv = bf16_round(gs), uv = bf16_round(us);
   if (limit > 0.0f) {
-    uv = fminf(fmaxf(uv, -limit), limit);
-    gv = fminf(gv, limit);
+    uv = clamp_keep_nan(uv, -limit, limit);
+    gv = gv > limit ? limit : gv;
   }
   return silu_f32(gv) * uv;
 }
@@ -150,13 +150,18 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       }
     }
     int my_sel = 0;
+    bool poison = false;  // hash id or table entry out of range: NaN weights, in-range reads
     if (d.tid2eid != nullptr) {
       int64_t id = ids[t];
-      id = id < 0 ? 0 : (id >= d.vocab ? d.vocab - 1 : id);
+      const bool bad_id = id < 0 || id >= d.vocab;
+      id = bad_id ? 0 : id;
+      bool bad_e = false;
       if (lane < k) {
         const int e = d.tid2eid[id * k + lane];
-        my_sel = e < 0 ? 0 : (e >= E ? E - 1 : e);
+        bad_e = e < 0 || e >= E;
+        my_sel = bad_e ? 0 : e;
       }
+      poison = bad_id || __ballot(bad_e) != 0ull;
     } else {
       unsigned taken = 0u;
 #pragma unroll 1
@@ -195,6 +200,7 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
     float v = mine;
     if (d.score_func != WZ_SCORE_SOFTMAX) v = v / tot;
     v = v * d.route_scale;
+    if (poison) v = __builtin_nanf("");
     if (lane < k) {
       ws.weights[t * k + lane] = v;
       ws.idx[t * k + lane] = my_sel;
@@ -329,11 +335,11 @@ __device__ void quant_row(uint8_t* __restrict__ q, float* __restrict__ s, const 
     }
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
-    amax = wave_max_xor(amax, 1);
-    amax = wave_max_xor(amax, 2);
-    amax = wave_max_xor(amax, 4);
-    amax = wave_max_xor(amax, 8);
+    for (int i = 0; i < 8; ++i) amax = absmax(amax, f[i]);
+    amax = wave_absmax_xor(amax, 1);
+    amax = wave_absmax_xor(amax, 2);
+    amax = wave_absmax_xor(amax, 4);
+    amax = wave_absmax_xor(amax, 8);
     const ActScale sc = act_scale(amax, pow2);
     if (valid) {
       const uint32_t lo = pack_fp8x4(quant_div(f[0], sc, pow2), quant_div(f[1], sc, pow2),
@@ -982,11 +988,11 @@ __global__ __launch_bounds__(kW2Threads) void w2_lds_kernel(wz_moe_desc d, MoeWs
       }
       float amax = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
-      amax = wave_max_xor(amax, 1);
-      amax = wave_max_xor(amax, 2);
-      amax = wave_max_xor(amax, 4);
-      amax = wave_max_xor(amax, 8);
+      for (int e = 0; e < 8; ++e) amax = absmax(amax, f[e]);
+      amax = wave_absmax_xor(amax, 1);
+      amax = wave_absmax_xor(amax, 2);
+      amax = wave_absmax_xor(amax, 4);
+      amax = wave_absmax_xor(amax, 8);
       const ActScale sc = act_scale(amax, POW2);
       if (c < nch) {
         const int row = c / CPR, off = (c % CPR) * 8;

@@ -236,12 +236,17 @@ __global__ __launch_bounds__(256) void topk_refine_kernel(const uint16_t* __rest
   }
   int my_sel = 0;
   float mine = 0.0f;  // exact score of the lane's slot (lane < k)
+  bool poison = false;  // hash id or table entry out of range: NaN weights, in-range reads
   if (tid2eid != nullptr) {
     int64_t id = input_ids[t];
-    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+    poison = id < 0 || id >= vocab;
+    id = poison ? 0 : id;
     for (int j = 0; j < k; ++j) {
       int e = tid2eid[id * k + j];
-      e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+      if (e < 0 || e >= E) {
+        poison = true;
+        e = 0;
+      }
       const float s = score_of(exact_logit(xv, xr, W + int64_t(e) * D, D, lane), score_func);
       if (lane == j) {
         my_sel = e;
@@ -323,7 +328,7 @@ __global__ __launch_bounds__(256) void topk_refine_kernel(const uint16_t* __rest
   }
   float tot = 0.0f;
   for (int j = 0; j < k; ++j) tot += __shfl(mine, j, kWave);  // slot order, fp32
-  const float v = mine / tot * route_scale;
+  const float v = poison ? __builtin_nanf("") : mine / tot * route_scale;
   if (lane < k) {
     weights[int64_t(t) * k + lane] = v;
     idx[int64_t(t) * k + lane] = my_sel;
@@ -640,8 +645,8 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
           if (r < nrows) {
             float gv = bf16_round(acc[2 * q][m][i]), uv = bf16_round(acc[2 * q + 1][m][i]);
             if (d.swiglu_limit > 0.0f) {
-              uv = fminf(fmaxf(uv, -d.swiglu_limit), d.swiglu_limit);
-              gv = fminf(gv, d.swiglu_limit);
+              uv = clamp_keep_nan(uv, -d.swiglu_limit, d.swiglu_limit);
+              gv = gv > d.swiglu_limit ? d.swiglu_limit : gv;
             }
             const float hv = silu_f32(gv) * uv;
             if (DENSE) {

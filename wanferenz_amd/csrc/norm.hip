@@ -110,11 +110,11 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
     }
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
-    amax = wave_max_xor(amax, 1);
-    amax = wave_max_xor(amax, 2);
-    amax = wave_max_xor(amax, 4);
-    amax = wave_max_xor(amax, 8);
+    for (int i = 0; i < 8; ++i) amax = absmax(amax, f[i]);
+    amax = wave_absmax_xor(amax, 1);
+    amax = wave_absmax_xor(amax, 2);
+    amax = wave_absmax_xor(amax, 4);
+    amax = wave_absmax_xor(amax, 8);
     const ActScale sc = act_scale(amax, pow2);
     if (valid) {
       const uint32_t lo = pack_fp8x4(quant_div(f[0], sc, pow2), quant_div(f[1], sc, pow2),
@@ -146,14 +146,14 @@ __global__ __launch_bounds__(256) void wire_pack_kernel(const uint16_t* __restri
     const v4i v = load16(xr + c * 8);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      amax = fmaxf(amax, fmaxf(fabsf(bf16lo(uint32_t(v[i]))), fabsf(bf16hi(uint32_t(v[i])))));
+      amax = absmax(absmax(amax, bf16lo(uint32_t(v[i]))), bf16hi(uint32_t(v[i])));
   }
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, kWave));
+  for (int m = 32; m >= 1; m >>= 1) amax = wave_absmax_xor(amax, m);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
-  const float t = fminf(fmaxf(amax / 448.0f, 1e-8f), 3.3895313892515355e38f);
+  amax = absmax(absmax(part[0], part[1]), absmax(part[2], part[3]));
+  const float t = clamp_keep_nan(amax / 448.0f, 1e-8f, 3.3895313892515355e38f);
   const uint16_t sb = f32_to_bf16(t);
   const float sf = bf16_to_f32(sb);
   if (threadIdx.x == 0) scale[row] = sb;
@@ -162,8 +162,8 @@ __global__ __launch_bounds__(256) void wire_pack_kernel(const uint16_t* __restri
     float f[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f[2 * i] = fminf(fmaxf(bf16lo(uint32_t(v[i])) / sf, -kFp8Max), kFp8Max);
-      f[2 * i + 1] = fminf(fmaxf(bf16hi(uint32_t(v[i])) / sf, -kFp8Max), kFp8Max);
+      f[2 * i] = clamp_keep_nan(bf16lo(uint32_t(v[i])) / sf, -kFp8Max, kFp8Max);
+      f[2 * i + 1] = clamp_keep_nan(bf16hi(uint32_t(v[i])) / sf, -kFp8Max, kFp8Max);
     }
     *reinterpret_cast<uint2*>(q + row * D + c * 8) =
         make_uint2(pack_fp8x4(f[0], f[1], f[2], f[3]), pack_fp8x4(f[4], f[5], f[6], f[7]));

@@ -12,11 +12,12 @@
 
 namespace wz {
 
-// mode 0: routed w13, 1: routed w2, 2: shared w13 (FP8), 3: shared w2 (FP8)
+// mode 0: routed w13 (src0 = w1 rows, src1 = w3 rows of expert 0, `estride`
+// bytes between experts), 1: routed w2, 2: shared w13 (FP8), 3: shared w2 (FP8)
 __global__ __launch_bounds__(256) void pack_weights_kernel(const uint8_t* __restrict__ src0,
                                                            const uint8_t* __restrict__ src1,
                                                            uint8_t* __restrict__ dst, int64_t n16,
-                                                           int mode, int E, int D, int I) {
+                                                           int mode, int64_t estride, int D, int I) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= n16) return;
   const int lane = int(i & 63), r = lane & 15, g = lane >> 4;
@@ -30,16 +31,14 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const uint8_t* __rest
     blk /= KB;
     const int ft = int(blk % FT);
     const int64_t e = blk / FT;
-    const int64_t row = e * 2 * I + int64_t(m) * I + ft * 16 + r;
-    src = src0 + row * (D / 2) + kb * 64 + g * 16;
+    src = (m == 0 ? src0 : src1) + e * estride + int64_t(ft * 16 + r) * (D / 2) + kb * 64 + g * 16;
   } else if (mode == 1) {
     const int KB = I / 128, DT = D / 16;
     const int kb = int(blk % KB);
     blk /= KB;
     const int dt = int(blk % DT);
     const int64_t e = blk / DT;
-    const int64_t row = e * D + dt * 16 + r;
-    src = src0 + row * (I / 2) + kb * 64 + g * 16;
+    src = src0 + e * estride + int64_t(dt * 16 + r) * (I / 2) + kb * 64 + g * 16;
   } else if (mode == 2) {
     const int KB = D / 128;
     const int h = int(blk & 1);
@@ -60,18 +59,19 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const uint8_t* __rest
   *reinterpret_cast<v4i*>(dst + i * 16) = load16(src);
 }
 
-// mode 0: routed w13 scales [E, 2I, D/32]; 1: routed w2 scales [E, D, I/32]
-__global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restrict__ src,
+// mode 0: routed w13 scales (src0 = w1 rows [I, D/32], src1 = w3 rows, `estride`
+// bytes between experts); 1: routed w2 scales [D, I/32] per expert
+__global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restrict__ src0,
+                                                          const uint8_t* __restrict__ src1,
                                                           uint32_t* __restrict__ dst, int64_t n4,
-                                                          int mode, int D, int I) {
+                                                          int mode, int64_t estride, int D, int I) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= n4) return;
   const int lane = int(i & 63), r = lane & 15, g = lane >> 4;
   int64_t blk = i >> 6;
-  int64_t row;
-  int K, KB, kg;
+  const uint8_t* row;
+  int KB, kg;
   if (mode == 0) {
-    K = D;
     KB = D / 128;
     const int KG = (KB + 3) / 4, FT = I / 16;
     const int m = int(blk & 1);
@@ -80,22 +80,21 @@ __global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restr
     blk /= KG;
     const int ft = int(blk % FT);
     const int64_t e = blk / FT;
-    row = e * 2 * I + int64_t(m) * I + ft * 16 + r;
+    row = (m == 0 ? src0 : src1) + e * estride + int64_t(ft * 16 + r) * (D / 32);
   } else {
-    K = I;
     KB = I / 128;
     const int KG = (KB + 3) / 4, DT = D / 16;
     kg = int(blk % KG);
     blk /= KG;
     const int dt = int(blk % DT);
     const int64_t e = blk / DT;
-    row = e * D + dt * 16 + r;
+    row = src0 + e * estride + int64_t(dt * 16 + r) * (I / 32);
   }
   uint32_t v = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int kb = kg * 4 + j;
-    if (kb < KB) v |= uint32_t(src[row * (K / 32) + kb * 4 + g]) << (8 * j);
+    if (kb < KB) v |= uint32_t(row[kb * 4 + g]) << (8 * j);
   }
   dst[i] = v;
 }
@@ -128,8 +127,34 @@ namespace wz {
 int launch_pack_fp8(const void* w, int64_t N, int64_t K, void* dst, hipStream_t stream) {
   const int64_t n16 = N * K / 16;
   WZ_LAUNCH("fp8_pack", stream, pack_weights_kernel, dim3(unsigned((n16 + 255) / 256)), dim3(256), 0,
-            static_cast<const uint8_t*>(w), nullptr, static_cast<uint8_t*>(dst), n16, 3, 1, int(N), int(K));
+            static_cast<const uint8_t*>(w), nullptr, static_cast<uint8_t*>(dst), n16, 3, int64_t(0), int(N),
+            int(K));
   return check_launch("fp8_pack");
+}
+
+static int pack_w(const void* a, const void* b, void* dst, int64_t bytes, int mode, int64_t estride, int D, int I,
+                  hipStream_t stream) {
+  const int64_t n16 = bytes / 16;
+  WZ_LAUNCH("moe_pack", stream, pack_weights_kernel, dim3(unsigned((n16 + 255) / 256)), dim3(256), 0,
+            static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(b), static_cast<uint8_t*>(dst), n16, mode,
+            estride, D, I);
+  return check_launch("moe_pack weights");
+}
+
+static int pack_s(const void* a, const void* b, void* dst, int64_t bytes, int mode, int64_t estride, int D, int I,
+                  hipStream_t stream) {
+  const int64_t n4 = bytes / 4;
+  WZ_LAUNCH("moe_pack", stream, pack_scales_kernel, dim3(unsigned((n4 + 255) / 256)), dim3(256), 0,
+            static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(b), static_cast<uint32_t*>(dst), n4, mode,
+            estride, D, I);
+  return check_launch("moe_pack scales");
+}
+
+static int pack_dims_ok(const wz_moe_desc* d, const char* what) {
+  if (d->dim <= 0 || d->inter <= 0 || d->dim % 128 || d->inter % 128 || d->n_experts <= 0)
+    return set_error(WZ_EINVAL, "%s: dim=%d, inter=%d must be positive multiples of 128, n_experts=%d > 0", what,
+                     d->dim, d->inter, d->n_experts);
+  return WZ_OK;
 }
 
 }  // namespace wz
@@ -141,32 +166,51 @@ extern "C" int wz_moe_pack(const wz_moe_desc* d, void* w13p, void* w13p_s, void*
     return set_error(WZ_EINVAL, "moe_pack: reference banks missing");
   if (!w13p || !w13p_s || !w2p || !w2p_s || !sh13p || !sh2p)
     return set_error(WZ_EINVAL, "moe_pack: null output");
-  if (d->dim % 128 || d->inter % 128) return set_error(WZ_EINVAL, "moe_pack: dims must be multiples of 128");
-  const int E = d->n_experts, D = d->dim, I = d->inter;
-  struct W {
-    const void* a;
-    const void* b;
-    void* dst;
-    int which, mode;
-  } ws[] = {{d->w13, nullptr, w13p, 0, 0}, {d->w2, nullptr, w2p, 2, 1},
-            {d->sh_w1, d->sh_w3, sh13p, 4, 2}, {d->sh_w2, nullptr, sh2p, 5, 3}};
-  for (const W& w : ws) {
-    const int64_t n16 = packed_bytes(d, w.which) / 16;
-    WZ_LAUNCH("moe_pack", stream, pack_weights_kernel, dim3(unsigned((n16 + 255) / 256)), dim3(256), 0,
-              static_cast<const uint8_t*>(w.a), static_cast<const uint8_t*>(w.b), static_cast<uint8_t*>(w.dst),
-              n16, w.mode, E, D, I);
-    if (int rc = check_launch("moe_pack weights")) return rc;
-  }
-  struct S {
-    const void* src;
-    void* dst;
-    int which, mode;
-  } ss[] = {{d->w13_s, w13p_s, 1, 0}, {d->w2_s, w2p_s, 3, 1}};
-  for (const S& s : ss) {
-    const int64_t n4 = packed_bytes(d, s.which) / 4;
-    WZ_LAUNCH("moe_pack", stream, pack_scales_kernel, dim3(unsigned((n4 + 255) / 256)), dim3(256), 0,
-              static_cast<const uint8_t*>(s.src), static_cast<uint32_t*>(s.dst), n4, s.mode, D, I);
-    if (int rc = check_launch("moe_pack scales")) return rc;
-  }
-  return WZ_OK;
+  if (int rc = pack_dims_ok(d, "moe_pack")) return rc;
+  const int D = d->dim, I = d->inter;
+  const uint8_t* w13 = static_cast<const uint8_t*>(d->w13);
+  const uint8_t* w13s = static_cast<const uint8_t*>(d->w13_s);
+  const int64_t w1b = int64_t(I) * D / 2, s1b = int64_t(I) * D / 32;
+  if (int rc = pack_w(w13, w13 + w1b, w13p, packed_bytes(d, 0), 0, 2 * w1b, D, I, stream)) return rc;
+  if (int rc = pack_w(d->w2, nullptr, w2p, packed_bytes(d, 2), 1, w1b, D, I, stream)) return rc;
+  if (int rc = pack_w(d->sh_w1, d->sh_w3, sh13p, packed_bytes(d, 4), 2, 0, D, I, stream)) return rc;
+  if (int rc = pack_w(d->sh_w2, nullptr, sh2p, packed_bytes(d, 5), 3, 0, D, I, stream)) return rc;
+  if (int rc = pack_s(w13s, w13s + s1b, w13p_s, packed_bytes(d, 1), 0, 2 * s1b, D, I, stream)) return rc;
+  return pack_s(d->w2_s, nullptr, w2p_s, packed_bytes(d, 3), 1, s1b, D, I, stream);
+}
+
+extern "C" int wz_moe_pack_expert(const wz_moe_desc* d, int64_t e, const void* w1, const void* w1_s,
+                                  const void* w3, const void* w3_s, const void* w2, const void* w2_s,
+                                  hipStream_t stream) {
+  using namespace wz;
+  if (!d) return set_error(WZ_EINVAL, "moe_pack_expert: null descriptor");
+  if (int rc = pack_dims_ok(d, "moe_pack_expert")) return rc;
+  if (e < 0 || e >= d->n_experts)
+    return set_error(WZ_EINVAL, "moe_pack_expert: expert %lld outside 0..%d", (long long)e, d->n_experts - 1);
+  if (!w1 || !w1_s || !w3 || !w3_s || !w2 || !w2_s) return set_error(WZ_EINVAL, "moe_pack_expert: null input");
+  if (!d->w13p || !d->w13p_s || !d->w2p || !d->w2p_s)
+    return set_error(WZ_EINVAL, "moe_pack_expert: the descriptor's packed banks are not set");
+  const int D = d->dim, I = d->inter;
+  const int64_t E = d->n_experts;
+  auto slot = [&](const void* bank, int which) {
+    return const_cast<uint8_t*>(static_cast<const uint8_t*>(bank)) + packed_bytes(d, which) / E * e;
+  };
+  if (int rc = pack_w(w1, w3, slot(d->w13p, 0), packed_bytes(d, 0) / E, 0, 0, D, I, stream)) return rc;
+  if (int rc = pack_w(w2, nullptr, slot(d->w2p, 2), packed_bytes(d, 2) / E, 1, 0, D, I, stream)) return rc;
+  if (int rc = pack_s(w1_s, w3_s, slot(d->w13p_s, 1), packed_bytes(d, 1) / E, 0, 0, D, I, stream)) return rc;
+  return pack_s(w2_s, nullptr, slot(d->w2p_s, 3), packed_bytes(d, 3) / E, 1, 0, D, I, stream);
+}
+
+extern "C" int wz_moe_pack_shared(const wz_moe_desc* d, const void* sh_w1, const void* sh_w3, const void* sh_w2,
+                                  hipStream_t stream) {
+  using namespace wz;
+  if (!d) return set_error(WZ_EINVAL, "moe_pack_shared: null descriptor");
+  if (int rc = pack_dims_ok(d, "moe_pack_shared")) return rc;
+  if (!sh_w1 || !sh_w3 || !sh_w2) return set_error(WZ_EINVAL, "moe_pack_shared: null input");
+  if (!d->sh13p || !d->sh2p) return set_error(WZ_EINVAL, "moe_pack_shared: the descriptor's packed banks are not set");
+  const int D = d->dim, I = d->inter;
+  void* sh13p = const_cast<void*>(d->sh13p);
+  void* sh2p = const_cast<void*>(d->sh2p);
+  if (int rc = pack_w(sh_w1, sh_w3, sh13p, packed_bytes(d, 4), 2, 0, D, I, stream)) return rc;
+  return pack_w(sh_w2, nullptr, sh2p, packed_bytes(d, 5), 3, 0, D, I, stream);
 }

@@ -27,11 +27,11 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   }
   float amax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
-  amax = wave_max_xor(amax, 1);
-  amax = wave_max_xor(amax, 2);
-  amax = wave_max_xor(amax, 4);
-  amax = wave_max_xor(amax, 8);
+  for (int i = 0; i < 8; ++i) amax = absmax(amax, f[i]);
+  amax = wave_absmax_xor(amax, 1);
+  amax = wave_absmax_xor(amax, 2);
+  amax = wave_absmax_xor(amax, 4);
+  amax = wave_absmax_xor(amax, 8);
   const bool pow2 = kind != WZ_SCALE_F32;
   const ActScale sc = act_scale(amax, pow2);
   if (!valid) return;

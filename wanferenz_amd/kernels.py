@@ -68,16 +68,22 @@ def _finish(c: torch.Tensor) -> torch.Tensor:
 
 
 def act_quant(x, block_size=128, scale_fmt=None, scale_dtype=torch.float32, inplace=False):
-    """x [..., K] bf16 -> (e4m3 [..., K], scales [..., K/128]); reference.py:117-146."""
+    """x [..., K] bf16 -> (e4m3 [..., K], scales [..., K/128]); reference.py:117-146.
+
+    The MoE / FP8-linear path quantises in 128-element blocks.  The model also
+    calls act_quant on the attention path with other block sizes and with
+    ``inplace=True`` (the QAT round trip of torch_ops.py:44-47, e.g.
+    architecture.py:470, 632): once :func:`install` has rebound act_quant,
+    those calls go to the binding it replaced, unchanged."""
     N_ = x.size(-1)
-    assert N_ % block_size == 0
-    if block_size != 128:
-        raise NotImplementedError("act_quant: only the 128-element activation block is on this path")
-    if inplace:
+    if block_size != 128 or inplace:
+        prev = _REF.get("act_quant")
+        if prev is not None:
+            return prev(x, block_size, scale_fmt, scale_dtype, inplace)
         raise NotImplementedError(
-            "act_quant(inplace=True) is the attention QAT round trip (torch_ops.py:44-47), "
-            "outside the MoE/FP8-linear path"
-        )
+            "act_quant: only block_size=128 with inplace=False runs on this path; other forms go to the "
+            "binding install() replaced, and none was installed")
+    assert N_ % block_size == 0
     if x.dtype != torch.bfloat16:
         raise TypeError(f"act_quant: expected bf16 activations, got {x.dtype}")
     _require_cuda(x)
@@ -90,8 +96,52 @@ def act_quant(x, block_size=128, scale_fmt=None, scale_dtype=torch.float32, inpl
     return y, s
 
 
+# Pack FP8 weight Parameters into the GEMV tile format on their first use outside
+# graph capture (fp8_gemm / linear keep the packed copy on the Parameter).
+PACK_FP8_WEIGHTS = True
+
+
+def _packed_of(b):
+    """The packed copy of FP8 weight ``b`` ([N, K] e4m3 Parameter), packing it once.
+
+    The copy is kept on the Parameter (``b._wz_packed``) with the storage
+    address and version it was made from, and remade when either changes.
+    Returns None where the tile format does not apply (N % 16, K % 128), for
+    tensors that are not Parameters (no place to keep a copy), or while a graph
+    is being captured and no current copy exists."""
+    if not PACK_FP8_WEIGHTS or not isinstance(b, torch.nn.Parameter) or b.dim() != 2:
+        return None
+    Nn, K = b.shape
+    if Nn % 16 or K % 128 or b.dtype not in (_E4M3, torch.uint8):
+        return None
+    key = (b.data_ptr(), b._version)
+    got = getattr(b, "_wz_packed", None)
+    if got is not None and got[0] == key:
+        return got[1]
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    packed = torch.empty(Nn * K, dtype=torch.uint8, device=b.device)
+    N.call("wz_fp8_pack", N.ptr(b), Nn, K, N.ptr(packed), N.stream_handle(b.device))
+    b._wz_packed = (key, packed)
+    return packed
+
+
+def pack_fp8_weights(module) -> int:
+    """Pack every FP8 weight Parameter of ``module`` now (before a graph capture,
+    so captured steps find the packed copies); returns how many were packed."""
+    n = 0
+    for p in module.parameters():
+        if p.dtype == _E4M3 and p.is_cuda and _packed_of(p) is not None:
+            n += 1
+    return n
+
+
 def fp8_gemm(a, a_s, b, b_s, scale_dtype=torch.float32):
-    """C[..., N] = dequant(a) @ dequant(b)^T in bf16; reference.py:292-311."""
+    """C[..., N] = dequant(a) @ dequant(b)^T in bf16; reference.py:292-311.
+
+    A weight Parameter is served from its packed copy (GEMV for up to 16 rows,
+    the dense tile GEMM above), as the reference's decode retile serves it
+    (fp8_vector.py:289-297); any other weight from its row-major bytes."""
     assert a.is_contiguous() and b.is_contiguous(), "Input tensors must be contiguous"
     assert a_s.is_contiguous() and b_s.is_contiguous(), "Scaling factor tensors must be contiguous"
     _require_cuda(a, a_s, b, b_s)
@@ -101,8 +151,16 @@ def fp8_gemm(a, a_s, b, b_s, scale_dtype=torch.float32):
     if b.size(1) != K:
         raise ValueError(f"fp8_gemm: a has K={K}, b has K={b.size(1)}")
     c = torch.empty(*a.size()[:-1], Nn, dtype=torch.bfloat16, device=a.device)
-    N.call("wz_fp8_gemm", N.ptr(a), N.ptr(a_s), N.ptr(b), N.ptr(b_s), N.ptr(c), M, Nn, K,
-           _scale_kind_of(a_s), _wscale_kind_of(b_s), N.stream_handle(a.device))
+    akind, wkind = _scale_kind_of(a_s), _wscale_kind_of(b_s)
+    packed = _packed_of(b)
+    if packed is not None:
+        need = int(N.lib().wz_fp8_gemm_packed_workspace_bytes(M, K, akind))
+        ws = torch.empty(need, dtype=torch.uint8, device=a.device) if need else None
+        N.call("wz_fp8_gemm_packed", N.ptr(a), N.ptr(a_s), N.ptr(packed), N.ptr(b_s), N.ptr(c), M, Nn, K, akind,
+               wkind, N.ptr(ws), need, N.stream_handle(a.device))
+    else:
+        N.call("wz_fp8_gemm", N.ptr(a), N.ptr(a_s), N.ptr(b), N.ptr(b_s), N.ptr(c), M, Nn, K, akind, wkind,
+               N.stream_handle(a.device))
     return _finish(c)
 
 
@@ -315,25 +373,63 @@ def add(a, b, out=None):
     return out
 
 
-_fp8_gemm_marker = "_v4_hip_fp8_gemm"
+def _model_module_of(fn):
+    import sys
+
+    return sys.modules.get(getattr(fn, "__module__", "") or "")
+
+
+def linear(x, weight, bias=None):
+    """linear() of the model (architecture.py:121-134) with the FP8 case fused:
+    act_quant of x runs inside the GEMV / GEMM prologue on the packed weight
+    (the same codes and scales as act_quant, so the same product).  The block
+    size and scale format are the model module's globals, read at call time as
+    the reference reads them; an FP4 weight runs act_quant + fp4_gemm, anything
+    else F.linear, as in the reference."""
+    assert bias is None
+    mod = _LINEAR_MOD
+    if weight.dtype == _E4M3 and x.dtype == torch.bfloat16 and getattr(mod, "block_size", 128) == 128:
+        packed = _packed_of(weight)
+        if packed is not None and x.is_contiguous():
+            _require_cuda(x)
+            scale_fmt = getattr(mod, "scale_fmt", None)
+            K = x.size(-1)
+            M = x.numel() // K
+            Nn = weight.size(0)
+            akind = N.WZ_SCALE_F32 if scale_fmt is None else N.WZ_SCALE_UE8M0_F32
+            y = torch.empty(*x.size()[:-1], Nn, dtype=torch.bfloat16, device=x.device)
+            need = int(N.lib().wz_fp8_linear_workspace_bytes(M, K))
+            ws = torch.empty(need, dtype=torch.uint8, device=x.device) if need else None
+            N.call("wz_fp8_linear_packed", N.ptr(x), N.ptr(packed), N.ptr(weight.scale), N.ptr(y), M, Nn, K,
+                   akind, _wscale_kind_of(weight.scale), N.ptr(ws), need, N.stream_handle(x.device))
+            return _finish(y)
+    return _REF["linear"](x, weight, bias)
+
+
 fp8_gemm._v4_hip_fp8_gemm = True
 fp4_gemm._v4_hip_fp4_gemm = True
 act_quant._v4_hip_act_quant = True
+linear._v4_hip_linear = True
 
 _REF = {}
+_LINEAR_MOD = None
 
 
 def _installed():
-    return (("act_quant", act_quant), ("fp8_gemm", fp8_gemm), ("fp4_gemm", fp4_gemm), ("sparse_attn", sparse_attn))
+    return (("act_quant", act_quant), ("fp8_gemm", fp8_gemm), ("fp4_gemm", fp4_gemm), ("sparse_attn", sparse_attn),
+            ("linear", linear))
 
 
-def install(mod) -> bool:
-    """Rebind act_quant / fp8_gemm / fp4_gemm / sparse_attn on a loaded reference
-    model module (each one the module has).
+def install(mod, model=None) -> bool:
+    """Rebind act_quant / fp8_gemm / fp4_gemm / sparse_attn / linear on a loaded
+    reference model module (each one the module has).
 
     Idempotent via the marker attributes; the replaced functions are kept in
     ``_REF`` (the reference's _REF_FP8_GEMM pattern, fp8_vector.py:472-491).
+    With ``model`` given, its FP8 weights are packed now (pack_fp8_weights), so a
+    graph captured afterwards runs the packed GEMV from the first step.
     """
+    global _LINEAR_MOD
     took = False
     for name, fn in _installed():
         if not hasattr(mod, name):
@@ -344,6 +440,10 @@ def install(mod) -> bool:
         _REF.setdefault(name, cur)
         setattr(mod, name, fn)
         took = True
+    if hasattr(mod, "linear"):
+        _LINEAR_MOD = mod
+    if model is not None:
+        pack_fp8_weights(model)
     return took
 
 

@@ -89,56 +89,137 @@ class MoEWeights:
     tid2eid: Optional[torch.Tensor] = None  # int32 [vocab, k]
 
 
-def _u8(t: torch.Tensor) -> torch.Tensor:
-    return t.view(torch.uint8) if t.dtype != torch.float32 else t
+_BYTE_TYPES = (torch.uint8, torch.float4_e2m1fn_x2, torch.float8_e8m0fnu, torch.float8_e4m3fn, torch.int8)
+
+
+def _need(name, t, shape, dtypes=None):
+    if t is None:
+        raise ValueError(f"MoE weights: {name} missing")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"MoE weights: {name} has shape {tuple(t.shape)}, want {tuple(shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"MoE weights: {name} must be contiguous")
+    if not t.is_cuda:
+        raise RuntimeError(f"MoE weights: {name} must be on the GPU (no CPU fallback)")
+    if dtypes and t.dtype not in dtypes:
+        raise TypeError(f"MoE weights: {name} dtype {t.dtype} not in {dtypes}")
+
+
+def _check_gate(cfg: MoEConfig, gate_w, gate_bias, tid2eid):
+    E, D, k = cfg.n_experts, cfg.dim, cfg.topk
+    _need("gate_w", gate_w, (E, D), (torch.bfloat16,))
+    if tid2eid is None:
+        if gate_bias is not None:
+            _need("gate_bias", gate_bias, (E,), (torch.float32,))
+    elif (tid2eid.dim() != 2 or tid2eid.size(1) != k or tid2eid.dtype != torch.int32 or not tid2eid.is_cuda
+          or not tid2eid.is_contiguous()):
+        raise ValueError("MoE weights: tid2eid must be a contiguous int32 [vocab, k] GPU tensor")
+
+
+def _shared_scale_types(cfg: MoEConfig):
+    return (torch.float32,) if cfg.shared_w_scale_kind == N.WZ_WSCALE_F32 else _BYTE_TYPES
+
+
+def _check_shared(cfg: MoEConfig, sh):
+    """sh = (w1, w1_s, w3, w3_s, w2, w2_s) of the FP8 shared expert; weights may be None
+    (only the scales are checked then)."""
+    D, I = cfg.dim, cfg.inter
+    nb = lambda n: (n + 127) // 128  # noqa: E731
+    shapes = ((I, D), (nb(I), nb(D)), (I, D), (nb(I), nb(D)), (D, I), (nb(D), nb(I)))
+    for j, (name, t, shape) in enumerate(zip(("sh_w1", "sh_w1_s", "sh_w3", "sh_w3_s", "sh_w2", "sh_w2_s"), sh, shapes)):
+        if j % 2 == 0 and t is None:
+            continue
+        _need(name, t, shape, _BYTE_TYPES if j % 2 == 0 else _shared_scale_types(cfg))
+
+
+def _check_expert(cfg: MoEConfig, e, ex):
+    D, I = cfg.dim, cfg.inter
+    shapes = ((I, D // 2), (I, D // 32), (I, D // 2), (I, D // 32), (D, I // 2), (D, I // 32))
+    for name, t, shape in zip(("w1", "w1_s", "w3", "w3_s", "w2", "w2_s"), ex, shapes):
+        _need(f"expert {e} {name}", t, shape, _BYTE_TYPES)
 
 
 def _check_layout(cfg: MoEConfig, w: MoEWeights):
-    D, I, E, k = cfg.dim, cfg.inter, cfg.n_experts, cfg.topk
+    D, I, E = cfg.dim, cfg.inter, cfg.n_experts
+    _check_gate(cfg, w.gate_w, w.gate_bias, w.tid2eid)
+    _need("w13", w.w13, (E, 2 * I, D // 2), _BYTE_TYPES)
+    _need("w13_s", w.w13_s, (E, 2 * I, D // 32), _BYTE_TYPES)
+    _need("w2", w.w2, (E, D, I // 2), _BYTE_TYPES)
+    _need("w2_s", w.w2_s, (E, D, I // 32), _BYTE_TYPES)
+    _check_shared(cfg, (w.sh_w1, w.sh_w1_s, w.sh_w3, w.sh_w3_s, w.sh_w2, w.sh_w2_s))
 
-    def need(name, t, shape, dtypes=None):
-        if t is None:
-            raise ValueError(f"MoE weights: {name} missing")
-        if tuple(t.shape) != tuple(shape):
-            raise ValueError(f"MoE weights: {name} has shape {tuple(t.shape)}, want {tuple(shape)}")
-        if not t.is_contiguous():
-            raise ValueError(f"MoE weights: {name} must be contiguous")
-        if not t.is_cuda:
-            raise RuntimeError(f"MoE weights: {name} must be on the GPU (no CPU fallback)")
-        if dtypes and t.dtype not in dtypes:
-            raise TypeError(f"MoE weights: {name} dtype {t.dtype} not in {dtypes}")
 
-    byte_types = (torch.uint8, torch.float4_e2m1fn_x2, torch.float8_e8m0fnu, torch.float8_e4m3fn, torch.int8)
-    need("gate_w", w.gate_w, (E, D), (torch.bfloat16,))
-    if w.tid2eid is None:
-        if w.gate_bias is not None:
-            need("gate_bias", w.gate_bias, (E,), (torch.float32,))
-    else:
-        if w.tid2eid.dim() != 2 or w.tid2eid.size(1) != k or w.tid2eid.dtype != torch.int32:
-            raise ValueError("MoE weights: tid2eid must be int32 [vocab, k]")
-    need("w13", w.w13, (E, 2 * I, D // 2), byte_types)
-    need("w13_s", w.w13_s, (E, 2 * I, D // 32), byte_types)
-    need("w2", w.w2, (E, D, I // 2), byte_types)
-    need("w2_s", w.w2_s, (E, D, I // 32), byte_types)
-    sdt = (torch.float32,) if cfg.shared_w_scale_kind == N.WZ_WSCALE_F32 else byte_types
-    need("sh_w1", w.sh_w1, (I, D), byte_types)
-    need("sh_w3", w.sh_w3, (I, D), byte_types)
-    need("sh_w2", w.sh_w2, (D, I), byte_types)
-    need("sh_w1_s", w.sh_w1_s, ((I + 127) // 128, (D + 127) // 128), sdt)
-    need("sh_w3_s", w.sh_w3_s, ((I + 127) // 128, (D + 127) // 128), sdt)
-    need("sh_w2_s", w.sh_w2_s, ((D + 127) // 128, (I + 127) // 128), sdt)
+def _ptr(t):
+    return None if t is None else t.data_ptr()
 
 
 class HipMoE:
-    """One MoE layer served by the HIP library (see module docstring)."""
+    """One MoE layer served by the HIP library (see module docstring).
 
-    def __init__(self, cfg: MoEConfig, weights: MoEWeights, max_tokens: int = 16):
+    The layer holds the packed expert banks (the only copy the kernels read),
+    the gate, the tid2eid table of a hash layer and the shared expert's block
+    scales.  ``HipMoE(cfg, weights)`` packs a reference-layout bank and keeps
+    ``weights`` (``self.weights``) unless ``keep_reference=False``;
+    :meth:`from_experts` packs expert by expert and never holds a
+    reference-layout bank.
+    """
+
+    def __init__(self, cfg: MoEConfig, weights: MoEWeights, max_tokens: int = 16, keep_reference: bool = True):
         if cfg.score_func not in SCORE_FUNCS:
             raise ValueError(f"unknown score_func {cfg.score_func!r}")
         _check_layout(cfg, weights)
-        self.cfg = cfg
-        self.weights = weights
         w = weights
+        self._setup(cfg, w.gate_w, w.gate_bias, w.tid2eid, (w.sh_w1_s, w.sh_w3_s, w.sh_w2_s))
+        d = self.desc
+        for name in ("w13", "w13_s", "w2", "w2_s", "sh_w1", "sh_w3", "sh_w2"):
+            setattr(d, name, getattr(w, name).data_ptr())
+        self._alloc_packed()
+        N.call("wz_moe_pack", ctypes.byref(d), *(self.packed[n].data_ptr() for n in PACKED_NAMES),
+               N.stream_handle(self.device))
+        self.weights = weights if keep_reference else None
+        if not keep_reference:
+            self._forget_reference()
+        self._ws = None
+        self._ws_tokens = 0
+        self.reserve(max_tokens)
+
+    @classmethod
+    def from_experts(cls, cfg: MoEConfig, gate_w, gate_bias, experts, shared, tid2eid=None,
+                     max_tokens: int = 16) -> "HipMoE":
+        """Build the layer one expert at a time, with no reference-layout bank.
+
+        ``experts(e)`` returns expert e's ``(w1, w1_s, w3, w3_s, w2, w2_s)`` device
+        tensors (e2m1x2 / e8m0 bytes, shapes of one reference Expert); each is
+        packed into its slot (wz_moe_pack_expert) and may be dropped by the caller
+        right after.  ``shared`` is ``(w1, w1_s, w3, w3_s, w2, w2_s)`` of the FP8
+        shared expert; only its scales are kept.
+        """
+        if cfg.score_func not in SCORE_FUNCS:
+            raise ValueError(f"unknown score_func {cfg.score_func!r}")
+        _check_gate(cfg, gate_w, gate_bias, tid2eid)
+        _check_shared(cfg, shared)
+        self = object.__new__(cls)
+        self._setup(cfg, gate_w, gate_bias, tid2eid, (shared[1], shared[3], shared[5]))
+        self._alloc_packed()
+        stream = N.stream_handle(self.device)
+        for e in range(cfg.n_experts):
+            ex = experts(e)
+            _check_expert(cfg, e, ex)
+            N.call("wz_moe_pack_expert", ctypes.byref(self.desc), e, *(t.data_ptr() for t in ex), stream)
+        N.call("wz_moe_pack_shared", ctypes.byref(self.desc), shared[0].data_ptr(), shared[2].data_ptr(),
+               shared[4].data_ptr(), stream)
+        self.weights = None
+        self._ws = None
+        self._ws_tokens = 0
+        self.reserve(max_tokens)
+        return self
+
+    def _setup(self, cfg, gate_w, gate_bias, tid2eid, shared_scales):
+        self.cfg = cfg
+        self.gate_w, self.tid2eid = gate_w, tid2eid
+        self.gate_bias = None if tid2eid is not None else gate_bias
+        self.shared_scales = tuple(shared_scales)
+        self.device = gate_w.device
         d = WzMoeDesc()
         d.dim, d.inter, d.n_experts, d.topk = cfg.dim, cfg.inter, cfg.n_experts, cfg.topk
         d.score_func = SCORE_FUNCS[cfg.score_func]
@@ -146,44 +227,39 @@ class HipMoE:
         d.shared_w_scale_kind = cfg.shared_w_scale_kind
         d.route_scale = cfg.route_scale
         d.swiglu_limit = cfg.swiglu_limit
-        d.vocab = 0 if w.tid2eid is None else w.tid2eid.size(0)
-        d.gate_w = w.gate_w.data_ptr()
-        d.gate_bias = None if (w.gate_bias is None or w.tid2eid is not None) else w.gate_bias.data_ptr()
-        d.tid2eid = None if w.tid2eid is None else w.tid2eid.data_ptr()
-        for name in ("w13", "w13_s", "w2", "w2_s", "sh_w1", "sh_w1_s", "sh_w3", "sh_w3_s", "sh_w2", "sh_w2_s"):
-            setattr(d, name, getattr(w, name).data_ptr())
+        d.vocab = 0 if tid2eid is None else tid2eid.size(0)
+        d.gate_w = gate_w.data_ptr()
+        d.gate_bias = _ptr(self.gate_bias)
+        d.tid2eid = _ptr(tid2eid)
+        d.sh_w1_s, d.sh_w3_s, d.sh_w2_s = (t.data_ptr() for t in self.shared_scales)
         self.desc = d
-        self.device = w.gate_w.device
-        self.packed = self._pack()
-        self._ws = None
-        self._ws_tokens = 0
-        self.reserve(max_tokens)
 
-    def _pack(self) -> dict:
-        """Build the MFMA-ready packed banks the decode kernels stream (pack.hip)."""
+    def _alloc_packed(self):
         d = self.desc
-        bufs = {}
+        self.packed = {}
         for i, name in enumerate(PACKED_NAMES):
             n = int(N.lib().wz_moe_packed_bytes(ctypes.byref(d), i))
-            bufs[name] = torch.empty(n, dtype=torch.uint8, device=self.device)
-        N.call("wz_moe_pack", ctypes.byref(d), *(bufs[n].data_ptr() for n in PACKED_NAMES),
-               N.stream_handle(self.device))
-        for name in PACKED_NAMES:
-            setattr(d, name, bufs[name].data_ptr())
-        return bufs
+            self.packed[name] = torch.empty(n, dtype=torch.uint8, device=self.device)
+            setattr(d, name, self.packed[name].data_ptr())
+
+    def _forget_reference(self):
+        for name in ("w13", "w13_s", "w2", "w2_s", "sh_w1", "sh_w3", "sh_w2"):
+            setattr(self.desc, name, None)
 
     def with_gate_bias(self, bias: torch.Tensor, max_tokens: int = 16) -> "HipMoE":
         """A layer over the same expert banks (packed once) with another fp32 gate bias [E]."""
         import dataclasses
 
-        if self.weights.tid2eid is not None:
+        if self.tid2eid is not None:
             raise ValueError("HipMoE: a hash-routed layer has no gate bias")
         bias = bias.to(device=self.device, dtype=torch.float32).contiguous()
         if bias.shape != (self.cfg.n_experts,):
             raise ValueError(f"HipMoE: gate bias must be [{self.cfg.n_experts}], got {tuple(bias.shape)}")
         other = object.__new__(HipMoE)
         other.cfg = self.cfg
-        other.weights = dataclasses.replace(self.weights, gate_bias=bias)
+        other.gate_w, other.tid2eid, other.gate_bias = self.gate_w, None, bias
+        other.shared_scales = self.shared_scales
+        other.weights = None if self.weights is None else dataclasses.replace(self.weights, gate_bias=bias)
         other.desc = WzMoeDesc()
         ctypes.memmove(ctypes.byref(other.desc), ctypes.byref(self.desc), ctypes.sizeof(WzMoeDesc))
         other.desc.gate_bias = bias.data_ptr()
@@ -217,33 +293,60 @@ class HipMoE:
         return self._ws
 
     # -- compute -------------------------------------------------------------
-    def forward(self, x: torch.Tensor, input_ids: Optional[torch.Tensor] = None,
-                out: Optional[torch.Tensor] = None, routing_out=None) -> torch.Tensor:
-        """x [..., D] bf16 -> y [..., D] bf16 (MoE.forward, architecture.py:777-794)."""
-        D = self.cfg.dim
+    def _tokens(self, x: torch.Tensor) -> torch.Tensor:
         if x.dtype != torch.bfloat16:
             raise TypeError(f"HipMoE: x must be bf16, got {x.dtype}")
-        if not x.is_cuda:
-            raise RuntimeError("HipMoE: x must be on the GPU (no CPU fallback)")
-        xv = x.reshape(-1, D)
-        if not xv.is_contiguous():
-            xv = xv.contiguous()
-        T = xv.size(0)
-        ids = None
-        if self.weights.tid2eid is not None:
-            if input_ids is None:
-                raise ValueError("HipMoE: a hash-routed layer needs input_ids")
-            ids = input_ids.reshape(-1).to(torch.int64)
-            if ids.numel() != T:
-                raise ValueError("HipMoE: input_ids must have one id per token")
-            ids = ids.contiguous()
+        if x.device != self.device:
+            raise RuntimeError(f"HipMoE: x is on {x.device}, the layer on {self.device} (no CPU fallback)")
+        if x.size(-1) != self.cfg.dim:
+            raise ValueError(f"HipMoE: x has rows of {x.size(-1)}, the layer dim is {self.cfg.dim}")
+        return x.reshape(-1, self.cfg.dim).contiguous()
+
+    def _ids(self, input_ids, T: int):
+        """int64 ids on the layer's device for a hash-routed layer, else None.
+
+        Ids given on the host are range-checked there (IndexError, as the
+        reference's ``tid2eid[input_ids]`` raises); device ids are not read back:
+        an id outside the table gives that token NaN routing weights and a NaN
+        output row instead (the kernels never read outside the table)."""
+        if self.tid2eid is None:
+            return None
+        if input_ids is None:
+            raise ValueError("HipMoE: a hash-routed layer needs input_ids")
+        ids = input_ids.reshape(-1)
+        if ids.numel() != T:
+            raise ValueError(f"HipMoE: input_ids has {ids.numel()} ids for {T} tokens")
+        if not ids.is_cuda and T:
+            lo, hi = int(ids.min()), int(ids.max())
+            if lo < 0 or hi >= self.tid2eid.size(0):
+                raise IndexError(f"HipMoE: input id {lo if lo < 0 else hi} outside the tid2eid table "
+                                 f"of {self.tid2eid.size(0)} rows")
+        return ids.to(self.device, torch.int64).contiguous()
+
+    def _check_out(self, t, shape, dtype, what):
+        if t.dtype != dtype or t.device != self.device or not t.is_contiguous() or t.numel() != shape[0] * shape[1]:
+            raise ValueError(f"HipMoE: {what} must be a contiguous {dtype} tensor of {shape[0]}x{shape[1]} "
+                             f"elements on {self.device}, got {t.dtype} {tuple(t.shape)} on {t.device}")
+
+    def forward(self, x: torch.Tensor, input_ids: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None, routing_out=None) -> torch.Tensor:
+        """x [..., D] bf16 -> y [..., D] bf16 (MoE.forward, architecture.py:777-794), any number of tokens.
+
+        ``out`` (bf16, T*D elements) receives y when given; ``routing_out`` =
+        (weights fp32 [T, k], indices int64 [T, k]) receives the routing."""
+        xv = self._tokens(x)
+        T, D, k = xv.size(0), self.cfg.dim, self.cfg.topk
+        ids = self._ids(input_ids, T)
+        if out is not None:
+            self._check_out(out, (T, D), torch.bfloat16, "out")
         y = out if out is not None else torch.empty_like(xv)
-        ws = self._ws_for(T)
         wp = ip = None
         if routing_out is not None:
+            self._check_out(routing_out[0], (T, k), torch.float32, "routing weights")
+            self._check_out(routing_out[1], (T, k), torch.int64, "routing indices")
             wp, ip = routing_out[0].data_ptr(), routing_out[1].data_ptr()
-        N.call("wz_moe_forward", ctypes.byref(self.desc), xv.data_ptr(),
-               None if ids is None else ids.data_ptr(), T, y.data_ptr(), wp, ip,
+        ws = self._ws_for(T)
+        N.call("wz_moe_forward", ctypes.byref(self.desc), xv.data_ptr(), _ptr(ids), T, y.data_ptr(), wp, ip,
                ws.data_ptr(), ws.numel(), N.stream_handle(self.device))
         return y.view(x.shape)
 
@@ -256,23 +359,21 @@ class HipMoE:
         The workspace still holds that call's routing tables and intermediates;
         this is for timing a stage alone (eagerly or captured in a graph).
         """
-        xv = x.reshape(-1, self.cfg.dim)
+        xv = self._tokens(x)
         T = xv.size(0)
-        if T > self._ws_tokens:
-            raise RuntimeError("HipMoE.replay_stage: no preceding forward with this many tokens")
-        ids = None if input_ids is None else input_ids.reshape(-1).to(torch.int64).contiguous()
-        N.call("wz_moe_replay_stage", ctypes.byref(self.desc), xv.data_ptr(),
-               None if ids is None else ids.data_ptr(), T, int(stage), out.data_ptr(),
-               self._ws.data_ptr(), self._ws.numel(), N.stream_handle(self.device))
+        if T > self._ws_tokens or T * self.cfg.topk > 16384:
+            raise RuntimeError("HipMoE.replay_stage: no preceding single-chunk forward with this many tokens")
+        self._check_out(out, (T, self.cfg.dim), torch.bfloat16, "out")
+        ids = self._ids(input_ids, T)
+        N.call("wz_moe_replay_stage", ctypes.byref(self.desc), xv.data_ptr(), _ptr(ids), T, int(stage),
+               out.data_ptr(), self._ws.data_ptr(), self._ws.numel(), N.stream_handle(self.device))
 
     def route(self, x: torch.Tensor, input_ids: Optional[torch.Tensor] = None):
         """Gate.forward + canonical permutation: (weights, indices, offsets, perm_token, perm_slot)."""
         D, E, k = self.cfg.dim, self.cfg.n_experts, self.cfg.topk
-        xv = x.reshape(-1, D).contiguous()
+        xv = self._tokens(x)
         T = xv.size(0)
-        ids = None
-        if self.weights.tid2eid is not None:
-            ids = input_ids.reshape(-1).to(torch.int64).contiguous()
+        ids = self._ids(input_ids, T)
         dev = self.device
         weights = torch.empty(T, k, dtype=torch.float32, device=dev)
         indices = torch.empty(T, k, dtype=torch.int64, device=dev)
@@ -280,10 +381,9 @@ class HipMoE:
         ptok = torch.empty(T * k, dtype=torch.int32, device=dev)
         pslot = torch.empty(T * k, dtype=torch.int32, device=dev)
         ws = self._ws_for(T)
-        N.call("wz_moe_route", ctypes.byref(self.desc), xv.data_ptr(),
-               None if ids is None else ids.data_ptr(), T, weights.data_ptr(), indices.data_ptr(),
-               offsets.data_ptr(), ptok.data_ptr(), pslot.data_ptr(), ws.data_ptr(), ws.numel(),
-               N.stream_handle(dev))
+        N.call("wz_moe_route", ctypes.byref(self.desc), xv.data_ptr(), _ptr(ids), T, weights.data_ptr(),
+               indices.data_ptr(), offsets.data_ptr(), ptok.data_ptr(), pslot.data_ptr(), ws.data_ptr(),
+               ws.numel(), N.stream_handle(dev))
         return weights, indices, offsets, ptok, pslot
 
 
@@ -291,6 +391,8 @@ class HipMoE:
 
 _REF_FORWARD = None
 _MOD = None
+# hip_moe_of's default: empty the module's expert weights once packed (one copy in HBM)
+RELEASE_EXPERTS = True
 
 
 def _act_kind_of_module(mod) -> int:
@@ -301,55 +403,44 @@ def _act_kind_of_module(mod) -> int:
     return N.WZ_SCALE_UE8M0 if scale_dtype == torch.float8_e8m0fnu else N.WZ_SCALE_UE8M0_F32
 
 
-def bank_of(moe) -> Optional[dict]:
-    """The expert bank of a reference MoE, building it the way _relayout_moe does.
+def _bytes(p) -> torch.Tensor:
+    return p.detach().view(torch.uint8)
 
-    Per-expert parameters become views into one contiguous bank per group
-    (w13 = w1 rows then w3 rows; w2), fp4_grouped.py:142-188, so the routed
-    experts ARE the bank and no duplicate is kept.
+
+def _release(params):
+    """Point each parameter at an empty tensor of its dtype: the packed banks are the
+    layer's only copy from here on (the reference's bank layout with preserve=False,
+    serving/partition.py:398-405, likewise leaves no per-expert storage behind)."""
+    empty = {}
+    for p in params:
+        key = (p.dtype, p.device)
+        if key not in empty:
+            empty[key] = torch.empty(0, dtype=p.dtype, device=p.device)
+        p.data = empty[key]
+
+
+def hip_moe_of(moe, mod=None, release: Optional[bool] = None) -> Optional[HipMoE]:
+    """Build (once) and cache the HipMoE view of a reference MoE module.
+
+    Each routed expert's w1/w3/w2 parameters are packed straight into the packed
+    banks (wz_moe_pack_expert), and the shared expert's into its FP8 tiles.  With
+    ``release`` (default: the module flag ``RELEASE_EXPERTS``, on) the packed
+    weight parameters are emptied afterwards, so the layer holds one copy of its
+    experts; the gate and the block scales of the shared expert stay.  A released
+    layer cannot be served by the kept reference forward any more.
     """
-    bank = getattr(moe, "_grouped_bank", None)
-    if bank:
-        return bank
-    lo, hi = moe.experts_start_idx, moe.experts_end_idx
-    experts = [moe.experts[i] for i in range(lo, hi)]
-    if not experts or experts[0].w1.weight.dtype != torch.float4_e2m1fn_x2:
-        return None
-    groups = (("w13", ("w1", "w3")), ("w2", ("w2",)))
-    bank = {}
-    with torch.no_grad():
-        for key, kinds in groups:
-            for attr, suffix in (("weight", ""), ("scale", "_s")):
-                first = [getattr(getattr(experts[0], kk), attr) for kk in kinds]
-                rows = [t.shape[0] for t in first]
-                shape = (len(experts), sum(rows)) + tuple(first[0].shape[1:])
-                b = torch.empty(shape, dtype=first[0].dtype, device=first[0].device)
-                bu = b.view(torch.uint8)
-                for j, e in enumerate(experts):
-                    off = 0
-                    for n, kk in zip(rows, kinds):
-                        p = getattr(getattr(e, kk), attr)
-                        bu[j, off:off + n].copy_(p.detach().view(torch.uint8))
-                        p.data = b[j, off:off + n]
-                        off += n
-                bank[key + suffix] = b
-    moe._grouped_bank = bank
-    return bank
-
-
-def hip_moe_of(moe, mod=None) -> Optional[HipMoE]:
-    """Build (once) and cache the HipMoE view of a reference MoE module."""
     h = getattr(moe, "_hip_moe", None)
     if h is not None:
         return h
     mod = mod or _MOD
-    bank = bank_of(moe)
-    if bank is None:
+    release = RELEASE_EXPERTS if release is None else release
+    lo, hi = moe.experts_start_idx, moe.experts_end_idx
+    if hi - lo <= 0 or moe.experts[lo].w1.weight.dtype != torch.float4_e2m1fn_x2:
         return None
     sh = moe.shared_experts
     if sh.w1.weight.dtype != torch.float8_e4m3fn:
         return None
-    e0 = moe.experts[moe.experts_start_idx]
+    e0 = moe.experts[lo]
     gate = moe.gate
     cfg = MoEConfig(
         dim=moe.dim, inter=e0.w1.weight.shape[0], n_experts=moe.n_routed_experts,
@@ -358,14 +449,29 @@ def hip_moe_of(moe, mod=None) -> Optional[HipMoE]:
         act_scale_kind=_act_kind_of_module(mod),
         shared_w_scale_kind=N.WZ_WSCALE_E8M0 if sh.w1.scale.dtype == torch.float8_e8m0fnu else N.WZ_WSCALE_F32,
     )
-    w = MoEWeights(
-        gate_w=gate.weight.data, gate_bias=None if gate.bias is None else gate.bias.data,
-        w13=bank["w13"], w13_s=bank["w13_s"], w2=bank["w2"], w2_s=bank["w2_s"],
-        sh_w1=sh.w1.weight.data, sh_w1_s=sh.w1.scale.data, sh_w3=sh.w3.weight.data,
-        sh_w3_s=sh.w3.scale.data, sh_w2=sh.w2.weight.data, sh_w2_s=sh.w2.scale.data,
-        tid2eid=gate.tid2eid.data if getattr(gate, "hash", False) else None,
-    )
-    h = HipMoE(cfg, w)
+
+    def expert(e):
+        ex = moe.experts[e]
+        return tuple(_bytes(getattr(getattr(ex, kind), attr)) for kind in ("w1", "w3", "w2")
+                     for attr in ("weight", "scale"))
+
+    def scale(lin):
+        return lin.scale.detach() if lin.scale.dtype == torch.float32 else _bytes(lin.scale)
+
+    shared = (_bytes(sh.w1.weight), scale(sh.w1), _bytes(sh.w3.weight), scale(sh.w3), _bytes(sh.w2.weight),
+              scale(sh.w2))
+    with torch.no_grad():
+        h = HipMoE.from_experts(
+            cfg, gate.weight.detach(), None if gate.bias is None else gate.bias.detach(), expert, shared,
+            tid2eid=gate.tid2eid.detach() if getattr(gate, "hash", False) else None)
+        if release:
+            # the reference's relayout may have left a bank the experts' views point into
+            moe._grouped_bank = None
+            _release([getattr(getattr(moe.experts[e], kind), "weight") for e in range(lo, hi)
+                      for kind in ("w1", "w3", "w2")] + [sh.w1.weight, sh.w3.weight, sh.w2.weight])
+            _release([getattr(getattr(moe.experts[e], kind), "scale") for e in range(lo, hi)
+                      for kind in ("w1", "w3", "w2")])
+            moe._hip_released = True
     moe._hip_moe = h
     return h
 
@@ -426,7 +532,35 @@ def coverage(module) -> dict:
     return out
 
 
-def moe_chain(mod) -> str:
-    """Status string of the installed MoE chain (controls.moe_chain, controls.py:38-68)."""
-    f = mod.MoE.forward
-    return "hip>ref" if getattr(f, "_v4_hip_moe", False) else "ref"
+# Install markers of the MoE.forward replacements the reference ships
+# (serving/controls.py:38-42), with the labels its moe_chain prints.
+_CHAIN_MARKERS = (("_v4_hip_moe", "hip"), ("_v4_multi", "multi"), ("_v4_grouped", "grouped"),
+                  ("_v4_decode_fast", "decode"))
+
+
+def moe_chain(mod) -> list:
+    """The installed MoE.forward chain, outermost first (controls.moe_chain,
+    serving/controls.py:45-68): each replacement is recognised by its marker and
+    followed to the forward it kept (``_REF_FORWARD`` of the module that defines
+    it); the chain ends at ``"ref"``, ``"ORPHAN"`` (a marked forward whose module
+    is gone) or ``"CYCLE"``."""
+    import sys
+
+    fn = getattr(getattr(mod, "MoE", None), "forward", None)
+    out, seen = [], set()
+    while fn is not None:
+        if id(fn) in seen:
+            out.append("CYCLE")
+            break
+        seen.add(id(fn))
+        label = next((lab for marker, lab in _CHAIN_MARKERS if getattr(fn, marker, False)), None)
+        if label is None:
+            out.append("ref")
+            break
+        out.append(label)
+        owner = sys.modules.get(getattr(fn, "__module__", "") or "")
+        if owner is None:
+            out.append("ORPHAN")
+            break
+        fn = getattr(owner, "_REF_FORWARD", None)
+    return out

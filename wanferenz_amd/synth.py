@@ -21,6 +21,9 @@ The generators follow the recipes of the reference's own tests and probes:
 
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 
 GOLDEN = np.uint64(0x9E3779B97F4A7C15)
@@ -213,10 +216,100 @@ def zipf_bias(n_experts: int, s: float = 1.1, beta: float = 0.05, seed: int = 1)
     """Gate bias that skews expert popularity towards a Zipf(s) law.
 
     bias_e = beta * log(p_e) with p_e proportional to rank_e^-s, where rank is a
-    seeded random permutation of the experts; beta sets the strength.
+    seeded random permutation of the experts; beta sets the strength
+    (:func:`calibrate_zipf` finds the beta at which the routed popularity is
+    Zipf(s); the V4 value is in ``zipf_v4.json``).
     """
     d = draws(stream_key(seed, 77), 0, n_experts)
     rank = np.argsort(np.argsort(d)) + 1
     p = rank.astype(np.float64) ** (-s)
     p /= p.sum()
     return (beta * np.log(p)).astype(np.float32)
+
+
+def zipf_exponent(counts) -> float:
+    """Maximum-likelihood exponent of a finite Zipf law over len(counts) ranks fitted to
+    the rank-frequency data ``counts`` (selections per expert, any order).
+
+    The likelihood of s is prod_r (r^-s / H(s))^c_r with H(s) = sum_r r^-s; its
+    stationary point equates the observed mean of log(rank) with the model's,
+    sum_r c_r log r / C = sum_r r^-s log r / H(s), whose right side falls as s
+    grows, so bisection finds it."""
+    c = np.sort(np.asarray(counts, np.float64))[::-1]
+    r = np.arange(1, c.size + 1, dtype=np.float64)
+    target = float((c * np.log(r)).sum() / c.sum())
+    lo, hi = 0.0, 8.0
+    for _ in range(60):
+        m = 0.5 * (lo + hi)
+        w = r ** -m
+        if (w * np.log(r)).sum() / w.sum() > target:
+            lo = m
+        else:
+            hi = m
+    return 0.5 * (lo + hi)
+
+
+def route_counts(x_bits: np.ndarray, gate_w_bits: np.ndarray, bias: np.ndarray, k: int) -> np.ndarray:
+    """Selections per expert of the biased sqrt-softplus top-k gate (Gate.forward,
+    architecture.py:696-718, routing only) over tokens x: workload synthesis, in
+    float64 products rounded to float32 scores; lower index first on ties."""
+    a = (f32_from_bf16_bits(x_bits).astype(np.float64) @ f32_from_bf16_bits(gate_w_bits).astype(np.float64).T)
+    a = a.astype(np.float32).astype(np.float64)
+    sc = np.sqrt(np.where(a > 20.0, a, np.log1p(np.exp(np.minimum(a, 20.0)))).astype(np.float32).astype(np.float64))
+    key = (sc.astype(np.float32) + bias.astype(np.float32)).astype(np.float32)
+    idx = np.argsort(-key.astype(np.float64), axis=1, kind="stable")[:, :k]
+    return np.bincount(idx.ravel(), minlength=gate_w_bits.shape[0])
+
+
+ZIPF_V4_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "zipf_v4.json")
+
+
+def zipf_v4_calibration_batch(T: int = 2048):
+    """The calibration inputs of the V4 prefill workload: the gate of synthetic layer 0
+    (seed 0, N(0, 0.02) bf16 [256, 4096]) and T tokens of N(0, 1) bf16 (seed 2)."""
+    E, D = 256, 4096
+    gw = normal_bf16(stream_key(0, layer_stream(0, S_GATE_W)), (E, D), 0.02)
+    x = normal_bf16(stream_key(2, S_X), (T, D), 1.0)
+    return x, gw
+
+
+def calibrate_zipf(s: float = 1.1, k: int = 6, T: int = 2048, iters: int = 40) -> dict:
+    """Bisection on beta so that the top-k routing of the calibration batch has a
+    Zipf exponent (``zipf_exponent``) of s; returns beta, the fitted exponent and
+    the achieved selections per expert."""
+    x, gw = zipf_v4_calibration_batch(T)
+    E = gw.shape[0]
+
+    def fit(beta):
+        c = route_counts(x, gw, zipf_bias(E, s, beta), k)
+        return zipf_exponent(c), c
+
+    lo, hi = 0.0, 2.0
+    for _ in range(iters):
+        mid = 0.5 * (lo + hi)
+        if fit(mid)[0] < s:
+            lo = mid
+        else:
+            hi = mid
+    beta = float(np.float32(0.5 * (lo + hi)))
+    got, counts = fit(beta)
+    return {"s": s, "k": k, "T": T, "beta": beta, "fitted_exponent": got,
+            "counts_per_expert": counts.astype(int).tolist(),
+            "max_expert_rows": int(counts.max()), "experts_unused": int((counts == 0).sum())}
+
+
+def zipf_v4_beta() -> float:
+    """The committed calibration's beta (``python -m wanferenz_amd.synth calibrate`` writes it)."""
+    with open(ZIPF_V4_FILE) as f:
+        return float(json.load(f)["beta"])
+
+
+if __name__ == "__main__":
+    import sys
+
+    if sys.argv[1:] == ["calibrate"]:
+        r = calibrate_zipf()
+        with open(ZIPF_V4_FILE, "w") as f:
+            json.dump(r, f, indent=1)
+        print(f"beta {r['beta']:.6f} fitted exponent {r['fitted_exponent']:.4f} max rows {r['max_expert_rows']} "
+              f"unused {r['experts_unused']} -> {ZIPF_V4_FILE}")
