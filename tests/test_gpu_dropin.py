@@ -79,6 +79,36 @@ def test_installed_moe_forward_matches_golden(gpu, mod, name, release, monkeypat
     assert torch.equal(y, y2) and moe._hip_steps == 2
 
 
+def test_prepare_packs_at_load_and_the_step_captures(gpu, mod):
+    """prepare() packs the model's MoE layers at load (the reference's load-time bank,
+    partition.py:398-405); a decode step through the installed MoE.forward then
+    captures in a graph whose replays equal the eager step."""
+    case = CASES["top6_t8"]
+    inp = make_inputs(case)
+    moe = mm.moe_from_case(case, inp, gpu)
+    model = torch.nn.ModuleList([moe])
+    wm.install(mod)
+    assert wm.prepare(model, mod, max_tokens=case.T) == 1
+    assert moe._hip_moe is not None and moe.experts[0].w1.weight.numel() == 0
+    x = bf16_tensor(inp.x, gpu).view(1, case.T, case.dim)
+    ids = torch.from_numpy(inp.input_ids).to(gpu).view(1, case.T)
+    eager = mod.MoE.forward(moe, x, ids).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            mod.MoE.forward(moe, x, ids)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = mod.MoE.forward(moe, x, ids)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        mod.MoE.forward(moe, x, ids)  # eager work between replays
+
+
 def test_installed_moe_serves_any_prompt_length(gpu, mod):
     """MoE.forward takes any T (architecture.py:777-794).  At top-2, T = 8193 is
     one token past a single call's 16384 routed pairs: the layer runs it as a

@@ -476,6 +476,31 @@ def hip_moe_of(moe, mod=None, release: Optional[bool] = None) -> Optional[HipMoE
     return h
 
 
+def _servable(moe, mod) -> Optional[str]:
+    """Why the HIP layer cannot serve ``moe`` (a decline reason), or None."""
+    if int(getattr(mod, "world_size", 1) or 1) > 1:
+        return "world_size>1"
+    if moe.experts_start_idx != 0 or moe.experts_end_idx != moe.n_routed_experts:
+        return "partial-experts"
+    return None
+
+
+def prepare(module, mod=None, max_tokens: int = 16) -> int:
+    """Pack every MoE layer of ``module`` that the HIP path serves, now (at load,
+    before any graph capture), with a workspace for ``max_tokens``: the role of
+    the reference's load-time bank layout (serving/partition.py:398-405), so the
+    first captured step allocates nothing.  Returns the number of layers packed."""
+    mod = mod or _MOD
+    n = 0
+    for m in module.modules():
+        if hasattr(m, "experts") and hasattr(m, "experts_start_idx") and _servable(m, mod) is None:
+            h = hip_moe_of(m, mod)
+            if h is not None:
+                h.reserve(max_tokens)
+                n += 1
+    return n
+
+
 def _decline(moe, why, x, input_ids):
     tally = getattr(moe, "_hip_declined", None)
     if tally is None:
@@ -486,10 +511,9 @@ def _decline(moe, why, x, input_ids):
 
 def hip_forward(self, x, input_ids):
     """Replacement for MoE.forward(self, x, input_ids) (architecture.py:777-794)."""
-    if int(getattr(_MOD, "world_size", 1) or 1) > 1:
-        return _decline(self, "world_size>1", x, input_ids)
-    if self.experts_start_idx != 0 or self.experts_end_idx != self.n_routed_experts:
-        return _decline(self, "partial-experts", x, input_ids)
+    why = _servable(self, _MOD)
+    if why is not None:
+        return _decline(self, why, x, input_ids)
     h = hip_moe_of(self)
     if h is None:
         return _decline(self, "not-mxfp4-bank", x, input_ids)
