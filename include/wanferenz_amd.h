@@ -206,6 +206,20 @@ int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const int64_t* inpu
                    void* y_bf16, float* weights_out, int64_t* indices_out, void* ws,
                    size_t ws_bytes, hipStream_t stream);
 
+/* wz_moe_forward without a caller workspace: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The scratch is a device array
+ * inside the library, WZ_MOE_NOALLOC_SCRATCH_BYTES (16 MiB) per GPU, held until the
+ * process ends: enough for a V4-shape layer (D 4096, I 2048, 256 experts, top-6) up
+ * to T = 156 tokens, and for any T where wz_moe_workspace_bytes(d, T) fits.  A larger
+ * call fails with WZ_ESPACE and launches nothing.  The function allocates nothing;
+ * its arrival counters are cleared by a fill kernel at the start of every call.
+ * All calls on one GPU share its scratch array: calls that overlap on one GPU
+ * (concurrent streams, or host threads) race and must be serialised by the caller. */
+#define WZ_MOE_NOALLOC_SCRATCH_BYTES (16 << 20)
+int wz_moe_forward_noalloc(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids, int64_t T,
+                           void* y_bf16, float* weights_out, int64_t* indices_out, hipStream_t stream);
+
 /* Profiling replay: re-launch one kernel stage of the preceding wz_moe_forward call
  * made with the same d, x, T, y and ws (the workspace still holds that call's
  * routing tables and intermediates), so a stage can be timed on its own or

@@ -25,6 +25,8 @@
 //   combine    y[t] = bf16(sum_{experts asc} out[t,e] + shared[t]).
 #include "moe_common.h"
 
+#include <mutex>
+
 namespace wz {
 
 // ------------------------------------------------------------------ gate ----
@@ -530,4 +532,69 @@ extern "C" int wz_moe_replay_stage(const wz_moe_desc* d, const void* x_bf16, con
   }
   if (stage == WZ_STAGE_COMBINE) return launch_combine(w, T, d->topk, d->dim, y_bf16, stream);
   return launch_prefill_experts(d, w, x_bf16, T, stream, stage);
+}
+
+// ------------------------------------------------------- no-allocation entry ----
+//
+// wz_moe_forward with the workspace in a file-scope device array instead of a
+// caller-provided buffer, for callers that cannot allocate.  Each GPU the
+// library runs on holds its own copy of `scratch` until the process ends.  A
+// device address is taken once per device with hipGetSymbolAddress and used
+// for every kernel argument; host code never passes the array's name itself.
+
+namespace wz {
+
+static __device__ __align__(256) uint8_t scratch[WZ_MOE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::once_flag g_scratch_once[kMaxDevices];
+static int g_scratch_rc[kMaxDevices];
+
+// The device address of this device's scratch array (nullptr on failure, with the error set).
+static uint8_t* scratch_for_current_device(const char* what) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error(WZ_EINVAL, "%s: no current device (or device index >= %d)", what, kMaxDevices);
+    return nullptr;
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_rc[dev] = int(e);
+    g_scratch_ptr[dev] = e == hipSuccess ? p : nullptr;
+  });
+  if (!g_scratch_ptr[dev]) {
+    set_error(WZ_ELAUNCH, "%s: hipGetSymbolAddress of the scratch array failed on device %d (hip error %d)", what,
+              dev, g_scratch_rc[dev]);
+    return nullptr;
+  }
+  return static_cast<uint8_t*>(g_scratch_ptr[dev]);
+}
+
+}  // namespace wz
+
+extern "C" int wz_moe_forward_noalloc(const wz_moe_desc* d, const void* x_bf16, const int64_t* input_ids,
+                                      int64_t T, void* y_bf16, float* weights_out, int64_t* indices_out,
+                                      hipStream_t stream) {
+  using namespace wz;
+  if (!d) return set_error(WZ_EINVAL, "moe_forward_noalloc: null descriptor");
+  if (d->topk <= 0 || d->topk > 16) return set_error(WZ_EINVAL, "moe_forward_noalloc: topk=%d outside 1..16", d->topk);
+  if (T < 0) return set_error(WZ_EINVAL, "moe_forward_noalloc: T=%lld < 0", (long long)T);
+  if (T == 0) return WZ_OK;
+  const size_t need = wz_moe_workspace_bytes(d, T);
+  if (need > size_t(WZ_MOE_NOALLOC_SCRATCH_BYTES))
+    return set_error(WZ_ESPACE,
+                     "moe_forward_noalloc: this layer at T=%lld needs %zu bytes of scratch, more than the %d "
+                     "the library holds per device; call wz_moe_forward with a workspace instead",
+                     (long long)T, need, WZ_MOE_NOALLOC_SCRATCH_BYTES);
+  uint8_t* ws = scratch_for_current_device("moe_forward_noalloc");
+  if (!ws) return WZ_ELAUNCH;
+  // the arrival counters must start at zero: clear them on every call (a fill
+  // kernel, so the call stays capturable without a memset node)
+  WZ_LAUNCH("moe_ws_init", stream, zero_words_kernel, dim3(kCounterWords / 256), dim3(256), 0,
+            reinterpret_cast<uint32_t*>(ws), kCounterWords);
+  if (int rc = check_launch("moe_forward_noalloc counters")) return rc;
+  return wz_moe_forward(d, x_bf16, input_ids, T, y_bf16, weights_out, indices_out, ws,
+                        size_t(WZ_MOE_NOALLOC_SCRATCH_BYTES), stream);
 }
