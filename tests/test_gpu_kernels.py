@@ -274,8 +274,14 @@ def test_add_bf16_is_one_rounding(gpu):
     assert np.array_equal(f32_of_bf16(out).ravel(), ref.ravel())
 
 
+# the dense projections of the decode block: cfg-3 widths, then the V4 attention
+# projections wq_a, wkv, wq_b, wo_b and the indexer's wq_b (fp8_vector.py:505-510)
+PROJ_SHAPES = [(4096, 1024), (1024, 4096), (4096, 4096), (16384, 4096),
+               (512, 4096), (32768, 1024), (4096, 8192), (8192, 1024)]
+
+
 @pytest.mark.parametrize("w_fp32", [True, False])
-@pytest.mark.parametrize("N,K", [(4096, 1024), (1024, 4096), (4096, 4096), (16384, 4096)])
+@pytest.mark.parametrize("N,K", PROJ_SHAPES)
 @pytest.mark.parametrize("M", [1, 8, 128])
 def test_fp8_linear_projection_shapes(gpu, w_fp32, N, K, M):
     """fp8_linear (act_quant fused) at the dense projection shapes, weights generated on
@@ -313,7 +319,7 @@ def test_fp8_linear_projection_shapes(gpu, w_fp32, N, K, M):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 256, 4096), (5, 512, 1024), (16, 128, 2048), (40, 256, 4096),
-                                   (3, 128, 1536)])
+                                   (3, 128, 1536), (1, 512, 8192), (16, 384, 8192), (2, 4096, 1024)])
 def test_fp8_linear_packed_exact(gpu, M, N, K):
     """x in {0, +-0.5, +-1, +-1.5} with one 2.0 per 128-block quantises exactly (ue8m0
     scale 2^-7), weight codes of the same values with unit scales: every partial sum
@@ -337,6 +343,38 @@ def test_fp8_linear_packed_exact(gpu, M, N, K):
     ref = om.fp8_gemm(rq, rs, w, e8m0_decode(ws))
     assert np.array_equal(bits16(y), bf16_bits(ref))
 
+
+
+@pytest.mark.parametrize("N,K", [(16 * (1024 * 9 + 8), 1024), (16 * (1024 * 5 + 8), 2048),
+                                 (16 * (512 * 5 + 8), 4096), (16 * (256 * 5 + 8), 8192)])
+def test_fp8_gemv_ring_every_tile(gpu, N, K):
+    """The packed GEMV at an N where every workgroup (at most 4 per CU) streams more than
+    twice its ring depth of 16-column tiles, with a ragged last round: every tile of the
+    output is compared with a float32 torch statement of fp8_gemm on the dequantised
+    operands (act_quant by the oracle), row block by row block."""
+    M = 3
+    w = torch.empty(N, K, dtype=torch.uint8, device=gpu)
+    synth.device_fill(w, synth.stream_key(N + K + 1, synth.S_FP8_W), synth.FILL_E4M3)
+    ws = torch.empty(N // 128, K // 128, dtype=torch.uint8, device=gpu)
+    synth.device_fill(ws, synth.stream_key(N + K + 1, synth.S_FP8_W_S), synth.FILL_E8M0, 112, 116)
+    ws = ws.view(torch.float8_e8m0fnu)
+    xb = _x(N + K, M, K)
+    lin = kernels.PackedFp8Linear(w.view(torch.float8_e4m3fn), ws, "ue8m0")
+    y = f32_of_bf16(lin(bf16_tensor(xb, gpu)))
+    rq, rs = om.act_quant(from_bf16_bits(xb), 128, True)
+    xd = torch.from_numpy(np.ascontiguousarray(om.dequant_act(rq, rs), dtype=np.float32)).to(gpu)
+    wsf = ws.view(torch.uint8).to(torch.int32)
+    wsf = torch.ldexp(torch.ones_like(wsf, dtype=torch.float32), wsf - 127)
+    ref = torch.empty(M, N, dtype=torch.float32, device=gpu)
+    for r0 in range(0, N, 8192):
+        wd = w[r0:r0 + 8192].view(torch.float8_e4m3fn).float().view(-1, K // 128, 128)
+        wd = (wd * wsf[r0 // 128:(r0 + 8192) // 128].repeat_interleave(128, 0)[:, :, None]).view(-1, K)
+        ref[:, r0:r0 + 8192] = xd @ wd.T
+    torch.cuda.synchronize()
+    ref = ref.cpu().numpy()
+    for r0 in range(0, N, 16 * 512):
+        rel, cos = _close(y[:, r0:r0 + 16 * 512], ref[:, r0:r0 + 16 * 512])
+        assert rel <= TOL_REL and cos >= TOL_COS, (r0, rel, cos)
 
 def _wire_rows(seed, M, D):
     from oracle.numerics import bf16_bits

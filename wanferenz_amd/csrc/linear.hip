@@ -8,12 +8,13 @@
 // in lane order, so every weight load instruction of a wave reads 1 KB
 // contiguous; the row-major layout spreads each instruction over 16 rows.
 //
-// M <= 16, K in {1024, 2048, 4096}: fp8_gemv_kernel.  Persistent workgroups of
-//   8 waves; wave w owns K-blocks [w NKB, (w+1) NKB) of every 16-column tile.
-//   The wave quantises its slice of x once (act_quant fused into the A
-//   operand) and keeps it in registers, then the workgroup streams tiles
-//   b, b+G, ... with the next tile's weights in flight during the current
-//   tile's MFMAs; the eight K partials meet in LDS, summed in wave order.
+// M <= 16, K in {1024, 2048, 4096, 8192}: fp8_gemv_kernel.  Persistent
+//   workgroups of W waves; wave w owns K-blocks [w NKB, (w+1) NKB) of every
+//   16-column tile.  The wave quantises its slice of x once (act_quant fused
+//   into the A operand) and keeps it in registers, then the workgroup streams
+//   tiles b, b+G, ... through a ring of NB register buffers, so NB tiles'
+//   weights are in flight during the current tile's MFMAs; the W K-partials
+//   meet in LDS, summed in wave order.
 // Otherwise: act_quant into the caller's workspace, then the dense tile GEMM
 //   (launch_dense_fp8: M-tiles of <= 64 rows staged in LDS).
 #include "mfma_ops.h"
@@ -27,18 +28,32 @@ int launch_pack_fp8(const void* w, int64_t N, int64_t K, void* dst, hipStream_t 
 int launch_dense_fp8(const uint8_t* wp, const void* w_s, int w_kind, const uint8_t* xq, const float* xs,
                      bool a_pow2, uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
-constexpr int kGvWaves = 8;
-constexpr int kGvThreads = kGvWaves * 64;
 constexpr int kGvMaxM = 16;
 
-// K-blocks per wave of the GEMV, 0 when K does not split into 8 x {1, 2, 4}
-// (K = 1024, 2048, 4096; wider K would keep more A registers than fit).
-static int gemv_nkb(int64_t K) {
-  const int64_t kb = K / 128;
-  if (K % 1024) return 0;
-  const int64_t n = kb / kGvWaves;
-  return (n == 1 || n == 2 || n == 4) ? int(n) : 0;
-}
+// GEMV shapes: W waves per workgroup, wave w owns K-blocks [w NKB, (w+1) NKB)
+// of every 16-column tile, NB tiles in flight per workgroup (a ring of
+// register buffers).  K = 128 W NKB.  Each shape keeps about 256 KB of
+// weights in flight per CU at the occupancy its registers allow (the layout
+// of the MoE w1/w3 stream: few waves, long per-lane K runs).
+// (W, NKB, NB, minimum waves per SIMD, XF) per K, the fastest of a sweep of
+// 4-, 8- and 16-wave shapes at the V4 and cfg-3 projection widths (T = 1, 8):
+// at K >= 4096 sixteen waves halve each wave's share of the fused act_quant,
+// which sits in front of the first weight request; at K = 1024 the weight
+// requests go out before it.
+#ifndef WZ_GV_K1024
+#define WZ_GV_K1024 8, 1, 4, 4, true
+#endif
+#ifndef WZ_GV_K2048
+#define WZ_GV_K2048 8, 2, 3, 3, false
+#endif
+#ifndef WZ_GV_K4096
+#define WZ_GV_K4096 16, 2, 2, 4, false
+#endif
+#ifndef WZ_GV_K8192
+#define WZ_GV_K8192 16, 4, 1, 4, false
+#endif
+
+static bool gemv_shape_ok(int64_t K) { return K == 1024 || K == 2048 || K == 4096 || K == 8192; }
 
 template <int NKB>
 struct GvBuf {
@@ -49,22 +64,31 @@ struct GvBuf {
 
 // QA: x is pre-quantised e4m3 [M, K] with block scales xs [M, K/128] of kind
 // a_kind (fp8_gemm's a, a_s); otherwise x is bf16 and act_quant is fused.
-template <int NKB, bool QA>
-__global__ __launch_bounds__(kGvThreads) void fp8_gemv_kernel(const void* __restrict__ x,
-                                                              const void* __restrict__ xs, int a_kind,
-                                                              const uint8_t* __restrict__ wp,
-                                                              const void* __restrict__ w_s, int w_kind,
-                                                              uint16_t* __restrict__ y, int M, int N, int K,
-                                                              int a_pow2i) {
-  __shared__ float red[2][kGvWaves * 4 * kWave];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Workgroup b takes tiles b, b + G, ... (n_my of them); tile j sits in ring
+// slot j % NB, and slot s is refilled with tile j + NB as soon as tile j's
+// MFMAs have issued, so NB tiles stay in flight.  The W K-partials of a tile
+// meet in LDS and are summed in wave order.  AP2 / BP2: power-of-two
+// activation / e8m0 weight scales (compile-time, so the scaled MFMA chains
+// without a runtime branch around it).
+template <int W, int NKB, int NB, int MINW, bool XF, bool QA, bool AP2, bool BP2>
+__global__ __launch_bounds__(W * 64, MINW) void fp8_gemv_kernel(const void* __restrict__ x, const void* __restrict__ xs,
+                                                         int a_kind, const uint8_t* __restrict__ wp,
+                                                         const void* __restrict__ w_s, int w_kind,
+                                                         uint16_t* __restrict__ y, int M, int N, int K,
+                                                         int a_pow2i) {
+  __shared__ float red[2][W * 4 * kWave];
+  // the wave index is uniform: tile addresses and weight scales stay scalar
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = lane & 15, g = lane >> 4;
-  const bool a_pow2 = a_pow2i != 0, bp = w_kind == WZ_WSCALE_E8M0;
+  constexpr bool a_pow2 = AP2, bp = BP2;
+  constexpr int wkind = BP2 ? WZ_WSCALE_E8M0 : WZ_WSCALE_F32;
   const int KB = K / 128, kb0 = wave * NKB, items = N / 16, G = gridDim.x;
   const int first = blockIdx.x;
   if (first >= items) return;
+  const int n_my = (items - first + G - 1) / G;
 
-  auto fetch = [&](GvBuf<NKB>& b, int item) {
+  auto fetch = [&](GvBuf<NKB>& b, int j) {
+    const int item = first + j * G;
     const uint8_t* t = wp + (int64_t(item) * KB + kb0) * 2048 + lane * 16;
 #pragma unroll
     for (int q = 0; q < NKB; ++q) {
@@ -72,14 +96,15 @@ __global__ __launch_bounds__(kGvThreads) void fp8_gemv_kernel(const void* __rest
       b.w[q] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
 #pragma unroll
-    for (int q = 0; q < NKB; ++q) fp8_wscale(w_s, int64_t(item >> 3) * KB + kb0 + q, w_kind, b.se[q], b.sf[q]);
+    for (int q = 0; q < NKB; ++q) fp8_wscale(w_s, int64_t(item >> 3) * KB + kb0 + q, wkind, b.se[q], b.sf[q]);
   };
 
-  // this wave's K slice of the (<= 16) token rows, quantised once.  The
-  // weights are requested after the quantisation: issuing them first (weights
-  // then x, or x then weights with the quantisation in between) measured
-  // 0.3-1.3 us slower per launch.
+  // this wave's K slice of the (<= 16) token rows, quantised once.  XF: the
+  // bf16 rows are requested, then the first tile's weights, and the
+  // quantisation runs while those are in flight (the x loads, issued first,
+  // return first); otherwise the rows are quantised before any weight request.
   AOp a[NKB];
+  ARaw xr[QA || !XF ? 1 : NKB];
   if constexpr (QA) {
     const uint8_t* xrow = nl < M ? static_cast<const uint8_t*>(x) + int64_t(nl) * K : nullptr;
     const void* srow = a_kind == WZ_SCALE_UE8M0
@@ -90,15 +115,29 @@ __global__ __launch_bounds__(kGvThreads) void fp8_gemv_kernel(const void* __rest
   } else {
     const uint16_t* xrow = nl < M ? static_cast<const uint16_t*>(x) + int64_t(nl) * K : nullptr;
 #pragma unroll
-    for (int q = 0; q < NKB; ++q) a[q] = a_from_bf16(xrow, kb0 + q, g, a_pow2);
+    for (int q = 0; q < NKB; ++q) {
+      if constexpr (XF)
+        xr[q] = a_load_bf16(xrow, kb0 + q, g);
+      else
+        a[q] = a_from_bf16(xrow, kb0 + q, g, AP2);
+    }
   }
-  GvBuf<NKB> b0, b1;
-  fetch(b0, first);
-  auto process = [&](const GvBuf<NKB>& b, int item, int par) {
+  auto quant_x = [&]() {
+    if constexpr (!QA && XF) {
+#pragma unroll
+      for (int q = 0; q < NKB; ++q) a[q] = a_quant_bf16(xr[q], AP2);
+    }
+  };
+  // keeps the weight requests below the quantisation: hoisted above it, they
+  // would hold their registers beside the raw rows' and spill
+  if constexpr (!QA && !XF) __builtin_amdgcn_sched_barrier(0);
+
+  auto process = [&](const GvBuf<NKB>& b, int j) {
+    const int item = first + j * G;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < NKB; ++q) mma_step<kFmtFp8, kFmtFp8>(acc, a[q], b.w[q], b.se[q], b.sf[q], a_pow2, bp, lane);
-    float* r = red[par];
+    float* r = red[j & 1];
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[(wave * 4 + i) * kWave + lane] = acc[i];
     __syncthreads();
@@ -107,32 +146,56 @@ __global__ __launch_bounds__(kGvThreads) void fp8_gemv_kernel(const void* __rest
       for (int i = 0; i < 4; ++i) {
         float v = r[i * kWave + lane];
 #pragma unroll
-        for (int w = 1; w < kGvWaves; ++w) v += r[(w * 4 + i) * kWave + lane];
+        for (int w = 1; w < W; ++w) v += r[(w * 4 + i) * kWave + lane];
         const int row = g * 4 + i;
         if (row < M) y[int64_t(row) * N + item * 16 + nl] = f32_to_bf16(v);
       }
     }
   };
 
-  int i = first;
-  for (; i + 2 * G < items; i += 2 * G) {
-    fetch(b1, i + G);
-    process(b0, i, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    fetch(b0, i + 2 * G);
-    process(b1, i + G, 1);
-    __builtin_amdgcn_sched_barrier(0);
+  GvBuf<NKB> buf[NB];
+  fetch(buf[0], 0);
+  quant_x();
+  if (n_my < NB) {
+    // fewer tiles than ring slots: all of them in flight at once
+#pragma unroll
+    for (int s = 1; s < NB - 1; ++s)
+      if (s < n_my) fetch(buf[s], s);
+#pragma unroll
+    for (int s = 0; s < NB - 1; ++s)
+      if (s < n_my) process(buf[s], s);
+    return;
   }
-  if (i + G < items) {
-    fetch(b1, i + G);
-    process(b0, i, 0);
-    process(b1, i + G, 1);
-  } else {
-    process(b0, i, 0);
+#pragma unroll
+  for (int s = 1; s < NB; ++s) fetch(buf[s], s);
+  int j = 0;
+  // steady state: every refill is a tile of this workgroup
+  for (; j + 2 * NB <= n_my; j += NB) {
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      process(buf[s], j + s);
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(buf[s], j + s + NB);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
+  // the last NB .. 2 NB - 1 tiles
+#pragma unroll
+  for (int s = 0; s < NB; ++s) {
+    process(buf[s], j + s);
+    if (j + s + NB < n_my) fetch(buf[s], j + s + NB);
+  }
+#pragma unroll
+  for (int s = 0; s < NB; ++s)
+    if (j + NB + s < n_my) process(buf[s], j + NB + s);
 }
 
-static int gemv_grid(int64_t N, int nkb);
+template <int W, int NKB, int NB, int MINW, bool XF, bool QA>
+static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
+                       uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream);
+
+static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s,
+                         int w_kind, uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream);
 
 static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
@@ -150,7 +213,7 @@ extern "C" int wz_fp8_pack(const void* w_e4m3, int64_t N, int64_t K, void* packe
 extern "C" size_t wz_fp8_linear_workspace_bytes(int64_t M, int64_t K) {
   using namespace wz;
   if (M <= 0 || K <= 0) return 0;
-  if (M <= kGvMaxM && gemv_nkb(K)) return 0;
+  if (M <= kGvMaxM && gemv_shape_ok(K)) return 0;
   return align256(size_t(M) * size_t(K)) + size_t(M) * size_t(K / 128) * 4;
 }
 
@@ -169,22 +232,9 @@ extern "C" int wz_fp8_linear_packed(const void* x_bf16, const void* w_packed, co
   if (M == 0) return WZ_OK;
   if (!x_bf16 || !w_packed || !w_s || !y_bf16) return set_error(WZ_EINVAL, "fp8_linear_packed: null pointer");
   const bool pow2 = act_scale_kind != WZ_SCALE_F32;
-  const int nkb = gemv_nkb(K);
-  if (M <= kGvMaxM && nkb) {
-    const dim3 grid(unsigned(gemv_grid(N, nkb)));
-    const uint8_t* w = static_cast<const uint8_t*>(w_packed);
-    uint16_t* y = static_cast<uint16_t*>(y_bf16);
-#define WZ_GEMV(NKBV)                                                                                   \
-  WZ_LAUNCH("fp8_gemv", stream, (fp8_gemv_kernel<NKBV, false>), grid, dim3(kGvThreads), 0, x_bf16,         \
-            static_cast<const void*>(nullptr), 0, w, w_s, w_scale_kind, y, int(M), int(N), int(K), pow2 ? 1 : 0)
-    switch (nkb) {
-      case 1: WZ_GEMV(1); break;
-      case 2: WZ_GEMV(2); break;
-      default: WZ_GEMV(4); break;
-    }
-#undef WZ_GEMV
-    return check_launch("fp8_gemv");
-  }
+  if (M <= kGvMaxM && gemv_shape_ok(K))
+    return gemv_dispatch(false, x_bf16, nullptr, 0, static_cast<const uint8_t*>(w_packed), w_s, w_scale_kind,
+                         static_cast<uint16_t*>(y_bf16), M, N, K, pow2, stream);
   const size_t need = wz_fp8_linear_workspace_bytes(M, K);
   if (!ws || ws_bytes < need)
     return set_error(WZ_ESPACE, "fp8_linear_packed: workspace of %zu bytes needed for M=%lld K=%lld, got %zu", need,
@@ -204,10 +254,49 @@ __global__ void e8m0_to_f32_kernel(const uint8_t* __restrict__ src, float* __res
   if (i < n) dst[i] = e8m0_to_f32(src[i]);
 }
 
-static int gemv_grid(int64_t N, int nkb) {
-  // resident workgroups: one per CU at NKB = 4 (193 VGPRs), two below
-  const int64_t items = N / 16, per_cu = nkb == 4 ? 1 : 2;
-  return int(std::min<int64_t>(items, per_cu * int64_t(cu_count())));
+// Resident workgroups per CU of one GEMV instantiation (its registers and
+// LDS decide), asked once.  The grid is that many per CU, or one per tile.
+template <int W, int NKB, int NB, int MINW, bool XF, bool QA, bool AP2, bool BP2>
+static int launch_gemv_k(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
+                         uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  static const int per_cu = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fp8_gemv_kernel<W, NKB, NB, MINW, XF, QA, AP2, BP2>, W * 64, 0) !=
+            hipSuccess ||
+        n < 1)
+      n = 1;
+    return n;
+  }();
+  const dim3 grid(unsigned(std::min<int64_t>(N / 16, int64_t(per_cu) * cu_count())));
+  WZ_LAUNCH("fp8_gemv", stream, (fp8_gemv_kernel<W, NKB, NB, MINW, XF, QA, AP2, BP2>), grid, dim3(W * 64), 0, x, xs, a_kind,
+            w, w_s, w_kind, y, int(M), int(N), int(K), AP2 ? 1 : 0);
+  return check_launch("fp8_gemv");
+}
+
+template <int W, int NKB, int NB, int MINW, bool XF, bool QA>
+static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
+                       uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream) {
+  const bool bp = w_kind == WZ_WSCALE_E8M0;
+  if (pow2)
+    return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, true>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, stream)
+              : launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, false>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, stream);
+  return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, true>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, stream)
+            : launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, false>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, stream);
+}
+
+static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s,
+                         int w_kind, uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream) {
+#define WZ_GV(...)                                                                                          \
+  return qa ? launch_gemv<__VA_ARGS__, true>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, pow2, stream)          \
+            : launch_gemv<__VA_ARGS__, false>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, pow2, stream)
+  switch (K) {
+    case 1024: WZ_GV(WZ_GV_K1024);
+    case 2048: WZ_GV(WZ_GV_K2048);
+    case 4096: WZ_GV(WZ_GV_K4096);
+    case 8192: WZ_GV(WZ_GV_K8192);
+    default: return set_error(WZ_EINVAL, "fp8 gemv: no shape for K=%lld", (long long)K);
+  }
+#undef WZ_GV
 }
 
 }  // namespace wz
@@ -215,7 +304,7 @@ static int gemv_grid(int64_t N, int nkb) {
 extern "C" size_t wz_fp8_gemm_packed_workspace_bytes(int64_t M, int64_t K, int act_scale_kind) {
   using namespace wz;
   if (M <= 0 || K <= 0) return 0;
-  if (M <= kGvMaxM && gemv_nkb(K)) return 0;
+  if (M <= kGvMaxM && gemv_shape_ok(K)) return 0;
   return act_scale_kind == WZ_SCALE_UE8M0 ? size_t(M) * size_t(K / 128) * 4 : 0;
 }
 
@@ -234,22 +323,10 @@ extern "C" int wz_fp8_gemm_packed(const void* a_e4m3, const void* a_s, const voi
   if (M == 0) return WZ_OK;
   if (!a_e4m3 || !a_s || !w_packed || !w_s || !c_bf16) return set_error(WZ_EINVAL, "fp8_gemm_packed: null pointer");
   const bool pow2 = act_scale_kind != WZ_SCALE_F32;
-  const int nkb = gemv_nkb(K);
   const uint8_t* w = static_cast<const uint8_t*>(w_packed);
   uint16_t* c = static_cast<uint16_t*>(c_bf16);
-  if (M <= kGvMaxM && nkb) {
-    const dim3 grid(unsigned(gemv_grid(N, nkb)));
-#define WZ_GEMV(NKBV)                                                                                            \
-  WZ_LAUNCH("fp8_gemv", stream, (fp8_gemv_kernel<NKBV, true>), grid, dim3(kGvThreads), 0, a_e4m3, a_s,           \
-            act_scale_kind, w, w_s, w_scale_kind, c, int(M), int(N), int(K), pow2 ? 1 : 0)
-    switch (nkb) {
-      case 1: WZ_GEMV(1); break;
-      case 2: WZ_GEMV(2); break;
-      default: WZ_GEMV(4); break;
-    }
-#undef WZ_GEMV
-    return check_launch("fp8_gemv");
-  }
+  if (M <= kGvMaxM && gemv_shape_ok(K))
+    return gemv_dispatch(true, a_e4m3, a_s, act_scale_kind, w, w_s, w_scale_kind, c, M, N, K, pow2, stream);
   const float* xs = static_cast<const float*>(a_s);
   if (act_scale_kind == WZ_SCALE_UE8M0) {
     const size_t need = wz_fp8_gemm_packed_workspace_bytes(M, K, act_scale_kind);
