@@ -21,14 +21,20 @@ Printed JSON line (one):
               live: the stage replayed alone for all layers from a captured
               graph, HIP events on the replay stream (stage_times)
   stage_us    the same per-launch measurement for every stage of the layer
-  cpu_baseline the oracle (numpy restatement of the reference CPU path) on one
-              T-token layer, single thread
+  cpu_baseline the torch float32 restatement of the reference CPU path
+              (oracle/torch_ref.py) on layer 0: all cores (<= 16) at T tokens and
+              one core at T = 1, median of 10 after 3 warm-ups, CPU model, the HIP
+              layer's agreement on the same tokens and the near-tie tokens
   per_T       the same layer measured at T = 1, 2, 4, 8
-  prefill     the same layer at T = 128, 512, 2048 with a Zipf(1.1) gate bias
-              (load-imbalanced experts): µs/layer, tokens/s, algorithmic HBM
-              GB/s, and MFMA utilisation = 6*D*I*(T*k + T) flops / time against
-              the dense FP8 (5.0 PFLOP/s, the rate of an e4m3 x e2m1 scaled
-              MFMA) and FP4 (10.1 PFLOP/s) peaks
+  prefill     the same layer at T = 128, 512, 2048 with the calibrated Zipf(1.1)
+              gate bias (beta in wanferenz_amd/zipf_v4.json; the fitted exponent
+              of each batch's routing is reported): µs/layer, tokens/s,
+              algorithmic HBM GB/s, and MFMA utilisation = 6*D*I*(T*k + T) flops /
+              time against the dense FP8 (5.0 PFLOP/s, the rate of an e4m3 x e2m1
+              scaled MFMA) and FP4 (10.1 PFLOP/s) peaks
+  prefill_hot_experts  T = 2048 with every token on experts 0..5 (2048 rows
+              each): the w13 / w2 launches' MFMA rate on full tiles
+  fp4_gemm_m2048  one expert's w1|w3 and w2 GEMMs alone at M = 2048 (wz_fp4_gemm)
   fp8_gemv    the FP8 linear at the dense projection shapes (packed and row-major)
   grouped_fp4 the grouped MXFP4 GEMM of the banked decode path (6 experts' w1|w3, w2)
   sparse_attn sparse attention at 64 heads of 512, topk 640: decode B = 1, 4, 8
@@ -206,7 +212,7 @@ def stage_times(layers, xs, outs, reps=20):
     """Mean µs per launch of each stage of the layer.
 
     Each stage alone (wz_moe_replay_stage: the same kernels on the state the
-    last forward left in the workspace) is captured for all layers into one
+    last forward left in the workspace) that launches anything is captured for all layers into one
     graph, so its launches run back to back with no launch gaps and no event
     packets between kernels; HIP events on the replay stream bracket ``reps``
     replays.  Rotating over all layers keeps the weights out of the caches as
@@ -214,9 +220,19 @@ def stage_times(layers, xs, outs, reps=20):
     """
     import torch
 
+    from wanferenz_amd import _native as N
+
     T = xs[0][1].size(0)
     res = {}
+    lib = N.lib()
     for name, st in STAGES:
+        # a stage that launches nothing on this path (hquant and combine when w2
+        # quantises and combines itself) has no time of its own
+        lib.wz_prof_begin(64)
+        layers[0][0].replay_stage(xs[0][1], st, outs[0])
+        n_launch = lib.wz_prof_end()
+        if n_launch <= 0:
+            continue
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for (moe, _), (_, x), out in zip(layers, xs, outs):
@@ -513,12 +529,14 @@ def prefill_flops(T: int) -> float:
 
 
 def measure_prefill(layers, Ts, dev):
-    """Prefill T-token layers with a Zipf gate bias over the first layers' banks."""
+    """Prefill T-token layers with the calibrated Zipf(1.1) gate bias (beta from
+    wanferenz_amd/zipf_v4.json) over the first layers' banks."""
     import torch
 
     from wanferenz_amd import synth
 
-    zb = torch.from_numpy(synth.zipf_bias(E)).to(dev)
+    beta = synth.zipf_v4_beta()
+    zb = torch.from_numpy(synth.zipf_bias(E, 1.1, beta)).to(dev)
     tmax = max(Ts)
     players = [(moe.with_gate_bias(zb, max_tokens=tmax), host) for moe, host in layers]
     res = {}
@@ -544,47 +562,168 @@ def measure_prefill(layers, Ts, dev):
                        "mfma_frac_fp8": round(tflops / FP8_PEAK_TFLOPS, 4),
                        "mfma_frac_fp4": round(tflops / FP4_PEAK_TFLOPS, 4),
                        "max_expert_rows": int(max(l.max() for l in loads)),
+                       "zipf_beta": round(beta, 6),
+                       "zipf_exponent": round(float(np.mean([synth.zipf_exponent(l) for l in loads])), 3),
                        "mean_active_experts": round(float(np.mean([(l > 0).sum() for l in loads])), 1),
                        "steps": steps,
                        "stage_us": {k: round(v, 2) for k, v in kt.items()}}
     return res
 
 
-def cpu_baseline(layers, cfg, T, dev):
-    """Oracle on one T-token step of layer 0 (weights of the touched experts copied from HBM)."""
+def measure_hot_experts(layers, dev, T=2048):
+    """Hot-expert tiles: the prefill layer at T tokens with a gate bias that sends
+    every token to experts 0..5, so each of the six holds T rows (the M = 2048
+    expert of a skewed batch) and every w1/w3 and w2 tile is full.  MFMA rate of
+    the w13 and w2 launches = 2 * rows * N * K flops (routed rows T*k, plus the T
+    shared-expert rows) / the launch's mean duration (stage replay)."""
     import torch
-    from threadpoolctl import threadpool_limits
 
-    from oracle import moe as om
-    from oracle.numerics import e8m0_decode, from_bf16_bits
+    bias = torch.zeros(E, dtype=torch.float32, device=dev)
+    bias[:K_TOP] = 100.0
+    players = [(moe.with_gate_bias(bias, max_tokens=T), host) for moe, host in layers]
+    xs = make_inputs(len(players), T, dev, salt=7000)
+    steps = max(6, min(60, 24576 // T))
+    graphs, outs = capture(players, xs, steps)
+    secs, _ = time_steps(graphs, steps, max(2, steps // 4), len(players))
+    kt = stage_times(players, xs, outs, reps=max(2, steps // 3))
+    rows = T * K_TOP + T
+    res = {"T": T, "rows_per_expert": T, "us_per_layer": round(secs / steps * 1e6, 1),
+           "stage_us": {k: round(v, 2) for k, v in kt.items()}}
+    for st, flops in (("w13", 2.0 * rows * (2 * I) * D), ("w2", 2.0 * rows * D * I)):
+        tf = flops / (kt[st] * 1e-6) / 1e12
+        res[st] = {"TFLOP_s": round(tf, 1), "mfma_frac_fp8_rate": round(tf / FP8_PEAK_TFLOPS, 4),
+                   "mfma_frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4)}
+    return res
+
+
+def measure_fp4_gemm_2048(dev, reps=10):
+    """One expert's GEMMs alone at M = 2048 rows (wz_fp4_gemm: e4m3 activations with
+    ue8m0 block scales x MXFP4 weights): w1|w3 (N = 2I, K = D) and w2 (N = D, K = I).
+    Two weight copies alternate; flops = 2 M N K; rate against the e4m3 x e2m1
+    scaled-MFMA rate (the FP8 rate, 5.0 PFLOP/s) and the FP4 peak."""
+    import torch
+
+    from wanferenz_amd import kernels, synth
+
+    M = 2048
+    res = {}
+    for name, Nn, K in (("w13", 2 * I, D), ("w2", D, I)):
+        xb = synth.normal_bf16(synth.stream_key(M + K, synth.S_FP8_X), (M, K), 1.0)
+        x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
+        q, qs = kernels.act_quant(x, 128, "ue8m0", torch.float8_e8m0fnu)
+        ws = []
+        for r in range(2):
+            w = torch.empty(Nn, K // 2, dtype=torch.uint8, device=dev)
+            synth.device_fill(w, synth.stream_key(r, synth.S_W13), synth.FILL_U8)
+            s = torch.empty(Nn, K // 32, dtype=torch.uint8, device=dev)
+            synth.device_fill(s, synth.stream_key(r, synth.S_W13_S), synth.FILL_E8M0, 118, 122)
+            ws.append((w.view(torch.float4_e2m1fn_x2), s.view(torch.float8_e8m0fnu)))
+
+        def launches():
+            for w, s in ws:
+                kernels.fp4_gemm(q, qs, w, s, torch.float8_e8m0fnu)
+
+        us = graph_timed(launches, reps) / len(ws)
+        tf = 2.0 * M * Nn * K / (us * 1e-6) / 1e12
+        res[name] = {"M": M, "N": Nn, "K": K, "us": round(us, 2), "TFLOP_s": round(tf, 1),
+                     "mfma_frac_fp8_rate": round(tf / FP8_PEAK_TFLOPS, 4),
+                     "mfma_frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4)}
+    return res
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def _torch_layer(moe, used):
+    """The layer's touched routed experts and its shared expert, copied to host
+    memory in the checkpoint's formats, for the torch restatement."""
+    import torch
+
+    from oracle import torch_ref as tr
+
+    w = moe.weights
+
+    def e8m0(t):
+        return torch.ldexp(torch.ones(t.shape), t.cpu().to(torch.int32).float() - 127.0)
+
+    experts = {}
+    for e in used:
+        w13, s13 = w.w13[e].cpu(), e8m0(w.w13_s[e])
+        experts[e] = (tr.QLinear("fp4", w13[:I], s13[:I]), tr.QLinear("fp4", w13[I:], s13[I:]),
+                      tr.QLinear("fp4", w.w2[e].cpu(), e8m0(w.w2_s[e])))
+    shared = tuple(tr.QLinear("fp8", a.cpu(), e8m0(b)) for a, b in
+                   ((w.sh_w1, w.sh_w1_s), (w.sh_w3, w.sh_w3_s), (w.sh_w2, w.sh_w2_s)))
+    return tr.MoELayer(w.gate_w.cpu(), w.gate_bias.cpu(), experts, shared, E, K_TOP,
+                       "sqrtsoftplus", 1.5, 10.0, True)
+
+
+def cpu_baseline(layers, cfg, T, dev):
+    """The torch float32 restatement of the reference CPU path (oracle/torch_ref.py,
+    op for op after torch_ops.py and architecture.py) on layer 0 of the benchmark:
+    all cores (at most 16, the box's CPU share) on the T-token step, and one core
+    (the reference's OMP_NUM_THREADS=1) on a 1-token step; 3 warm-up runs, then the
+    median of 10.  Each run dequantises the weights it multiplies, as the reference
+    CPU path does.  The same inputs go through the HIP layer: expert indices must
+    match, outputs within 1e-2 relative / 0.9999 cosine; near-tie tokens are listed."""
+    import torch
+
+    from oracle import torch_ref as tr
     from wanferenz_amd import synth
 
-    moe, host = layers[0]
-    w = moe.weights
-    xb = synth.normal_bf16(synth.stream_key(1000, synth.layer_stream(0, synth.S_X)), (T, D), 1.0)
-    xf = from_bf16_bits(xb)
-    g = om.gate(xf, from_bf16_bits(host["gate_w"]), host["gate_bias"], K_TOP, "sqrtsoftplus", 1.5)
-    used = sorted(set(g.indices.ravel().tolist()))
-    ex = [None] * E
-    for e in used:
-        w13 = w.w13[e].cpu().numpy()
-        s13 = e8m0_decode(w.w13_s[e].cpu().numpy())
-        ex[e] = (om.Fp4Linear(w13[:I], s13[:I]), om.Fp4Linear(w13[I:], s13[I:]),
-                 om.Fp4Linear(w.w2[e].cpu().numpy(), e8m0_decode(w.w2_s[e].cpu().numpy())))
-    shared = (om.Fp8Linear(w.sh_w1.cpu().numpy(), e8m0_decode(w.sh_w1_s.cpu().numpy())),
-              om.Fp8Linear(w.sh_w3.cpu().numpy(), e8m0_decode(w.sh_w3_s.cpu().numpy())),
-              om.Fp8Linear(w.sh_w2.cpu().numpy(), e8m0_decode(w.sh_w2_s.cpu().numpy())))
-    p = om.MoEParams(D, I, E, K_TOP, from_bf16_bits(host["gate_w"]), host["gate_bias"], ex, shared,
-                     "sqrtsoftplus", 1.5, 10.0, True, None)
-    with threadpool_limits(1):
-        t0 = time.perf_counter()
-        om.moe_forward(p, xf)
-        secs = time.perf_counter() - t0
-    nbytes = layer_bytes(len(used), T)
-    return {"value": round(nbytes / secs / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"one V4 MoE layer at T={T} (U={len(used)} experts, {nbytes/1e6:.1f} MB "
-                      f"algorithmic) through the numpy oracle, 1 thread: {secs:.2f} s",
-            "us_per_layer": round(secs * 1e6, 1)}
+    moe, _ = layers[0]
+    n_all = max(1, min(16, len(os.sched_getaffinity(0))))
+    res = {"cpu_model": _cpu_model()}
+    prev_threads, prev_dtype = torch.get_num_threads(), torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        for leg, Tl, nt in (("all_cores", T, n_all), ("one_core", 1, 1)):
+            bits = synth.normal_bf16(synth.stream_key(1000, synth.layer_stream(0, synth.S_X)), (Tl, D), 1.0)
+            xc = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+            _, idx_c, scores = tr.gate_forward(xc, moe.weights.gate_w.cpu(), moe.weights.gate_bias.cpu(), K_TOP,
+                                               "sqrtsoftplus", 1.5)
+            used = sorted(set(idx_c.flatten().tolist()))
+            p = _torch_layer(moe, used)
+            torch.set_num_threads(nt)
+            times = []
+            for i in range(13):
+                t0 = time.perf_counter()
+                y_c, _, idx_c = tr.moe_forward(p, xc)
+                times.append(time.perf_counter() - t0)
+            med = float(np.median(times[3:]))
+            # the HIP layer on the same tokens
+            out = torch.empty(Tl, D, dtype=torch.bfloat16, device=dev)
+            moe.forward(xc.to(dev), out=out)
+            _, idx_g, _, _, _ = moe.route(xc.to(dev))
+            torch.cuda.synchronize()
+            yg, yc = out.float().cpu().numpy(), y_c.float().numpy()
+            rel = float(np.abs(yg - yc).max() / max(np.abs(yc).max(), 1e-30))
+            cos = float((yg * yc).sum() / max(np.linalg.norm(yg) * np.linalg.norm(yc), 1e-30))
+            nbytes = layer_bytes(len(used), Tl)
+            res[leg] = {"T": Tl, "threads": nt, "us_per_layer": round(med * 1e6, 1),
+                        "tokens_per_s": round(Tl / med, 2), "GB_s": round(nbytes / med / 1e9, 4),
+                        "runs": len(times) - 3, "warmup": 3, "distinct_experts": len(used),
+                        "indices_match": bool(torch.equal(idx_g.cpu().long(), idx_c.long())),
+                        "max_rel_err": round(rel, 6), "cosine": round(cos, 7),
+                        "near_tie_tokens": tr.near_ties(scores, K_TOP)}
+    finally:
+        torch.set_num_threads(prev_threads)
+        torch.set_default_dtype(prev_dtype)
+    a = res["all_cores"]
+    res.update({"value": a["GB_s"], "unit": "GB/s", "cores": a["threads"], "kind": "port",
+                "sample": f"one V4 MoE layer (layer 0 of the benchmark, T={a['T']}, U={a['distinct_experts']}) "
+                          f"through the torch float32 restatement of the reference CPU path on "
+                          f"{a['threads']} threads: median of 10 after 3 warm-ups; one_core: T=1, 1 thread"})
+    return res
 
 
 def main():
@@ -655,6 +794,8 @@ def main():
     if args.prefill:
         Ts = [int(t) for t in args.prefill.split(",") if t]
         out["prefill"] = measure_prefill(layers[:max(1, args.prefill_layers)], Ts, dev)
+        out["prefill_hot_experts"] = measure_hot_experts(layers[:max(1, args.prefill_layers)], dev)
+        out["fp4_gemm_m2048"] = measure_fp4_gemm_2048(dev)
     if not args.no_gemv:
         out["fp8_gemv"] = measure_gemv(dev)
         out["grouped_fp4"] = measure_grouped_fp4(dev)
