@@ -109,6 +109,9 @@ def parse():
     ap.add_argument("--prefill", default="128,512,2048",
                     help="comma-separated prefill T values ('' to skip)")
     ap.add_argument("--prefill-layers", type=int, default=3)
+    ap.add_argument("--prefill-legs", default="zipf,hot,gemm",
+                    help="prefill legs to run: zipf (calibrated skew), hot (every token on experts "
+                         "0..5), gemm (one expert's GEMMs alone at M = 2048)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 5 times (the reference kernel of "
                          "known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -793,9 +796,13 @@ def main():
         out["per_T"] = sweep
     if args.prefill:
         Ts = [int(t) for t in args.prefill.split(",") if t]
-        out["prefill"] = measure_prefill(layers[:max(1, args.prefill_layers)], Ts, dev)
-        out["prefill_hot_experts"] = measure_hot_experts(layers[:max(1, args.prefill_layers)], dev)
-        out["fp4_gemm_m2048"] = measure_fp4_gemm_2048(dev)
+        legs = set(args.prefill_legs.split(","))
+        if "zipf" in legs:
+            out["prefill"] = measure_prefill(layers[:max(1, args.prefill_layers)], Ts, dev)
+        if "hot" in legs:
+            out["prefill_hot_experts"] = measure_hot_experts(layers[:max(1, args.prefill_layers)], dev)
+        if "gemm" in legs:
+            out["fp4_gemm_m2048"] = measure_fp4_gemm_2048(dev)
     if not args.no_gemv:
         out["fp8_gemv"] = measure_gemv(dev)
         out["grouped_fp4"] = measure_grouped_fp4(dev)
