@@ -161,10 +161,7 @@ __device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
 __device__ __forceinline__ uint32_t dpp_min_u32(uint32_t v) { return ~dpp_max_u32(~v); }
 
 // Agent-scope arrival counter: returns true in the last of `n` arrivals and
-// resets the counter for the next launch.  Producers publish their global
-// writes with release_agent() before arriving; the last arrival calls
-// acquire_agent() before reading them.  (An agent-scope release writes back
-// this XCD's L2 and the acquire invalidates it, so keep arrivals few.)
+// resets the counter for the next launch.
 __device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t n) {
   const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (old == n - 1) {
@@ -174,12 +171,21 @@ __device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t n) {
   return false;
 }
 
-__device__ __forceinline__ void release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-
-// Device-scope relaxed accesses: performed at the device coherence point, so a
-// value stored this way by one workgroup, with the storing wave's stores
-// drained (vm_drain) before it signals, is seen by another workgroup's
-// load_agent without an L2 writeback / invalidate.
+// Publication of the routing scores from the gate workgroups to the last
+// arrival (route_decode_kernel).  The producers store with agent-scope relaxed
+// atomics (store_agent), drain their vector-memory counter (vm_drain), meet at
+// a barrier, and one thread adds to the counter; the last arrival reads with
+// agent-scope relaxed atomics (load_agent).  What makes this sufficient is how
+// gfx950 performs agent-scope atomics: a relaxed agent-scope load or store is
+// issued with the sc1 bit, which makes it act at the device coherence point
+// (the store writes through this XCD's L2, the load does not hit a stale L2
+// copy); s_waitcnt 0 returns only once the store has been acknowledged there;
+// and the agent-scope add is performed at that same point after the barrier.
+// An agent-scope release fence is the same wait plus an L2 writeback that only
+// non-atomic stores need, and the acquire an L2 invalidate that only
+// non-atomic loads need.  Written as a release/acquire add instead (the form
+// the HIP memory model guarantees), every gate workgroup's release writes back
+// its XCD's L2: measured +5 us per route launch at T = 1..4.
 __device__ __forceinline__ void store_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -187,6 +193,5 @@ __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0); }
-__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
 
 }  // namespace wz
