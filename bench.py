@@ -40,7 +40,8 @@ Printed JSON line (one):
   sparse_attn sparse attention at 64 heads of 512, topk 640: decode B = 1, 4, 8
               (µs, gathered-row GB/s) and prefill S = 512, 2048 (bf16 MFMA
               utilisation)
-  decode_stage 12 blocks of norms, projections and MoE in one graph per step
+  decode_stage 12 V4 blocks (fused norms, the five FP8 attention-side projections,
+              residuals, MoE) in one graph per step
 """
 
 from __future__ import annotations
@@ -395,21 +396,24 @@ def measure_grouped_fp4(dev, reps=10):
     return res
 
 
-STAGE_Q, STAGE_WIDE = 1024, 16384
-
-
 def stage_proj_bytes(T: int) -> int:
-    """FP8 projection bytes of one stage block: e4m3 weights + e8m0 128x128 scales +
-    bf16 activations in and out."""
+    """FP8 projection bytes of one V4 stage block (wq_a, wkv, wq_b, indexer wq_b, wo_b):
+    e4m3 weights + e8m0 128x128 scales + the activations in (e4m3 for the four fed by a
+    fused norm, bf16 for wo_b) and out (bf16), + wo_b's residual read."""
+    from wanferenz_amd import stage
+
     tot = 0
-    for Nn, K in ((STAGE_Q, D), (D, STAGE_Q), (D, D), (STAGE_WIDE, D)):
-        tot += Nn * K + ((Nn + 127) // 128) * ((K + 127) // 128) + 2 * T * (K + Nn)
-    return tot
+    shapes = stage.projection_shapes(D, **stage.V4_DIMS)
+    for j, (Nn, K) in enumerate(shapes):
+        a_in = (2 if j == len(shapes) - 1 else 1) * T * K + (T * K // 128)
+        tot += Nn * K + ((Nn + 127) // 128) * ((K + 127) // 128) + a_in + 2 * T * Nn
+    return tot + 2 * T * D
 
 
 def measure_stage(layers, dev, T=4, steps=256, warmup=16):
-    """The decode stage: every MoE layer as one block with its FP8 projections,
-    RMSNorms and residual adds, one hipGraph per step (wanferenz_amd/stage.py).
+    """The decode stage: every MoE layer as one V4 block with the five FP8 projections
+    of its attention side, fused norms and residual adds, one hipGraph per step
+    (wanferenz_amd/stage.py).
 
     A fresh x ~ N(0, 1) per step (seed = step), staged into the graph's input
     buffer by a device copy inside the timed region.  Bytes per step: each
@@ -420,8 +424,7 @@ def measure_stage(layers, dev, T=4, steps=256, warmup=16):
 
     from wanferenz_amd import stage, synth
 
-    blocks = [stage.synthetic_block(moe, D, STAGE_Q, STAGE_WIDE, seed=100 + l, device=dev)
-              for l, (moe, _) in enumerate(layers)]
+    blocks = [stage.synthetic_block(moe, D, seed=100 + l, device=dev) for l, (moe, _) in enumerate(layers)]
     st = stage.DecodeStage(blocks, T)
     xs = np.stack([synth.normal_bf16(synth.stream_key(s, synth.S_X), (T, D), 1.0) for s in range(steps)])
     xg = torch.from_numpy(xs.view(np.int16)).view(torch.bfloat16).to(dev)
@@ -451,9 +454,12 @@ def measure_stage(layers, dev, T=4, steps=256, warmup=16):
     gbs = step_bytes / (us * 1e-6) / 1e9
     del st, blocks
     torch.cuda.empty_cache()
-    return {"workload": f"decode stage: {nb} blocks x (RMSNorm, FP8 projections {STAGE_Q}x{D}, {D}x{STAGE_Q}, "
-                        f"{D}x{D}, {STAGE_WIDE}x{D}, residual, RMSNorm, MoE layer, residual), T={T}, one hipGraph "
-                        f"per step, fresh x per step",
+    dims = stage.V4_DIMS
+    return {"workload": f"decode stage: {nb} V4 blocks x (add + RMSNorm + act_quant, FP8 wq_a "
+                        f"{dims['q_lora']}x{D} and wkv {dims['head_dim']}x{D}, q_norm + act_quant, wq_b "
+                        f"{dims['q_width']}x{dims['q_lora']} and indexer wq_b {dims['idx_width']}x{dims['q_lora']}, "
+                        f"wo_b {D}x{dims['idx_width']} with the residual in its epilogue, RMSNorm, MoE layer), "
+                        f"T={T}, one hipGraph per step, fresh x per step",
             "T": T, "blocks": nb, "steps": steps, "us_per_step": round(us, 1),
             "us_per_block": round(us / nb, 2), "tokens_per_s": round(T * steps / secs, 1),
             "mean_distinct_experts": round(U_mean, 2), "bytes_per_step": int(step_bytes),

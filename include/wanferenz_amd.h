@@ -82,7 +82,7 @@ int wz_fp8_linear(const void* x_bf16, const void* w_e4m3, const void* w_s, void*
  * (act_quant + fp8_gemm, reference.py:117-146, 292-311); w_s [ceil(N/128), K/128]
  * float32 or e8m0 (w_scale_kind); act_scale_kind selects the activation scale rule
  * (WZ_SCALE_F32: amax/448, otherwise the power-of-two ue8m0 rule).  M <= 16 with
- * K in {1024, 2048, 4096} needs no workspace; otherwise ws must hold
+ * K in {1024, 2048, 4096, 8192} needs no workspace; otherwise ws must hold
  * wz_fp8_linear_workspace_bytes(M, K) bytes (the quantised x). */
 int wz_fp8_pack(const void* w_e4m3, int64_t N, int64_t K, void* packed, hipStream_t stream);
 size_t wz_fp8_linear_workspace_bytes(int64_t M, int64_t K);
@@ -94,13 +94,27 @@ int wz_fp8_linear_packed(const void* x_bf16, const void* w_packed, const void* w
  * pre-quantised activations a_e4m3 [M, K] with a_s [M, K/128] (act_scale_kind) —
  * fp8_gemm(a, a_s, b, b_s), reference.py:292-311, served the way the reference's
  * decode retile serves it (_fp8_gemm_fast, fp8_vector.py:289-297): M <= 16 with
- * K in {1024, 2048, 4096} runs the GEMV, otherwise the dense tile GEMM.  ws must
+ * K in {1024, 2048, 4096, 8192} runs the GEMV, otherwise the dense tile GEMM.  ws must
  * hold wz_fp8_gemm_packed_workspace_bytes(M, K, act_scale_kind) bytes (nonzero
  * only for e8m0 activation scales outside the GEMV). */
 size_t wz_fp8_gemm_packed_workspace_bytes(int64_t M, int64_t K, int act_scale_kind);
 int wz_fp8_gemm_packed(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
                        void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind, int w_scale_kind,
                        void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* The two entries above with the decoder block's residual step fused into the
+ * producer: y = residual + linear(..), the product rounded to bf16 and the fp32
+ * sum rounded once, as the bf16 tensor add x + attn(x) of Block.forward
+ * (architecture.py:853-874).  No counterpart in the reference's kernel set (its
+ * add is a separate torch op); for a decode stage that keeps the residual
+ * stream out of an extra pass.  residual [M, N] bf16 must not overlap y; the
+ * workspace rules are those of the entry without the residual. */
+int wz_fp8_linear_packed_add(const void* x_bf16, const void* w_packed, const void* w_s, const void* residual_bf16,
+                             void* y_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind, int w_scale_kind,
+                             void* ws, size_t ws_bytes, hipStream_t stream);
+int wz_fp8_gemm_packed_add(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
+                           const void* residual_bf16, void* c_bf16, int64_t M, int64_t N, int64_t K,
+                           int act_scale_kind, int w_scale_kind, void* ws, size_t ws_bytes, hipStream_t stream);
 
 /* fp4_gemm: C[M,N] bf16 = (a * a_s) @ (e2m1(w) * w_s)^T, weight scale e8m0 per 32 K.
  * Replaces fp4_gemm(a, a_s, b, b_s, scale_dtype) — reference.py:572-591 / torch_ops.py:102-108.
@@ -258,6 +272,14 @@ int wz_add_bf16(const void* a, const void* b, void* out, int64_t n, hipStream_t 
  * -> q e4m3 [T, D], s [T, D/128] (scale_kind as wz_act_quant_fp8). */
 int wz_rmsnorm_quant(const void* x_bf16, const float* weight, void* q_e4m3, void* s, int64_t T,
                      int64_t D, float eps, int scale_kind, hipStream_t stream);
+
+/* The residual step of the decoder block (h = x + b, Block.forward
+ * architecture.py:853-874, a bf16 tensor add) fused with the next RMSNorm and
+ * its act_quant (wz_rmsnorm_quant): sum_bf16 (optional, may be null) receives
+ * h, q / s the FP8 input of the next linear.  No counterpart in the reference's
+ * kernel set (three torch ops there). */
+int wz_add_rmsnorm_quant(const void* x_bf16, const void* b_bf16, const float* weight, void* sum_bf16,
+                         void* q_e4m3, void* s, int64_t T, int64_t D, float eps, int scale_kind, hipStream_t stream);
 
 /* Sparse attention over gathered KV rows — sparse_attn(q, kv, attn_sink, topk_idxs,
  * softmax_scale), torch_ops.py:114-146 / reference.py:314-418: blockwise online

@@ -422,6 +422,52 @@ def test_rms_norm_quant_is_norm_then_act_quant(gpu, scale_fmt, scale_dtype, T, D
     assert np.array_equal(got_s.reshape(rs.shape), rs)
 
 
+@pytest.mark.parametrize("T,D", [(4, 4096), (3, 1024), (16, 256)])
+def test_add_rms_norm_quant_is_add_then_norm_quant(gpu, T, D):
+    """The residual step fused into the norm: h equals the bf16 add of x and b bit for
+    bit (the oracle's fp32 sum rounded once), and (q, s) equal rms_norm_quant of h."""
+    from oracle.numerics import bf16_round
+
+    xb, bb = _x(61 + T, T, D, 2.0), _x(62 + T, T, D, 1.0)
+    wgt = synth.fill_f32_uniform(synth.stream_key(63, synth.S_NORM), 0, D, 0.5, 1.5)
+    x, b, w = bf16_tensor(xb, gpu).view(T, D), bf16_tensor(bb, gpu).view(T, D), f32_tensor(wgt, gpu)
+    h, q, s = kernels.add_rms_norm_quant(x, b, w, 1e-6)
+    q2, s2 = kernels.rms_norm_quant(h, w, 1e-6)
+    torch.cuda.synchronize()
+    ref = bf16_round((from_bf16_bits(xb) + from_bf16_bits(bb)).astype(np.float32)).reshape(T, D)
+    assert np.array_equal(f32_of_bf16(h), ref)
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8))
+    assert torch.equal(s.view(torch.uint8), s2.view(torch.uint8))
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 4096, 8192), (1, 1024, 4096), (16, 512, 1024), (40, 256, 1024),
+                                   (3, 128, 1536)])
+def test_fp8_linear_residual_epilogue(gpu, M, N, K):
+    """y = residual + linear(x): the GEMV epilogue (M <= 16, K in the GEMV set) and the
+    tile GEMM followed by an add both give bf16(bf16(linear(x)) + residual), i.e. the
+    packed linear's own output added to the residual as a bf16 tensor add, bit for bit;
+    the pre-quantised entry (gemm) does the same from rms_norm_quant-style input."""
+    from oracle.numerics import bf16_round
+
+    w, ws = __import__("wanferenz_amd.stage", fromlist=["synthetic_linear"]).synthetic_linear(
+        N, K, M * 7 + N + K, gpu, fp32_scales=False)
+    lin = kernels.PackedFp8Linear(w, ws, "ue8m0")
+    xb, rb = _x(M * 3 + K, M, K), _x(M * 5 + N, M, N, 4.0)
+    x, r = bf16_tensor(xb, gpu).view(M, K), bf16_tensor(rb, gpu).view(M, N)
+    plain = lin(x)
+    fused = lin(x, residual=r)
+    q, qs = kernels.act_quant(x, 128, "ue8m0", torch.float8_e8m0fnu)
+    plain_q = lin.gemm(q, qs)
+    fused_q = lin.gemm(q, qs, residual=r)
+    torch.cuda.synchronize()
+    ref = bf16_round((f32_of_bf16(plain) + from_bf16_bits(rb).reshape(M, N)).astype(np.float32))
+    assert np.array_equal(f32_of_bf16(fused), ref)
+    assert torch.equal(plain_q, plain)
+    assert torch.equal(fused_q, fused)
+    with pytest.raises(Exception):
+        lin(x, out=r, residual=r)  # the residual may not be the output
+
+
 @pytest.mark.parametrize("act_fmt", ["ue8m0", None])
 @pytest.mark.parametrize("G,N,K", [(6, 4096, 4096), (6, 4096, 2048), (1, 256, 1024), (40, 128, 512)])
 def test_grouped_fp4_gemm(gpu, act_fmt, G, N, K):

@@ -30,6 +30,8 @@ SIGNATURES = {
     "wz_fp8_linear_packed": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t, _P]),
     "wz_fp8_gemm_packed_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I]),
     "wz_fp8_gemm_packed": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t, _P]),
+    "wz_fp8_linear_packed_add": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t, _P]),
+    "wz_fp8_gemm_packed_add": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t, _P]),
     "wz_moe_workspace_bytes": (ctypes.c_size_t, [_P, _I64]),
     "wz_moe_packed_bytes": (ctypes.c_size_t, [_P, _I]),
     "wz_moe_pack": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),
@@ -43,6 +45,7 @@ SIGNATURES = {
     "wz_rmsnorm": (_I, [_P, _P, _P, _I64, _I64, _F, _P]),
     "wz_add_bf16": (_I, [_P, _P, _P, _I64, _P]),
     "wz_rmsnorm_quant": (_I, [_P, _P, _P, _P, _I64, _I64, _F, _I, _P]),
+    "wz_add_rmsnorm_quant": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _I, _P]),
     "wz_fp8_wire_pack": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "wz_sparse_attn_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "wz_sparse_attn": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P]),

@@ -74,8 +74,8 @@ template <int W, int NKB, int NB, int MINW, bool XF, bool QA, bool AP2, bool BP2
 __global__ __launch_bounds__(W * 64, MINW) void fp8_gemv_kernel(const void* __restrict__ x, const void* __restrict__ xs,
                                                          int a_kind, const uint8_t* __restrict__ wp,
                                                          const void* __restrict__ w_s, int w_kind,
-                                                         uint16_t* __restrict__ y, int M, int N, int K,
-                                                         int a_pow2i) {
+                                                         const uint16_t* __restrict__ res, uint16_t* __restrict__ y,
+                                                         int M, int N, int K, int a_pow2i) {
   __shared__ float red[2][W * 4 * kWave];
   // the wave index is uniform: tile addresses and weight scales stay scalar
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -148,7 +148,12 @@ __global__ __launch_bounds__(W * 64, MINW) void fp8_gemv_kernel(const void* __re
 #pragma unroll
         for (int w = 1; w < W; ++w) v += r[(w * 4 + i) * kWave + lane];
         const int row = g * 4 + i;
-        if (row < M) y[int64_t(row) * N + item * 16 + nl] = f32_to_bf16(v);
+        if (row < M) {
+          const int64_t o = int64_t(row) * N + item * 16 + nl;
+          // res: the residual stream, y = x + linear(..): the product rounded
+          // to bf16, then the fp32 sum rounded once (a bf16 tensor add)
+          y[o] = f32_to_bf16(res ? bf16_round(v) + __uint_as_float(uint32_t(res[o]) << 16) : v);
+        }
       }
     }
   };
@@ -195,7 +200,8 @@ static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t*
                        uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream);
 
 static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s,
-                         int w_kind, uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream);
+                         int w_kind, const uint16_t* res, uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2,
+                         hipStream_t stream);
 
 static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
@@ -217,10 +223,23 @@ extern "C" size_t wz_fp8_linear_workspace_bytes(int64_t M, int64_t K) {
   return align256(size_t(M) * size_t(K)) + size_t(M) * size_t(K / 128) * 4;
 }
 
-extern "C" int wz_fp8_linear_packed(const void* x_bf16, const void* w_packed, const void* w_s, void* y_bf16,
-                                    int64_t M, int64_t N, int64_t K, int act_scale_kind, int w_scale_kind,
-                                    void* ws, size_t ws_bytes, hipStream_t stream) {
-  using namespace wz;
+namespace wz {
+
+// The residual operand of the *_add entry points: y = residual + linear(..),
+// fused into the GEMV's epilogue; on the tile-GEMM path a bf16 add follows.
+static int add_residual(const uint16_t* res, uint16_t* y, int64_t M, int64_t N, int rc, hipStream_t stream) {
+  if (rc || !res) return rc;
+  return wz_add_bf16(res, y, y, M * N, stream);
+}
+
+static int overlap(const void* a, const void* b, size_t bytes) {
+  const char *pa = static_cast<const char*>(a), *pb = static_cast<const char*>(b);
+  return pa < pb + bytes && pb < pa + bytes;
+}
+
+static int linear_packed(const char* name, const void* x_bf16, const void* w_packed, const void* w_s,
+                         const uint16_t* res, void* y_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
+                         int w_scale_kind, void* ws, size_t ws_bytes, hipStream_t stream) {
   if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 128)
     return set_error(WZ_EINVAL, "fp8_linear_packed: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
                      (long long)K);
@@ -230,21 +249,45 @@ extern "C" int wz_fp8_linear_packed(const void* x_bf16, const void* w_packed, co
       (w_scale_kind != WZ_WSCALE_F32 && w_scale_kind != WZ_WSCALE_E8M0))
     return set_error(WZ_EINVAL, "fp8_linear_packed: bad scale kinds %d/%d", act_scale_kind, w_scale_kind);
   if (M == 0) return WZ_OK;
-  if (!x_bf16 || !w_packed || !w_s || !y_bf16) return set_error(WZ_EINVAL, "fp8_linear_packed: null pointer");
+  if (!x_bf16 || !w_packed || !w_s || !y_bf16) return set_error(WZ_EINVAL, "%s: null pointer", name);
+  if (res && overlap(res, y_bf16, size_t(M) * size_t(N) * 2))
+    return set_error(WZ_EINVAL, "%s: the residual and the output overlap", name);
   const bool pow2 = act_scale_kind != WZ_SCALE_F32;
+  uint16_t* y = static_cast<uint16_t*>(y_bf16);
   if (M <= kGvMaxM && gemv_shape_ok(K))
-    return gemv_dispatch(false, x_bf16, nullptr, 0, static_cast<const uint8_t*>(w_packed), w_s, w_scale_kind,
-                         static_cast<uint16_t*>(y_bf16), M, N, K, pow2, stream);
+    return gemv_dispatch(false, x_bf16, nullptr, 0, static_cast<const uint8_t*>(w_packed), w_s, w_scale_kind, res, y,
+                         M, N, K, pow2, stream);
   const size_t need = wz_fp8_linear_workspace_bytes(M, K);
   if (!ws || ws_bytes < need)
-    return set_error(WZ_ESPACE, "fp8_linear_packed: workspace of %zu bytes needed for M=%lld K=%lld, got %zu", need,
+    return set_error(WZ_ESPACE, "%s: workspace of %zu bytes needed for M=%lld K=%lld, got %zu", name, need,
                      (long long)M, (long long)K, ws_bytes);
   uint8_t* xq = static_cast<uint8_t*>(ws);
   float* xs = reinterpret_cast<float*>(xq + align256(size_t(M) * size_t(K)));
   const int qkind = pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
   if (int rc = launch_act_quant(x_bf16, M, K, xq, xs, qkind, stream)) return rc;
-  return launch_dense_fp8(static_cast<const uint8_t*>(w_packed), w_s, w_scale_kind, xq, xs, pow2,
-                          static_cast<uint16_t*>(y_bf16), M, N, K, stream);
+  return add_residual(res, y, M, N,
+                      launch_dense_fp8(static_cast<const uint8_t*>(w_packed), w_s, w_scale_kind, xq, xs, pow2, y, M,
+                                       N, K, stream),
+                      stream);
+}
+
+}  // namespace wz
+
+extern "C" int wz_fp8_linear_packed(const void* x_bf16, const void* w_packed, const void* w_s, void* y_bf16,
+                                    int64_t M, int64_t N, int64_t K, int act_scale_kind, int w_scale_kind,
+                                    void* ws, size_t ws_bytes, hipStream_t stream) {
+  return wz::linear_packed("fp8_linear_packed", x_bf16, w_packed, w_s, nullptr, y_bf16, M, N, K, act_scale_kind,
+                           w_scale_kind, ws, ws_bytes, stream);
+}
+
+extern "C" int wz_fp8_linear_packed_add(const void* x_bf16, const void* w_packed, const void* w_s,
+                                        const void* residual_bf16, void* y_bf16, int64_t M, int64_t N, int64_t K,
+                                        int act_scale_kind, int w_scale_kind, void* ws, size_t ws_bytes,
+                                        hipStream_t stream) {
+  if (!residual_bf16) return wz::set_error(WZ_EINVAL, "fp8_linear_packed_add: null residual");
+  return wz::linear_packed("fp8_linear_packed_add", x_bf16, w_packed, w_s,
+                           static_cast<const uint16_t*>(residual_bf16), y_bf16, M, N, K, act_scale_kind,
+                           w_scale_kind, ws, ws_bytes, stream);
 }
 
 namespace wz {
@@ -258,7 +301,7 @@ __global__ void e8m0_to_f32_kernel(const uint8_t* __restrict__ src, float* __res
 // LDS decide), asked once.  The grid is that many per CU, or one per tile.
 template <int W, int NKB, int NB, int MINW, bool XF, bool QA, bool AP2, bool BP2>
 static int launch_gemv_k(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
-                         uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+                         const uint16_t* res, uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
   static const int per_cu = [] {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fp8_gemv_kernel<W, NKB, NB, MINW, XF, QA, AP2, BP2>, W * 64, 0) !=
@@ -269,26 +312,28 @@ static int launch_gemv_k(const void* x, const void* xs, int a_kind, const uint8_
   }();
   const dim3 grid(unsigned(std::min<int64_t>(N / 16, int64_t(per_cu) * cu_count())));
   WZ_LAUNCH("fp8_gemv", stream, (fp8_gemv_kernel<W, NKB, NB, MINW, XF, QA, AP2, BP2>), grid, dim3(W * 64), 0, x, xs, a_kind,
-            w, w_s, w_kind, y, int(M), int(N), int(K), AP2 ? 1 : 0);
+            w, w_s, w_kind, res, y, int(M), int(N), int(K), AP2 ? 1 : 0);
   return check_launch("fp8_gemv");
 }
 
 template <int W, int NKB, int NB, int MINW, bool XF, bool QA>
 static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
-                       uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream) {
+                       const uint16_t* res, uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2,
+                       hipStream_t stream) {
   const bool bp = w_kind == WZ_WSCALE_E8M0;
   if (pow2)
-    return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, true>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, stream)
-              : launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, false>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, stream);
-  return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, true>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, stream)
-            : launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, false>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, stream);
+    return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, true>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, stream)
+              : launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, false>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, stream);
+  return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, true>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, stream)
+            : launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, false>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, stream);
 }
 
 static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s,
-                         int w_kind, uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream) {
+                         int w_kind, const uint16_t* res, uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2,
+                         hipStream_t stream) {
 #define WZ_GV(...)                                                                                          \
-  return qa ? launch_gemv<__VA_ARGS__, true>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, pow2, stream)          \
-            : launch_gemv<__VA_ARGS__, false>(x, xs, a_kind, w, w_s, w_kind, y, M, N, K, pow2, stream)
+  return qa ? launch_gemv<__VA_ARGS__, true>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, pow2, stream)          \
+            : launch_gemv<__VA_ARGS__, false>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, pow2, stream)
   switch (K) {
     case 1024: WZ_GV(WZ_GV_K1024);
     case 2048: WZ_GV(WZ_GV_K2048);
@@ -308,30 +353,31 @@ extern "C" size_t wz_fp8_gemm_packed_workspace_bytes(int64_t M, int64_t K, int a
   return act_scale_kind == WZ_SCALE_UE8M0 ? size_t(M) * size_t(K / 128) * 4 : 0;
 }
 
-extern "C" int wz_fp8_gemm_packed(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
-                                  void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
-                                  int w_scale_kind, void* ws, size_t ws_bytes, hipStream_t stream) {
-  using namespace wz;
+namespace wz {
+
+static int gemm_packed(const char* name, const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
+                       const uint16_t* res, void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
+                       int w_scale_kind, void* ws, size_t ws_bytes, hipStream_t stream) {
   if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 128)
-    return set_error(WZ_EINVAL, "fp8_gemm_packed: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
-                     (long long)K);
-  if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
-    return set_error(WZ_EINVAL, "fp8_gemm_packed: dimension too large");
+    return set_error(WZ_EINVAL, "%s: bad shape M=%lld N=%lld K=%lld", name, (long long)M, (long long)N, (long long)K);
+  if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30)) return set_error(WZ_EINVAL, "%s: dimension too large", name);
   if (act_scale_kind < WZ_SCALE_F32 || act_scale_kind > WZ_SCALE_UE8M0_F32 ||
       (w_scale_kind != WZ_WSCALE_F32 && w_scale_kind != WZ_WSCALE_E8M0))
-    return set_error(WZ_EINVAL, "fp8_gemm_packed: bad scale kinds %d/%d", act_scale_kind, w_scale_kind);
+    return set_error(WZ_EINVAL, "%s: bad scale kinds %d/%d", name, act_scale_kind, w_scale_kind);
   if (M == 0) return WZ_OK;
-  if (!a_e4m3 || !a_s || !w_packed || !w_s || !c_bf16) return set_error(WZ_EINVAL, "fp8_gemm_packed: null pointer");
+  if (!a_e4m3 || !a_s || !w_packed || !w_s || !c_bf16) return set_error(WZ_EINVAL, "%s: null pointer", name);
+  if (res && overlap(res, c_bf16, size_t(M) * size_t(N) * 2))
+    return set_error(WZ_EINVAL, "%s: the residual and the output overlap", name);
   const bool pow2 = act_scale_kind != WZ_SCALE_F32;
   const uint8_t* w = static_cast<const uint8_t*>(w_packed);
   uint16_t* c = static_cast<uint16_t*>(c_bf16);
   if (M <= kGvMaxM && gemv_shape_ok(K))
-    return gemv_dispatch(true, a_e4m3, a_s, act_scale_kind, w, w_s, w_scale_kind, c, M, N, K, pow2, stream);
+    return gemv_dispatch(true, a_e4m3, a_s, act_scale_kind, w, w_s, w_scale_kind, res, c, M, N, K, pow2, stream);
   const float* xs = static_cast<const float*>(a_s);
   if (act_scale_kind == WZ_SCALE_UE8M0) {
     const size_t need = wz_fp8_gemm_packed_workspace_bytes(M, K, act_scale_kind);
     if (!ws || ws_bytes < need)
-      return set_error(WZ_ESPACE, "fp8_gemm_packed: workspace of %zu bytes needed for M=%lld K=%lld, got %zu", need,
+      return set_error(WZ_ESPACE, "%s: workspace of %zu bytes needed for M=%lld K=%lld, got %zu", name, need,
                        (long long)M, (long long)K, ws_bytes);
     const int64_t n = M * (K / 128);
     WZ_LAUNCH("e8m0_to_f32", stream, e8m0_to_f32_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
@@ -339,5 +385,27 @@ extern "C" int wz_fp8_gemm_packed(const void* a_e4m3, const void* a_s, const voi
     if (int rc = check_launch("fp8_gemm_packed scales")) return rc;
     xs = static_cast<const float*>(ws);
   }
-  return launch_dense_fp8(w, w_s, w_scale_kind, static_cast<const uint8_t*>(a_e4m3), xs, pow2, c, M, N, K, stream);
+  return add_residual(
+      res, c, M, N,
+      launch_dense_fp8(w, w_s, w_scale_kind, static_cast<const uint8_t*>(a_e4m3), xs, pow2, c, M, N, K, stream),
+      stream);
+}
+
+}  // namespace wz
+
+extern "C" int wz_fp8_gemm_packed(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
+                                  void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
+                                  int w_scale_kind, void* ws, size_t ws_bytes, hipStream_t stream) {
+  return wz::gemm_packed("fp8_gemm_packed", a_e4m3, a_s, w_packed, w_s, nullptr, c_bf16, M, N, K, act_scale_kind,
+                         w_scale_kind, ws, ws_bytes, stream);
+}
+
+extern "C" int wz_fp8_gemm_packed_add(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
+                                      const void* residual_bf16, void* c_bf16, int64_t M, int64_t N, int64_t K,
+                                      int act_scale_kind, int w_scale_kind, void* ws, size_t ws_bytes,
+                                      hipStream_t stream) {
+  if (!residual_bf16) return wz::set_error(WZ_EINVAL, "fp8_gemm_packed_add: null residual");
+  return wz::gemm_packed("fp8_gemm_packed_add", a_e4m3, a_s, w_packed, w_s,
+                         static_cast<const uint16_t*>(residual_bf16), c_bf16, M, N, K, act_scale_kind, w_scale_kind,
+                         ws, ws_bytes, stream);
 }

@@ -66,10 +66,15 @@ __global__ __launch_bounds__(256) void add_bf16_kernel(const uint16_t* __restric
 // FP8 linear): the bf16-rounded normalised row is quantised per 128 columns
 // (torch_ops.py:33-49) without a round trip through memory.  Same arithmetic
 // as rmsnorm_kernel followed by act_quant_kernel.  The row stays in registers:
-// D <= 256 threads x 8 x kRqChunks.
+// D <= 256 threads x 8 x kRqChunks.  With b, the row is first the residual
+// step x + b (fp32 sum rounded once to bf16, add_bf16_kernel's arithmetic),
+// which is also written to sum (when given): the block's residual add fused
+// into the next norm.
 constexpr int kRqChunks = 4;
 
 __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ b,
+                                                            uint16_t* __restrict__ sum,
                                                             const float* __restrict__ w,
                                                             uint8_t* __restrict__ q, void* __restrict__ s,
                                                             int D, float eps, int kind) {
@@ -83,6 +88,16 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
   for (int j = 0; j < kRqChunks; ++j) {
     const int c = threadIdx.x + 256 * j;
     v[j] = c < D / 8 ? load16(xr + c * 8) : v4i{0, 0, 0, 0};
+    if (b && c < D / 8) {
+      const v4i vb = load16(b + row * D + c * 8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = bf16lo(uint32_t(v[j][i])) + bf16lo(uint32_t(vb[i]));
+        const float hi = bf16hi(uint32_t(v[j][i])) + bf16hi(uint32_t(vb[i]));
+        v[j][i] = int(uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16));
+      }
+      if (sum) *reinterpret_cast<v4i*>(sum + row * D + c * 8) = v[j];
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float a = bf16lo(uint32_t(v[j][i])), b = bf16hi(uint32_t(v[j][i]));
@@ -204,8 +219,26 @@ extern "C" int wz_rmsnorm_quant(const void* x_bf16, const float* weight, void* q
   if (T == 0) return WZ_OK;
   if (!x_bf16 || !weight || !q_e4m3 || !s) return set_error(WZ_EINVAL, "rmsnorm_quant: null pointer");
   WZ_LAUNCH("rmsnorm_quant", stream, rmsnorm_quant_kernel, dim3(unsigned(T)), dim3(256), 0,
-            static_cast<const uint16_t*>(x_bf16), weight, static_cast<uint8_t*>(q_e4m3), s, int(D), eps, scale_kind);
+            static_cast<const uint16_t*>(x_bf16), nullptr, nullptr, weight, static_cast<uint8_t*>(q_e4m3), s, int(D),
+            eps, scale_kind);
   return check_launch("rmsnorm_quant");
+}
+
+extern "C" int wz_add_rmsnorm_quant(const void* x_bf16, const void* b_bf16, const float* weight, void* sum_bf16,
+                                    void* q_e4m3, void* s, int64_t T, int64_t D, float eps, int scale_kind,
+                                    hipStream_t stream) {
+  using namespace wz;
+  if (T < 0 || D <= 0 || D % 128 || D > 256 * 8 * kRqChunks)
+    return set_error(WZ_EINVAL, "add_rmsnorm_quant: D=%lld must be a multiple of 128 up to %d", (long long)D,
+                     256 * 8 * kRqChunks);
+  if (scale_kind < WZ_SCALE_F32 || scale_kind > WZ_SCALE_UE8M0_F32)
+    return set_error(WZ_EINVAL, "add_rmsnorm_quant: unknown scale kind %d", scale_kind);
+  if (T == 0) return WZ_OK;
+  if (!x_bf16 || !b_bf16 || !weight || !q_e4m3 || !s) return set_error(WZ_EINVAL, "add_rmsnorm_quant: null pointer");
+  WZ_LAUNCH("add_rmsnorm_quant", stream, rmsnorm_quant_kernel, dim3(unsigned(T)), dim3(256), 0,
+            static_cast<const uint16_t*>(x_bf16), static_cast<const uint16_t*>(b_bf16),
+            static_cast<uint16_t*>(sum_bf16), weight, static_cast<uint8_t*>(q_e4m3), s, int(D), eps, scale_kind);
+  return check_launch("add_rmsnorm_quant");
 }
 
 extern "C" int wz_fp8_wire_pack(const void* x_bf16, void* q_e4m3, void* scale_bf16, int64_t M, int64_t D,

@@ -252,18 +252,55 @@ class PackedFp8Linear:
             self._ws = torch.empty(need, dtype=torch.uint8, device=self.packed.device)
         return self
 
-    def __call__(self, x, out=None):
+    def _out(self, lead, M, out, residual, device):
+        y = torch.empty(*lead, self.N, dtype=torch.bfloat16, device=device) if out is None else out
+        if residual is not None:
+            assert residual.is_contiguous() and residual.dtype == torch.bfloat16
+            if residual.numel() != M * self.N:
+                raise ValueError(f"PackedFp8Linear: residual has {residual.numel()} elements for [{M}, {self.N}]")
+        return y
+
+    def __call__(self, x, out=None, residual=None):
+        """linear(x, weight); with ``residual``, residual + linear(x, weight) in one
+        launch (the block's bf16 residual add fused into the epilogue)."""
         assert x.is_contiguous() and x.size(-1) == self.K
         _require_cuda(x)
         if x.dtype != torch.bfloat16:
             raise TypeError(f"PackedFp8Linear: bf16 input expected, got {x.dtype}")
         M = x.numel() // self.K
         self.reserve(M)
-        y = torch.empty(*x.size()[:-1], self.N, dtype=torch.bfloat16, device=x.device) if out is None else out
+        y = self._out(x.size()[:-1], M, out, residual, x.device)
         ws = self._ws
-        N.call("wz_fp8_linear_packed", N.ptr(x), N.ptr(self.packed), N.ptr(self.scale), N.ptr(y), M, self.N,
-               self.K, self.act_kind, self.w_kind, N.ptr(ws), 0 if ws is None else ws.numel(),
-               N.stream_handle(x.device))
+        tail = (M, self.N, self.K, self.act_kind, self.w_kind, N.ptr(ws), 0 if ws is None else ws.numel(),
+                N.stream_handle(x.device))
+        if residual is None:
+            N.call("wz_fp8_linear_packed", N.ptr(x), N.ptr(self.packed), N.ptr(self.scale), N.ptr(y), *tail)
+        else:
+            N.call("wz_fp8_linear_packed_add", N.ptr(x), N.ptr(self.packed), N.ptr(self.scale), N.ptr(residual),
+                   N.ptr(y), *tail)
+        return y
+
+    def gemm(self, q, q_s, out=None, residual=None):
+        """fp8_gemm(q, q_s, weight, scale) from pre-quantised activations (e4m3 [..., K]
+        with scales [..., K/128], e.g. from rms_norm_quant), optionally + residual."""
+        assert q.is_contiguous() and q_s.is_contiguous() and q.size(-1) == self.K
+        _require_cuda(q, q_s)
+        M = q.numel() // self.K
+        kind = _scale_kind_of(q_s)
+        need = int(N.lib().wz_fp8_gemm_packed_workspace_bytes(M, self.K, kind))
+        if need and (self._ws is None or self._ws.numel() < need):
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("PackedFp8Linear.gemm: workspace needed during a graph capture")
+            self._ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+        y = self._out(q.size()[:-1], M, out, residual, q.device)
+        ws = self._ws
+        tail = (M, self.N, self.K, kind, self.w_kind, N.ptr(ws), 0 if ws is None else ws.numel(),
+                N.stream_handle(q.device))
+        if residual is None:
+            N.call("wz_fp8_gemm_packed", N.ptr(q), N.ptr(q_s), N.ptr(self.packed), N.ptr(self.scale), N.ptr(y), *tail)
+        else:
+            N.call("wz_fp8_gemm_packed_add", N.ptr(q), N.ptr(q_s), N.ptr(self.packed), N.ptr(self.scale),
+                   N.ptr(residual), N.ptr(y), *tail)
         return y
 
 
@@ -283,21 +320,47 @@ def rms_norm(x, weight, eps=1e-6, out=None):
     return y
 
 
-def rms_norm_quant(x, weight, eps=1e-6, scale_fmt="ue8m0", scale_dtype=_E8M0):
+def _norm_quant_out(x, scale_fmt, scale_dtype, out):
+    D = x.size(-1)
+    kind = _act_kind(scale_fmt, scale_dtype)
+    if out is None:
+        q = torch.empty(x.shape, dtype=_E4M3, device=x.device)
+        s = torch.empty(*x.shape[:-1], D // 128, dtype=_E8M0 if kind == N.WZ_SCALE_UE8M0 else torch.float32,
+                        device=x.device)
+    else:
+        q, s = out
+    return kind, q, s
+
+
+def rms_norm_quant(x, weight, eps=1e-6, scale_fmt="ue8m0", scale_dtype=_E8M0, out=None):
     """act_quant(rms_norm(x, weight, eps)) in one pass (architecture.py:217-230 then
-    reference.py:117-146): -> (e4m3 [..., D], scales [..., D/128])."""
+    reference.py:117-146): -> (e4m3 [..., D], scales [..., D/128]); ``out``: (q, s)
+    buffers to fill."""
     assert x.is_contiguous() and weight.is_contiguous()
     _require_cuda(x, weight)
     if x.dtype != torch.bfloat16 or weight.dtype != torch.float32:
         raise TypeError(f"rms_norm_quant: x must be bf16 and weight float32 (got {x.dtype}, {weight.dtype})")
     D = x.size(-1)
-    kind = _act_kind(scale_fmt, scale_dtype)
-    q = torch.empty(x.shape, dtype=_E4M3, device=x.device)
-    s = torch.empty(*x.shape[:-1], D // 128, dtype=_E8M0 if kind == N.WZ_SCALE_UE8M0 else torch.float32,
-                    device=x.device)
+    kind, q, s = _norm_quant_out(x, scale_fmt, scale_dtype, out)
     N.call("wz_rmsnorm_quant", N.ptr(x), N.ptr(weight), N.ptr(q), N.ptr(s), x.numel() // D, D, float(eps), kind,
            N.stream_handle(x.device))
     return q, s
+
+
+def add_rms_norm_quant(x, b, weight, eps=1e-6, scale_fmt="ue8m0", scale_dtype=_E8M0, sum_out=None, out=None):
+    """The residual step h = x + b (bf16 add) fused with rms_norm_quant(h, weight):
+    -> (h, e4m3 [..., D], scales [..., D/128]).  h is written to ``sum_out`` (a new
+    tensor when None)."""
+    assert x.is_contiguous() and b.is_contiguous() and weight.is_contiguous() and x.shape == b.shape
+    _require_cuda(x, b, weight)
+    if x.dtype != torch.bfloat16 or b.dtype != torch.bfloat16 or weight.dtype != torch.float32:
+        raise TypeError("add_rms_norm_quant: x and b must be bf16 and weight float32")
+    D = x.size(-1)
+    h = torch.empty_like(x) if sum_out is None else sum_out
+    kind, q, s = _norm_quant_out(x, scale_fmt, scale_dtype, out)
+    N.call("wz_add_rmsnorm_quant", N.ptr(x), N.ptr(b), N.ptr(weight), N.ptr(h), N.ptr(q), N.ptr(s),
+           x.numel() // D, D, float(eps), kind, N.stream_handle(x.device))
+    return h, q, s
 
 
 def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale, workspace=None):

@@ -1,27 +1,35 @@
-"""A decode stage: blocks of FP8 projections + RMSNorm + residual around the MoE layer.
+"""A decode stage: V4 decoder blocks' FP8 projections, norms and residuals around the MoE.
 
 The step on either side of the MoE in a decoder block (Block.forward,
-architecture.py:853-874): the pre-norms (RMSNorm, :217-230), the FP8 linears of
-the attention side (linear(), :121-132) and the MoE (:777-794), chained over a
+architecture.py:853-874) at the V4-Flash projection shapes, chained over a
 stack of blocks and captured as one HIP graph per step, the way the reference
-captures its decode step (decoder.py:465-488).  Two simplifications keep this
-to the kernels on the measured path: the hyper-connection mixing
-(hc_pre / hc_post, :821-850) is a plain residual add, and attention itself
-(sparse_attn) is not run — its projections are, with their outputs feeding the
-chain where the shapes allow.
+captures its decode step (decoder.py:465-488).  The attention side runs every
+FP8 projection of Attention.forward (architecture.py:611-672) and of the
+indexer on its real input: wq_a and wkv on the normed hidden state, q_norm,
+then wq_b and the indexer's wq_b on the normed query latent (fp8_vector.py:505-513
+lists the same five shapes).  Attention itself, its rotary embedding and the
+bf16 grouped wo_a product are not run (sparse_attn is measured on its own), so
+the input of wo_b — [T, n_groups * o_lora_rank] — is taken from the indexer's
+query projection, which has that width at V4 (8192).  The hyper-connection
+mixing (hc_pre / hc_post, :821-850) is a plain residual add.
 
 Per block, with h the [T, D] residual stream (bf16):
 
-    a = rms_norm(h, attn_norm)
-    u = P_down(a)            N x K = q_dim x D     (e.g. 1024 x 4096)
-    v = P_up(u)              D x q_dim             (4096 x 1024)
-    w = P_sq(v)              D x D                 (4096 x 4096)
-    z = P_wide(a)            wide x D              (16384 x 4096; consumed by attention)
-    h = h + w
-    m = rms_norm(h, ffn_norm)
-    h = h + moe(m)
+    (h, hq) = add_rms_norm_quant(h, e_prev, attn_norm)   # block 0: rms_norm_quant(h)
+    qa = wq_a(hq)                 q_lora x D        (1024 x 4096)
+    kv = wkv(hq)                  head_dim x D      (512 x 4096)
+    qq = rms_norm_quant(qa, q_norm)
+    q  = wq_b(qq)                 heads*hd x q_lora (32768 x 1024)
+    iq = idx_wq_b(qq)             idx x q_lora      (8192 x 1024)
+    h1 = h + wo_b(iq)             D x o             (4096 x 8192), residual in the epilogue
+    m  = rms_norm(h1, ffn_norm)
+    e  = moe(m)
+    (after the last block: h = h1 + e)
 
-Every buffer is allocated once, so a step is a fixed sequence of launches.
+Each FP8 input is produced quantised by the norm that precedes it
+(rms_norm_quant), the residual add of the attention side sits in wo_b's
+epilogue and that of the MoE side in the next block's norm.  Every buffer is
+allocated once, so a step is a fixed sequence of launches.
 """
 
 from __future__ import annotations
@@ -34,16 +42,25 @@ import torch
 from . import kernels
 from . import synth
 
+# V4-Flash attention-side widths (architecture.py ModelArgs): q_lora_rank,
+# head_dim, n_heads * head_dim, index_n_heads * index_head_dim.
+V4_DIMS = dict(q_lora=1024, head_dim=512, q_width=32768, idx_width=8192)
+
 
 @dataclass
 class StageBlock:
-    attn_norm: torch.Tensor          # fp32 [D]
-    ffn_norm: torch.Tensor           # fp32 [D]
-    p_down: kernels.PackedFp8Linear  # [q, D]
-    p_up: kernels.PackedFp8Linear    # [D, q]
-    p_sq: kernels.PackedFp8Linear    # [D, D]
-    p_wide: kernels.PackedFp8Linear  # [wide, D]
-    moe: object                      # HipMoE
+    attn_norm: torch.Tensor              # fp32 [D]
+    q_norm: torch.Tensor                 # fp32 [q_lora]
+    ffn_norm: torch.Tensor               # fp32 [D]
+    wq_a: kernels.PackedFp8Linear        # [q_lora, D]
+    wkv: kernels.PackedFp8Linear         # [head_dim, D]
+    wq_b: kernels.PackedFp8Linear        # [q_width, q_lora]
+    idx_wq_b: kernels.PackedFp8Linear    # [idx_width, q_lora]
+    wo_b: kernels.PackedFp8Linear        # [D, idx_width]
+    moe: object                          # HipMoE
+
+    def projections(self):
+        return (self.wq_a, self.wkv, self.wq_b, self.idx_wq_b, self.wo_b)
 
 
 def synthetic_linear(N: int, K: int, seed: int, device, fp32_scales: bool = True):
@@ -62,20 +79,31 @@ def synthetic_linear(N: int, K: int, seed: int, device, fp32_scales: bool = True
     return w.view(torch.float8_e4m3fn), s
 
 
-def synthetic_block(moe, D: int, q_dim: int, wide: int, seed: int, device) -> StageBlock:
+def projection_shapes(D: int, q_lora: int, head_dim: int, q_width: int, idx_width: int):
+    """(N, K) of wq_a, wkv, wq_b, idx_wq_b, wo_b."""
+    return ((q_lora, D), (head_dim, D), (q_width, q_lora), (idx_width, q_lora), (D, idx_width))
+
+
+def synthetic_block(moe, D: int, seed: int, device, q_lora: int = 1024, head_dim: int = 512,
+                    q_width: int = 32768, idx_width: int = 8192) -> StageBlock:
     """Projections with e8m0 block scales (the model's FP8 weights carry e8m0 scales,
     architecture.py:158-168); 2^-15..2^-11 keeps a K = 4096 product of uniform e4m3
     codes O(1), so the residual stream keeps its scale block after block."""
     lins = []
-    for j, (N, K) in enumerate(((q_dim, D), (D, q_dim), (D, D), (wide, D))):
+    for j, (N, K) in enumerate(projection_shapes(D, q_lora, head_dim, q_width, idx_width)):
         w, s = synthetic_linear(N, K, seed * 16 + j, device, fp32_scales=False)
         lins.append(kernels.PackedFp8Linear(w, s, "ue8m0"))
     norms = []
-    for j in range(2):
-        t = torch.empty(D, dtype=torch.float32, device=device)
+    for j, n in enumerate((D, q_lora, D)):
+        t = torch.empty(n, dtype=torch.float32, device=device)
         synth.device_fill(t, synth.stream_key(seed * 16 + 8 + j, synth.S_NORM), synth.FILL_F32_UNIFORM, 0.5, 1.5)
         norms.append(t)
-    return StageBlock(norms[0], norms[1], *lins, moe)
+    return StageBlock(norms[0], norms[1], norms[2], *lins, moe)
+
+
+def projection_bytes(b: StageBlock) -> int:
+    """Weight bytes (e4m3 codes + one byte per 128 x 128 block scale) of a block's projections."""
+    return sum(l.N * l.K + ((l.N + 127) // 128) * ((l.K + 127) // 128) for l in b.projections())
 
 
 class DecodeStage:
@@ -86,44 +114,63 @@ class DecodeStage:
         self.blocks: List[StageBlock] = list(blocks)
         self.T, self.eps = T, eps
         b0 = self.blocks[0]
-        D, dev = b0.p_sq.N, b0.p_sq.packed.device
+        D, dev = b0.wo_b.N, b0.wo_b.packed.device
         self.D = D
         bf = dict(dtype=torch.bfloat16, device=dev)
+
+        def q8(n):
+            return (torch.empty(T, n, dtype=kernels._E4M3, device=dev),
+                    torch.empty(T, n // 128, dtype=kernels._E8M0, device=dev))
+
         self.x_in = torch.zeros(T, D, **bf)
-        self.h = torch.zeros(T, D, **bf)
-        self.a = torch.empty(T, D, **bf)
-        self.u = torch.empty(T, b0.p_down.N, **bf)
-        self.v = torch.empty(T, D, **bf)
-        self.w = torch.empty(T, D, **bf)
-        self.z = torch.empty(T, b0.p_wide.N, **bf)
+        # the residual stream: each new value goes to the next of three buffers, so
+        # no kernel writes the buffer it reads
+        self.h = [torch.zeros(T, D, **bf) for _ in range(3)]
+        self.hq = q8(D)
+        self.qa = torch.empty(T, b0.wq_a.N, **bf)
+        self.kv = torch.empty(T, b0.wkv.N, **bf)
+        self.qq = q8(b0.wq_a.N)
+        self.q = torch.empty(T, b0.wq_b.N, **bf)
+        self.iq = torch.empty(T, b0.idx_wq_b.N, **bf)
         self.m = torch.empty(T, D, **bf)
         self.e = torch.empty(T, D, **bf)
+        self.y = torch.empty(T, D, **bf)
         for b in self.blocks:
-            for lin in (b.p_down, b.p_up, b.p_sq, b.p_wide):
+            for lin in b.projections():
                 lin.reserve(T)
             b.moe.reserve(T)
         self.graph = None
 
     def _run(self, routing=None, trace=None):
-        T, eps = self.T, self.eps
-        self.h.copy_(self.x_in)
+        eps = self.eps
+        h = self.x_in
+        nxt = iter(self.h * (2 * len(self.blocks)))
         for i, b in enumerate(self.blocks):
-            h_in = None if trace is None else self.h.clone()
-            kernels.rms_norm(self.h, b.attn_norm, eps, out=self.a)
-            b.p_down(self.a, out=self.u)
-            b.p_up(self.u, out=self.v)
-            b.p_sq(self.v, out=self.w)
-            b.p_wide(self.a, out=self.z)
-            kernels.add(self.h, self.w, out=self.h)
-            h_mid = None if trace is None else self.h.clone()
-            kernels.rms_norm(self.h, b.ffn_norm, eps, out=self.m)
+            h_in, e_in = (None, None) if trace is None else (h.clone(), None if i == 0 else self.e.clone())
+            if i == 0:
+                kernels.rms_norm_quant(h, b.attn_norm, eps, out=self.hq)
+            else:
+                # the previous block's MoE residual, fused into this block's norm
+                hs = next(nxt)
+                kernels.add_rms_norm_quant(h, self.e, b.attn_norm, eps, sum_out=hs, out=self.hq)
+                h = hs
+            b.wq_a.gemm(*self.hq, out=self.qa)
+            b.wkv.gemm(*self.hq, out=self.kv)
+            kernels.rms_norm_quant(self.qa, b.q_norm, eps, out=self.qq)
+            b.wq_b.gemm(*self.qq, out=self.q)
+            b.idx_wq_b.gemm(*self.qq, out=self.iq)
+            h1 = next(nxt)
+            b.wo_b(self.iq, out=h1, residual=h)
+            kernels.rms_norm(h1, b.ffn_norm, eps, out=self.m)
             b.moe.forward(self.m, out=self.e, routing_out=None if routing is None else routing[i])
-            kernels.add(self.h, self.e, out=self.h)
             if trace is not None:
-                trace.append({"h_in": h_in, "a": self.a.clone(), "u": self.u.clone(), "v": self.v.clone(),
-                              "w": self.w.clone(), "z": self.z.clone(), "h_mid": h_mid, "m": self.m.clone(),
-                              "e": self.e.clone(), "h_out": self.h.clone()})
-        return self.h
+                trace.append({"h_in": h_in, "e_in": e_in, "h": h.clone(), "hq": self.hq[0].clone(),
+                              "hs": self.hq[1].clone(), "qa": self.qa.clone(), "kv": self.kv.clone(),
+                              "qq": self.qq[0].clone(), "qs": self.qq[1].clone(), "q": self.q.clone(),
+                              "iq": self.iq.clone(), "h1": h1.clone(), "m": self.m.clone(), "e": self.e.clone()})
+            h = h1
+        kernels.add(h, self.e, out=self.y)
+        return self.y
 
     def step(self, x: torch.Tensor, routing=None, trace=None) -> torch.Tensor:
         """One eager step.  ``routing``: optional per-block (weights [T, k] fp32,
@@ -148,4 +195,4 @@ class DecodeStage:
     def replay(self, x: torch.Tensor) -> torch.Tensor:
         self.x_in.copy_(x)
         self.graph.replay()
-        return self.h
+        return self.y
