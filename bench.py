@@ -456,8 +456,9 @@ def measure_stage(layers, dev, T=4, steps=256, warmup=16):
     torch.cuda.empty_cache()
     dims = stage.V4_DIMS
     return {"workload": f"decode stage: {nb} V4 blocks x (add + RMSNorm + act_quant, FP8 wq_a "
-                        f"{dims['q_lora']}x{D} and wkv {dims['head_dim']}x{D}, q_norm + act_quant, wq_b "
-                        f"{dims['q_width']}x{dims['q_lora']} and indexer wq_b {dims['idx_width']}x{dims['q_lora']}, "
+                        f"{dims['q_lora']}x{D} with wkv {dims['head_dim']}x{D} in one launch, q_norm + act_quant, "
+                        f"wq_b {dims['q_width']}x{dims['q_lora']} with indexer wq_b "
+                        f"{dims['idx_width']}x{dims['q_lora']} in one launch, "
                         f"wo_b {D}x{dims['idx_width']} with the residual in its epilogue, RMSNorm, MoE layer), "
                         f"T={T}, one hipGraph per step, fresh x per step",
             "T": T, "blocks": nb, "steps": steps, "us_per_step": round(us, 1),

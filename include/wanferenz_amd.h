@@ -116,6 +116,18 @@ int wz_fp8_gemm_packed_add(const void* a_e4m3, const void* a_s, const void* w_pa
                            const void* residual_bf16, void* c_bf16, int64_t M, int64_t N, int64_t K,
                            int act_scale_kind, int w_scale_kind, void* ws, size_t ws_bytes, hipStream_t stream);
 
+/* Two FP8 projections of the same quantised input in one launch, as the
+ * decoder block has them (wq_a and wkv on the normed hidden state, wq_b and the
+ * indexer's wq_b on the normed query latent, architecture.py:611-672): the
+ * weights stacked row-wise [W0; W1] (N = N0 + N1 rows, N0 % 128 == 0) and packed
+ * once (wz_fp8_pack), w_s their stacked block scales; c0 [M, N0] and c1 [M, N1]
+ * receive fp8_gemm(a, a_s, W0, s0) and fp8_gemm(a, a_s, W1, s1).  No counterpart
+ * in the reference's kernel set (two launches there).  Workspace rules of
+ * wz_fp8_gemm_packed. */
+int wz_fp8_gemm_packed_pair(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
+                            void* c0_bf16, int64_t N0, void* c1_bf16, int64_t M, int64_t N, int64_t K,
+                            int act_scale_kind, int w_scale_kind, void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* fp4_gemm: C[M,N] bf16 = (a * a_s) @ (e2m1(w) * w_s)^T, weight scale e8m0 per 32 K.
  * Replaces fp4_gemm(a, a_s, b, b_s, scale_dtype) — reference.py:572-591 / torch_ops.py:102-108.
  * a_e4m3 [M,K], a_s [M,K/128], w_fp4x2 [N,K/2], w_s_e8m0 [N,K/32]. */

@@ -468,6 +468,23 @@ def test_fp8_linear_residual_epilogue(gpu, M, N, K):
         lin(x, out=r, residual=r)  # the residual may not be the output
 
 
+@pytest.mark.parametrize("M,N0,N1,K", [(4, 1024, 512, 4096), (4, 32768, 8192, 1024), (1, 256, 128, 8192),
+                                        (24, 256, 384, 1024), (3, 128, 48, 256)])
+def test_fp8_pair_equals_two_linears(gpu, M, N0, N1, K):
+    """Two stacked projections in one launch give each projection's own output bit
+    for bit (GEMV path at M <= 16 and K in its set, the two tile GEMMs otherwise)."""
+    from wanferenz_amd import stage
+
+    w0, s0 = stage.synthetic_linear(N0, K, N0 + K, gpu, fp32_scales=False)
+    w1, s1 = stage.synthetic_linear(N1, K, N1 + K + 1, gpu, fp32_scales=False)
+    pair = kernels.PackedFp8Pair(w0, s0, w1, s1)
+    l0, l1 = kernels.PackedFp8Linear(w0, s0), kernels.PackedFp8Linear(w1, s1)
+    q, qs = kernels.act_quant(bf16_tensor(_x(M + K, M, K), gpu).view(M, K), 128, "ue8m0", torch.float8_e8m0fnu)
+    y0, y1 = pair.gemm(q, qs)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, l0.gemm(q, qs)) and torch.equal(y1, l1.gemm(q, qs))
+
+
 @pytest.mark.parametrize("act_fmt", ["ue8m0", None])
 @pytest.mark.parametrize("G,N,K", [(6, 4096, 4096), (6, 4096, 2048), (1, 256, 1024), (40, 128, 512)])
 def test_grouped_fp4_gemm(gpu, act_fmt, G, N, K):

@@ -32,6 +32,8 @@ SIGNATURES = {
     "wz_fp8_gemm_packed": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t, _P]),
     "wz_fp8_linear_packed_add": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t, _P]),
     "wz_fp8_gemm_packed_add": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t, _P]),
+    "wz_fp8_gemm_packed_pair": (_I, [_P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t,
+                                     _P]),
     "wz_moe_workspace_bytes": (ctypes.c_size_t, [_P, _I64]),
     "wz_moe_packed_bytes": (ctypes.c_size_t, [_P, _I]),
     "wz_moe_pack": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),

@@ -75,7 +75,8 @@ __global__ __launch_bounds__(W * 64, MINW) void fp8_gemv_kernel(const void* __re
                                                          int a_kind, const uint8_t* __restrict__ wp,
                                                          const void* __restrict__ w_s, int w_kind,
                                                          const uint16_t* __restrict__ res, uint16_t* __restrict__ y,
-                                                         int M, int N, int K, int a_pow2i) {
+                                                         uint16_t* __restrict__ y_hi, int n_split, int M, int N,
+                                                         int K, int a_pow2i) {
   __shared__ float red[2][W * 4 * kWave];
   // the wave index is uniform: tile addresses and weight scales stay scalar
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -148,11 +149,15 @@ __global__ __launch_bounds__(W * 64, MINW) void fp8_gemv_kernel(const void* __re
 #pragma unroll
         for (int w = 1; w < W; ++w) v += r[(w * 4 + i) * kWave + lane];
         const int row = g * 4 + i;
-        if (row < M) {
-          const int64_t o = int64_t(row) * N + item * 16 + nl;
+        const int col = item * 16 + nl;
+        if (row < M && col < n_split) {
+          const int64_t o = int64_t(row) * n_split + col;
           // res: the residual stream, y = x + linear(..): the product rounded
           // to bf16, then the fp32 sum rounded once (a bf16 tensor add)
           y[o] = f32_to_bf16(res ? bf16_round(v) + __uint_as_float(uint32_t(res[o]) << 16) : v);
+        } else if (row < M) {
+          // columns past n_split: the second of two stacked weights, its own buffer
+          y_hi[int64_t(row) * (N - n_split) + (col - n_split)] = f32_to_bf16(v);
         }
       }
     }
@@ -200,8 +205,8 @@ static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t*
                        uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream);
 
 static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s,
-                         int w_kind, const uint16_t* res, uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2,
-                         hipStream_t stream);
+                         int w_kind, const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M,
+                         int64_t N, int64_t K, bool pow2, hipStream_t stream);
 
 static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
@@ -256,7 +261,7 @@ static int linear_packed(const char* name, const void* x_bf16, const void* w_pac
   uint16_t* y = static_cast<uint16_t*>(y_bf16);
   if (M <= kGvMaxM && gemv_shape_ok(K))
     return gemv_dispatch(false, x_bf16, nullptr, 0, static_cast<const uint8_t*>(w_packed), w_s, w_scale_kind, res, y,
-                         M, N, K, pow2, stream);
+                         nullptr, N, M, N, K, pow2, stream);
   const size_t need = wz_fp8_linear_workspace_bytes(M, K);
   if (!ws || ws_bytes < need)
     return set_error(WZ_ESPACE, "%s: workspace of %zu bytes needed for M=%lld K=%lld, got %zu", name, need,
@@ -301,7 +306,8 @@ __global__ void e8m0_to_f32_kernel(const uint8_t* __restrict__ src, float* __res
 // LDS decide), asked once.  The grid is that many per CU, or one per tile.
 template <int W, int NKB, int NB, int MINW, bool XF, bool QA, bool AP2, bool BP2>
 static int launch_gemv_k(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
-                         const uint16_t* res, uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+                         const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
+                         int64_t K, hipStream_t stream) {
   static const int per_cu = [] {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fp8_gemv_kernel<W, NKB, NB, MINW, XF, QA, AP2, BP2>, W * 64, 0) !=
@@ -312,28 +318,28 @@ static int launch_gemv_k(const void* x, const void* xs, int a_kind, const uint8_
   }();
   const dim3 grid(unsigned(std::min<int64_t>(N / 16, int64_t(per_cu) * cu_count())));
   WZ_LAUNCH("fp8_gemv", stream, (fp8_gemv_kernel<W, NKB, NB, MINW, XF, QA, AP2, BP2>), grid, dim3(W * 64), 0, x, xs, a_kind,
-            w, w_s, w_kind, res, y, int(M), int(N), int(K), AP2 ? 1 : 0);
+            w, w_s, w_kind, res, y, y_hi, int(n_split), int(M), int(N), int(K), AP2 ? 1 : 0);
   return check_launch("fp8_gemv");
 }
 
 template <int W, int NKB, int NB, int MINW, bool XF, bool QA>
 static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
-                       const uint16_t* res, uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2,
-                       hipStream_t stream) {
+                       const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
+                       int64_t K, bool pow2, hipStream_t stream) {
   const bool bp = w_kind == WZ_WSCALE_E8M0;
   if (pow2)
-    return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, true>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, stream)
-              : launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, false>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, stream);
-  return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, true>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, stream)
-            : launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, false>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, stream);
+    return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, true>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, stream)
+              : launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, stream);
+  return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, true>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, stream)
+            : launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, stream);
 }
 
 static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s,
-                         int w_kind, const uint16_t* res, uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2,
-                         hipStream_t stream) {
+                         int w_kind, const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M,
+                         int64_t N, int64_t K, bool pow2, hipStream_t stream) {
 #define WZ_GV(...)                                                                                          \
-  return qa ? launch_gemv<__VA_ARGS__, true>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, pow2, stream)          \
-            : launch_gemv<__VA_ARGS__, false>(x, xs, a_kind, w, w_s, w_kind, res, y, M, N, K, pow2, stream)
+  return qa ? launch_gemv<__VA_ARGS__, true>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream)          \
+            : launch_gemv<__VA_ARGS__, false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream)
   switch (K) {
     case 1024: WZ_GV(WZ_GV_K1024);
     case 2048: WZ_GV(WZ_GV_K2048);
@@ -372,7 +378,8 @@ static int gemm_packed(const char* name, const void* a_e4m3, const void* a_s, co
   const uint8_t* w = static_cast<const uint8_t*>(w_packed);
   uint16_t* c = static_cast<uint16_t*>(c_bf16);
   if (M <= kGvMaxM && gemv_shape_ok(K))
-    return gemv_dispatch(true, a_e4m3, a_s, act_scale_kind, w, w_s, w_scale_kind, res, c, M, N, K, pow2, stream);
+    return gemv_dispatch(true, a_e4m3, a_s, act_scale_kind, w, w_s, w_scale_kind, res, c, nullptr, N, M, N, K, pow2,
+                         stream);
   const float* xs = static_cast<const float*>(a_s);
   if (act_scale_kind == WZ_SCALE_UE8M0) {
     const size_t need = wz_fp8_gemm_packed_workspace_bytes(M, K, act_scale_kind);
@@ -408,4 +415,33 @@ extern "C" int wz_fp8_gemm_packed_add(const void* a_e4m3, const void* a_s, const
   return wz::gemm_packed("fp8_gemm_packed_add", a_e4m3, a_s, w_packed, w_s,
                          static_cast<const uint16_t*>(residual_bf16), c_bf16, M, N, K, act_scale_kind, w_scale_kind,
                          ws, ws_bytes, stream);
+}
+
+extern "C" int wz_fp8_gemm_packed_pair(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
+                                       void* c0_bf16, int64_t N0, void* c1_bf16, int64_t M, int64_t N, int64_t K,
+                                       int act_scale_kind, int w_scale_kind, void* ws, size_t ws_bytes,
+                                       hipStream_t stream) {
+  using namespace wz;
+  if (N0 <= 0 || N0 >= N || N0 % 128)
+    return set_error(WZ_EINVAL, "fp8_gemm_packed_pair: split N0=%lld must be a multiple of 128 inside N=%lld",
+                     (long long)N0, (long long)N);
+  if (!c1_bf16) return set_error(WZ_EINVAL, "fp8_gemm_packed_pair: null pointer");
+  if (M > 0 && M <= kGvMaxM && gemv_shape_ok(K) && N % 16 == 0 && K % 128 == 0 && N <= (1 << 30) && K <= (1 << 30)) {
+    if (act_scale_kind < WZ_SCALE_F32 || act_scale_kind > WZ_SCALE_UE8M0_F32 ||
+        (w_scale_kind != WZ_WSCALE_F32 && w_scale_kind != WZ_WSCALE_E8M0))
+      return set_error(WZ_EINVAL, "fp8_gemm_packed_pair: bad scale kinds %d/%d", act_scale_kind, w_scale_kind);
+    if (!a_e4m3 || !a_s || !w_packed || !w_s || !c0_bf16) return set_error(WZ_EINVAL, "fp8_gemm_packed_pair: null pointer");
+    return gemv_dispatch(true, a_e4m3, a_s, act_scale_kind, static_cast<const uint8_t*>(w_packed), w_s, w_scale_kind,
+                         nullptr, static_cast<uint16_t*>(c0_bf16), static_cast<uint16_t*>(c1_bf16), N0, M, N, K,
+                         act_scale_kind != WZ_SCALE_F32, stream);
+  }
+  // outside the GEMV: the two weights one after the other (the packed tiles of
+  // rows N0.. and their block-scale rows start where the first weight's end)
+  if (int rc = gemm_packed("fp8_gemm_packed_pair", a_e4m3, a_s, w_packed, w_s, nullptr, c0_bf16, M, N0, K,
+                           act_scale_kind, w_scale_kind, ws, ws_bytes, stream))
+    return rc;
+  const size_t sbytes = w_scale_kind == WZ_WSCALE_E8M0 ? 1 : 4;
+  return gemm_packed("fp8_gemm_packed_pair", a_e4m3, a_s, static_cast<const uint8_t*>(w_packed) + size_t(N0) * K,
+                     static_cast<const uint8_t*>(w_s) + size_t(N0 / 128) * size_t((K + 127) / 128) * sbytes,
+                     nullptr, c1_bf16, M, N - N0, K, act_scale_kind, w_scale_kind, ws, ws_bytes, stream);
 }

@@ -304,6 +304,57 @@ class PackedFp8Linear:
         return y
 
 
+class PackedFp8Pair:
+    """Two FP8 linears that read the same input (wq_a and wkv of the attention side,
+    wq_b and the indexer's wq_b; architecture.py:611-672), their weights stacked
+    row-wise and packed once, served by one launch (wz_fp8_gemm_packed_pair).
+    ``gemm(q, q_s)`` -> (fp8_gemm(q, q_s, w0, s0), fp8_gemm(q, q_s, w1, s1)).  The
+    first weight's rows must be a multiple of 128 (its block scales end on a row)."""
+
+    def __init__(self, w0, s0, w1, s1, scale_fmt="ue8m0"):
+        for t in (w0, s0, w1, s1):
+            assert t.is_contiguous()
+        _require_cuda(w0, s0, w1, s1)
+        if w0.size(1) != w1.size(1) or w0.size(0) % 128 or s0.dtype != s1.dtype:
+            raise ValueError("PackedFp8Pair: weights must share K, the first must have a multiple of 128 rows, "
+                             "and the scales one dtype")
+        self.N0, self.N1, self.K = w0.size(0), w1.size(0), w0.size(1)
+        self.N = self.N0 + self.N1
+        self.w_kind = _wscale_kind_of(s0)
+        self.scale = torch.cat([s0.view(torch.uint8) if s0.dtype == _E8M0 else s0,
+                                s1.view(torch.uint8) if s1.dtype == _E8M0 else s1]).contiguous()
+        w = torch.cat([w0.view(torch.uint8), w1.view(torch.uint8)]).contiguous()
+        self.packed = torch.empty(self.N * self.K, dtype=torch.uint8, device=w0.device)
+        N.call("wz_fp8_pack", N.ptr(w), self.N, self.K, N.ptr(self.packed), N.stream_handle(w0.device))
+        torch.cuda.current_stream(w0.device).synchronize()  # the stacked copy is freed on return
+        self._ws = None
+
+    def reserve(self, M: int, q_dtype=_E8M0):
+        kind = N.WZ_SCALE_UE8M0 if q_dtype == _E8M0 else N.WZ_SCALE_F32
+        need = int(N.lib().wz_fp8_gemm_packed_workspace_bytes(M, self.K, kind))
+        if need and (self._ws is None or self._ws.numel() < need):
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(f"PackedFp8Pair: reserve({M}) before capturing a graph")
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.packed.device)
+        return self
+
+    def gemm(self, q, q_s, out=None):
+        assert q.is_contiguous() and q_s.is_contiguous() and q.size(-1) == self.K
+        _require_cuda(q, q_s)
+        M = q.numel() // self.K
+        self.reserve(M, q_s.dtype)
+        lead = q.size()[:-1]
+        if out is None:
+            out = (torch.empty(*lead, self.N0, dtype=torch.bfloat16, device=q.device),
+                   torch.empty(*lead, self.N1, dtype=torch.bfloat16, device=q.device))
+        y0, y1 = out
+        ws = self._ws
+        N.call("wz_fp8_gemm_packed_pair", N.ptr(q), N.ptr(q_s), N.ptr(self.packed), N.ptr(self.scale), N.ptr(y0),
+               self.N0, N.ptr(y1), M, self.N, self.K, _scale_kind_of(q_s), self.w_kind, N.ptr(ws),
+               0 if ws is None else ws.numel(), N.stream_handle(q.device))
+        return y0, y1
+
+
 def rms_norm(x, weight, eps=1e-6, out=None):
     """RMSNorm.forward (architecture.py:217-230): bf16(weight * (x * rsqrt(mean(x^2) + eps))),
     fp32 math, one row per token; weight is the module's fp32 parameter."""

@@ -27,9 +27,11 @@ Per block, with h the [T, D] residual stream (bf16):
     (after the last block: h = h1 + e)
 
 Each FP8 input is produced quantised by the norm that precedes it
-(rms_norm_quant), the residual add of the attention side sits in wo_b's
-epilogue and that of the MoE side in the next block's norm.  Every buffer is
-allocated once, so a step is a fixed sequence of launches.
+(rms_norm_quant), the two projections that read one input run as one launch
+(wq_a with wkv, wq_b with the indexer's wq_b: kernels.PackedFp8Pair), the
+residual add of the attention side sits in wo_b's epilogue and that of the MoE
+side in the next block's norm.  Every buffer is allocated once, so a step is a
+fixed sequence of launches.
 """
 
 from __future__ import annotations
@@ -52,15 +54,10 @@ class StageBlock:
     attn_norm: torch.Tensor              # fp32 [D]
     q_norm: torch.Tensor                 # fp32 [q_lora]
     ffn_norm: torch.Tensor               # fp32 [D]
-    wq_a: kernels.PackedFp8Linear        # [q_lora, D]
-    wkv: kernels.PackedFp8Linear         # [head_dim, D]
-    wq_b: kernels.PackedFp8Linear        # [q_width, q_lora]
-    idx_wq_b: kernels.PackedFp8Linear    # [idx_width, q_lora]
+    qa_kv: kernels.PackedFp8Pair         # wq_a [q_lora, D] and wkv [head_dim, D], one launch
+    q_idx: kernels.PackedFp8Pair         # wq_b [q_width, q_lora] and idx wq_b [idx_width, q_lora]
     wo_b: kernels.PackedFp8Linear        # [D, idx_width]
     moe: object                          # HipMoE
-
-    def projections(self):
-        return (self.wq_a, self.wkv, self.wq_b, self.idx_wq_b, self.wo_b)
 
 
 def synthetic_linear(N: int, K: int, seed: int, device, fp32_scales: bool = True):
@@ -89,21 +86,15 @@ def synthetic_block(moe, D: int, seed: int, device, q_lora: int = 1024, head_dim
     """Projections with e8m0 block scales (the model's FP8 weights carry e8m0 scales,
     architecture.py:158-168); 2^-15..2^-11 keeps a K = 4096 product of uniform e4m3
     codes O(1), so the residual stream keeps its scale block after block."""
-    lins = []
-    for j, (N, K) in enumerate(projection_shapes(D, q_lora, head_dim, q_width, idx_width)):
-        w, s = synthetic_linear(N, K, seed * 16 + j, device, fp32_scales=False)
-        lins.append(kernels.PackedFp8Linear(w, s, "ue8m0"))
+    ws = [synthetic_linear(N, K, seed * 16 + j, device, fp32_scales=False)
+          for j, (N, K) in enumerate(projection_shapes(D, q_lora, head_dim, q_width, idx_width))]
     norms = []
     for j, n in enumerate((D, q_lora, D)):
         t = torch.empty(n, dtype=torch.float32, device=device)
         synth.device_fill(t, synth.stream_key(seed * 16 + 8 + j, synth.S_NORM), synth.FILL_F32_UNIFORM, 0.5, 1.5)
         norms.append(t)
-    return StageBlock(norms[0], norms[1], norms[2], *lins, moe)
-
-
-def projection_bytes(b: StageBlock) -> int:
-    """Weight bytes (e4m3 codes + one byte per 128 x 128 block scale) of a block's projections."""
-    return sum(l.N * l.K + ((l.N + 127) // 128) * ((l.K + 127) // 128) for l in b.projections())
+    return StageBlock(norms[0], norms[1], norms[2], kernels.PackedFp8Pair(*ws[0], *ws[1], "ue8m0"),
+                      kernels.PackedFp8Pair(*ws[2], *ws[3], "ue8m0"), kernels.PackedFp8Linear(*ws[4], "ue8m0"), moe)
 
 
 class DecodeStage:
@@ -127,16 +118,16 @@ class DecodeStage:
         # no kernel writes the buffer it reads
         self.h = [torch.zeros(T, D, **bf) for _ in range(3)]
         self.hq = q8(D)
-        self.qa = torch.empty(T, b0.wq_a.N, **bf)
-        self.kv = torch.empty(T, b0.wkv.N, **bf)
-        self.qq = q8(b0.wq_a.N)
-        self.q = torch.empty(T, b0.wq_b.N, **bf)
-        self.iq = torch.empty(T, b0.idx_wq_b.N, **bf)
+        self.qa = torch.empty(T, b0.qa_kv.N0, **bf)
+        self.kv = torch.empty(T, b0.qa_kv.N1, **bf)
+        self.qq = q8(b0.qa_kv.N0)
+        self.q = torch.empty(T, b0.q_idx.N0, **bf)
+        self.iq = torch.empty(T, b0.q_idx.N1, **bf)
         self.m = torch.empty(T, D, **bf)
         self.e = torch.empty(T, D, **bf)
         self.y = torch.empty(T, D, **bf)
         for b in self.blocks:
-            for lin in b.projections():
+            for lin in (b.qa_kv, b.q_idx, b.wo_b):
                 lin.reserve(T)
             b.moe.reserve(T)
         self.graph = None
@@ -154,11 +145,9 @@ class DecodeStage:
                 hs = next(nxt)
                 kernels.add_rms_norm_quant(h, self.e, b.attn_norm, eps, sum_out=hs, out=self.hq)
                 h = hs
-            b.wq_a.gemm(*self.hq, out=self.qa)
-            b.wkv.gemm(*self.hq, out=self.kv)
+            b.qa_kv.gemm(*self.hq, out=(self.qa, self.kv))
             kernels.rms_norm_quant(self.qa, b.q_norm, eps, out=self.qq)
-            b.wq_b.gemm(*self.qq, out=self.q)
-            b.idx_wq_b.gemm(*self.qq, out=self.iq)
+            b.q_idx.gemm(*self.qq, out=(self.q, self.iq))
             h1 = next(nxt)
             b.wo_b(self.iq, out=h1, residual=h)
             kernels.rms_norm(h1, b.ffn_norm, eps, out=self.m)
