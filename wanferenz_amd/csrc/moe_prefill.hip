@@ -712,12 +712,31 @@ __device__ __forceinline__ int xcd_contiguous(int b, int d0, int n) {
   return before + (b - fx) / kXcds;
 }
 
+// (M-tile, N-block) of routed block r, r < n_mt * nblk: groups of gm M-tiles
+// take their N-blocks in parts of gn.  A window of consecutive blocks (the
+// workgroups resident on one XCD, 64) then covers gm M-tiles x (64 / gm)
+// N-blocks: an N-block's weight tiles come from beyond L2 once per gm M-tiles
+// and an M-tile's rows once per nblk / gn parts.  gm = 1, gn = nblk is M-tile
+// major (an M-tile's rows fetched once; right when experts hold one or two
+// M-tiles); gm = gn = 8 suits hot experts with many M-tiles (their weights came
+// once per 4 M-tiles in M-tile-major order).  A bijection on [0, n_mt * nblk):
+// the last group holds n_mt % gm M-tiles and the last part nblk % gn N-blocks.
+__device__ __forceinline__ void tile_order(int r, int n_mt, int nblk, int gm, int gn, int& mt, int& nt) {
+  const int full = n_mt / gm, per = gm * nblk;
+  const int q = r / per, rr = r % per;
+  const int h = q < full ? gm : n_mt - full * gm;  // M-tiles in this group
+  // only the last part can be narrower, so part p starts at p * gn * h
+  const int part = rr / (gn * h), i = rr % (gn * h);
+  mt = q * gm + i % h;
+  nt = part * gn + i / h;
+}
+
 // One launch serves the shared expert's dense tiles (block ids first, so the
 // few long-running shared tiles start early) and the routed experts' M-tiles.
 // W13 selects w1/w3 + SwiGLU or w2; CR / CS: scale chaining of routed / shared.
 template <bool W13, bool CR, bool CS>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_gemm_kernel(
-    wz_moe_desc d, MoeWs ws, int T, int nblk, int nblk_dense, int dense_blocks) {
+    wz_moe_desc d, MoeWs ws, int T, int nblk, int nblk_dense, int dense_blocks, int gm, int gn) {
   __shared__ __align__(16) uint8_t a_s[3][kPM * kARow];
   __shared__ float as_s[3][kPM];
   const int b = blockIdx.x;
@@ -727,7 +746,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     const int n = ws.n_mt[0] * nblk;  // routed blocks with work
     if (b - dense_blocks >= n) return;
     const int r = xcd_contiguous(b, dense_blocks, n);
-    gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, r / nblk, r % nblk, a_s, as_s);
+    int mt, nt;
+    tile_order(r, ws.n_mt[0], nblk, gm, gn, mt, nt);
+    gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, mt, nt, a_s, as_s);
   }
 }
 
@@ -758,14 +779,19 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
   const bool cs = cr && d->shared_w_scale_kind == WZ_WSCALE_E8M0;
   const int Ti = int(T), dn13 = int(mt_dense * nb13d), dn2 = int(mt_dense * nb2d);
   const dim3 blk(kPThreads), g13(unsigned(dn13 + mt_max * nb13)), g2(unsigned(dn2 + mt_max * nb2));
+  // routed block order (tile_order): 8 M-tiles x 8 N-blocks per group at T >= 1024,
+  // where skewed batches give hot experts many M-tiles (T = 2048, calibrated skew:
+  // 1327 -> 1250 us per layer); M-tile major below (T = 128: 341 vs 367 us)
+  const bool grouped = T >= 1024;
+  const int gm = grouped ? 8 : 1, gn13 = grouped ? 8 : nb13, gn2 = grouped ? 8 : nb2;
   if (only < 0 || only == WZ_STAGE_W13) {
     if (cr && cs) {
-      WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, true, true>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13);
+      WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, true, true>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13, gm, gn13);
     } else if (cr) {
-      WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, true, false>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13);
+      WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, true, false>), g13, blk, 0, *d, w, Ti, nb13, nb13d, dn13, gm, gn13);
     } else {
       WZ_LAUNCH("moe_w13", stream, (prefill_gemm_kernel<true, false, false>), g13, blk, 0, *d, w, Ti, nb13, nb13d,
-                dn13);
+                dn13, gm, gn13);
     }
     if (int rc = check_launch("moe w13")) return rc;
   }
@@ -775,11 +801,11 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
   }
   if (only < 0 || only == WZ_STAGE_W2) {
     if (cr && cs) {
-      WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, true, true>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
+      WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, true, true>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2, gm, gn2);
     } else if (cr) {
-      WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, true, false>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
+      WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, true, false>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2, gm, gn2);
     } else {
-      WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, false, false>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2);
+      WZ_LAUNCH("moe_w2", stream, (prefill_gemm_kernel<false, false, false>), g2, blk, 0, *d, w, Ti, nb2, nb2d, dn2, gm, gn2);
     }
     if (int rc = check_launch("moe w2")) return rc;
   }
@@ -811,13 +837,13 @@ int launch_dense_fp8(const uint8_t* wp, const void* w_s, int w_kind, const uint8
   const dim3 grid{unsigned(dense)}, blk{unsigned(kPThreads)};
   if (cs) {
     WZ_LAUNCH("fp8_linear", stream, (prefill_gemm_kernel<false, true, true>), grid, blk, 0, d, w, int(M), 1, nb2d,
-              dense);
+              dense, 1, 1);
   } else if (a_pow2) {
     WZ_LAUNCH("fp8_linear", stream, (prefill_gemm_kernel<false, true, false>), grid, blk, 0, d, w, int(M), 1, nb2d,
-              dense);
+              dense, 1, 1);
   } else {
     WZ_LAUNCH("fp8_linear", stream, (prefill_gemm_kernel<false, false, false>), grid, blk, 0, d, w, int(M), 1,
-              nb2d, dense);
+              nb2d, dense, 1, 1);
   }
   return check_launch("fp8_linear dense");
 }
