@@ -394,6 +394,7 @@ __global__ __launch_bounds__(1024) void mtile_kernel(MoeWs ws, int E, int P, int
 
 struct TileRows {
   int row0, nrows, e;
+  bool keep;  // other M-tiles read the same weight tiles: keep them in L2
 };
 
 // Tile of the grid: routed tiles come from the M-tile table; dense tiles
@@ -403,11 +404,13 @@ __device__ __forceinline__ bool tile_of(const MoeWs& ws, int mt, bool dense, int
     tr.row0 = mt * kPM;
     tr.nrows = min(kPM, T - tr.row0);
     tr.e = 0;
+    tr.keep = T > kPM;
     return tr.nrows > 0;
   }
   if (mt >= ws.n_mt[0]) return false;
   const int u = clampi(ws.mt_u[mt], 0, E - 1);
   tr.e = clampi(ws.active[u], 0, E - 1);
+  tr.keep = ws.act_cnt[u] > kPM;
   tr.row0 = clampi(ws.mt_row0[mt], 0, P);
   tr.nrows = clampi(ws.mt_n[mt], 0, min(kPM, P - tr.row0));
   return tr.nrows > 0;
@@ -448,8 +451,12 @@ struct BTiles {
 //
 // CHAIN: activation and weight scales are both powers of two, so they ride in
 // the MFMA's e8m0 scale operands and the accumulators chain over K; otherwise
-// each K-block partial is scaled on the VALU (mma_step).
-template <int MODE, bool CHAIN, int NM>
+// each K-block partial is scaled on the VALU (mma_step).  KEEP: the weight
+// tiles are read by other M-tiles too (an expert with more than one M-tile,
+// the shared expert over several), so they are loaded as ordinary cached
+// loads; otherwise non-temporal, as a single-use stream that should not evict
+// the activation rows the N-blocks of an M-tile share.
+template <int MODE, bool CHAIN, int NM, bool KEEP>
 __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs& ws, int T, const TileRows& tr,
                                                int nt, uint8_t (*a_s)[kPM * kARow], float (*as_s)[kPM]) {
   constexpr bool W13 = MODE < 2, DENSE = (MODE & 1) != 0;
@@ -507,20 +514,21 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
     as_s[buf][sr] = asv;  // the row's four threads store the same scale: no divergent branch
   };
 
+  auto wload = [](const uint8_t* p) { return KEEP ? load16(p) : load16_nt(p); };
   auto b_fetch = [&](BTiles<NTW>& b, int kb) {
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
       if (MODE == 0) {
         const int64_t t = int64_t(e) * NCT + cl[j];
         const uint8_t* w = static_cast<const uint8_t*>(d.w13p) + ((t * KB + kb) * 2 + which[j]) * 1024;
-        b.lo[j] = load16_nt(w + lane * 16);
+        b.lo[j] = wload(w + lane * 16);
         const uint32_t* sw = static_cast<const uint32_t*>(d.w13p_s) + ((t * KG + (kb >> 2)) * 2 + which[j]) * 64;
         b.sw[j] = sw[lane];
         b.f[j] = 1.0f;
       } else if (MODE == 2) {
         const int64_t t = int64_t(e) * NCT + cl[j];
         const uint8_t* w = static_cast<const uint8_t*>(d.w2p) + (t * KB + kb) * 1024;
-        b.lo[j] = load16_nt(w + lane * 16);
+        b.lo[j] = wload(w + lane * 16);
         const uint32_t* sw = static_cast<const uint32_t*>(d.w2p_s) + (t * KG + (kb >> 2)) * 64;
         b.sw[j] = sw[lane];
         b.f[j] = 1.0f;
@@ -534,8 +542,8 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
           w = static_cast<const uint8_t*>(d.sh2p) + (int64_t(cl[j]) * KB + kb) * 2048;
           s = d.sh_w2_s;
         }
-        b.lo[j] = load16_nt(w + lane * 16);
-        b.hi[j] = load16_nt(w + 1024 + lane * 16);
+        b.lo[j] = wload(w + lane * 16);
+        b.hi[j] = wload(w + 1024 + lane * 16);
         const int64_t si = int64_t(cl[j] >> 3) * KB + kb;
         if (CHAIN) {
           b.sw[j] = static_cast<const uint8_t*>(s)[si];
@@ -685,12 +693,21 @@ __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws,
   TileRows tr;
   if (!tile_of(ws, mt, (MODE & 1) != 0, T, T * d.topk, d.n_experts, tr)) return;
   static_assert(kPM == 64, "tile heights up to 4 row tiles");
-  if (tr.nrows <= 16)
-    gemm_tile_body<MODE, CHAIN, 1>(d, ws, T, tr, nt, a_s, as_s);
-  else if (tr.nrows <= 32)
-    gemm_tile_body<MODE, CHAIN, 2>(d, ws, T, tr, nt, a_s, as_s);
-  else
-    gemm_tile_body<MODE, CHAIN, 4>(d, ws, T, tr, nt, a_s, as_s);
+  if (tr.keep) {
+    if (tr.nrows <= 16)
+      gemm_tile_body<MODE, CHAIN, 1, true>(d, ws, T, tr, nt, a_s, as_s);
+    else if (tr.nrows <= 32)
+      gemm_tile_body<MODE, CHAIN, 2, true>(d, ws, T, tr, nt, a_s, as_s);
+    else
+      gemm_tile_body<MODE, CHAIN, 4, true>(d, ws, T, tr, nt, a_s, as_s);
+  } else {
+    if (tr.nrows <= 16)
+      gemm_tile_body<MODE, CHAIN, 1, false>(d, ws, T, tr, nt, a_s, as_s);
+    else if (tr.nrows <= 32)
+      gemm_tile_body<MODE, CHAIN, 2, false>(d, ws, T, tr, nt, a_s, as_s);
+    else
+      gemm_tile_body<MODE, CHAIN, 4, false>(d, ws, T, tr, nt, a_s, as_s);
+  }
 }
 
 // Workgroups are dispatched to the XCDs round-robin (block b to XCD b % 8),
