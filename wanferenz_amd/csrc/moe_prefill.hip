@@ -712,21 +712,28 @@ __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws,
 
 // Workgroups are dispatched to the XCDs round-robin (block b to XCD b % 8),
 // each XCD with its own L2.  The routed blocks [d0, d0 + n) are renumbered so
-// that each XCD takes one contiguous run of (M-tile, N-block) pairs: the
-// N-blocks of an M-tile then share its gathered activation rows in one L2, and
-// consecutive M-tiles of an expert (which read the same weight tiles) run on
-// the same XCD at about the same time.  A bijection on [d0, d0 + n) for any
-// XCD count, so only locality depends on the dispatch order.
-__device__ __forceinline__ int xcd_contiguous(int b, int d0, int n) {
-  constexpr int kXcds = 8;
+// that each XCD takes runs of 64 consecutive (M-tile, N-block) pairs (as many
+// as its CUs hold at once, two per CU): an M-tile's N-blocks then share its
+// gathered activation rows in one L2, and the M-tiles of a group read the same
+// weight tiles there.  Run j goes to XCD j % 8, so the many runs of a hot
+// expert spread over every XCD instead of piling onto one (one XCD had held
+// all 368 blocks of the hottest expert of a T = 2048 batch and ended 25 %
+// after the first).  The last, partial round of 8 runs is split contiguously.
+// A bijection on [d0, d0 + n) for any n (checked exhaustively on the CPU), so
+// only locality depends on the dispatch order.
+__device__ __forceinline__ int xcd_runs(int b, int d0, int n) {
+  constexpr int kXcds = 8, kRun = 64;
   const int x = b % kXcds;
-  int before = 0;  // routed blocks on the XCDs ahead of x
+  const int fx = d0 + ((x - d0) & (kXcds - 1));  // first routed block on XCD x
+  const int k = (b - fx) / kXcds;                // b's place among them
+  const int full = n / (kXcds * kRun);           // complete rounds of 8 runs
+  if (k < full * kRun) return ((k / kRun) * kXcds + x) * kRun + k % kRun;
+  int before = 0;  // blocks of the last round on the XCDs ahead of x
   for (int y = 0; y < x; ++y) {
-    const int fy = d0 + ((y - d0) & (kXcds - 1));  // first routed block on XCD y
-    before += fy < d0 + n ? (d0 + n - fy + kXcds - 1) / kXcds : 0;
+    const int fy = d0 + ((y - d0) & (kXcds - 1));
+    before += (fy < d0 + n ? (d0 + n - fy + kXcds - 1) / kXcds : 0) - full * kRun;
   }
-  const int fx = d0 + ((x - d0) & (kXcds - 1));
-  return before + (b - fx) / kXcds;
+  return full * kXcds * kRun + before + (k - full * kRun);
 }
 
 // (M-tile, N-block) of routed block r, r < n_mt * nblk: groups of gm M-tiles
@@ -762,7 +769,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
   } else {
     const int n = ws.n_mt[0] * nblk;  // routed blocks with work
     if (b - dense_blocks >= n) return;
-    const int r = xcd_contiguous(b, dense_blocks, n);
+    const int r = xcd_runs(b, dense_blocks, n);
     int mt, nt;
     tile_order(r, ws.n_mt[0], nblk, gm, gn, mt, nt);
     gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, mt, nt, a_s, as_s);
