@@ -25,7 +25,7 @@ namespace wz {
 constexpr int kPM = kPrefillTileRows;  // pair rows per M-tile (64: the tile bodies then fit two
                                        // workgroups per CU, twice the weight bytes in flight)
 constexpr int kPThreads = 256;    // 4 waves
-constexpr int kARow = 144;        // LDS row stride of the staged A tile (bytes)
+constexpr int kNA = 4;            // LDS buffers of the staged A tile (K-steps kb .. kb + 3)
 
 // ------------------------------------------------------------------- gate ---
 //
@@ -416,12 +416,19 @@ __device__ __forceinline__ bool tile_of(const MoeWs& ws, int mt, bool dense, int
   return tr.nrows > 0;
 }
 
+// A K-step in LDS: 64 rows of 128 bytes, the 16-byte chunk q of row r at slot
+// q ^ a_swz(r), so the 16 rows an A operand read touches (one chunk each) fall
+// in distinct banks; the rows' scales at as_s[(r / 16) * 64 + r % 16].
+__device__ __forceinline__ int a_swz(int row) { return (row >> 1) & 7; }
+
 __device__ __forceinline__ AOp a_from_lds(const uint8_t* a_s, const float* as_s, int row, int g, bool pow2) {
   AOp a;
-  const uint8_t* p = a_s + row * kARow + g * 16;
-  const v4i lo = *reinterpret_cast<const v4i*>(p), hi = *reinterpret_cast<const v4i*>(p + 64);
+  const uint8_t* p = a_s + row * 128;
+  const int sw = a_swz(row);
+  const v4i lo = *reinterpret_cast<const v4i*>(p + ((g ^ sw) << 4));
+  const v4i hi = *reinterpret_cast<const v4i*>(p + (((g + 4) ^ sw) << 4));
   a.v = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  const float s = as_s[row];
+  const float s = as_s[(row >> 4) * 64 + (row & 15)];
   a.sf = s;
   a.se8 = pow2 ? int((__float_as_uint(s) >> 23) & 0xFFu) : kE8m0One;
   return a;
@@ -445,9 +452,10 @@ struct BTiles {
 // A wave owns NTW weight tiles of 16 output columns (routed w13: 4, i.e. 2
 // feature tiles x {w1, w3}; routed w2: 2 column tiles; shared FP8 tiles are
 // twice the bytes, so 2), and one A operand read from LDS feeds NTW MFMAs.
-// The K loop is software-pipelined: the B tiles of K-steps kb+1 and kb+2 are
-// in flight while kb computes, and the A block of kb+1 sits in registers on
-// its way to LDS; A goes through three LDS buffers with one barrier per step.
+// The K loop is software-pipelined three K-steps deep: while step kb computes,
+// the B tiles (registers) and the A rows (LDS, direct buffer loads that need
+// no registers) of steps kb+1 .. kb+3 are in flight; A goes through kNA = 4
+// LDS buffers with one barrier per step.
 //
 // CHAIN: activation and weight scales are both powers of two, so they ride in
 // the MFMA's e8m0 scale operands and the accumulators chain over K; otherwise
@@ -458,7 +466,7 @@ struct BTiles {
 // the activation rows the N-blocks of an M-tile share.
 template <int MODE, bool CHAIN, int NM, bool KEEP>
 __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs& ws, int T, const TileRows& tr,
-                                               int nt, uint8_t (*a_s)[kPM * kARow], float (*as_s)[kPM]) {
+                                               int nt, uint8_t (*a_s)[kPM * 128], float (*as_s)[256]) {
   constexpr bool W13 = MODE < 2, DENSE = (MODE & 1) != 0;
   constexpr int WF = DENSE ? kFmtFp8 : kFmtFp4;
   // weight tiles per wave: routed w1/w3 4 (2 feature tiles x {w1, w3}); routed
@@ -466,7 +474,7 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
   // FP8 shared tiles, twice the bytes, 2
   constexpr int NTW = (DENSE || MODE == 2) ? 2 : 4;
   constexpr int CPW = W13 ? NTW / 2 : NTW;    // 16-column output tiles per wave
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = lane & 15, g = lane >> 4;
   const int D = d.dim, I = d.inter, k = d.topk, P = T * k;
   const int K = W13 ? D : I, KB = K / 128, KG = (KB + 3) / 4;
@@ -491,27 +499,40 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
     jv[j] = ct[j] < NCT;
   }
 
-  // A staging: thread -> (row, half of the 128-byte K-block)
-  const int sr = tid >> 2, sq = tid & 3;  // 4 threads per row, 32 bytes each
-  const int rr = min(sr, nrows - 1);
-  int src;
-  if (MODE == 0) src = clampi(ws.perm_token[row0 + rr], 0, T - 1);
-  else if (MODE == 1) src = row0 + rr;
-  else if (MODE == 2) src = row0 + rr;
-  else src = P + row0 + rr;
-  const uint8_t* arow = (W13 ? ws.xq : ws.hq) + int64_t(src) * K + sq * 32;
-  const float* asrow = (W13 ? ws.xs : ws.hs) + int64_t(src) * KB;
-  v4i av[2];
-  float asv;
-  auto a_fetch = [&](int kb) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) av[i] = load16(arow + kb * 128 + 16 * i);
-    asv = asrow[kb];
+  // A staging: wave w brings rows 16w .. 16w + 15 of a K-step into LDS with
+  // two 1-KB direct loads (lane l: row 16w + 8i + l / 8, slot l % 8, which
+  // holds the row's chunk (l % 8) ^ a_swz(row)) and their scales with one
+  // 4-byte load (lane l: row 16w + l % 16).  Rows past nrows repeat the last
+  // row (their outputs are dropped).  A wave whose 16 rows are all past nrows
+  // issues its loads against an empty buffer range: they return without
+  // touching memory, and every wave issues the same loads (no branch).
+  auto src_of = [&](int r) {
+    const int rr = min(r, nrows - 1);
+    if (MODE == 0) return clampi(ws.perm_token[row0 + rr], 0, T - 1);
+    if (MODE == 3) return P + row0 + rr;
+    return row0 + rr;
   };
-  auto a_put = [&](int buf) {
+  const bool a_rows = 16 * wave < nrows;
+  uint32_t avo[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<v4i*>(&a_s[buf][sr * kARow + sq * 32 + 16 * i]) = av[i];
-    as_s[buf][sr] = asv;  // the row's four threads store the same scale: no divergent branch
+  for (int i = 0; i < 2; ++i) {
+    const int row = 16 * wave + 8 * i + (lane >> 3);
+    avo[i] = uint32_t(src_of(row)) * uint32_t(K) + uint32_t(((lane & 7) ^ a_swz(row)) << 4);
+  }
+  const uint32_t svo = uint32_t(src_of(16 * wave + (lane & 15))) * uint32_t(KB) * 4u;
+  const int64_t a_nrows = W13 ? T : P + T;  // rows of xq / hq
+  const __amdgpu_buffer_rsrc_t a_rs = __builtin_amdgcn_make_buffer_rsrc(
+      W13 ? ws.xq : ws.hq, short(0), a_rows ? int(a_nrows * K) : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t s_rs = __builtin_amdgcn_make_buffer_rsrc(
+      W13 ? ws.xs : ws.hs, short(0), a_rows ? int(a_nrows * KB * 4) : 0, 0x00020000);
+  const uint32_t a_lds = lds_addr(&a_s[0][0]), s_lds = lds_addr(&as_s[0][0]);
+  auto a_issue = [&](int kb) {
+    const uint32_t buf = uint32_t(kb & (kNA - 1));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      load_lds_16(a_rs, __builtin_amdgcn_readfirstlane(a_lds + buf * (kPM * 128) + (2 * wave + i) * 1024), avo[i],
+                  uint32_t(kb) * 128u);
+    load_lds_4(s_rs, __builtin_amdgcn_readfirstlane(s_lds + (buf * 256 + wave * 64) * 4), svo, uint32_t(kb) * 4u);
   };
 
   auto wload = [](const uint8_t* p) { return KEEP ? load16(p) : load16_nt(p); };
@@ -569,7 +590,7 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
     for (int j = 0; j < NTW; ++j) e8[j] = DENSE ? int(b.sw[j]) : int((b.sw[j] >> (8 * (kb & 3))) & 0xFFu);
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      const AOp a = a_from_lds(a_s[buf], as_s[buf], m * 16 + nl, g, CHAIN || a_pow2);
+      const AOp a = a_from_lds(a_s[buf & (kNA - 1)], as_s[buf & (kNA - 1)], m * 16 + nl, g, CHAIN || a_pow2);
 #pragma unroll
       for (int j = 0; j < NTW; ++j) {
         const v8i bv = DENSE ? v8i{b.lo[j][0], b.lo[j][1], b.lo[j][2], b.lo[j][3], b.hi[j][0], b.hi[j][1],
@@ -583,60 +604,80 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
     }
   };
 
-  // Invariant at step kb: LDS buffer kb % 3 holds A(kb), av holds A(kb+1),
-  // B registers hold B(kb) (landed), B(kb+1) and B(kb+2) (in flight).
+  // Step kb: wait for B(kb) -- every register of it, so the wait covers the
+  // whole fetch -- then a barrier, compute from LDS buffer kb % 4, then
+  // request B(kb + 3) into the registers just used and A(kb + 3) into the
+  // buffer read in step kb - 1 (every wave has passed this step's barrier, so
+  // none still reads it).  B(kb + 3) goes out before A(kb + 3), so A(kb) is
+  // the first load after B(kb): the compiler's wait for B(kb) counts only the
+  // loads it sees (the B fetches after it), every direct A load after B(kb)
+  // is among the loads it leaves outstanding too, and loads complete in
+  // order, so the oldest such loads -- A(kb) first -- have landed when it
+  // returns.  Every load is unconditional in the steady state, so those counts
+  // stay exact across the barriers.
+  auto b_touch = [](const BTiles<NTW>& b) {
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      asm volatile("" : : "v"(b.lo[j]), "v"(b.sw[j]));
+      if (DENSE) asm volatile("" : : "v"(b.hi[j]));
+      if (DENSE && !CHAIN) asm volatile("" : : "v"(b.f[j]));
+    }
+  };
+  auto step_sync = [&](const BTiles<NTW>& b) {
+    b_touch(b);
+    asm volatile("s_barrier" : : : "memory");
+  };
   BTiles<NTW> b0, b1, b2;
-  a_fetch(0);
   b_fetch(b0, 0);
-  a_put(0);
+  a_issue(0);
   if (KB > 1) {
-    a_fetch(1);
     b_fetch(b1, 1);
+    a_issue(1);
   }
-  if (KB > 2) b_fetch(b2, 2);
-  __syncthreads();
+  if (KB > 2) {
+    b_fetch(b2, 2);
+    a_issue(2);
+  }
   int kb = 0;
-  // steady state: every step refills, no conditional loads (sched_barrier keeps
-  // each step's MFMAs ahead of the loads that refill their B registers)
   for (; kb + 5 < KB; kb += 3) {
-    compute(0, b0, kb);
+    step_sync(b0);
+    compute(kb, b0, kb);
     __builtin_amdgcn_sched_barrier(0);
-    a_put(1);
-    a_fetch(kb + 2);
     b_fetch(b0, kb + 3);
-    __syncthreads();
-    compute(1, b1, kb + 1);
+    a_issue(kb + 3);
+    step_sync(b1);
+    compute(kb + 1, b1, kb + 1);
     __builtin_amdgcn_sched_barrier(0);
-    a_put(2);
-    a_fetch(kb + 3);
     b_fetch(b1, kb + 4);
-    __syncthreads();
-    compute(2, b2, kb + 2);
+    a_issue(kb + 4);
+    step_sync(b2);
+    compute(kb + 2, b2, kb + 2);
     __builtin_amdgcn_sched_barrier(0);
-    a_put(0);
-    a_fetch(kb + 4);
     b_fetch(b2, kb + 5);
-    __syncthreads();
+    a_issue(kb + 5);
   }
   // last K-steps
   for (; kb < KB; kb += 3) {
-    compute(0, b0, kb);
-    if (kb + 1 < KB) a_put(1);
-    if (kb + 2 < KB) a_fetch(kb + 2);
-    if (kb + 3 < KB) b_fetch(b0, kb + 3);
-    __syncthreads();
+    step_sync(b0);
+    compute(kb, b0, kb);
+    if (kb + 3 < KB) {
+      b_fetch(b0, kb + 3);
+      a_issue(kb + 3);
+    }
     if (kb + 1 >= KB) break;
-    compute(1, b1, kb + 1);
-    if (kb + 2 < KB) a_put(2);
-    if (kb + 3 < KB) a_fetch(kb + 3);
-    if (kb + 4 < KB) b_fetch(b1, kb + 4);
-    __syncthreads();
+    step_sync(b1);
+    compute(kb + 1, b1, kb + 1);
+    if (kb + 4 < KB) {
+      b_fetch(b1, kb + 4);
+      a_issue(kb + 4);
+    }
     if (kb + 2 >= KB) break;
-    compute(2, b2, kb + 2);
-    if (kb + 3 < KB) a_put(0);
-    if (kb + 4 < KB) a_fetch(kb + 4);
-    if (kb + 5 < KB) b_fetch(b2, kb + 5);
-    __syncthreads();
+    step_sync(b2);
+    compute(kb + 2, b2, kb + 2);
+    if (kb + 5 < KB) {
+      b_fetch(b2, kb + 5);
+      a_issue(kb + 5);
+    }
   }
 
   // epilogue
@@ -689,7 +730,7 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
 // tiles of 16, so its MFMA loops carry no row branches.
 template <int MODE, bool CHAIN>
 __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws, int T, int mt, int nt,
-                                          uint8_t (*a_s)[kPM * kARow], float (*as_s)[kPM]) {
+                                          uint8_t (*a_s)[kPM * 128], float (*as_s)[256]) {
   TileRows tr;
   if (!tile_of(ws, mt, (MODE & 1) != 0, T, T * d.topk, d.n_experts, tr)) return;
   static_assert(kPM == 64, "tile heights up to 4 row tiles");
@@ -761,8 +802,8 @@ __device__ __forceinline__ void tile_order(int r, int n_mt, int nblk, int gm, in
 template <bool W13, bool CR, bool CS>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_gemm_kernel(
     wz_moe_desc d, MoeWs ws, int T, int nblk, int nblk_dense, int dense_blocks, int gm, int gn) {
-  __shared__ __align__(16) uint8_t a_s[3][kPM * kARow];
-  __shared__ float as_s[3][kPM];
+  __shared__ __align__(1024) uint8_t a_s[kNA][kPM * 128];
+  __shared__ __align__(16) float as_s[kNA][256];
   const int b = blockIdx.x;
   if (b < dense_blocks) {
     gemm_tile<W13 ? 1 : 3, CS>(d, ws, T, b / nblk_dense, b % nblk_dense, a_s, as_s);
@@ -855,6 +896,7 @@ int launch_dense_fp8(const uint8_t* wp, const void* w_s, int w_kind, const uint8
   w.hq = const_cast<uint8_t*>(xq);
   w.hs = const_cast<float*>(xs);
   w.sh_out = y;
+  if (M * K >= (int64_t(1) << 31)) return set_error(WZ_EINVAL, "fp8_linear: M * K must be below 2^31");
   const int nb2d = int((N / 16 + 7) / 8);
   const int dense = int((M + kPM - 1) / kPM) * nb2d;
   const bool cs = a_pow2 && w_kind == WZ_WSCALE_E8M0;
