@@ -187,46 +187,92 @@ __global__ __launch_bounds__(256) void gate_mfma_ksplit_kernel(const uint16_t* _
 // loads of a chunk group are issued before the products.
 constexpr int kXC = 8;
 
-__device__ __forceinline__ float exact_logit(const v4i (&xv)[kXC], const uint16_t* __restrict__ xrow,
-                                             const uint16_t* __restrict__ w, int D, int lane) {
-  double acc = 0.0;
-  for (int base = 0; base < D; base += kXC * 512) {
-    v4i wv[kXC], xb[kXC];
+// acc + this lane's products of one chunk group, in chunk, word, half order.
+// The empty asm after each chunk keeps the compiler from converting every
+// product of the group to fp64 ahead of the sum (64 doubles in registers).
+__device__ __forceinline__ double exact_dot_lane(const v4i (&xb)[kXC], const v4i (&wv)[kXC], double acc) {
 #pragma unroll
-    for (int c = 0; c < kXC; ++c) {
-      const int off = base + (lane + 64 * c) * 8;
-      wv[c] = off < D ? load16(w + off) : v4i{0, 0, 0, 0};
-      xb[c] = base == 0 ? xv[c] : (off < D ? load16(xrow + off) : v4i{0, 0, 0, 0});
+  for (int c = 0; c < kXC; ++c) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc += double(bf16lo(uint32_t(xb[c][j])) * bf16lo(uint32_t(wv[c][j])));
+      acc += double(bf16hi(uint32_t(xb[c][j])) * bf16hi(uint32_t(wv[c][j])));
     }
-#pragma unroll
-    for (int c = 0; c < kXC; ++c)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc += double(bf16lo(uint32_t(xb[c][j])) * bf16lo(uint32_t(wv[c][j])));
-        acc += double(bf16hi(uint32_t(xb[c][j])) * bf16hi(uint32_t(wv[c][j])));
-      }
+    asm volatile("" : "+v"(acc));
   }
+  return acc;
+}
+
+__device__ __forceinline__ float wave_sum_f64(double acc) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, kWave);
   return float(acc);
 }
 
-constexpr int kRSlots = kMaxExperts / 64;
-constexpr float kChunkErr = float(kGateChunk + 1) / 8388608.0f;  // (chunk + 1) * 2^-23
+// Exact logits of the token row against NW weight rows w[0..NW-1]: every
+// row's loads of a chunk group are issued before any product, so NW rows cost
+// one memory round trip per chunk group.
+template <int NW>
+__device__ __forceinline__ void exact_logits(const v4i (&xv)[kXC], const uint16_t* __restrict__ xrow,
+                                             const uint16_t* const (&w)[NW], int D, int lane, float (&out)[NW]) {
+  double acc[NW];
+#pragma unroll
+  for (int n = 0; n < NW; ++n) acc[n] = 0.0;
+  {  // the first chunk group: the token row is in xv already
+    v4i wv[NW][kXC];
+#pragma unroll
+    for (int c = 0; c < kXC; ++c) {
+      const int off = (lane + 64 * c) * 8;
+#pragma unroll
+      for (int n = 0; n < NW; ++n) wv[n][c] = off < D ? load16(w[n] + off) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int n = 0; n < NW; ++n) acc[n] = exact_dot_lane(xv, wv[n], acc[n]);
+  }
+  for (int base = kXC * 512; base < D; base += kXC * 512) {
+    v4i wv[NW][kXC], xb[kXC];
+#pragma unroll
+    for (int c = 0; c < kXC; ++c) {
+      const int off = base + (lane + 64 * c) * 8;
+#pragma unroll
+      for (int n = 0; n < NW; ++n) wv[n][c] = off < D ? load16(w[n] + off) : v4i{0, 0, 0, 0};
+      xb[c] = off < D ? load16(xrow + off) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int n = 0; n < NW; ++n) acc[n] = exact_dot_lane(xb, wv[n], acc[n]);
+  }
+#pragma unroll
+  for (int n = 0; n < NW; ++n) out[n] = wave_sum_f64(acc[n]);
+}
 
-__global__ __launch_bounds__(256) void topk_refine_kernel(const uint16_t* __restrict__ x,
-                                                          const uint16_t* __restrict__ W,
-                                                          const float* __restrict__ approx,
-                                                          const float* __restrict__ absdot,
-                                                          const float* __restrict__ bias,
-                                                          const int32_t* __restrict__ tid2eid,
-                                                          const int64_t* __restrict__ input_ids, int64_t vocab,
-                                                          int T, int E, int D, int k, int score_func,
-                                                          float route_scale, float* __restrict__ weights,
-                                                          int32_t* __restrict__ idx) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + wave;
-  if (t >= T) return;
+constexpr float kChunkErr = float(kGateChunk + 1) / 8388608.0f;  // (chunk + 1) * 2^-23
+constexpr int kRefineWaves = 4;
+
+// G waves per token (4: one token per workgroup, for small batches; 1: four
+// tokens per workgroup, whose waves then keep more tokens in flight at large
+// T).  The waves of a token derive the same candidate set from the MFMA
+// logits' bounds (each computes a share of the bounds, met in LDS); the
+// candidates' exact logits are shared out over them (candidate r of the set,
+// in expert order, to wave r % G, two rows per round trip) and meet in LDS,
+// where the token's first wave picks the top-k.  kRSlots: 64-expert slots per
+// lane (E <= 64 kRSlots).
+template <int kRSlots, int G>
+__global__ __launch_bounds__(kRefineWaves * 64, 2) void topk_refine_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ W, const float* __restrict__ approx,
+    const float* __restrict__ absdot, const float* __restrict__ bias, const int32_t* __restrict__ tid2eid,
+    const int64_t* __restrict__ input_ids, int64_t vocab, int T, int E, int D, int k, int score_func,
+    float route_scale, float* __restrict__ weights, int32_t* __restrict__ idx) {
+  constexpr int NG = kRefineWaves / G;  // tokens per workgroup
+  __shared__ float s_sx[NG][kMaxExperts];  // exact score of a candidate (hash: of table slot j)
+  __shared__ float s_kx[NG][kMaxExperts];  // its selection key; -inf: not a candidate
+  __shared__ float s_lo[NG][kMaxExperts], s_hi[NG][kMaxExperts];  // key bounds (-inf past E)
+  __shared__ int s_list[kRefineWaves][kMaxExperts / G];            // each wave's candidates
+  __shared__ int s_hash[NG][17];  // hash: the table's experts (k <= 16); [16]: poison flag
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave / G, gw = wave % G;
+  const int t0 = blockIdx.x * NG + grp;
+  const bool live = t0 < T;
+  const int t = min(t0, T - 1);  // a spare wave works on the last token and stores nothing
   const uint16_t* xr = x + int64_t(t) * D;
   v4i xv[kXC];
 #pragma unroll
@@ -234,41 +280,66 @@ __global__ __launch_bounds__(256) void topk_refine_kernel(const uint16_t* __rest
     const int off = (lane + 64 * c) * 8;
     xv[c] = off < D ? load16(xr + off) : v4i{0, 0, 0, 0};
   }
+  for (int e = gw * 64 + lane; e < E; e += G * 64) {
+    s_kx[grp][e] = -INFINITY;
+    s_sx[grp][e] = 0.0f;
+  }
   int my_sel = 0;
-  float mine = 0.0f;  // exact score of the lane's slot (lane < k)
+  float mine = 0.0f;    // exact score of the lane's slot (lane < k)
   bool poison = false;  // hash id or table entry out of range: NaN weights, in-range reads
   if (tid2eid != nullptr) {
-    int64_t id = input_ids[t];
-    poison = id < 0 || id >= vocab;
-    id = poison ? 0 : id;
-    for (int j = 0; j < k; ++j) {
-      int e = tid2eid[id * k + j];
-      if (e < 0 || e >= E) {
-        poison = true;
-        e = 0;
+    if (gw == 0) {  // the k table slots, one per lane
+      int64_t id = input_ids[t];
+      const bool bad_id = id < 0 || id >= vocab;
+      id = bad_id ? 0 : id;
+      bool bad_e = false;
+      if (lane < k) {
+        const int e = tid2eid[id * k + lane];
+        bad_e = e < 0 || e >= E;
+        s_hash[grp][lane] = bad_e ? 0 : e;
       }
-      const float s = score_of(exact_logit(xv, xr, W + int64_t(e) * D, D, lane), score_func);
-      if (lane == j) {
-        my_sel = e;
-        mine = s;
-      }
+      const bool any_bad = bad_id || __ballot(bad_e) != 0ull;
+      if (lane == 0) s_hash[grp][16] = any_bad ? 1 : 0;
+    }
+    __syncthreads();
+    for (int j = gw; j < k; j += G) {
+      const uint16_t* const w1[1] = {W + int64_t(s_hash[grp][j]) * D};
+      float lg[1];
+      exact_logits<1>(xv, xr, w1, D, lane, lg);
+      if (lane == 0) s_sx[grp][j] = score_of(lg[0], score_func);
+    }
+    __syncthreads();
+    if (gw != 0 || !live) return;
+    poison = s_hash[grp][16] != 0;
+    if (lane < k) {
+      my_sel = s_hash[grp][lane];
+      mine = s_sx[grp][lane];
     }
   } else {
+    // key bounds, slot i by the token's wave i % G
     const float L = score_func == WZ_SCORE_SIGMOID ? 0.25f : 0.61f;
-    float lo[kRSlots], hi[kRSlots];
 #pragma unroll
-    for (int i = 0; i < kRSlots; ++i) {
+    for (int i = gw; i < kRSlots; i += G) {
       const int e = lane + 64 * i;
-      lo[i] = hi[i] = -INFINITY;
+      float l = -INFINITY, h = -INFINITY;
       if (e < E) {
         const float a = approx[int64_t(t) * E + e];
         const float S = absdot[int64_t(t) * E + e] * 1.001f;
         const float f = score_of(a, score_func);
         const float key = bias ? f + bias[e] : f;
-        const float G = L * (kChunkErr * S + 2.4e-7f * fabsf(a)) + 4.8e-7f * (fabsf(f) + fabsf(key)) + 1e-30f;
-        lo[i] = key - G;
-        hi[i] = key + G;
+        const float Gb = L * (kChunkErr * S + 2.4e-7f * fabsf(a)) + 4.8e-7f * (fabsf(f) + fabsf(key)) + 1e-30f;
+        l = key - Gb;
+        h = key + Gb;
       }
+      s_lo[grp][e] = l;
+      s_hi[grp][e] = h;
+    }
+    __syncthreads();  // bounds in LDS, s_kx cleared
+    float lo[kRSlots], hi[kRSlots];
+#pragma unroll
+    for (int i = 0; i < kRSlots; ++i) {
+      lo[i] = s_lo[grp][lane + 64 * i];
+      hi[i] = s_hi[grp][lane + 64 * i];
     }
     // theta = k-th largest lower bound
     unsigned taken = 0u;
@@ -284,23 +355,44 @@ __global__ __launch_bounds__(256) void topk_refine_kernel(const uint16_t* __rest
       theta = best.v;
       if ((best.i & 63) == lane) taken |= 1u << (best.i >> 6);
     }
-    // exact keys of the candidates (upper bound reaches theta)
+    // this wave's share of the candidates (upper bound reaches theta): the
+    // set in expert order, candidate r to wave r % G, listed in LDS
+    int r = 0;  // candidates in the slots so far
+#pragma unroll
+    for (int i = 0; i < kRSlots; ++i) {
+      const bool c = lane + 64 * i < E && hi[i] >= theta;
+      const unsigned long long m = __ballot(c);
+      const int R = r + __popcll(m & ((1ull << lane) - 1ull));  // this lane's candidate's rank
+      if (c && R % G == gw) s_list[wave][R / G] = lane + 64 * i;
+      r += __popcll(m);
+    }
+    const int n = (r - gw + G - 1) / G;  // ranks = gw (mod G) below r
+    // exact keys, two candidates per round trip (an odd last one is computed
+    // twice and stored once)
+#pragma unroll 1
+    for (int q = 0; q < n; q += 2) {
+      const int e0 = s_list[wave][q], e1 = s_list[wave][min(q + 1, n - 1)];
+      const uint16_t* const w2[2] = {W + int64_t(e0) * D, W + int64_t(e1) * D};
+      float lg[2];
+      exact_logits<2>(xv, xr, w2, D, lane, lg);
+      if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int e = h ? e1 : e0;
+          const float sc = score_of(lg[h], score_func);
+          s_sx[grp][e] = sc;
+          s_kx[grp][e] = bias ? sc + bias[e] : sc;
+        }
+      }
+    }
+    __syncthreads();
+    if (gw != 0 || !live) return;
     float sx[kRSlots], kx[kRSlots];
 #pragma unroll
     for (int i = 0; i < kRSlots; ++i) {
-      sx[i] = 0.0f;
-      kx[i] = -INFINITY;
-      unsigned long long m = __ballot(lane + 64 * i < E && hi[i] >= theta);
-      while (m) {
-        const int l = __ffsll(static_cast<long long>(m)) - 1;
-        m &= m - 1;
-        const int e = l + 64 * i;
-        const float s = score_of(exact_logit(xv, xr, W + int64_t(e) * D, D, lane), score_func);
-        if (lane == l) {
-          sx[i] = s;
-          kx[i] = bias ? s + bias[e] : s;
-        }
-      }
+      const int e = lane + 64 * i;
+      sx[i] = e < E ? s_sx[grp][e] : 0.0f;
+      kx[i] = e < E ? s_kx[grp][e] : -INFINITY;
     }
     // top-k of the exact keys (ties -> lower index)
     taken = 0u;
@@ -355,9 +447,27 @@ int launch_prefill_gate(const wz_moe_desc* d, const MoeWs& w, const void* x, con
       if (int rc = check_launch("moe gate")) return rc;
     }
   }
-  WZ_LAUNCH("moe_topk", stream, topk_refine_kernel, dim3(unsigned((T + 3) / 4)), dim3(256), 0, xb, gw, w.scores,
-            w.biased, d->tid2eid ? nullptr : d->gate_bias, d->tid2eid, input_ids, d->vocab, int(T), E, D, d->topk,
-            d->score_func, d->route_scale, w.weights, w.idx);
+  const float* gb = d->tid2eid ? nullptr : d->gate_bias;
+  // one token per workgroup below 1024 tokens (T = 128 / 512: route 48.6 /
+  // 59.7 -> 36.9 / 48.2 us), four per workgroup above (more tokens in flight)
+  const bool wide = T < 1024;
+  const unsigned grid = unsigned(wide ? T : (T + kRefineWaves - 1) / kRefineWaves);
+#define WZ_TOPK(KS, G)                                                                                     \
+  WZ_LAUNCH("moe_topk", stream, (topk_refine_kernel<KS, G>), dim3(grid), dim3(kRefineWaves * 64), 0, xb, gw, \
+            w.scores, w.biased, gb, d->tid2eid, input_ids, d->vocab, int(T), E, D, d->topk, d->score_func,     \
+            d->route_scale, w.weights, w.idx)
+  if (E <= 256) {
+    if (wide)
+      WZ_TOPK(4, kRefineWaves);
+    else
+      WZ_TOPK(4, 1);
+  } else {
+    if (wide)
+      WZ_TOPK(kMaxExperts / 64, kRefineWaves);
+    else
+      WZ_TOPK(kMaxExperts / 64, 1);
+  }
+#undef WZ_TOPK
   return check_launch("moe topk");
 }
 
