@@ -213,34 +213,42 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
                                                              int32_t* __restrict__ perm_token,
                                                              int32_t* __restrict__ perm_slot,
                                                              int32_t* __restrict__ pos) {
-  __shared__ int cnt[kMaxExperts];
-  __shared__ int base[kMaxExperts];
-  __shared__ int run[kMaxExperts];
-  __shared__ int wcnt[kRouteThreads / 64][kMaxExperts];
+  constexpr int kW = kRouteThreads / 64;  // waves
+  __shared__ int wcnt[kW][kMaxExperts];   // pairs of expert e in wave w's chunk, then their first slot
   __shared__ int wsum[128];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int P = T * k;
-  for (int e = tid; e < kMaxExperts; e += kRouteThreads) {
-    cnt[e] = 0;
-    run[e] = 0;
-  }
+  // wave w owns pairs [w C, (w + 1) C): its chunk in 64-pair rounds, so the
+  // placement below needs no barrier per round
+  const int C = (P + kW * 64 - 1) / (kW * 64) * 64;
+  const int p0 = wave * C, p1 = min(P, p0 + C);
+  for (int i = tid; i < kW * kMaxExperts; i += kRouteThreads) (&wcnt[0][0])[i] = 0;
   __syncthreads();
-  for (int p = tid; p < P; p += kRouteThreads) atomicAdd(&cnt[idx[p]], 1);
+  for (int p = p0 + lane; p < p1; p += 64) atomicAdd(&wcnt[wave][clampi(idx[p], 0, E - 1)], 1);
   __syncthreads();
-  // offsets and the active-expert list (E <= 1024 = block size)
-  int c = tid < E ? cnt[tid] : 0;
+  // per expert: its count, then each wave's first slot (expert base + the
+  // pairs of the waves before it); offsets and the active-expert list
+  // (E <= 1024 = block size)
+  int c = 0;
+  if (tid < E)
+    for (int w = 0; w < kW; ++w) c += wcnt[w][tid];
   int total;
-  int ex = block_excl_scan(c, wsum, total);
-  int flag = c > 0 ? 1 : 0;
+  const int ex = block_excl_scan(c, wsum, total);
+  const int flag = c > 0 ? 1 : 0;
   int nact;
-  int u = block_excl_scan(flag, wsum, nact);
+  const int u = block_excl_scan(flag, wsum, nact);
   if (tid < E) {
-    base[tid] = ex;
     offsets[tid] = ex;
     if (flag) {
       active[u] = tid;
       act_off[u] = ex;
       act_cnt[u] = c;
+    }
+    int run = ex;
+    for (int w = 0; w < kW; ++w) {
+      const int n = wcnt[w][tid];
+      wcnt[w][tid] = run;
+      run += n;
     }
   }
   if (tid == 0) {
@@ -248,14 +256,15 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
     n_active[0] = nact;
   }
   __syncthreads();
-  // stable placement, 1024 pairs per round
+  // stable placement: a pair's slot is its wave's next slot for its expert
+  // plus its rank among the round's lanes with the same expert
   int nbits = 1;
   while ((1 << nbits) < E) ++nbits;
   const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int c0 = 0; c0 < P; c0 += kRouteThreads) {
-    const int p = c0 + tid;
-    const bool valid = p < P;
-    const int e = valid ? idx[p] : 0;
+  for (int c0 = p0; c0 < p1; c0 += 64) {
+    const int p = c0 + lane;
+    const bool valid = p < p1;
+    const int e = valid ? clampi(idx[p], 0, E - 1) : 0;
     unsigned long long mask = __ballot(valid);
     if (!valid) mask = ~mask;
     for (int bit = 0; bit < nbits; ++bit) {
@@ -265,26 +274,14 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
     }
     const int rank = __popcll(mask & lt);
     const bool leader = (mask & lt) == 0ull;
-    for (int i = tid; i < (kRouteThreads / 64) * kMaxExperts; i += kRouteThreads)
-      (&wcnt[0][0])[i] = 0;
-    __syncthreads();
-    if (valid && leader) wcnt[wave][e] = __popcll(mask);
-    __syncthreads();
     if (valid) {
-      int before = run[e];
-      for (int w = 0; w < wave; ++w) before += wcnt[w][e];
-      const int q = base[e] + before + rank;
+      const int q = wcnt[wave][e] + rank;
       perm_token[q] = p / k;
       perm_slot[q] = p % k;
       pos[p] = q;
     }
-    __syncthreads();
-    for (int ee = tid; ee < E; ee += kRouteThreads) {
-      int s = 0;
-      for (int w = 0; w < kRouteThreads / 64; ++w) s += wcnt[w][ee];
-      run[ee] += s;
-    }
-    __syncthreads();
+    // every lane has read its slot base (program order within the wave)
+    if (valid && leader) wcnt[wave][e] += __popcll(mask);
   }
 }
 
