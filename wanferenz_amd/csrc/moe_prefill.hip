@@ -64,67 +64,115 @@ __device__ __forceinline__ v4i abs_bf16x8(v4i a) {
   return v4i{a[0] & 0x7FFF7FFF, a[1] & 0x7FFF7FFF, a[2] & 0x7FFF7FFF, a[3] & 0x7FFF7FFF};
 }
 
-// One workgroup per (16 tokens, 16 experts) tile; its 4 waves split K and
-// meet in LDS.  A lane loads 8 consecutive bf16 of its row for two 16x16x16
-// MFMAs; A and B use the same lane -> K assignment, so each K element's two
-// factors meet in one product.
-// One workgroup: 32 tokens x 64 experts; wave w owns expert tile w (16 experts)
-// for both 16-token tiles, over the full K, so a loaded W fragment feeds two
-// MFMAs and the token fragments are shared by the four waves through L1.
-__global__ __launch_bounds__(256) void gate_mfma_kernel(const uint16_t* __restrict__ x,
-                                                        const uint16_t* __restrict__ W,
-                                                        float* __restrict__ approx, float* __restrict__ absdot,
-                                                        int T, int E, int D) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// One workgroup: 32 tokens x 64 experts in four waves; wave w computes every
+// (16-token, 16-expert) tile of the block over K quarter w, so each token and
+// weight fragment is loaded once per workgroup (waves that split the experts
+// instead loaded every token fragment four times and took 48-51 us at
+// T = 2048, bound by L1 accesses).  Each 64-wide K chunk is summed from zero
+// by four MFMAs and added into the quarter's fp64 accumulator; the quarters
+// meet in LDS in quarter order.
+constexpr int kGateQ = 4;  // K quarters, one per wave
+__global__ __launch_bounds__(64 * kGateQ) void gate_mfma_kernel(const uint16_t* __restrict__ x,
+                                                               const uint16_t* __restrict__ W,
+                                                               float* __restrict__ approx,
+                                                               float* __restrict__ absdot, int T, int E, int D) {
+  __shared__ double red[kGateQ - 1][4][2][4][64];  // quarters 1.., expert tile, token tile, i, lane
+  __shared__ float reds[kGateQ - 1][4][2][4][64];
+  const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int egs = (E + 63) / 64;
   const int tg = blockIdx.x / egs, eg = blockIdx.x % egs;
   const int nl = lane & 15, g = lane >> 4;
-  const int ex = eg * 64 + wave * 16 + nl;
   // clamped rows: every load is unconditional; rows past T / E are never stored
-  const uint16_t* wr = W + int64_t(min(ex, E - 1)) * D;
+  const uint16_t* wr[4];
+#pragma unroll
+  for (int et = 0; et < 4; ++et) wr[et] = W + int64_t(min(eg * 64 + et * 16 + nl, E - 1)) * D;
   const uint16_t* xr0 = x + int64_t(min(tg * 32 + nl, T - 1)) * D;
   const uint16_t* xr1 = x + int64_t(min(tg * 32 + 16 + nl, T - 1)) * D;
-  double acc[2][4] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
-  v4f sabs[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  const int nch = D / kGateChunk, c0 = (q * nch) / kGateQ, c1 = ((q + 1) * nch) / kGateQ;
+  double acc[4][2][4];
+  v4f sabs[4][2];
   const v4f z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int k0 = 0; k0 < D; k0 += kGateChunk) {
-    v4i a0[2], a1[2], b[2];
+#pragma unroll
+  for (int et = 0; et < 4; ++et)
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      sabs[et][m] = z;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[et][m][i] = 0.0;
+    }
+#pragma unroll 2
+  for (int ch = c0; ch < c1; ++ch) {
+    const int k0 = ch * kGateChunk;
+    v4i a0[2], a1[2], b[4][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       a0[h] = load16(xr0 + k0 + 32 * h + 8 * g);
       a1[h] = load16(xr1 + k0 + 32 * h + 8 * g);
-      b[h] = load16(wr + k0 + 32 * h + 8 * g);
+#pragma unroll
+      for (int et = 0; et < 4; ++et) b[et][h] = load16(wr[et] + k0 + 32 * h + 8 * g);
     }
-    v4f p0 = z, p1 = z;
+    v4i a0a[2], a1a[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      p0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a0[h]), v4s_lo(b[h]), p0, 0, 0, 0);
-      p0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a0[h]), v4s_hi(b[h]), p0, 0, 0, 0);
-      p1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a1[h]), v4s_lo(b[h]), p1, 0, 0, 0);
-      p1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a1[h]), v4s_hi(b[h]), p1, 0, 0, 0);
-      const v4i a0a = abs_bf16x8(a0[h]), a1a = abs_bf16x8(a1[h]), ba = abs_bf16x8(b[h]);
-      sabs[0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a0a), v4s_lo(ba), sabs[0], 0, 0, 0);
-      sabs[0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a0a), v4s_hi(ba), sabs[0], 0, 0, 0);
-      sabs[1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a1a), v4s_lo(ba), sabs[1], 0, 0, 0);
-      sabs[1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a1a), v4s_hi(ba), sabs[1], 0, 0, 0);
+      a0a[h] = abs_bf16x8(a0[h]);
+      a1a[h] = abs_bf16x8(a1[h]);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[0][i] += double(p0[i]);
-      acc[1][i] += double(p1[i]);
-    }
-  }
+    for (int et = 0; et < 4; ++et) {
+      v4f p0 = z, p1 = z;
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
+      for (int h = 0; h < 2; ++h) {
+        p0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a0[h]), v4s_lo(b[et][h]), p0, 0, 0, 0);
+        p0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a0[h]), v4s_hi(b[et][h]), p0, 0, 0, 0);
+        p1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a1[h]), v4s_lo(b[et][h]), p1, 0, 0, 0);
+        p1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a1[h]), v4s_hi(b[et][h]), p1, 0, 0, 0);
+        const v4i ba = abs_bf16x8(b[et][h]);
+        sabs[et][0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a0a[h]), v4s_lo(ba), sabs[et][0], 0, 0, 0);
+        sabs[et][0] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a0a[h]), v4s_hi(ba), sabs[et][0], 0, 0, 0);
+        sabs[et][1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_lo(a1a[h]), v4s_lo(ba), sabs[et][1], 0, 0, 0);
+        sabs[et][1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4s_hi(a1a[h]), v4s_hi(ba), sabs[et][1], 0, 0, 0);
+      }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = tg * 32 + m * 16 + g * 4 + i;
-      if (t < T && ex < E) {
-        approx[int64_t(t) * E + ex] = float(acc[m][i]);
-        absdot[int64_t(t) * E + ex] = sabs[m][i];
+      for (int i = 0; i < 4; ++i) {
+        acc[et][0][i] += double(p0[i]);
+        acc[et][1][i] += double(p1[i]);
       }
     }
+  }
+  if (q > 0) {
+#pragma unroll
+    for (int et = 0; et < 4; ++et)
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          red[q - 1][et][m][i][lane] = acc[et][m][i];
+          reds[q - 1][et][m][i][lane] = sabs[et][m][i];
+        }
+  }
+  __syncthreads();
+  if (q > 0) return;
+#pragma unroll
+  for (int et = 0; et < 4; ++et) {
+    const int ex = eg * 64 + et * 16 + nl;
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        double v = acc[et][m][i];
+        float sv = sabs[et][m][i];
+#pragma unroll
+        for (int qq = 0; qq < kGateQ - 1; ++qq) {
+          v += red[qq][et][m][i][lane];
+          sv += reds[qq][et][m][i][lane];
+        }
+        const int t = tg * 32 + m * 16 + g * 4 + i;
+        if (t < T && ex < E) {
+          approx[int64_t(t) * E + ex] = float(v);
+          absdot[int64_t(t) * E + ex] = sv;
+        }
+      }
+  }
 }
 
 // Small T: one workgroup per 16 tokens x 16 experts, the four waves split K
@@ -442,8 +490,8 @@ int launch_prefill_gate(const wz_moe_desc* d, const MoeWs& w, const void* x, con
       if (int rc = check_launch("moe gate")) return rc;
     } else {
       const int64_t tiles = ((T + 31) / 32) * ((E + 63) / 64);
-      WZ_LAUNCH("moe_gate", stream, gate_mfma_kernel, dim3(unsigned(tiles)), dim3(256), 0, xb, gw, w.scores,
-                w.biased, int(T), E, D);
+      WZ_LAUNCH("moe_gate", stream, gate_mfma_kernel, dim3(unsigned(tiles)), dim3(64 * kGateQ), 0, xb, gw,
+                w.scores, w.biased, int(T), E, D);
       if (int rc = check_launch("moe gate")) return rc;
     }
   }
