@@ -624,7 +624,8 @@ struct BTiles {
 // the activation rows the N-blocks of an M-tile share.
 template <int MODE, bool CHAIN, int NM, bool KEEP>
 __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs& ws, int T, const TileRows& tr,
-                                               int nt, uint8_t (*a_s)[kPM * 128], float (*as_s)[256]) {
+                                               int nt, uint8_t (*a_s)[kPM * 128], float (*as_s)[256],
+                                               float (*am_s)[kPM]) {
   constexpr bool W13 = MODE < 2, DENSE = (MODE & 1) != 0;
   constexpr int WF = DENSE ? kFmtFp8 : kFmtFp4;
   // weight tiles per wave: routed w1/w3 4 (2 feature tiles x {w1, w3}); routed
@@ -736,6 +737,19 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
     }
   };
 
+  // routed w1/w3: the routing weight of each of this lane's output rows,
+  // requested now so the epilogue does not wait on three dependent loads
+  float wts[NM][4];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wts[m][i] = 0.0f;
+      if (MODE == 0) {
+        const int p = row0 + min(m * 16 + g * 4 + i, nrows - 1);
+        wts[m][i] = ws.weights[int64_t(clampi(ws.perm_token[p], 0, T - 1)) * k + clampi(ws.perm_slot[p], 0, k - 1)];
+      }
+    }
   v4f acc[NTW][NM];
 #pragma unroll
   for (int j = 0; j < NTW; ++j)
@@ -840,16 +854,19 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
 
   // epilogue
   if (W13) {
+    // h = SwiGLU (the routed rows times their routing weight), rounded to
+    // bf16 as the expert's intermediate is (architecture.py:739-741)
+    float hb[CPW][NM][4];
 #pragma unroll
     for (int q = 0; q < CPW; ++q) {
-      if (!jv[2 * q]) continue;
       const int f = ct[2 * q] * 16 + nl;
 #pragma unroll
       for (int m = 0; m < NM; ++m)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = m * 16 + g * 4 + i;
-          if (r < nrows) {
+          hb[q][m][i] = 0.0f;
+          if (jv[2 * q] && r < nrows) {
             float gv = bf16_round(acc[2 * q][m][i]), uv = bf16_round(acc[2 * q + 1][m][i]);
             if (d.swiglu_limit > 0.0f) {
               uv = clamp_keep_nan(uv, -d.swiglu_limit, d.swiglu_limit);
@@ -859,11 +876,52 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
             if (DENSE) {
               ws.sh_h[int64_t(row0 + r) * I + f] = f32_to_bf16(hv);
             } else {
-              const int p = row0 + r;
-              const float wt =
-                  ws.weights[int64_t(clampi(ws.perm_token[p], 0, T - 1)) * k + clampi(ws.perm_slot[p], 0, k - 1)];
-              ws.h[int64_t(p) * I + f] = f32_to_bf16(wt * hv);
+              hb[q][m][i] = bf16_round(wts[m][i] * hv);
             }
+          }
+        }
+    }
+    if (!DENSE) {
+      // act_quant of the routed h rows (torch_ops.py:33-49, the arithmetic of
+      // act_quant_kernel): this workgroup's 128 features [128 nt, +128) are
+      // exactly one quantisation block, so a row's amax is this lane's two
+      // features, then its 16 lanes, then the 4 waves through LDS; codes go
+      // to hq and the block scale to hs (no bf16 h and no hquant launch).
+      float am[NM][4];
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = 0.0f;
+#pragma unroll
+          for (int q = 0; q < CPW; ++q) v = absmax(v, hb[q][m][i]);
+          v = wave_absmax_xor(v, 1);
+          v = wave_absmax_xor(v, 2);
+          v = wave_absmax_xor(v, 4);
+          v = wave_absmax_xor(v, 8);
+          am[m][i] = v;
+          if (nl == 0) am_s[wave][m * 16 + g * 4 + i] = v;
+        }
+      __syncthreads();
+      const int KBh = I / 128;
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = m * 16 + g * 4 + i;
+          float amax = am[m][i];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) amax = absmax(amax, am_s[w][r]);
+          const ActScale sc = act_scale(amax, a_pow2);
+          if (r < nrows) {
+            const int64_t p = row0 + r;
+#pragma unroll
+            for (int q = 0; q < CPW; ++q) {
+              if (!jv[2 * q]) continue;
+              const uint32_t b = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(quant_div(hb[q][m][i], sc, a_pow2), 0.0f, 0, false));
+              ws.hq[p * I + ct[2 * q] * 16 + nl] = uint8_t(b & 0xFFu);
+            }
+            if (wave == 0 && nl == 0) ws.hs[p * KBh + nt] = sc.s;
           }
         }
     }
@@ -888,24 +946,24 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
 // tiles of 16, so its MFMA loops carry no row branches.
 template <int MODE, bool CHAIN>
 __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws, int T, int mt, int nt,
-                                          uint8_t (*a_s)[kPM * 128], float (*as_s)[256]) {
+                                          uint8_t (*a_s)[kPM * 128], float (*as_s)[256], float (*am_s)[kPM]) {
   TileRows tr;
   if (!tile_of(ws, mt, (MODE & 1) != 0, T, T * d.topk, d.n_experts, tr)) return;
   static_assert(kPM == 64, "tile heights up to 4 row tiles");
   if (tr.keep) {
     if (tr.nrows <= 16)
-      gemm_tile_body<MODE, CHAIN, 1, true>(d, ws, T, tr, nt, a_s, as_s);
+      gemm_tile_body<MODE, CHAIN, 1, true>(d, ws, T, tr, nt, a_s, as_s, am_s);
     else if (tr.nrows <= 32)
-      gemm_tile_body<MODE, CHAIN, 2, true>(d, ws, T, tr, nt, a_s, as_s);
+      gemm_tile_body<MODE, CHAIN, 2, true>(d, ws, T, tr, nt, a_s, as_s, am_s);
     else
-      gemm_tile_body<MODE, CHAIN, 4, true>(d, ws, T, tr, nt, a_s, as_s);
+      gemm_tile_body<MODE, CHAIN, 4, true>(d, ws, T, tr, nt, a_s, as_s, am_s);
   } else {
     if (tr.nrows <= 16)
-      gemm_tile_body<MODE, CHAIN, 1, false>(d, ws, T, tr, nt, a_s, as_s);
+      gemm_tile_body<MODE, CHAIN, 1, false>(d, ws, T, tr, nt, a_s, as_s, am_s);
     else if (tr.nrows <= 32)
-      gemm_tile_body<MODE, CHAIN, 2, false>(d, ws, T, tr, nt, a_s, as_s);
+      gemm_tile_body<MODE, CHAIN, 2, false>(d, ws, T, tr, nt, a_s, as_s, am_s);
     else
-      gemm_tile_body<MODE, CHAIN, 4, false>(d, ws, T, tr, nt, a_s, as_s);
+      gemm_tile_body<MODE, CHAIN, 4, false>(d, ws, T, tr, nt, a_s, as_s, am_s);
   }
 }
 
@@ -962,16 +1020,17 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     wz_moe_desc d, MoeWs ws, int T, int nblk, int nblk_dense, int dense_blocks, int gm, int gn) {
   __shared__ __align__(1024) uint8_t a_s[kNA][kPM * 128];
   __shared__ __align__(16) float as_s[kNA][256];
+  __shared__ float am_s[4][kPM];  // w1/w3 epilogue: each wave's row amax of its features
   const int b = blockIdx.x;
   if (b < dense_blocks) {
-    gemm_tile<W13 ? 1 : 3, CS>(d, ws, T, b / nblk_dense, b % nblk_dense, a_s, as_s);
+    gemm_tile<W13 ? 1 : 3, CS>(d, ws, T, b / nblk_dense, b % nblk_dense, a_s, as_s, am_s);
   } else {
     const int n = ws.n_mt[0] * nblk;  // routed blocks with work
     if (b - dense_blocks >= n) return;
     const int r = xcd_runs(b, dense_blocks, n);
     int mt, nt;
     tile_order(r, ws.n_mt[0], nblk, gm, gn, mt, nt);
-    gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, mt, nt, a_s, as_s);
+    gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, mt, nt, a_s, as_s, am_s);
   }
 }
 
@@ -1018,8 +1077,8 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
     }
     if (int rc = check_launch("moe w13")) return rc;
   }
+  // the routed h rows are quantised in the w1/w3 epilogue; the shared rows here
   if (only < 0 || only == WZ_STAGE_HQUANT) {
-    if (int rc = launch_act_quant(w.h, P, I, w.hq, w.hs, qkind, stream)) return rc;
     if (int rc = launch_act_quant(w.sh_h, T, I, w.hq + P * I, w.hs + P * (I / 128), qkind, stream)) return rc;
   }
   if (only < 0 || only == WZ_STAGE_W2) {
