@@ -212,7 +212,10 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
                                                              int32_t* __restrict__ n_active,
                                                              int32_t* __restrict__ perm_token,
                                                              int32_t* __restrict__ perm_slot,
-                                                             int32_t* __restrict__ pos) {
+                                                             int32_t* __restrict__ pos, int32_t* __restrict__ mt_u,
+                                                             int32_t* __restrict__ mt_row0,
+                                                             int32_t* __restrict__ mt_n, int32_t* __restrict__ n_mt,
+                                                             int mt_cap) {
   constexpr int kW = kRouteThreads / 64;  // waves
   __shared__ int wcnt[kW][kMaxExperts];   // pairs of expert e in wave w's chunk, then their first slot
   __shared__ int wsum[128];
@@ -255,6 +258,17 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
     offsets[E] = total;
     n_active[0] = nact;
   }
+  // the M-tile table of the prefill GEMMs: each active expert's pair rows cut
+  // into tiles of kPrefillTileRows, in active order
+  const int ntile = flag ? (c + kPrefillTileRows - 1) / kPrefillTileRows : 0;
+  int ntiles;
+  const int mt0 = block_excl_scan(ntile, wsum, ntiles);
+  for (int i = 0; i < ntile && mt0 + i < mt_cap; ++i) {
+    mt_u[mt0 + i] = u;
+    mt_row0[mt0 + i] = ex + i * kPrefillTileRows;
+    mt_n[mt0 + i] = min(kPrefillTileRows, c - i * kPrefillTileRows);
+  }
+  if (tid == 0) n_mt[0] = min(ntiles, mt_cap);
   __syncthreads();
   // stable placement: a pair's slot is its wave's next slot for its expert
   // plus its rank among the round's lanes with the same expert
@@ -412,8 +426,10 @@ static int launch_routing(const wz_moe_desc* d, const MoeWs& w, const void* x,
               d->route_scale, w.weights, w.idx);
     if (int rc = check_launch("moe topk")) return rc;
   }
+  const int64_t P = T * k, mt_cap = P / kPrefillTileRows + (P < E ? P : E) + 1;
   WZ_LAUNCH("moe_perm", stream, perm_kernel, dim3(1), dim3(kRouteThreads), 0, w.idx, int(T), E, k, w.offsets,
-            w.active, w.act_off, w.act_cnt, w.n_active, w.perm_token, w.perm_slot, w.pos);
+            w.active, w.act_off, w.act_cnt, w.n_active, w.perm_token, w.perm_slot, w.pos, w.mt_u, w.mt_row0,
+            w.mt_n, w.n_mt, int(mt_cap));
   return check_launch("moe perm");
 }
 

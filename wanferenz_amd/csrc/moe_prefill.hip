@@ -1,7 +1,8 @@
 // MoE prefill path (T > 16 tokens): expert-grouped MFMA GEMMs over the
 // canonical (expert, token, slot) pair order produced by the routing kernels.
 //
-//   mtile     each active expert's pair rows cut into tiles of 64 rows.
+//   (the routing's perm_kernel also cuts each active expert's pair rows into
+//   M-tiles of 64 rows)
 //   xquant    act_quant(x) once for all experts (quant.hip).
 //   w13       per (M-tile, 64 intermediate features): the gathered 128 fp8
 //             activation rows of one 128-wide K-block are staged in LDS; each
@@ -519,35 +520,6 @@ int launch_prefill_gate(const wz_moe_desc* d, const MoeWs& w, const void* x, con
   return check_launch("moe topk");
 }
 
-// ----------------------------------------------------------- M-tile table ---
-
-// One workgroup: cut each active expert's pair rows into tiles of kPM.
-__global__ __launch_bounds__(1024) void mtile_kernel(MoeWs ws, int E, int P, int mt_cap) {
-  __shared__ int wsum[16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n_act = min(ws.n_active[0], E);
-  const int c = tid < n_act ? clampi(ws.act_cnt[tid], 0, P) : 0;
-  const int nt = (c + kPM - 1) / kPM;
-  int inc = nt;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int o = __shfl_up(inc, d, kWave);
-    if (lane >= d) inc += o;
-  }
-  if (lane == 63) wsum[wave] = inc;
-  __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += wsum[w];
-  const int first = base + inc - nt;
-  const int row0 = tid < n_act ? ws.act_off[tid] : 0;
-  for (int i = 0; i < nt && first + i < mt_cap; ++i) {
-    ws.mt_u[first + i] = tid;
-    ws.mt_row0[first + i] = row0 + i * kPM;
-    ws.mt_n[first + i] = min(kPM, c - i * kPM);
-  }
-  if (tid == 1023) ws.n_mt[0] = min(base + inc, mt_cap);
-}
-
 // ------------------------------------------------------------ tile GEMMs ---
 
 struct TileRows {
@@ -1049,8 +1021,6 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
   const int qkind = d->act_scale_kind == WZ_SCALE_F32 ? WZ_SCALE_F32 : WZ_SCALE_UE8M0_F32;
   const int64_t mt_max = prefill_mt_max(P, E), mt_dense = (T + kPM - 1) / kPM;
   if (only < 0 || only == WZ_STAGE_ROUTE) {
-    WZ_LAUNCH("moe_mtile", stream, mtile_kernel, dim3(1), dim3(1024), 0, w, E, int(P), int(mt_max));
-    if (int rc = check_launch("moe mtile")) return rc;
     if (int rc = launch_act_quant(x, T, D, w.xq, w.xs, qkind, stream)) return rc;
   }
   // column tiles of 16 per WG: routed w1/w3 4 waves x 2 feature tiles, routed w2
