@@ -301,44 +301,61 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
 
 // --------------------------------------------------------------- combine ----
 
-__global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int D,
-                                                      uint16_t* __restrict__ y) {
+// One workgroup per (token, 2048 columns).  The token's pair rows are put in
+// ascending permuted position (= ascending expert id) once, by its first wave,
+// in LDS; a repeated expert of a hash-routed token counts once, by its last
+// slot (the row a decode step computes; architecture.py:790 index_put keeps
+// the last write).  Each thread then requests its 8 columns of all KMAX rows
+// at once (rows past k repeat the last one and are not added) and sums them
+// in that order, then adds the shared expert's row.
+template <int KMAX>
+__global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int D, uint16_t* __restrict__ y) {
+  __shared__ int s_p[KMAX];
+  __shared__ int s_use[KMAX];
   const int t = blockIdx.y;
   const int c = blockIdx.x * 256 + threadIdx.x;  // 8-column chunk
-  if (c * 8 >= D) return;
-  int ps[16];
   const int P = gridDim.y * k;
-  for (int j = 0; j < k; ++j) ps[j] = clampi(ws.pos[int64_t(t) * k + j], 0, P - 1);
-  // ascending permuted position == ascending expert id
-  for (int i = 1; i < k; ++i) {
-    int v = ps[i], j = i - 1;
-    while (j >= 0 && ps[j] > v) {
-      ps[j + 1] = ps[j];
-      --j;
+  if (threadIdx.x < 64) {
+    const int j = threadIdx.x;
+    const int p = j < k ? clampi(ws.pos[int64_t(t) * k + j], 0, P - 1) : 0x7FFFFFFF;
+    const int e = j < k ? ws.idx[int64_t(t) * k + j] : -1;
+    int rank = 0;  // positions are distinct: rank = slots with a lower position
+#pragma unroll
+    for (int jj = 0; jj < KMAX; ++jj) rank += __shfl(p, jj, kWave) < p ? 1 : 0;
+    // the slot ranked just above (same expert there: skip this one)
+    int e_next = -2;
+#pragma unroll
+    for (int jj = 0; jj < KMAX; ++jj) {
+      const int pj = __shfl(p, jj, kWave), ej = __shfl(e, jj, kWave);
+      int rj = 0;
+#pragma unroll
+      for (int q = 0; q < KMAX; ++q) rj += __shfl(p, q, kWave) < pj ? 1 : 0;
+      if (jj < k && rj == rank + 1) e_next = ej;
     }
-    ps[j + 1] = v;
+    if (j < k) {
+      s_p[rank] = p;
+      s_use[rank] = e_next == e ? 0 : 1;
+    }
   }
+  __syncthreads();
+  if (c * 8 >= D) return;
+  v4i v[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) v[r] = load16(ws.out2 + int64_t(s_p[min(r, k - 1)]) * D + c * 8);
+  const v4i sv = load16(ws.sh_out + int64_t(t) * D + c * 8);
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  for (int j = 0; j < k; ++j) {
-    const int p = ps[j];
-    // a repeated expert of a hash-routed token counts once: its last slot (the row
-    // a decode step computes; architecture.py:790 index_put keeps the last write)
-    if (j + 1 < k) {
-      const int pn = ps[j + 1];
-      const int pe = ws.idx[int64_t(clampi(ws.perm_token[p], 0, gridDim.y - 1)) * k + clampi(ws.perm_slot[p], 0, k - 1)];
-      const int ne = ws.idx[int64_t(clampi(ws.perm_token[pn], 0, gridDim.y - 1)) * k + clampi(ws.perm_slot[pn], 0, k - 1)];
-      if (pe == ne) continue;
-    }
-    const v4i v = load16(ws.out2 + int64_t(p) * D + c * 8);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[2 * i] += bf16lo(uint32_t(v[i]));
-      acc[2 * i + 1] += bf16hi(uint32_t(v[i]));
+  for (int r = 0; r < KMAX; ++r) {
+    if (r < k && s_use[r]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += bf16lo(uint32_t(v[r][i]));
+        acc[2 * i + 1] += bf16hi(uint32_t(v[r][i]));
+      }
     }
   }
-  const v4i sv = load16(ws.sh_out + int64_t(t) * D + c * 8);
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -349,10 +366,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int
   *reinterpret_cast<v4i*>(y + int64_t(t) * D + c * 8) = v4i{int(o[0]), int(o[1]), int(o[2]), int(o[3])};
 }
 
-// y = combine of the routed rows in out2 and the shared rows in sh_out.
 int launch_combine(const MoeWs& w, int64_t T, int k, int D, void* y, hipStream_t stream) {
-  WZ_LAUNCH("moe_combine", stream, combine_kernel, dim3(unsigned((D / 8 + 255) / 256), unsigned(T)), dim3(256), 0,
-            w, k, D, static_cast<uint16_t*>(y));
+  const dim3 grid(unsigned((D / 8 + 255) / 256), unsigned(T));
+  if (k <= 8) {
+    WZ_LAUNCH("moe_combine", stream, combine_kernel<8>, grid, dim3(256), 0, w, k, D, static_cast<uint16_t*>(y));
+  } else {
+    WZ_LAUNCH("moe_combine", stream, combine_kernel<16>, grid, dim3(256), 0, w, k, D, static_cast<uint16_t*>(y));
+  }
   return check_launch("moe combine");
 }
 
