@@ -607,10 +607,12 @@ def measure_hot_experts(layers, dev, T=2048):
 
 
 def measure_fp4_gemm_2048(dev, reps=10):
-    """One expert's GEMMs alone at M = 2048 rows (wz_fp4_gemm: e4m3 activations with
-    ue8m0 block scales x MXFP4 weights): w1|w3 (N = 2I, K = D) and w2 (N = D, K = I).
-    Two weight copies alternate; flops = 2 M N K; rate against the e4m3 x e2m1
-    scaled-MFMA rate (the FP8 rate, 5.0 PFLOP/s) and the FP4 peak."""
+    """One expert's GEMMs alone at M = 2048 rows (e4m3 activations with ue8m0 block
+    scales x MXFP4 weights): w1|w3 (N = 2I, K = D) and w2 (N = D, K = I), through the
+    packed-weight tile GEMM (wz_fp4_gemm_packed, the weight relaid once by
+    wz_fp4_pack) and through the row-major wz_fp4_gemm.  Two weight copies
+    alternate; flops = 2 M N K; rate against the e4m3 x e2m1 scaled-MFMA rate (the
+    FP8 rate, 5.0 PFLOP/s) and the FP4 peak."""
     import torch
 
     from wanferenz_amd import kernels, synth
@@ -628,16 +630,25 @@ def measure_fp4_gemm_2048(dev, reps=10):
             s = torch.empty(Nn, K // 32, dtype=torch.uint8, device=dev)
             synth.device_fill(s, synth.stream_key(r, synth.S_W13_S), synth.FILL_E8M0, 118, 122)
             ws.append((w.view(torch.float4_e2m1fn_x2), s.view(torch.float8_e8m0fnu)))
+        packed = [kernels.PackedFp4Linear(w, s).reserve(M, torch.float8_e8m0fnu) for w, s in ws]
+        out = torch.empty(M, Nn, dtype=torch.bfloat16, device=dev)
 
-        def launches():
+        def launches_packed():
+            for lin in packed:
+                lin.gemm(q, qs, out=out)
+
+        def launches_rowmajor():
             for w, s in ws:
                 kernels.fp4_gemm(q, qs, w, s, torch.float8_e8m0fnu)
 
-        us = graph_timed(launches, reps) / len(ws)
-        tf = 2.0 * M * Nn * K / (us * 1e-6) / 1e12
-        res[name] = {"M": M, "N": Nn, "K": K, "us": round(us, 2), "TFLOP_s": round(tf, 1),
-                     "mfma_frac_fp8_rate": round(tf / FP8_PEAK_TFLOPS, 4),
-                     "mfma_frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4)}
+        entry = {"M": M, "N": Nn, "K": K}
+        for tag, fn in (("packed", launches_packed), ("rowmajor", launches_rowmajor)):
+            us = graph_timed(fn, reps) / len(ws)
+            tf = 2.0 * M * Nn * K / (us * 1e-6) / 1e12
+            entry[tag] = {"us": round(us, 2), "TFLOP_s": round(tf, 1),
+                          "mfma_frac_fp8_rate": round(tf / FP8_PEAK_TFLOPS, 4),
+                          "mfma_frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4)}
+        res[name] = entry
     return res
 
 

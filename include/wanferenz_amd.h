@@ -135,6 +135,24 @@ int wz_fp4_gemm(const void* a_e4m3, const void* a_s, const void* w_fp4x2, const 
                 void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
                 hipStream_t stream);
 
+/* fp4_gemm on a packed weight, for row counts past decode (the M = 2048 product of
+ * one prefill expert): the same product as wz_fp4_gemm — reference.py:572-591 /
+ * torch_ops.py:102-108 — served by the tile GEMM of the MoE prefill instead of the
+ * row-major skinny kernel.  wz_fp4_pack relays w_fp4x2 [N, K/2] and w_s_e8m0
+ * [N, K/32] once (N % 16 == 0, K % 128 == 0) into the 16-row x 128-K tile format
+ * of the expert banks: packed N*K/2 bytes, packed_s wz_fp4_packed_scale_bytes(N, K)
+ * bytes — the relayout fp4_grouped._relayout_moe does for its bank, for one
+ * weight (fp4_grouped.py:142-188).  ws must hold
+ * wz_fp4_gemm_packed_workspace_bytes(M, K, act_scale_kind) bytes (nonzero only
+ * for e8m0 activation scales). */
+size_t wz_fp4_packed_scale_bytes(int64_t N, int64_t K);
+int wz_fp4_pack(const void* w_fp4x2, const void* w_s_e8m0, int64_t N, int64_t K, void* packed, void* packed_s,
+                hipStream_t stream);
+size_t wz_fp4_gemm_packed_workspace_bytes(int64_t M, int64_t K, int act_scale_kind);
+int wz_fp4_gemm_packed(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_packed_s,
+                       void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind, void* ws,
+                       size_t ws_bytes, hipStream_t stream);
+
 /* Grouped MXFP4 GEMM — grouped_fp4_gemm(a, a_s, w, w_s, scale_dtype),
  * fp4_grouped.py:96-128: row g of a against its own weight, C[g, :] =
  * dequant(a[g]) @ (e2m1(w[g]) * w_s[g])^T, i.e. fp4_gemm of one row per expert

@@ -150,6 +150,38 @@ def test_fp4_gemm_exact(gpu, M, N, K):
     assert np.array_equal(got, bf16_bits(ref))
 
 
+@pytest.mark.parametrize("act_fmt", ["ue8m0", None])
+@pytest.mark.parametrize("M,N,K", [(20, 256, 1024), (130, 128, 2048), (200, 384, 4096), (64, 16, 512)])
+def test_fp4_gemm_packed_random(gpu, act_fmt, M, N, K):
+    """fp4_gemm on the packed weight (the tile GEMM of the prefill) against the oracle."""
+    xb = _x(M + 5 * N + K, M, K)
+    sd = torch.float8_e8m0fnu if act_fmt else torch.float32
+    x = bf16_tensor(xb, gpu)
+    q, s = kernels.act_quant(x, 128, act_fmt, sd)
+    w, ws = _fp4_weight(N * 5 + K, N, K)
+    lin = kernels.PackedFp4Linear(u8_tensor(w, gpu, torch.float4_e2m1fn_x2), u8_tensor(ws, gpu, torch.float8_e8m0fnu))
+    got = f32_of_bf16(lin.gemm(q, s))
+    rq, rs = om.act_quant(from_bf16_bits(xb), 128, act_fmt is not None)
+    ref = om.fp4_gemm(rq, rs, w, e8m0_decode(ws))
+    rel, cos = _close(got, ref)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    assert (got == ref).mean() > 0.9, (got == ref).mean()
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 128, 1024), (100, 256, 2048), (64, 128, 4096)])
+def test_fp4_gemm_packed_exact(gpu, M, N, K):
+    """Small codes and unit scales through the packed tile GEMM: bit-exact bf16."""
+    a_codes = _exact_codes(M * K + 3, M * K, [0x00, 0x30, 0xB0, 0x38, 0xB8, 0x3C, 0xBC, 0x40, 0xC0]).reshape(M, K)
+    w = synth.fill_u8(synth.stream_key(N + 3, 7), 0, N * K // 2).reshape(N, K // 2)
+    ws = np.full((N, K // 32), 127, np.uint8)
+    a_s = np.full((M, K // 128), 127, np.uint8)
+    lin = kernels.PackedFp4Linear(u8_tensor(w, gpu, torch.float4_e2m1fn_x2), u8_tensor(ws, gpu, torch.float8_e8m0fnu))
+    c = lin.gemm(u8_tensor(a_codes, gpu, torch.float8_e4m3fn), u8_tensor(a_s, gpu, torch.float8_e8m0fnu))
+    from oracle.numerics import bf16_bits
+    ref = om.fp4_gemm(a_codes, e8m0_decode(a_s), w, e8m0_decode(ws))
+    assert np.array_equal(bits16(c), bf16_bits(ref))
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 128, 1024), (7, 256, 2048), (16, 128, 4096)])
 def test_fp8_gemm_exact(gpu, M, N, K):
     codes = [0x00, 0x30, 0xB0, 0x38, 0xB8, 0x3C, 0xBC, 0x40, 0xC0]

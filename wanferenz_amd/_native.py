@@ -25,6 +25,10 @@ SIGNATURES = {
     "wz_fp8_linear": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P]),
     "wz_fp4_gemm": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P]),
     "wz_grouped_fp4_gemm": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P]),
+    "wz_fp4_packed_scale_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "wz_fp4_pack": (_I, [_P, _P, _I64, _I64, _P, _P, _P]),
+    "wz_fp4_gemm_packed_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I]),
+    "wz_fp4_gemm_packed": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P, ctypes.c_size_t, _P]),
     "wz_fp8_pack": (_I, [_P, _I64, _I64, _P, _P]),
     "wz_fp8_linear_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "wz_fp8_linear_packed": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, ctypes.c_size_t, _P]),

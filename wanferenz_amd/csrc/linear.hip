@@ -27,6 +27,8 @@ int launch_act_quant(const void* x, int64_t rows, int64_t K, uint8_t* q, void* s
 int launch_pack_fp8(const void* w, int64_t N, int64_t K, void* dst, hipStream_t stream);
 int launch_dense_fp8(const uint8_t* wp, const void* w_s, int w_kind, const uint8_t* xq, const float* xs,
                      bool a_pow2, uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+int launch_dense_fp4(const uint8_t* wp, const uint32_t* wp_s, const uint8_t* xq, const float* xs, bool a_pow2,
+                     uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 constexpr int kGvMaxM = 16;
 
@@ -444,4 +446,39 @@ extern "C" int wz_fp8_gemm_packed_pair(const void* a_e4m3, const void* a_s, cons
   return gemm_packed("fp8_gemm_packed_pair", a_e4m3, a_s, static_cast<const uint8_t*>(w_packed) + size_t(N0) * K,
                      static_cast<const uint8_t*>(w_s) + size_t(N0 / 128) * size_t((K + 127) / 128) * sbytes,
                      nullptr, c1_bf16, M, N - N0, K, act_scale_kind, w_scale_kind, ws, ws_bytes, stream);
+}
+
+extern "C" size_t wz_fp4_gemm_packed_workspace_bytes(int64_t M, int64_t K, int act_scale_kind) {
+  if (M <= 0 || K <= 0) return 0;
+  return act_scale_kind == WZ_SCALE_UE8M0 ? size_t(M) * size_t(K / 128) * 4 : 0;
+}
+
+extern "C" int wz_fp4_gemm_packed(const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_packed_s,
+                                  void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind, void* ws,
+                                  size_t ws_bytes, hipStream_t stream) {
+  using namespace wz;
+  if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 128)
+    return set_error(WZ_EINVAL, "fp4_gemm_packed: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
+                     (long long)K);
+  if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
+    return set_error(WZ_EINVAL, "fp4_gemm_packed: dimension too large");
+  if (act_scale_kind < WZ_SCALE_F32 || act_scale_kind > WZ_SCALE_UE8M0_F32)
+    return set_error(WZ_EINVAL, "fp4_gemm_packed: unknown activation scale kind %d", act_scale_kind);
+  if (M == 0) return WZ_OK;
+  if (!a_e4m3 || !a_s || !w_packed || !w_packed_s || !c_bf16) return set_error(WZ_EINVAL, "fp4_gemm_packed: null pointer");
+  const float* xs = static_cast<const float*>(a_s);
+  if (act_scale_kind == WZ_SCALE_UE8M0) {
+    const size_t need = wz_fp4_gemm_packed_workspace_bytes(M, K, act_scale_kind);
+    if (!ws || ws_bytes < need)
+      return set_error(WZ_ESPACE, "fp4_gemm_packed: workspace of %zu bytes needed for M=%lld K=%lld, got %zu", need,
+                       (long long)M, (long long)K, ws_bytes);
+    const int64_t n = M * (K / 128);
+    WZ_LAUNCH("e8m0_to_f32", stream, e8m0_to_f32_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+              static_cast<const uint8_t*>(a_s), static_cast<float*>(ws), n);
+    if (int rc = check_launch("fp4_gemm_packed scales")) return rc;
+    xs = static_cast<const float*>(ws);
+  }
+  return launch_dense_fp4(static_cast<const uint8_t*>(w_packed), static_cast<const uint32_t*>(w_packed_s),
+                          static_cast<const uint8_t*>(a_e4m3), xs, act_scale_kind != WZ_SCALE_F32,
+                          static_cast<uint16_t*>(c_bf16), M, N, K, stream);
 }

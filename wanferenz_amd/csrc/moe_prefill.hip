@@ -579,6 +579,8 @@ struct BTiles {
 //   MODE 1: shared w1/w3 (packed FP8) over token rows        -> SwiGLU -> sh_h
 //   MODE 2: routed w2 (packed MXFP4) over h rows             -> out2
 //   MODE 3: shared w2 (packed FP8) over shared h rows        -> sh_out
+//   MODE 4: a dense MXFP4 linear (w2's tile format, one "expert") over rows
+//           in order                                         -> sh_out
 // A wave owns NTW weight tiles of 16 output columns (routed w13: 4, i.e. 2
 // feature tiles x {w1, w3}; routed w2: 2 column tiles; shared FP8 tiles are
 // twice the bytes, so 2), and one A operand read from LDS feeds NTW MFMAs.
@@ -598,12 +600,14 @@ template <int MODE, bool CHAIN, int NM, bool KEEP>
 __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs& ws, int T, const TileRows& tr,
                                                int nt, uint8_t (*a_s)[kPM * 128], float (*as_s)[256],
                                                float (*am_s)[kPM]) {
-  constexpr bool W13 = MODE < 2, DENSE = (MODE & 1) != 0;
+  // DENSE: FP8 weights (the shared expert, an FP8 linear); DROWS: rows in
+  // token order (no M-tile table)
+  constexpr bool W13 = MODE < 2, DENSE = MODE == 1 || MODE == 3, DROWS = DENSE || MODE == 4;
   constexpr int WF = DENSE ? kFmtFp8 : kFmtFp4;
   // weight tiles per wave: routed w1/w3 4 (2 feature tiles x {w1, w3}); routed
   // w2 2 (4 spilled registers at two workgroups per CU and measured 7 % slower);
   // FP8 shared tiles, twice the bytes, 2
-  constexpr int NTW = (DENSE || MODE == 2) ? 2 : 4;
+  constexpr int NTW = (DENSE || MODE >= 2) ? 2 : 4;
   constexpr int CPW = W13 ? NTW / 2 : NTW;    // 16-column output tiles per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = lane & 15, g = lane >> 4;
@@ -677,7 +681,7 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
         const uint32_t* sw = static_cast<const uint32_t*>(d.w13p_s) + ((t * KG + (kb >> 2)) * 2 + which[j]) * 64;
         b.sw[j] = sw[lane];
         b.f[j] = 1.0f;
-      } else if (MODE == 2) {
+      } else if (MODE == 2 || MODE == 4) {
         const int64_t t = int64_t(e) * NCT + cl[j];
         const uint8_t* w = static_cast<const uint8_t*>(d.w2p) + (t * KB + kb) * 1024;
         b.lo[j] = wload(w + lane * 16);
@@ -898,7 +902,7 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
         }
     }
   } else {
-    uint16_t* out = DENSE ? ws.sh_out : ws.out2;
+    uint16_t* out = DROWS ? ws.sh_out : ws.out2;
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
       if (!jv[j]) continue;
@@ -920,7 +924,7 @@ template <int MODE, bool CHAIN>
 __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws, int T, int mt, int nt,
                                           uint8_t (*a_s)[kPM * 128], float (*as_s)[256], float (*am_s)[kPM]) {
   TileRows tr;
-  if (!tile_of(ws, mt, (MODE & 1) != 0, T, T * d.topk, d.n_experts, tr)) return;
+  if (!tile_of(ws, mt, MODE == 1 || MODE == 3 || MODE == 4, T, T * d.topk, d.n_experts, tr)) return;
   static_assert(kPM == 64, "tile heights up to 4 row tiles");
   if (tr.keep) {
     if (tr.nrows <= 16)
@@ -1004,6 +1008,18 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     tile_order(r, ws.n_mt[0], nblk, gm, gn, mt, nt);
     gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, mt, nt, a_s, as_s, am_s);
   }
+}
+
+// A dense MXFP4 linear in tiles: block b = (M-tile b / nblk, N-block b % nblk).
+// CHAIN: power-of-two activation scales (they ride in the MFMA with the e8m0
+// weight scales).
+template <bool CHAIN>
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void dense_fp4_kernel(
+    wz_moe_desc d, MoeWs ws, int M, int nblk) {
+  __shared__ __align__(1024) uint8_t a_s[kNA][kPM * 128];
+  __shared__ __align__(16) float as_s[kNA][256];
+  __shared__ float am_s[4][kPM];
+  gemm_tile<4, CHAIN>(d, ws, M, int(blockIdx.x) / nblk, int(blockIdx.x) % nblk, a_s, as_s, am_s);
 }
 
 int launch_act_quant(const void* x, int64_t rows, int64_t K, uint8_t* q, void* s, int kind, hipStream_t stream);
@@ -1099,6 +1115,37 @@ int launch_dense_fp8(const uint8_t* wp, const void* w_s, int w_kind, const uint8
               nb2d, dense, 1, 1);
   }
   return check_launch("fp8_linear dense");
+}
+
+// Dense MXFP4 GEMM y[M, N] (bf16) = xq[M, K] . W^T for a weight packed by
+// wz_fp4_pack (the routed w2 tile format of one expert: 16-row x 128-K tiles of
+// e2m1, [N/16][K/128][1 KB], and its e8m0 scales packed four K-blocks to a
+// dword, [N/16][ceil(K/512)][64]); M-tiles of up to 64 rows staged in LDS,
+// 8 column tiles per workgroup.
+int launch_dense_fp4(const uint8_t* wp, const uint32_t* wp_s, const uint8_t* xq, const float* xs, bool a_pow2,
+                     uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  if (M * K >= (int64_t(1) << 31)) return set_error(WZ_EINVAL, "fp4_gemm_packed: M * K must be below 2^31");
+  wz_moe_desc d = {};
+  d.dim = int(N);
+  d.inter = int(K);
+  d.n_experts = 1;
+  d.topk = 0;
+  d.act_scale_kind = a_pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
+  d.w2p = wp;
+  d.w2p_s = wp_s;
+  MoeWs w = {};
+  w.hq = const_cast<uint8_t*>(xq);
+  w.hs = const_cast<float*>(xs);
+  w.sh_out = y;
+  const int nblk = int((N / 16 + 7) / 8);
+  const int blocks = int((M + kPM - 1) / kPM) * nblk;
+  const dim3 grid{unsigned(blocks)}, blk{unsigned(kPThreads)};
+  if (a_pow2) {
+    WZ_LAUNCH("fp4_gemm_packed", stream, dense_fp4_kernel<true>, grid, blk, 0, d, w, int(M), nblk);
+  } else {
+    WZ_LAUNCH("fp4_gemm_packed", stream, dense_fp4_kernel<false>, grid, blk, 0, d, w, int(M), nblk);
+  }
+  return check_launch("fp4_gemm_packed");
 }
 
 }  // namespace wz

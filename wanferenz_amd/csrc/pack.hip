@@ -214,3 +214,21 @@ extern "C" int wz_moe_pack_shared(const wz_moe_desc* d, const void* sh_w1, const
   if (int rc = pack_w(sh_w1, sh_w3, sh13p, packed_bytes(d, 4), 2, 0, D, I, stream)) return rc;
   return pack_w(sh_w2, nullptr, sh2p, packed_bytes(d, 5), 3, 0, D, I, stream);
 }
+
+extern "C" size_t wz_fp4_packed_scale_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || N % 16 || K % 128) return 0;
+  return size_t(N / 16) * size_t((K / 128 + 3) / 4) * 256;
+}
+
+extern "C" int wz_fp4_pack(const void* w_fp4x2, const void* w_s_e8m0, int64_t N, int64_t K, void* packed,
+                           void* packed_s, hipStream_t stream) {
+  using namespace wz;
+  if (N <= 0 || K <= 0 || N % 16 || K % 128)
+    return set_error(WZ_EINVAL, "fp4_pack: N=%lld must be a multiple of 16 and K=%lld of 128", (long long)N,
+                     (long long)K);
+  if (N > (1 << 30) || K > (1 << 30)) return set_error(WZ_EINVAL, "fp4_pack: dimension too large");
+  if (!w_fp4x2 || !w_s_e8m0 || !packed || !packed_s) return set_error(WZ_EINVAL, "fp4_pack: null pointer");
+  // the routed w2 relayout of a one-expert bank with D = N rows of K = I
+  if (int rc = pack_w(w_fp4x2, nullptr, packed, N * K / 2, 1, 0, int(N), int(K), stream)) return rc;
+  return pack_s(w_s_e8m0, nullptr, packed_s, int64_t(wz_fp4_packed_scale_bytes(N, K)), 1, 0, int(N), int(K), stream);
+}

@@ -218,6 +218,48 @@ def fp8_linear(x, weight, weight_scale, scale_fmt="ue8m0", scale_dtype=_E8M0):
     return _finish(y)
 
 
+class PackedFp4Linear:
+    """An MXFP4 weight (e2m1x2 [N, K/2] with e8m0 scales [N, K/32]) relaid once into
+    the expert banks' tile format (wz_fp4_pack), for fp4_gemm at row counts past
+    decode: ``gemm(q, q_s)`` = fp4_gemm(q, q_s, weight, scale) (reference.py:572-591)
+    -> bf16 [..., N] on the tile GEMM of the MoE prefill."""
+
+    def __init__(self, weight, weight_scale):
+        assert weight.is_contiguous() and weight_scale.is_contiguous()
+        _require_cuda(weight, weight_scale)
+        if weight_scale.dtype != _E8M0:
+            raise TypeError(f"PackedFp4Linear: MXFP4 weight scales are e8m0, got {weight_scale.dtype}")
+        self.N, self.K = weight.size(0), weight.size(1) * 2
+        dev = weight.device
+        self.packed = torch.empty(self.N * self.K // 2, dtype=torch.uint8, device=dev)
+        self.packed_s = torch.empty(int(N.lib().wz_fp4_packed_scale_bytes(self.N, self.K)), dtype=torch.uint8,
+                                    device=dev)
+        N.call("wz_fp4_pack", N.ptr(weight), N.ptr(weight_scale), self.N, self.K, N.ptr(self.packed),
+               N.ptr(self.packed_s), N.stream_handle(dev))
+        self._ws = None
+
+    def reserve(self, M: int, scale_dtype=torch.float32):
+        kind = N.WZ_SCALE_UE8M0 if scale_dtype == _E8M0 else N.WZ_SCALE_F32
+        need = int(N.lib().wz_fp4_gemm_packed_workspace_bytes(M, self.K, kind))
+        if need and (self._ws is None or self._ws.numel() < need):
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(f"PackedFp4Linear: reserve({M}) before capturing a graph")
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.packed.device)
+        return self
+
+    def gemm(self, q, q_s, out=None):
+        assert q.is_contiguous() and q_s.is_contiguous() and q.size(-1) == self.K
+        _require_cuda(q, q_s)
+        M = q.numel() // self.K
+        self.reserve(M, q_s.dtype)
+        y = torch.empty(*q.size()[:-1], self.N, dtype=torch.bfloat16, device=q.device) if out is None else out
+        ws = self._ws
+        N.call("wz_fp4_gemm_packed", N.ptr(q), N.ptr(q_s), N.ptr(self.packed), N.ptr(self.packed_s), N.ptr(y), M,
+               self.N, self.K, _scale_kind_of(q_s), N.ptr(ws), 0 if ws is None else ws.numel(),
+               N.stream_handle(q.device))
+        return _finish(y)
+
+
 class PackedFp8Linear:
     """An FP8 linear whose weight is relaid once into MFMA-ready tiles (wz_fp8_pack).
 
