@@ -775,17 +775,17 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
     b_touch(b);
     asm volatile("s_barrier" : : : "memory");
   };
+  // the first three steps' loads, unconditionally (K-steps past the end
+  // repeat the last one; nothing reads them): a load behind a branch would
+  // leave the compiler unsure how many loads follow B(0) at the loop head, and
+  // it would drain them all there
   BTiles<NTW> b0, b1, b2;
   b_fetch(b0, 0);
   a_issue(0);
-  if (KB > 1) {
-    b_fetch(b1, 1);
-    a_issue(1);
-  }
-  if (KB > 2) {
-    b_fetch(b2, 2);
-    a_issue(2);
-  }
+  b_fetch(b1, min(1, KB - 1));
+  a_issue(min(1, KB - 1));
+  b_fetch(b2, min(2, KB - 1));
+  a_issue(min(2, KB - 1));
   int kb = 0;
   for (; kb + 5 < KB; kb += 3) {
     step_sync(b0);
