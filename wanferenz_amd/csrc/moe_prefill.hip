@@ -26,7 +26,11 @@ namespace wz {
 constexpr int kPM = kPrefillTileRows;  // pair rows per M-tile (64: the tile bodies then fit two
                                        // workgroups per CU, twice the weight bytes in flight)
 constexpr int kPThreads = 256;    // 4 waves
-constexpr int kNA = 4;            // LDS buffers of the staged A tile (K-steps kb .. kb + 3)
+// K-steps of weights and A rows in flight ahead of the one computed (kStages
+// + 1 LDS buffers hold the staged A tiles).  Three: four for w1/w3 measured
+// the same (T = 2048 994 vs 997 us) at 256 VGPRs, and w2 then lost its third
+// workgroup per CU.
+constexpr int stages_of(int) { return 3; }
 
 // ------------------------------------------------------------------- gate ---
 //
@@ -584,10 +588,10 @@ struct BTiles {
 // A wave owns NTW weight tiles of 16 output columns (routed w13: 4, i.e. 2
 // feature tiles x {w1, w3}; routed w2: 2 column tiles; shared FP8 tiles are
 // twice the bytes, so 2), and one A operand read from LDS feeds NTW MFMAs.
-// The K loop is software-pipelined three K-steps deep: while step kb computes,
-// the B tiles (registers) and the A rows (LDS, direct buffer loads that need
-// no registers) of steps kb+1 .. kb+3 are in flight; A goes through kNA = 4
-// LDS buffers with one barrier per step.
+// The K loop is software-pipelined kStages K-steps deep: while step kb
+// computes, the B tiles (registers) and the A rows (LDS, direct buffer loads
+// that need no registers) of steps kb+1 .. kb+kStages are in flight; A goes
+// through kNA = kStages + 1 LDS buffers with one barrier per step.
 //
 // CHAIN: activation and weight scales are both powers of two, so they ride in
 // the MFMA's e8m0 scale operands and the accumulators chain over K; otherwise
@@ -608,6 +612,7 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
   // w2 2 (4 spilled registers at two workgroups per CU and measured 7 % slower);
   // FP8 shared tiles, twice the bytes, 2
   constexpr int NTW = (DENSE || MODE >= 2) ? 2 : 4;
+  constexpr int kStages = stages_of(MODE), kNA = kStages + 1;
   constexpr int CPW = W13 ? NTW / 2 : NTW;    // 16-column output tiles per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = lane & 15, g = lane >> 4;
@@ -662,7 +667,7 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
       W13 ? ws.xs : ws.hs, short(0), a_rows ? int(a_nrows * KB * 4) : 0, 0x00020000);
   const uint32_t a_lds = lds_addr(&a_s[0][0]), s_lds = lds_addr(&as_s[0][0]);
   auto a_issue = [&](int kb) {
-    const uint32_t buf = uint32_t(kb & (kNA - 1));
+    const uint32_t buf = uint32_t(kb % kNA);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       load_lds_16(a_rs, __builtin_amdgcn_readfirstlane(a_lds + buf * (kPM * 128) + (2 * wave + i) * 1024), avo[i],
@@ -738,7 +743,7 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
     for (int j = 0; j < NTW; ++j) e8[j] = DENSE ? int(b.sw[j]) : int((b.sw[j] >> (8 * (kb & 3))) & 0xFFu);
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      const AOp a = a_from_lds(a_s[buf & (kNA - 1)], as_s[buf & (kNA - 1)], m * 16 + nl, g, CHAIN || a_pow2);
+      const AOp a = a_from_lds(a_s[buf % kNA], as_s[buf % kNA], m * 16 + nl, g, CHAIN || a_pow2);
 #pragma unroll
       for (int j = 0; j < NTW; ++j) {
         const v8i bv = DENSE ? v8i{b.lo[j][0], b.lo[j][1], b.lo[j][2], b.lo[j][3], b.hi[j][0], b.hi[j][1],
@@ -752,11 +757,12 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
     }
   };
 
-  // Step kb: wait for B(kb) -- every register of it, so the wait covers the
-  // whole fetch -- then a barrier, compute from LDS buffer kb % 4, then
-  // request B(kb + 3) into the registers just used and A(kb + 3) into the
-  // buffer read in step kb - 1 (every wave has passed this step's barrier, so
-  // none still reads it).  B(kb + 3) goes out before A(kb + 3), so A(kb) is
+  // Step kb (S = kStages): wait for B(kb) -- every register of it, so the wait
+  // covers the whole fetch -- then a barrier, compute from LDS buffer
+  // kb % (S + 1), then request B(kb + S) into the registers just used and
+  // A(kb + S) into the buffer read in step kb - 1 (every wave has passed this
+  // step's barrier, so none still reads it).  B(kb + S) goes out before
+  // A(kb + S), so A(kb) is
   // the first load after B(kb): the compiler's wait for B(kb) counts only the
   // loads it sees (the B fetches after it), every direct A load after B(kb)
   // is among the loads it leaves outstanding too, and loads complete in
@@ -775,56 +781,39 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
     b_touch(b);
     asm volatile("s_barrier" : : : "memory");
   };
-  // the first three steps' loads, unconditionally (K-steps past the end
+  // the first kStages steps' loads, unconditionally (K-steps past the end
   // repeat the last one; nothing reads them): a load behind a branch would
   // leave the compiler unsure how many loads follow B(0) at the loop head, and
   // it would drain them all there
-  BTiles<NTW> b0, b1, b2;
-  b_fetch(b0, 0);
-  a_issue(0);
-  b_fetch(b1, min(1, KB - 1));
-  a_issue(min(1, KB - 1));
-  b_fetch(b2, min(2, KB - 1));
-  a_issue(min(2, KB - 1));
+  BTiles<NTW> bt[kStages];
+#pragma unroll
+  for (int j = 0; j < kStages; ++j) {
+    b_fetch(bt[j], min(j, KB - 1));
+    a_issue(min(j, KB - 1));
+  }
   int kb = 0;
-  for (; kb + 5 < KB; kb += 3) {
-    step_sync(b0);
-    compute(kb, b0, kb);
-    __builtin_amdgcn_sched_barrier(0);
-    b_fetch(b0, kb + 3);
-    a_issue(kb + 3);
-    step_sync(b1);
-    compute(kb + 1, b1, kb + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    b_fetch(b1, kb + 4);
-    a_issue(kb + 4);
-    step_sync(b2);
-    compute(kb + 2, b2, kb + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    b_fetch(b2, kb + 5);
-    a_issue(kb + 5);
+  // steady state: every step refills (its K-step + kStages is in range)
+  for (; kb + 2 * kStages - 1 < KB; kb += kStages) {
+#pragma unroll
+    for (int i = 0; i < kStages; ++i) {
+      step_sync(bt[i]);
+      compute(kb + i, bt[i], kb + i);
+      __builtin_amdgcn_sched_barrier(0);
+      b_fetch(bt[i], kb + i + kStages);
+      a_issue(kb + i + kStages);
+    }
   }
   // last K-steps
-  for (; kb < KB; kb += 3) {
-    step_sync(b0);
-    compute(kb, b0, kb);
-    if (kb + 3 < KB) {
-      b_fetch(b0, kb + 3);
-      a_issue(kb + 3);
-    }
-    if (kb + 1 >= KB) break;
-    step_sync(b1);
-    compute(kb + 1, b1, kb + 1);
-    if (kb + 4 < KB) {
-      b_fetch(b1, kb + 4);
-      a_issue(kb + 4);
-    }
-    if (kb + 2 >= KB) break;
-    step_sync(b2);
-    compute(kb + 2, b2, kb + 2);
-    if (kb + 5 < KB) {
-      b_fetch(b2, kb + 5);
-      a_issue(kb + 5);
+  for (; kb < KB; kb += kStages) {
+#pragma unroll
+    for (int i = 0; i < kStages; ++i) {
+      if (kb + i >= KB) break;
+      step_sync(bt[i]);
+      compute(kb + i, bt[i], kb + i);
+      if (kb + i + kStages < KB) {
+        b_fetch(bt[i], kb + i + kStages);
+        a_issue(kb + i + kStages);
+      }
     }
   }
 
@@ -994,8 +983,8 @@ __device__ __forceinline__ void tile_order(int r, int n_mt, int nblk, int gm, in
 template <bool W13, bool CR, bool CS>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_gemm_kernel(
     wz_moe_desc d, MoeWs ws, int T, int nblk, int nblk_dense, int dense_blocks, int gm, int gn) {
-  __shared__ __align__(1024) uint8_t a_s[kNA][kPM * 128];
-  __shared__ __align__(16) float as_s[kNA][256];
+  __shared__ __align__(1024) uint8_t a_s[stages_of(W13 ? 0 : 2) + 1][kPM * 128];
+  __shared__ __align__(16) float as_s[stages_of(W13 ? 0 : 2) + 1][256];
   __shared__ float am_s[4][kPM];  // w1/w3 epilogue: each wave's row amax of its features
   const int b = blockIdx.x;
   if (b < dense_blocks) {
@@ -1016,8 +1005,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
 template <bool CHAIN>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void dense_fp4_kernel(
     wz_moe_desc d, MoeWs ws, int M, int nblk) {
-  __shared__ __align__(1024) uint8_t a_s[kNA][kPM * 128];
-  __shared__ __align__(16) float as_s[kNA][256];
+  __shared__ __align__(1024) uint8_t a_s[stages_of(4) + 1][kPM * 128];
+  __shared__ __align__(16) float as_s[stages_of(4) + 1][256];
   __shared__ float am_s[4][kPM];
   gemm_tile<4, CHAIN>(d, ws, M, int(blockIdx.x) / nblk, int(blockIdx.x) % nblk, a_s, as_s, am_s);
 }
