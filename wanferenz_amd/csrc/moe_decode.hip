@@ -354,43 +354,50 @@ __device__ void quant_row(uint8_t* __restrict__ q, float* __restrict__ s, const 
 
 // Shared expert w1 / w3 for features 16 b .. 16 b + 15 with act_quant(x) fused
 // into the A-operand load (this runs in the route launch, before xq exists);
-// the four waves of `group` split K and meet in LDS.
+// the waves split K and meet in LDS.  AP2: power-of-two activation scales;
+// WP2: e8m0 weight block scales (both fix the loads at compile time).  Every
+// load of a wave's K range (token rows, weight tiles, their scales) is issued
+// before the first wait: token rows past T read row T - 1 (their outputs are
+// not stored) and K-blocks past the range re-read its last one (not added).
+// With the loads behind guards the compiler waited on each K-block in turn,
+// and these items, not the routing, ended the launch (T = 1: 16.9 us against
+// 14.4 us for the routing).
+template <bool AP2, bool WP2>
 __device__ __forceinline__ void w13_shared_item_bf16(const wz_moe_desc& d, const MoeWs& ws,
                                                      const uint16_t* __restrict__ x, int T, int b, float* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int kQ = 4;  // K-blocks per batch (D = 4096: the wave's whole range)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nl = lane & 15, g = lane >> 4;
   const int D = d.dim, I = d.inter;
-  const bool a_pow2 = d.act_scale_kind != WZ_SCALE_F32;
   const int KB = D / 128;
   const int kb0 = (wave * KB) / kRouteWaves, kb1 = ((wave + 1) * KB) / kRouteWaves;
-  const uint16_t* xrow = nl < T ? x + int64_t(nl) * D : nullptr;
+  const uint16_t* xrow = x + int64_t(min(nl, T - 1)) * D;
   const int f0 = b * 16;
   const uint8_t* tiles = static_cast<const uint8_t*>(d.sh13p) + int64_t(b) * KB * 4096;
-  const bool bp = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  const int wkind = WP2 ? WZ_WSCALE_E8M0 : WZ_WSCALE_F32;
   const int64_t sbase = int64_t(f0 >> 7) * KB;
   v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  for (int kb = kb0; kb < kb1; kb += 4) {
-    v8i w[2][4];
-    int se[2][4];
-    float sf[2][4];
-    ARaw xr[4];  // x first: its quantisation then overlaps the weight loads
+  for (int kb = kb0; kb < kb1; kb += kQ) {
+    v8i w[2][kQ];
+    int se[2][kQ];
+    float sf[2][kQ];
+    ARaw xr[kQ];  // x first: its quantisation then overlaps the weight loads
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (kb + q < kb1) xr[q] = a_load_bf16(xrow, kb + q, g);
+    for (int q = 0; q < kQ; ++q) xr[q] = a_load_bf16(xrow, min(kb + q, kb1 - 1), g);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < kQ; ++q) {
+      const int kk = min(kb + q, kb1 - 1);
+      w[0][q] = pk_fp8(tiles + int64_t(kk) * 4096, lane);
+      w[1][q] = pk_fp8(tiles + int64_t(kk) * 4096 + 2048, lane);
+      fp8_wscale(d.sh_w1_s, sbase + kk, wkind, se[0][q], sf[0][q]);
+      fp8_wscale(d.sh_w3_s, sbase + kk, wkind, se[1][q], sf[1][q]);
+    }
+#pragma unroll
+    for (int q = 0; q < kQ; ++q)
       if (kb + q < kb1) {
-        w[0][q] = pk_fp8(tiles + int64_t(kb + q) * 4096, lane);
-        w[1][q] = pk_fp8(tiles + int64_t(kb + q) * 4096 + 2048, lane);
-        fp8_wscale(d.sh_w1_s, sbase + kb + q, d.shared_w_scale_kind, se[0][q], sf[0][q]);
-        fp8_wscale(d.sh_w3_s, sbase + kb + q, d.shared_w_scale_kind, se[1][q], sf[1][q]);
-      }
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (kb + q < kb1) {
-        const AOp a = a_quant_bf16(xr[q], a_pow2);
-        mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], a_pow2, bp, lane);
-        mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], a_pow2, bp, lane);
+        const AOp a = a_quant_bf16(xr[q], AP2);
+        mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], AP2, WP2, lane);
+        mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], AP2, WP2, lane);
       }
   }
   // red: [kRouteWaves][2][4][64] floats; partials summed in wave order
@@ -535,7 +542,15 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     return;
   }
   b -= T;
-  w13_shared_item_bf16(d, ws, x, T, b, rbuf);
+  const bool wp2 = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  if (a_pow2 && wp2)
+    w13_shared_item_bf16<true, true>(d, ws, x, T, b, rbuf);
+  else if (a_pow2)
+    w13_shared_item_bf16<true, false>(d, ws, x, T, b, rbuf);
+  else if (wp2)
+    w13_shared_item_bf16<false, true>(d, ws, x, T, b, rbuf);
+  else
+    w13_shared_item_bf16<false, false>(d, ws, x, T, b, rbuf);
 }
 
 // -------------------------------------------------------------------- w13 ---
