@@ -91,17 +91,34 @@ constexpr int kMaxDecPairs = kDecodeMaxT * 16;
 constexpr int kMaxUT = kDecodeMaxT * kMaxDecPairs;
 
 // KS: 64-expert slots per lane (E <= 64 KS); 4 serve V4's 256 experts.
-template <int KS>
-__device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t* ids, int T, int u_max) {
-  __shared__ int s_e[kMaxDecPairs];
-  __shared__ int s_q[kMaxDecPairs];
-  __shared__ float s_w[kMaxDecPairs];
-  __shared__ int cnt[kMaxExperts];
-  __shared__ int base[kMaxExperts];
-  __shared__ int ucode[kMaxExperts];
-  __shared__ int wc[kRouteWaves][kMaxExperts];
-  __shared__ int s_umap[kMaxUT];
-  __shared__ float s_uwt[kMaxUT];
+// GEN: the softmax and hash-table routes are compiled in; without it (a
+// top-k gate with another score function, the V4 case) the code this one
+// workgroup runs, fetched cold once per launch, is that much shorter.
+struct RouteLds {
+  int s_e[kMaxDecPairs];
+  int s_q[kMaxDecPairs];
+  float s_w[kMaxDecPairs];
+  int cnt[kMaxExperts];
+  int base[kMaxExperts];
+  int ucode[kMaxExperts];
+  int wc[kRouteWaves][kMaxExperts];
+  int s_umap[kMaxUT];
+  float s_uwt[kMaxUT];
+  int s_last_of[kMaxDecPairs];
+};
+
+template <int KS, bool GEN>
+__device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t* ids, int T, int u_max,
+                           RouteLds& L) {
+  int* s_e = L.s_e;
+  int* s_q = L.s_q;
+  float* s_w = L.s_w;
+  int* cnt = L.cnt;
+  int* base = L.base;
+  int* ucode = L.ucode;
+  auto& wc = L.wc;
+  int* s_umap = L.s_umap;
+  float* s_uwt = L.s_uwt;
   const int E = d.n_experts, k = d.topk, P = T * k, UT = u_max * T;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr int kSlots = KS;
@@ -114,7 +131,7 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
     float sv[kSlots];
     uint32_t key[kSlots];
     float raw[kSlots], rawb[kSlots];
-    const bool smax = d.score_func == WZ_SCORE_SOFTMAX;
+    const bool smax = GEN && d.score_func == WZ_SCORE_SOFTMAX;
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       const int e = lane + 64 * i;
@@ -151,7 +168,7 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
     }
     int my_sel = 0;
     bool poison = false;  // hash id or table entry out of range: NaN weights, in-range reads
-    if (d.tid2eid != nullptr) {
+    if (GEN && d.tid2eid != nullptr) {
       int64_t id = ids[t];
       const bool bad_id = id < 0 || id >= d.vocab;
       id = bad_id ? 0 : id;
@@ -289,7 +306,7 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
   __syncthreads();
   // ---- (expert, token) map and per-token combine lists.  A token that lists an
   // expert twice keeps its last slot (architecture.py:790 index_put semantics). ----
-  __shared__ int s_last_of[kMaxDecPairs];
+  int* s_last_of = L.s_last_of;
   if (tid < P) {
     const int p = tid, t = p / k, j = p % k, e = s_e[p];
     int last = 1;
@@ -533,7 +550,12 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     if (tid == 0) s_last = arrive_last(&ws.counters[0], uint32_t(n_gate)) ? 1 : 0;
     __syncthreads();
     if (!s_last) return;
-    route_last<KS>(d, ws, ids, T, u_max);  // reads the scores with load_agent
+    // reads the scores with load_agent
+    __shared__ RouteLds rl;
+    if (d.score_func != WZ_SCORE_SOFTMAX && d.tid2eid == nullptr)
+      route_last<KS, false>(d, ws, ids, T, u_max, rl);
+    else
+      route_last<KS, true>(d, ws, ids, T, u_max, rl);
     return;
   }
   b -= n_gate;
