@@ -101,7 +101,6 @@ struct RouteLds {
   int cnt[kMaxExperts];
   int base[kMaxExperts];
   int ucode[kMaxExperts];
-  int wc[kRouteWaves][kMaxExperts];
   int s_umap[kMaxUT];
   float s_uwt[kMaxUT];
   int s_last_of[kMaxDecPairs];
@@ -116,7 +115,6 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
   int* cnt = L.cnt;
   int* base = L.base;
   int* ucode = L.ucode;
-  auto& wc = L.wc;
   int* s_umap = L.s_umap;
   float* s_uwt = L.s_uwt;
   const int E = d.n_experts, k = d.topk, P = T * k, UT = u_max * T;
@@ -225,98 +223,104 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       s_w[t * k + lane] = v;
     }
   }
-  for (int e = tid; e < kMaxExperts; e += kRouteThreads_) cnt[e] = 0;
-  for (int i = tid; i < UT; i += kRouteThreads_) s_umap[i] = -1;
-  __syncthreads();
-  for (int p = tid; p < P; p += kRouteThreads_) atomicAdd(&cnt[s_e[p]], 1);
-  __syncthreads();
-  // ---- exclusive scans of counts and of (count > 0), one expert per thread ----
+  // ---- the tables, by wave 0 alone: P <= 256 pairs and E <= 64 KS experts
+  // are a few rounds of a wave, and one wave needs no barrier between the
+  // steps (its LDS accesses are in program order).  A workgroup-wide version
+  // with a barrier per step took about 4 us here, most of it fetching its code
+  // (this runs once per launch, on one workgroup). ----
+  __syncthreads();  // the token waves' s_e / s_w
+  if (wave != 0) return;
+  for (int e = lane; e < kMaxExperts; e += kWave) cnt[e] = 0;
+  for (int i = lane; i < UT; i += kWave) s_umap[i] = -1;
+  for (int p = lane; p < P; p += kWave) atomicAdd(&cnt[s_e[p]], 1);
+  // exclusive scans of counts and of (count > 0) in expert order: lane l owns
+  // experts [KS l, KS l + KS)
   {
-    const int c = tid < E ? cnt[tid] : 0;
-    const int f = c > 0 ? 1 : 0;
-    int vi = c, fi = f;
+    int c[kSlots], csum = 0, fsum = 0;
 #pragma unroll
-    for (int dd = 1; dd < 64; dd <<= 1) {
-      const int ov = __shfl_up(vi, dd, kWave), of = __shfl_up(fi, dd, kWave);
+    for (int j = 0; j < kSlots; ++j) {
+      const int e = lane * kSlots + j;
+      c[j] = e < E ? cnt[e] : 0;
+      csum += c[j];
+      fsum += c[j] > 0 ? 1 : 0;
+    }
+    int ci = csum, fi = fsum;
+#pragma unroll
+    for (int dd = 1; dd < kWave; dd <<= 1) {
+      const int oc = __shfl_up(ci, dd, kWave), of = __shfl_up(fi, dd, kWave);
       if (lane >= dd) {
-        vi += ov;
+        ci += oc;
         fi += of;
       }
     }
-    if (lane == 63) {
-      wc[0][wave] = vi;
-      wc[1][wave] = fi;
-    }
-    __syncthreads();
-    int vb = 0, fb = 0;
-#pragma unroll 1
-    for (int w = 0; w < wave; ++w) {
-      vb += wc[0][w];
-      fb += wc[1][w];
-    }
-    const int ex = vb + vi - c, fx = fb + fi - f;
-    if (tid < E) {
-      base[tid] = ex;
-      ws.offsets[tid] = ex;
-      if (c > 0) {
-        ucode[tid] = fx;
-        ws.active[fx] = tid;
-        ws.act_off[fx] = ex;
-        ws.act_cnt[fx] = c;
+    int rc = ci - csum, rf = fi - fsum;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      const int e = lane * kSlots + j;
+      if (e < E) {
+        base[e] = rc;
+        ws.offsets[e] = rc;
+        if (c[j] > 0) {
+          ucode[e] = rf;
+          ws.active[rf] = e;
+          ws.act_off[rf] = rc;
+          ws.act_cnt[rf] = c[j];
+        }
       }
+      rc += c[j];
+      rf += c[j] > 0 ? 1 : 0;
     }
-    if (tid == kRouteThreads_ - 1) {
-      ws.offsets[E] = vb + vi;
-      ws.n_active[0] = fb + fi;
+    if (lane == kWave - 1) {
+      ws.offsets[E] = ci;
+      ws.n_active[0] = fi;
     }
   }
-  __syncthreads();
-  // ---- stable placement of the P <= 256 pairs: one pair per thread ----
+  // stable placement, 64 pairs a round: a pair's slot is its expert's next
+  // free slot plus its rank among the round's lanes with that expert
   {
     int nbits = 1;
     while ((1 << nbits) < E) ++nbits;
     const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    const int p = tid;
-    const bool valid = p < P;
-    const int e = valid ? s_e[p] : 0;
-    unsigned long long mask = __ballot(valid);
-    if (!valid) mask = ~mask;
-    for (int bit = 0; bit < nbits; ++bit) {
-      const bool on = (e >> bit) & 1;
-      const unsigned long long m = __ballot(on);
-      mask &= on ? m : ~m;
-    }
-    const int rank = __popcll(mask & lt);
-    const bool leader = (mask & lt) == 0ull;
-    for (int i = tid; i < kRouteWaves * E; i += kRouteThreads_) wc[i / E][i % E] = 0;
-    __syncthreads();
-    if (valid && leader) wc[wave][e] = __popcll(mask);
-    __syncthreads();
-    if (valid) {
-      int before = 0;
 #pragma unroll 1
-      for (int w = 0; w < wave; ++w) before += wc[w][e];
-      const int q = base[e] + before + rank;
-      ws.perm_token[q] = p / k;
-      ws.perm_slot[q] = p % k;
-      ws.pos[p] = q;
-      s_q[p] = q;
+    for (int p0 = 0; p0 < P; p0 += kWave) {
+      const int p = p0 + lane;
+      const bool valid = p < P;
+      const int e = valid ? s_e[p] : 0;
+      unsigned long long mask = __ballot(valid);
+      if (!valid) mask = ~mask;
+#pragma unroll 1
+      for (int bit = 0; bit < nbits; ++bit) {
+        const bool on = (e >> bit) & 1;
+        const unsigned long long m = __ballot(on);
+        mask &= on ? m : ~m;
+      }
+      const int rank = __popcll(mask & lt);
+      if (valid) {
+        const int q = base[e] + rank;
+        ws.perm_token[q] = p / k;
+        ws.perm_slot[q] = p % k;
+        ws.pos[p] = q;
+        s_q[p] = q;
+      }
+      // every lane has read its expert's slot (program order within the wave)
+      if (valid && (mask & lt) == 0ull) base[e] += __popcll(mask);
     }
   }
-  __syncthreads();
   // ---- (expert, token) map and per-token combine lists.  A token that lists an
   // expert twice keeps its last slot (architecture.py:790 index_put semantics). ----
   int* s_last_of = L.s_last_of;
-  if (tid < P) {
-    const int p = tid, t = p / k, j = p % k, e = s_e[p];
+#pragma unroll 1
+  for (int p = lane; p < P; p += kWave) {
+    const int t = p / k, j = p % k, e = s_e[p];
     int last = 1;
 #pragma unroll 1
     for (int jj = j + 1; jj < k; ++jj) last &= (s_e[t * k + jj] != e) ? 1 : 0;
     s_last_of[p] = last;
   }
-  __syncthreads();
-  if (tid < P && s_last_of[tid]) {
-    const int p = tid, t = p / k, e = s_e[p], q = s_q[p];
+#pragma unroll 1
+  for (int p = lane; p < P; p += kWave) {
+    if (!s_last_of[p]) continue;
+    const int t = p / k, e = s_e[p], q = s_q[p];
     int n = 0, rank = 0;
 #pragma unroll 1
     for (int jj = 0; jj < k; ++jj) {
@@ -329,8 +333,7 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
     ws.tok_pos[t * k + rank] = q;
     if (rank == 0) ws.tok_n[t] = n;
   }
-  __syncthreads();
-  for (int i = tid; i < UT; i += kRouteThreads_) {
+  for (int i = lane; i < UT; i += kWave) {
     ws.umap[i] = s_umap[i];
     ws.uwt[i] = s_uwt[i];
   }
