@@ -377,6 +377,42 @@ def test_v4_score_functions(v4_layer, score_func, T):
     print(f"V4 {score_func} T={T}: rel {rel:.2e} cos {cos:.8f} near-ties {near}")
 
 
+@pytest.mark.parametrize("score_func,T", [("sqrtsoftplus", 1), ("sqrtsoftplus", 4), ("sqrtsoftplus", 16),
+                                          ("softmax", 4), ("sigmoid", 11)])
+def test_decode_exact_ties(gpu, score_func, T):
+    """256 experts whose gate rows and biases come in groups of four equal ones
+    (e, e ^ 1, e + 128, (e ^ 1) + 128): every selection key ties exactly with
+    three others, in two lanes and two slots of a lane, and the top-k must take
+    the lower expert id first (torch.topk's order, the oracle's lexsort).
+    T = 16 (96 pairs) runs the decode routing's general table path, the others
+    its one-lane-per-pair path."""
+    import dataclasses
+
+    case = dataclasses.replace(CASES["top6_t8"], name=f"ties_{score_func}_t{T}", dim=512, inter=256,
+                               n_experts=256, T=T, seed=7, score_func=score_func)
+    inp = make_inputs(case)
+    grp = (np.arange(256) % 128) // 2
+    inp.gate_w = np.ascontiguousarray(inp.gate_w[grp])
+    inp.gate_bias = np.ascontiguousarray(inp.gate_bias[grp])
+    moe = upload_case(case, inp, gpu)
+    x = bf16_tensor(inp.x, gpu)
+    ref = om.moe_forward(oracle_params(case, inp), from_bf16_bits(inp.x))
+    rw = torch.empty(T, case.topk, dtype=torch.float32, device=gpu)
+    ri = torch.empty(T, case.topk, dtype=torch.int64, device=gpu)
+    y = moe.forward(x, routing_out=(rw, ri))
+    got_i = ri.cpu().numpy()
+    assert np.array_equal(got_i, ref.gate.indices), (got_i, ref.gate.indices)
+    # every token's top group of four is taken whole, in ascending id
+    for r in got_i:
+        assert r[0] % 2 == 0 and list(r[:4]) == [r[0], r[0] + 1, r[0] + 128, r[0] + 129], r
+    wd = np.abs(rw.cpu().numpy() - ref.gate.weights)
+    assert (wd <= 4 * np.spacing(np.abs(ref.gate.weights).astype(np.float32))).all(), wd.max()
+    got = f32_of_bf16(y)
+    rel, cos = om.max_rel_err(got, ref.y), om.cosine(got, ref.y)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    print(f"{case.name}: rel {rel:.2e} cos {cos:.8f}")
+
+
 @pytest.mark.parametrize("name,T", [("top6_t8", 4), ("toy_t4", 4), ("toy_t4", 16), ("top6_t8", 40)])
 def test_replay_stages_reproduce_the_forward(gpu, name, T):
     """wz_moe_replay_stage re-runs a stage of the last forward on its workspace state."""

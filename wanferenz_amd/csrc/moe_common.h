@@ -147,18 +147,39 @@ __device__ __forceinline__ uint32_t f32_key(float f) {
 
 // Wave-wide max of a uint32 through DPP row ops (no LDS round trips): quad
 // swaps and row mirrors give every lane its row's max, row_bcast15/31 fold
-// the four rows into lane 63, readlane broadcasts it.
+// the four rows into lane 63, readlane broadcasts it.  The masked-off rows of
+// the broadcasts read `old` = 0, the identity of an unsigned max, which lets
+// the compiler fold each move into its v_max_u32_dpp (one instruction a step
+// instead of two).
 __device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
-  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0xB1, 0xF, 0xF, false)));   // quad_perm 1,0,3,2
-  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x4E, 0xF, 0xF, false)));   // quad_perm 2,3,0,1
-  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x141, 0xF, 0xF, false)));  // row_half_mirror
-  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x140, 0xF, 0xF, false)));  // row_mirror
-  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x142, 0xA, 0xF, false)));  // row_bcast:15
-  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), 0x143, 0xC, 0xF, false)));  // row_bcast:31
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0xB1, 0xF, 0xF, true)));   // quad_perm 1,0,3,2
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x4E, 0xF, 0xF, true)));   // quad_perm 2,3,0,1
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x141, 0xF, 0xF, true)));  // row_half_mirror
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x140, 0xF, 0xF, true)));  // row_mirror
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x142, 0xA, 0xF, false)));  // row_bcast:15
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x143, 0xC, 0xF, false)));  // row_bcast:31
   return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
 }
 
 __device__ __forceinline__ uint32_t dpp_min_u32(uint32_t v) { return ~dpp_max_u32(~v); }
+
+// Wave-wide max of a uint32 left in every lane, in vector instructions only:
+// DPP steps give every lane its row's max, then the gfx950 row and half swaps
+// (v_permlane16_swap, v_permlane32_swap) exchange rows and halves.  With no
+// readlane, ballot or scalar step the chain never waits for a vector result
+// to reach the scalar unit, which in a lone wave costs more than the steps.
+__device__ __forceinline__ uint32_t wave_max_all_u32(uint32_t v) {
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0xB1, 0xF, 0xF, true)));   // quad_perm 1,0,3,2
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x4E, 0xF, 0xF, true)));   // quad_perm 2,3,0,1
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x141, 0xF, 0xF, true)));  // row_half_mirror
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x140, 0xF, 0xF, true)));  // row_mirror
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);  // rows 0 <-> 1, 2 <-> 3
+  v = max(uint32_t(r[0]), uint32_t(r[1]));
+  const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);  // lanes 0-31 <-> 32-63
+  return max(uint32_t(h[0]), uint32_t(h[1]));
+}
+
+__device__ __forceinline__ uint32_t wave_min_all_u32(uint32_t v) { return ~wave_max_all_u32(~v); }
 
 // Agent-scope arrival counter: returns true in the last of `n` arrivals and
 // resets the counter for the next launch.

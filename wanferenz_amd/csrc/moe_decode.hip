@@ -4,18 +4,19 @@
 // T <= 8), four or five otherwise; no host sync, no allocation
 // (graph-capturable):
 //
-//   route   WGs of 16 gate experts x one token: logits x.W^T (exact bf16 products, fp64
-//           sums); the last gate WG to arrive (agent-scope counter) does score
-//           function + bias + top-k + renormalise for every token
-//           (Gate.forward, architecture.py:696-718), the canonical (expert,
-//           token, slot) permutation (expert_batch.py:24-37), the active-
-//           expert list and the per-token combine lists.  Each gate wave
-//           evaluates the score function for its expert (lane t = token t),
-//           so the last WG only selects: top-k is k rounds of a DPP wave-max.
-//           In the same launch, T WGs quantise x (act_quant).
+//   route   gate WGs: each expert's logits x.W^T for all T tokens (exact bf16
+//           products, fp64 sums), its K range split over 1-8 waves; each gate
+//           thread applies the score function and the bias for one (expert,
+//           token).  The last gate WG to arrive (agent-scope counter) does
+//           top-k + renormalise for every token (Gate.forward,
+//           architecture.py:696-718), one wave per token, and one wave
+//           builds the active-expert list, the (expert, token) -> pair-row
+//           map and the per-token combine lists.  In the same launch T WGs
+//           quantise x (act_quant) and the rest stream the shared expert's
+//           w1 / w3, which needs no routing.
 //   w13     per (active expert, 16 intermediate features): MXFP4 w1 and w3
 //           tiles streamed once, SwiGLU + clamp + routing weight, bf16 h;
-//           the shared expert's FP8 w1/w3 tiles run first in the same grid.
+//           the shared expert's w1 / w3 ran in the route launch.
 //   hquant  act_quant of the h rows that are routed, and of the shared rows
 //           (only when w2_lds_kernel does not serve: that kernel quantises h
 //           into LDS itself).
@@ -95,26 +96,18 @@ constexpr int kMaxUT = kDecodeMaxT * kMaxDecPairs;
 // top-k gate with another score function, the V4 case) the code this one
 // workgroup runs, fetched cold once per launch, is that much shorter.
 struct RouteLds {
+  unsigned long long s_mask[kMaxExperts / 64];  // selected experts
   int s_e[kMaxDecPairs];
-  int s_q[kMaxDecPairs];
   float s_w[kMaxDecPairs];
-  int cnt[kMaxExperts];
-  int base[kMaxExperts];
-  int ucode[kMaxExperts];
   int s_umap[kMaxUT];
   float s_uwt[kMaxUT];
-  int s_last_of[kMaxDecPairs];
 };
 
 template <int KS, bool GEN>
 __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t* ids, int T, int u_max,
                            RouteLds& L) {
   int* s_e = L.s_e;
-  int* s_q = L.s_q;
   float* s_w = L.s_w;
-  int* cnt = L.cnt;
-  int* base = L.base;
-  int* ucode = L.ucode;
   int* s_umap = L.s_umap;
   float* s_uwt = L.s_uwt;
   const int E = d.n_experts, k = d.topk, P = T * k, UT = u_max * T;
@@ -165,6 +158,8 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       }
     }
     int my_sel = 0;
+    float mine = 0.0f;    // lane j < k: the score of the token's j-th expert
+    float tot = 0.0f;     // the k scores summed in slot order (fp32)
     bool poison = false;  // hash id or table entry out of range: NaN weights, in-range reads
     if (GEN && d.tid2eid != nullptr) {
       int64_t id = ids[t];
@@ -177,41 +172,70 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
         my_sel = bad_e ? 0 : e;
       }
       poison = bad_id || __ballot(bad_e) != 0ull;
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i) {
+        const float v = __shfl(sv[i], my_sel & 63, kWave);
+        if ((my_sel >> 6) == i) mine = v;
+      }
+      for (int j = 0; j < k; ++j) tot += __shfl(mine, j, kWave);
     } else {
-      unsigned taken = 0u;
+      // The lane's experts sorted by key, best first.  Adjacent swaps on a
+      // strictly larger key keep equal keys in slot order, i.e. ascending id;
+      // slots past E hold key 0 and come last in slot order, so they sort
+      // behind every valid expert and `live` counts the valid ones left.
+      uint32_t hk[kSlots];
+      int hs[kSlots];
+      float hv[kSlots];
+      int live = 0;
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i) {
+        hk[i] = key[i];
+        hs[i] = i;
+        hv[i] = sv[i];
+        live += lane + 64 * i < E ? 1 : 0;
+      }
+#pragma unroll
+      for (int a = 0; a < kSlots - 1; ++a)
+#pragma unroll
+        for (int i = 0; i + 1 < kSlots - a; ++i)
+          if (hk[i + 1] > hk[i]) {
+            const uint32_t tk = hk[i];
+            const int ts = hs[i];
+            const float tv = hv[i];
+            hk[i] = hk[i + 1];
+            hs[i] = hs[i + 1];
+            hv[i] = hv[i + 1];
+            hk[i + 1] = tk;
+            hs[i + 1] = ts;
+            hv[i + 1] = tv;
+          }
+      // k rounds: the wave max of the lanes' heads, the winner pops its head.
+      // Vector instructions only (selects, no branch on a lane condition), so
+      // the round never waits for a vector result in the scalar unit: with a
+      // ballot and a readlane per round it took ~0.33 us a round at T = 1.
 #pragma unroll 1
       for (int j = 0; j < k; ++j) {
-        // this lane's best remaining expert (lowest slot on equal keys = lowest id)
-        uint32_t best = 0u;
-        int bi = -1;
+        const uint32_t m = wave_max_all_u32(live > 0 ? hk[0] : 0u);
+        const bool cand = live > 0 && hk[0] == m;
+        // equal keys: the lowest expert id wins (torch.topk keeps the earlier index)
+        const int we = int(wave_min_all_u32(cand ? uint32_t(lane + 64 * hs[0]) : 0xFFFFFFFFu));
+        const int wl = __builtin_amdgcn_readfirstlane(we) & 63;
+        const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hv[0]), wl));
+        tot += wv;
+        const bool mine_j = lane == j;
+        my_sel = mine_j ? we : my_sel;
+        mine = mine_j ? wv : mine;
+        const bool pop = lane == wl;
 #pragma unroll
-        for (int i = 0; i < kSlots; ++i)
-          if (lane + 64 * i < E && !((taken >> i) & 1u) && (bi < 0 || key[i] > best)) {
-            best = key[i];
-            bi = i;
-          }
-        const uint32_t m = dpp_max_u32(bi >= 0 ? best : 0u);
-        const bool cand = bi >= 0 && best == m;
-        const unsigned long long mask = __ballot(cand);
-        int we;
-        if (__popcll(mask) == 1) {
-          const int wl = __ffsll((long long)mask) - 1;
-          we = wl + 64 * __builtin_amdgcn_readlane(bi, wl);
-        } else {  // equal keys: the lowest expert id wins (torch.topk keeps the earlier index)
-          we = int(dpp_min_u32(cand ? uint32_t(lane + 64 * bi) : 0xFFFFFFFFu));
+        for (int i = 0; i + 1 < kSlots; ++i) {
+          hk[i] = pop ? hk[i + 1] : hk[i];
+          hs[i] = pop ? hs[i + 1] : hs[i];
+          hv[i] = pop ? hv[i + 1] : hv[i];
         }
-        if ((we & 63) == lane) taken |= 1u << (we >> 6);
-        if (lane == j) my_sel = we;
+        hk[kSlots - 1] = pop ? 0u : hk[kSlots - 1];
+        live -= pop ? 1 : 0;
       }
     }
-    float mine = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
-      const float v = __shfl(sv[i], my_sel & 63, kWave);
-      if ((my_sel >> 6) == i) mine = v;
-    }
-    float tot = 0.0f;
-    for (int j = 0; j < k; ++j) tot += __shfl(mine, j, kWave);  // slot order, fp32
     float v = mine;
     if (d.score_func != WZ_SCORE_SOFTMAX) v = v / tot;
     v = v * d.route_scale;
@@ -223,115 +247,76 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
       s_w[t * k + lane] = v;
     }
   }
-  // ---- the tables, by wave 0 alone: P <= 256 pairs and E <= 64 KS experts
-  // are a few rounds of a wave, and one wave needs no barrier between the
-  // steps (its LDS accesses are in program order).  A workgroup-wide version
-  // with a barrier per step took about 4 us here, most of it fetching its code
-  // (this runs once per launch, on one workgroup). ----
+  // ---- the tables, by wave 0 alone (its LDS accesses are in program order,
+  // so no barrier separates the steps).  What the later launches read: the
+  // active-expert list, umap / uwt (active expert u, token t) -> the pair row
+  // and its weight, and the per-token combine lists.  A routed (expert, token)
+  // is stored at the row of its pair p = t k + j (the token's last slot with
+  // that expert, architecture.py:790 index_put semantics): any row < P unique
+  // to the (expert, token) serves, so no canonical permutation is needed
+  // here.  The active index of an expert is the count of selected experts
+  // below it, from a presence mask; a token's combine order (ascending expert
+  // id) compares its own k experts.  All of it is vector work with no loop
+  // over the pairs: this phase is one wave's dependent instruction chain, and
+  // the earlier count / scan / placement version took 3.3 us at T = 1, a
+  // loop over the pairs 2.6 us at T = 1 and 4.5 us at T = 4. ----
   __syncthreads();  // the token waves' s_e / s_w
   if (wave != 0) return;
-  for (int e = lane; e < kMaxExperts; e += kWave) cnt[e] = 0;
+  unsigned long long* s_mask = L.s_mask;
+  if (lane < KS) s_mask[lane] = 0ull;
+  for (int p = lane; p < P; p += kWave) {
+    const int e = s_e[p];
+    atomicOr(&s_mask[e >> 6], 1ull << (e & 63));
+  }
+  unsigned long long mw[KS];
+  int n_act = 0;
+#pragma unroll
+  for (int w = 0; w < KS; ++w) {
+    mw[w] = s_mask[w];
+    n_act += __popcll(mw[w]);
+  }
+  if (lane == 0) ws.n_active[0] = n_act;
   for (int i = lane; i < UT; i += kWave) s_umap[i] = -1;
-  for (int p = lane; p < P; p += kWave) atomicAdd(&cnt[s_e[p]], 1);
-  // exclusive scans of counts and of (count > 0) in expert order: lane l owns
-  // experts [KS l, KS l + KS)
-  {
-    int c[kSlots], csum = 0, fsum = 0;
-#pragma unroll
-    for (int j = 0; j < kSlots; ++j) {
-      const int e = lane * kSlots + j;
-      c[j] = e < E ? cnt[e] : 0;
-      csum += c[j];
-      fsum += c[j] > 0 ? 1 : 0;
-    }
-    int ci = csum, fi = fsum;
-#pragma unroll
-    for (int dd = 1; dd < kWave; dd <<= 1) {
-      const int oc = __shfl_up(ci, dd, kWave), of = __shfl_up(fi, dd, kWave);
-      if (lane >= dd) {
-        ci += oc;
-        fi += of;
-      }
-    }
-    int rc = ci - csum, rf = fi - fsum;
-#pragma unroll
-    for (int j = 0; j < kSlots; ++j) {
-      const int e = lane * kSlots + j;
-      if (e < E) {
-        base[e] = rc;
-        ws.offsets[e] = rc;
-        if (c[j] > 0) {
-          ucode[e] = rf;
-          ws.active[rf] = e;
-          ws.act_off[rf] = rc;
-          ws.act_cnt[rf] = c[j];
-        }
-      }
-      rc += c[j];
-      rf += c[j] > 0 ? 1 : 0;
-    }
-    if (lane == kWave - 1) {
-      ws.offsets[E] = ci;
-      ws.n_active[0] = fi;
-    }
-  }
-  // stable placement, 64 pairs a round: a pair's slot is its expert's next
-  // free slot plus its rank among the round's lanes with that expert
-  {
-    int nbits = 1;
-    while ((1 << nbits) < E) ++nbits;
-    const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-#pragma unroll 1
-    for (int p0 = 0; p0 < P; p0 += kWave) {
-      const int p = p0 + lane;
-      const bool valid = p < P;
-      const int e = valid ? s_e[p] : 0;
-      unsigned long long mask = __ballot(valid);
-      if (!valid) mask = ~mask;
-#pragma unroll 1
-      for (int bit = 0; bit < nbits; ++bit) {
-        const bool on = (e >> bit) & 1;
-        const unsigned long long m = __ballot(on);
-        mask &= on ? m : ~m;
-      }
-      const int rank = __popcll(mask & lt);
-      if (valid) {
-        const int q = base[e] + rank;
-        ws.perm_token[q] = p / k;
-        ws.perm_slot[q] = p % k;
-        ws.pos[p] = q;
-        s_q[p] = q;
-      }
-      // every lane has read its expert's slot (program order within the wave)
-      if (valid && (mask & lt) == 0ull) base[e] += __popcll(mask);
-    }
-  }
-  // ---- (expert, token) map and per-token combine lists.  A token that lists an
-  // expert twice keeps its last slot (architecture.py:790 index_put semantics). ----
-  int* s_last_of = L.s_last_of;
-#pragma unroll 1
   for (int p = lane; p < P; p += kWave) {
-    const int t = p / k, j = p % k, e = s_e[p];
-    int last = 1;
-#pragma unroll 1
-    for (int jj = j + 1; jj < k; ++jj) last &= (s_e[t * k + jj] != e) ? 1 : 0;
-    s_last_of[p] = last;
-  }
-#pragma unroll 1
-  for (int p = lane; p < P; p += kWave) {
-    if (!s_last_of[p]) continue;
-    const int t = p / k, e = s_e[p], q = s_q[p];
-    int n = 0, rank = 0;
-#pragma unroll 1
-    for (int jj = 0; jj < k; ++jj) {
-      const int o = s_last_of[t * k + jj];
-      n += o;
-      rank += (o && s_q[t * k + jj] < q) ? 1 : 0;
+    const int e = s_e[p], t = p / k, j = p - t * k;
+    int uc = 0;  // active index of e
+#pragma unroll
+    for (int w = 0; w < KS; ++w) {
+      const int ew = e >> 6;
+      const unsigned long long below = w < ew ? mw[w] : (w == ew ? mw[w] & ((1ull << (e & 63)) - 1ull) : 0ull);
+      uc += __popcll(below);
     }
-    s_umap[ucode[e] * T + t] = q;
-    s_uwt[ucode[e] * T + t] = s_w[p];
-    ws.tok_pos[t * k + rank] = q;
-    if (rank == 0) ws.tok_n[t] = n;
+    ws.active[uc] = e;  // every pair of the expert stores the same id
+    // the token's experts (reads past its k clamp to its last one, and are
+    // masked out of the counts)
+    int te[16];
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) te[jj] = s_e[t * k + min(jj, k - 1)];
+    bool last = true;
+    int rank = 0, n = 0;
+    if (GEN) {
+      // a hash table can repeat an expert within a token: only its last slot counts
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        bool lj = jj < k;
+#pragma unroll
+        for (int j2 = jj + 1; j2 < 16; ++j2) lj = lj && !(j2 < k && te[j2] == te[jj]);
+        if (jj > j && jj < k && te[jj] == e) last = false;
+        n += lj ? 1 : 0;
+        rank += (lj && te[jj] < e) ? 1 : 0;
+      }
+    } else {
+      // top-k never repeats an expert within a token
+      n = k;
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) rank += (jj < k && te[jj] < e) ? 1 : 0;
+    }
+    if (last) {
+      s_umap[uc * T + t] = p;
+      s_uwt[uc * T + t] = s_w[p];
+      ws.tok_pos[t * k + rank] = p;
+      if (rank == 0) ws.tok_n[t] = n;
+    }
   }
   for (int i = lane; i < UT; i += kWave) {
     ws.umap[i] = s_umap[i];
@@ -467,6 +452,14 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     const int task = b * kRouteWaves + wave;
     const int e = task / split, sp = task % split;
     const int nc = D / 8, c0 = (sp * nc) / split, c1 = ((sp + 1) * nc) / split;
+    // the selection-key bias of the (expert, token) this thread finishes below,
+    // requested now: read after the partial sums it was a dependent round trip
+    // (about 1 us) in front of the arrival
+    const int epb = kRouteWaves / split;
+    const int fin_e = b * epb + tid / max(T, 1);
+    const bool fin = tid < epb * T && fin_e < E;
+    const bool biased = d.score_func != WZ_SCORE_SOFTMAX && d.tid2eid == nullptr && d.gate_bias != nullptr;
+    const float fin_bias = (fin && biased) ? d.gate_bias[fin_e] : 0.0f;
     double acc[kDecodeMaxT];
 #pragma unroll
     for (int t = 0; t < kDecodeMaxT; ++t) acc[t] = 0.0;
@@ -531,21 +524,18 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     __syncthreads();
     // ---- one thread per (expert of this block, token): partials in wave
     // order, then the score function and the bias (the selection key) ----
-    const int epb = kRouteWaves / split;
-    if (tid < epb * T) {
-      const int es = tid / T, t = tid % T, e2 = b * epb + es;
-      if (e2 < E) {
-        double v = 0.0;
-        for (int s2 = 0; s2 < split; ++s2) v += part[es * split + s2][t];
-        const int64_t o = int64_t(t) * E + e2;
-        const float logit = float(v);
-        if (d.score_func == WZ_SCORE_SOFTMAX) {
-          store_agent(ws.scores + o, logit);
-        } else {
-          const float sc = score_of(logit, d.score_func);
-          store_agent(ws.scores + o, sc);
-          store_agent(ws.biased + o, (d.tid2eid == nullptr && d.gate_bias != nullptr) ? sc + d.gate_bias[e2] : sc);
-        }
+    if (fin) {
+      const int es = tid / T, t = tid % T, e2 = fin_e;
+      double v = 0.0;
+      for (int s2 = 0; s2 < split; ++s2) v += part[es * split + s2][t];
+      const int64_t o = int64_t(t) * E + e2;
+      const float logit = float(v);
+      if (d.score_func == WZ_SCORE_SOFTMAX) {
+        store_agent(ws.scores + o, logit);
+      } else {
+        const float sc = score_of(logit, d.score_func);
+        store_agent(ws.scores + o, sc);
+        store_agent(ws.biased + o, biased ? sc + fin_bias : sc);
       }
     }
     vm_drain();  // this wave's score stores are performed before the arrival below
@@ -829,7 +819,7 @@ constexpr int kW2Threads = kW2Waves * 64;
 __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, MoeWs ws, int T, int u_max,
                                                                 uint16_t* __restrict__ y) {
   constexpr int kShParts = 2;
-  __shared__ float out_s[kMaxDecPairs][16];  // routed pair (permuted position) x 16 columns
+  __shared__ float out_s[kMaxDecPairs][16];  // routed pair (its pair row) x 16 columns
   __shared__ float sh_s[kShParts][kDecodeMaxT][16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nl = lane & 15, g = lane >> 4;
@@ -920,7 +910,7 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
 // active routed expert over the full K; one workgroup per 16 output columns),
 // with the A operand read from LDS instead of registers.  The workgroup first
 // copies into LDS, with buffer loads straight to LDS, every e4m3 h row it can
-// need: one per routed (expert, token) pair, at its permuted position q < P,
+// need: one per routed (expert, token) pair, at its pair row q < P,
 // then the T shared rows.  A wave's registers then hold only weight tiles: the
 // NS = I / 128 one-KB tile slots of its job are all in flight at once, and
 // while it computes job j the tiles of its next job (j + 16) are requested
