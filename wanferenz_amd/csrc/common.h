@@ -126,6 +126,19 @@ __device__ __forceinline__ float wave_absmax_xor(float v, int mask) {
   return absmax(v, __shfl_xor(v, mask, kWave));
 }
 
+// absmax over each row of 16 lanes, every lane of the row gets it: DPP moves
+// within the row (quad xor 1, quad xor 2, then the half-row and row mirrors,
+// which pair each quad with the others), no LDS round trip.  The integer max
+// of the sign-cleared bits is absmax's reduction.
+__device__ __forceinline__ float row16_absmax(float v) {
+  uint32_t m = __float_as_uint(v) & 0x7FFFFFFFu;
+  m = max(m, uint32_t(__builtin_amdgcn_mov_dpp(int(m), 0xB1, 0xF, 0xF, false)));   // quad_perm [1,0,3,2]
+  m = max(m, uint32_t(__builtin_amdgcn_mov_dpp(int(m), 0x4E, 0xF, 0xF, false)));   // quad_perm [2,3,0,1]
+  m = max(m, uint32_t(__builtin_amdgcn_mov_dpp(int(m), 0x141, 0xF, 0xF, false)));  // row_half_mirror
+  m = max(m, uint32_t(__builtin_amdgcn_mov_dpp(int(m), 0x140, 0xF, 0xF, false)));  // row_mirror
+  return __uint_as_float(m);
+}
+
 // ---------------------------------------------------------------- MFMA -------
 
 template <int FMT_A, int FMT_B>

@@ -202,6 +202,149 @@ __global__ __launch_bounds__(W * 64, MINW) void fp8_gemv_kernel(const void* __re
     if (j + NB + s < n_my) process(buf[s], j + NB + s);
 }
 
+// One 16-column tile per workgroup (grid = N / 16), its K split over W waves
+// of NKB K-blocks: the shapes whose tiles fit the chip in about one wave of
+// workgroups, where each workgroup's weight share is a single burst and the
+// launch is one round trip.  Every load goes out before the first wait: the
+// x rows, then the wave's weight K-blocks and their scales; vmcnt counts in
+// issue order, so the x rows are waited for while the weights are still in
+// flight.
+//   QA: x is e4m3 with block scales; each lane loads its A fragments.
+//   else: x is bf16 and act_quant runs once per workgroup, densely: sixteen
+//   lanes per (row, 128-block) pair, eight elements each, rows < M only
+//   (pair 4 (w + j W) + lane / 16 in pass j of wave w, XP passes at most),
+//   into LDS as e4m3 rows padded by 16 bytes, which the MFMA A fragments are
+//   then read from.  The MFMA lane layout would have every wave quantise all
+//   16 row slots of its K-slice, at T = 4 three quarters of them empty.
+// The same block amax, scale and rounding as act_quant, and the ring kernel's
+// K split, so both kernels give the same bits.  Four waves sum the W
+// K-partials of the 16 x 16 tile in wave order.
+template <int W, int NKB, int XP, bool QA, bool AP2, bool BP2>
+__global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restrict__ x, const void* __restrict__ xs,
+                                                           int a_kind, const uint8_t* __restrict__ wp,
+                                                           const void* __restrict__ w_s,
+                                                           const uint16_t* __restrict__ res, uint16_t* __restrict__ y,
+                                                           uint16_t* __restrict__ y_hi, int n_split, int M, int N,
+                                                           int K) {
+  static_assert(W >= 4, "the epilogue uses four waves");
+  __shared__ float red[W * 4 * kWave];
+  extern __shared__ __align__(16) uint8_t gv_lds[];  // !QA: e4m3 rows [M][K + 16], then (e8m0, scale) per pair
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nl = lane & 15, g = lane >> 4;
+  const int KB = K / 128, kb0 = wave * NKB, item = blockIdx.x;
+  const int ldk = K + 16;
+
+  AOp a[NKB];
+  uint4 xr[QA ? 1 : XP];
+  const int P = M * KB;
+  if constexpr (QA) {
+    const int xrow = nl < M ? nl : M - 1;  // rows past M repeat row M - 1; their outputs are dropped
+    const uint8_t* row = static_cast<const uint8_t*>(x) + int64_t(xrow) * K;
+    const void* srow = a_kind == WZ_SCALE_UE8M0
+                           ? static_cast<const void*>(static_cast<const uint8_t*>(xs) + int64_t(xrow) * KB)
+                           : static_cast<const void*>(static_cast<const float*>(xs) + int64_t(xrow) * KB);
+#pragma unroll
+    for (int q = 0; q < NKB; ++q) a[q] = a_from_fp8_row(row, srow, kb0 + q, g, a_kind);
+  } else {
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      int pr = 4 * (wave + j * W) + g;
+      pr = pr < P ? pr : P - 1;
+      const int r = pr / KB, kb = pr - r * KB;
+      xr[j] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + int64_t(r) * K + kb * 128 + nl * 8);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  v8i w[NKB];
+  int se[NKB];
+  float sf[NKB];
+  const uint8_t* t = wp + (int64_t(item) * KB + kb0) * 2048 + lane * 16;
+#pragma unroll
+  for (int q = 0; q < NKB; ++q) {
+    const v4i lo = load16_nt(t + q * 2048), hi = load16_nt(t + q * 2048 + 1024);
+    w[q] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+#pragma unroll
+  for (int q = 0; q < NKB; ++q)
+    fp8_wscale(w_s, int64_t(item >> 3) * KB + kb0 + q, BP2 ? WZ_WSCALE_E8M0 : WZ_WSCALE_F32, se[q], sf[q]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  if constexpr (!QA) {
+    uint8_t* xq = gv_lds;
+    int2* xsc = reinterpret_cast<int2*>(gv_lds + M * ldk);
+    // each lane's amax of its eight elements, for every pass: the x loads
+    // are used here, ahead of the passes' branches, so none of them is sunk
+    // into a branch behind the weight loads (its wait would drain those)
+    float lmax[XP];
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+      float m = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = absmax(absmax(m, bf16lo(v[i])), bf16hi(v[i]));
+      asm volatile("" ::"v"(m));  // an unconditional use: the load stays here
+      lmax[j] = m;
+    }
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const int pr = 4 * (wave + j * W) + g;
+      if (4 * (wave + j * W) < P) {  // wave-uniform: the pass holds a pair
+        const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+        const float amax = row16_absmax(lmax[j]);
+        const ActScale sc = act_scale(amax, AP2);
+        const uint32_t q0 = pack_fp8x4(quant_div(bf16lo(v[0]), sc, AP2), quant_div(bf16hi(v[0]), sc, AP2),
+                                       quant_div(bf16lo(v[1]), sc, AP2), quant_div(bf16hi(v[1]), sc, AP2));
+        const uint32_t q1 = pack_fp8x4(quant_div(bf16lo(v[2]), sc, AP2), quant_div(bf16hi(v[2]), sc, AP2),
+                                       quant_div(bf16lo(v[3]), sc, AP2), quant_div(bf16hi(v[3]), sc, AP2));
+        if (pr < P) {
+          const int r = pr / KB, kb = pr - r * KB;
+          *reinterpret_cast<uint2*>(xq + r * ldk + kb * 128 + nl * 8) = make_uint2(q0, q1);
+          if (nl == 0) xsc[pr] = make_int2(AP2 ? sc.e8m0 : kE8m0One, __float_as_int(sc.s));
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NKB; ++q) {
+      a[q] = a_zero();
+      if (nl < M) {
+        const uint8_t* pa = xq + nl * ldk + (kb0 + q) * 128 + g * 16;
+        const uint4 lo = *reinterpret_cast<const uint4*>(pa), hi = *reinterpret_cast<const uint4*>(pa + 64);
+        a[q].v = v8i{int(lo.x), int(lo.y), int(lo.z), int(lo.w), int(hi.x), int(hi.y), int(hi.z), int(hi.w)};
+        const int2 s2 = xsc[nl * KB + kb0 + q];
+        a[q].se8 = s2.x;
+        a[q].sf = __int_as_float(s2.y);
+      }
+    }
+  }
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < NKB; ++q) mma_step<kFmtFp8, kFmtFp8>(acc, a[q], w[q], se[q], sf[q], AP2, BP2, lane);
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * kWave + lane] = acc[i];
+  __syncthreads();
+  if (wave < 4) {
+    const int i = wave, row = g * 4 + i;
+    if (row < M) {
+      float v = red[i * kWave + lane];
+#pragma unroll
+      for (int ww = 1; ww < W; ++ww) v += red[(ww * 4 + i) * kWave + lane];
+      const int col = item * 16 + nl;
+      if (col < n_split) {
+        const int64_t o = int64_t(row) * n_split + col;
+        y[o] = f32_to_bf16(res ? bf16_round(v) + __uint_as_float(uint32_t(res[o]) << 16) : v);
+      } else {
+        y_hi[int64_t(row) * (N - n_split) + (col - n_split)] = f32_to_bf16(v);
+      }
+    }
+  }
+}
+
+// dynamic LDS of the one-tile kernel's bf16 path: e4m3 rows + per-pair scales
+static size_t gemv1_lds_bytes(int64_t M, int64_t K) { return size_t(M) * size_t(K + 16) + size_t(M) * size_t(K / 128) * 8; }
+
 template <int W, int NKB, int NB, int MINW, bool XF, bool QA>
 static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
                        uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream);
@@ -336,9 +479,71 @@ static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t*
             : launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, stream);
 }
 
+template <int W, int NKB, int XP, bool QA>
+static int launch_gemv1(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
+                        const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
+                        int64_t K, bool pow2, hipStream_t stream) {
+  const dim3 grid(unsigned(N / 16)), block(W * 64);
+  const bool bp = w_kind == WZ_WSCALE_E8M0;
+  const size_t lds = QA ? 0 : gemv1_lds_bytes(M, K);
+#define WZ_GV1(AP, BP)                                                                                        \
+  WZ_LAUNCH("fp8_gemv1", stream, (fp8_gemv1_kernel<W, NKB, XP, QA, AP, BP>), grid, block, lds, x, xs, a_kind, w, \
+            w_s, res, y, y_hi, int(n_split), int(M), int(N), int(K))
+  if (pow2) {
+    if (bp) WZ_GV1(true, true); else WZ_GV1(true, false);
+  } else {
+    if (bp) WZ_GV1(false, true); else WZ_GV1(false, false);
+  }
+#undef WZ_GV1
+  return check_launch("fp8_gemv1");
+}
+
+// GEMV shape per K for the one-tile kernel: (W, NKB) as the ring kernel's, so
+// both split K the same way and give the same bits.  It serves N / 16 tiles up
+// to WZ_GV1_MAX_TILES; above that the ring kernel's persistent workgroups
+// (x quantised once per workgroup, several tiles streamed) are faster.
+#ifndef WZ_GV1_MAX_TILES
+#define WZ_GV1_MAX_TILES 512
+#endif
+#ifndef WZ_GV1_K1024
+#define WZ_GV1_K1024 8, 1, 4
+#endif
+#ifndef WZ_GV1_K2048
+#define WZ_GV1_K2048 8, 2, 8
+#endif
+#ifndef WZ_GV1_K4096
+#define WZ_GV1_K4096 16, 2, 8
+#endif
+#ifndef WZ_GV1_K8192
+#define WZ_GV1_K8192 16, 4, 8
+#endif
+
 static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s,
                          int w_kind, const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M,
                          int64_t N, int64_t K, bool pow2, hipStream_t stream) {
+  // the bf16 path quantises M x K / 128 pairs in passes of four per wave, the
+  // fewest of 1, 2, 4, 8 passes that cover them (at most the third value of
+  // each WZ_GV1_K*), and holds them in LDS
+  auto fits1 = [&](int W_, int XP_) { return M * (K / 128) <= 4 * W_ * XP_ && gemv1_lds_bytes(M, K) + size_t(W_) * 1024 <= 64 * 1024; };
+  if (N / 16 <= WZ_GV1_MAX_TILES) {
+#define WZ_G1_(W_, NKB_, XP_)                                                                                 \
+  if (qa) return launch_gemv1<W_, NKB_, 1, true>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream); \
+  if (fits1(W_, 1)) return launch_gemv1<W_, NKB_, 1, false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream); \
+  if (XP_ >= 2 && fits1(W_, 2)) return launch_gemv1<W_, NKB_, (XP_ >= 2 ? 2 : 1), false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream); \
+  if (XP_ >= 4 && fits1(W_, 4)) return launch_gemv1<W_, NKB_, (XP_ >= 4 ? 4 : 1), false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream); \
+  if (XP_ >= 8 && fits1(W_, 8)) return launch_gemv1<W_, NKB_, (XP_ >= 8 ? 8 : 1), false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream); \
+  break
+#define WZ_G1(...) WZ_G1_(__VA_ARGS__)
+    switch (K) {
+      case 1024: WZ_G1(WZ_GV1_K1024);
+      case 2048: WZ_G1(WZ_GV1_K2048);
+      case 4096: WZ_G1(WZ_GV1_K4096);
+      case 8192: WZ_G1(WZ_GV1_K8192);
+      default: break;
+    }
+#undef WZ_G1
+#undef WZ_G1_
+  }
 #define WZ_GV(...)                                                                                          \
   return qa ? launch_gemv<__VA_ARGS__, true>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream)          \
             : launch_gemv<__VA_ARGS__, false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream)

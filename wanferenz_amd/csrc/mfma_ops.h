@@ -97,6 +97,18 @@ __device__ __forceinline__ ARaw a_load_bf16(const uint16_t* row, int kb, int g) 
   return r;
 }
 
+// a_load_bf16 of a row that exists: no null test, so the loads of several
+// K-blocks go out back to back.
+__device__ __forceinline__ ARaw a_load_bf16_row(const uint16_t* row, int kb, int g) {
+  ARaw r;
+  const uint16_t* p = row + kb * 128 + g * 16;
+  r.w[0] = load16(p);
+  r.w[1] = load16(p + 8);
+  r.w[2] = load16(p + 64);
+  r.w[3] = load16(p + 72);
+  return r;
+}
+
 __device__ __forceinline__ AOp a_quant_bf16(const ARaw& r, bool pow2) {
   AOp a = a_zero();
   const v4i* w = r.w;
