@@ -311,6 +311,26 @@ int wz_rmsnorm_quant(const void* x_bf16, const float* weight, void* q_e4m3, void
 int wz_add_rmsnorm_quant(const void* x_bf16, const void* b_bf16, const float* weight, void* sum_bf16,
                          void* q_e4m3, void* s, int64_t T, int64_t D, float eps, int scale_kind, hipStream_t stream);
 
+/* The decoder block's norm and the FP8 projections it feeds in one launch:
+ * c0 / c1 = the two linears of wz_fp8_gemm_packed_pair on act_quant(RMSNorm(h))
+ * (architecture.py:217-230, reference.py:117-146; the attention side's
+ * attn_norm -> wq_a / wkv and q_norm -> wq_b / indexer wq_b,
+ * architecture.py:611-672, 853-874), where h = x, or h = x + b (the residual
+ * step, a bf16 add) when b_bf16 is given; sum_bf16 (optional, needs b)
+ * receives h.  x, b [M, K] bf16, norm_weight fp32 [K], K in {1024, 2048, 4096,
+ * 8192}; c1 null means one linear (N0 = N).  The codes the linears read are
+ * those of wz_add_rmsnorm_quant / wz_rmsnorm_quant bit for bit.  M is limited
+ * to wz_fp8_norm_linear_max_rows(K) (4 at K = 1024, 4096, 8192; 2 at 2048);
+ * larger M raises WZ_EINVAL (run the unfused ops).  Outputs must not overlap
+ * the inputs.  No counterpart in the reference's kernel set. */
+int wz_fp8_norm_linear_packed_pair(const void* x_bf16, const void* b_bf16, const float* norm_weight, float eps,
+                                   void* sum_bf16, const void* w_packed, const void* w_s, void* c0_bf16,
+                                   int64_t N0, void* c1_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
+                                   int w_scale_kind, hipStream_t stream);
+
+/* Rows wz_fp8_norm_linear_packed_pair serves at K (0: K unsupported). */
+int wz_fp8_norm_linear_max_rows(int64_t K);
+
 /* Sparse attention over gathered KV rows — sparse_attn(q, kv, attn_sink, topk_idxs,
  * softmax_scale), torch_ops.py:114-146 / reference.py:314-418: blockwise online
  * softmax with a per-head sink logit in the denominator, K = V = kv (one KV head).

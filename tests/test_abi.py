@@ -103,6 +103,24 @@ def test_argument_errors_are_reported_without_a_device():
     assert "n_experts" in _err()
 
 
+def test_fused_norm_linear_limits_and_errors():
+    L = N.lib()
+    assert [L.wz_fp8_norm_linear_max_rows(k) for k in (1024, 2048, 4096, 8192, 1536)] == [4, 2, 4, 4, 0]
+    f = L.wz_fp8_norm_linear_packed_pair
+    # K outside the GEMV set
+    assert f(None, None, None, ctypes.c_float(1e-6), None, None, None, None, 256, None, 1, 256, 1536, 1, 1, None) == -1
+    assert "K=1536" in _err()
+    # a split that is not a multiple of 128, and a sum without the addend
+    assert f(None, None, None, ctypes.c_float(1e-6), None, None, None, None, 48, ctypes.c_void_p(16), 1, 256, 1024,
+             1, 1, None) == -1
+    assert "split" in _err()
+    assert f(None, None, None, ctypes.c_float(1e-6), ctypes.c_void_p(16), None, None, None, 256, None, 1, 256, 1024,
+             1, 1, None) == -1
+    assert "addend" in _err()
+    # zero rows: nothing to do
+    assert f(None, None, None, ctypes.c_float(1e-6), None, None, None, None, 256, None, 0, 256, 1024, 1, 1, None) == 0
+
+
 def test_zero_tokens_is_a_no_op():
     L = N.lib()
     d = _desc()

@@ -522,6 +522,50 @@ def test_fp8_pair_equals_two_linears(gpu, M, N0, N1, K):
     assert torch.equal(y0, l0.gemm(q, qs)) and torch.equal(y1, l1.gemm(q, qs))
 
 
+@pytest.mark.parametrize("with_b", [False, True])
+@pytest.mark.parametrize("M,N0,N1,K,wfp32", [(4, 1024, 512, 4096, False), (1, 1024, 512, 4096, True),
+                                              (3, 32768, 8192, 1024, False), (4, 256, 128, 1024, True),
+                                              (2, 256, 48, 2048, False), (4, 128, 64, 8192, False),
+                                              (2, 128, 16, 8192, True)])
+def test_fused_norm_pair_equals_unfused(gpu, with_b, M, N0, N1, K, wfp32):
+    """PackedFp8Pair.norm_gemm (RMSNorm, with b the residual step first, quantised
+    inside the projections' launch) gives the unfused ops' outputs bit for bit:
+    add_rms_norm_quant / rms_norm_quant, then the pair's GEMV; the sum output equals
+    the add's.  Rows include a zero row (the norm's eps floor), a row of tiny values
+    and a row of large ones; M above norm_linear_rows(K) is refused."""
+    from oracle.numerics import bf16_bits
+    from wanferenz_amd import stage
+
+    w0, s0 = stage.synthetic_linear(N0, K, N0 + K + 7, gpu, fp32_scales=wfp32)
+    w1, s1 = stage.synthetic_linear(N1, K, N1 + K + 8, gpu, fp32_scales=wfp32)
+    pair = kernels.PackedFp8Pair(w0, s0, w1, s1)
+    xf = from_bf16_bits(_x(M * 3 + K, M, K)).reshape(M, K)
+    if M >= 2:
+        xf[0] = 0.0
+        xf[1] *= np.float32(1e-30)
+    if M >= 3:
+        xf[2] *= np.float32(3e4)
+    x = bf16_tensor(bf16_bits(xf), gpu).view(M, K)
+    nw = torch.from_numpy(np.linspace(0.5, 1.5, K, dtype=np.float32)).to(gpu)
+    b = bf16_tensor(_x(M * 5 + K + 1, M, K), gpu).view(M, K) if with_b else None
+    if with_b:
+        h, q, qs = kernels.add_rms_norm_quant(x, b, nw, 1e-6)
+        hf, y0, y1 = pair.norm_gemm(x, nw, 1e-6, b=b)
+        torch.cuda.synchronize()
+        assert torch.equal(hf, h)
+    else:
+        q, qs = kernels.rms_norm_quant(x, nw, 1e-6)
+        y0, y1 = pair.norm_gemm(x, nw, 1e-6)
+    r0, r1 = pair.gemm(q, qs)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, r0) and torch.equal(y1, r1)
+    rows = kernels.norm_linear_rows(K)
+    assert rows >= M
+    with pytest.raises(Exception):
+        big = bf16_tensor(_x(9, rows + 1, K), gpu).view(rows + 1, K)
+        pair.norm_gemm(big, nw, 1e-6)
+
+
 @pytest.mark.parametrize("act_fmt", ["ue8m0", None])
 @pytest.mark.parametrize("G,N,K", [(6, 4096, 4096), (6, 4096, 2048), (1, 256, 1024), (40, 128, 512)])
 def test_grouped_fp4_gemm(gpu, act_fmt, G, N, K):

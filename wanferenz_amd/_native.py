@@ -52,6 +52,9 @@ SIGNATURES = {
     "wz_add_bf16": (_I, [_P, _P, _P, _I64, _P]),
     "wz_rmsnorm_quant": (_I, [_P, _P, _P, _P, _I64, _I64, _F, _I, _P]),
     "wz_add_rmsnorm_quant": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _I, _P]),
+    "wz_fp8_norm_linear_packed_pair": (_I, [_P, _P, _P, _F, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I, _I,
+                                            _P]),
+    "wz_fp8_norm_linear_max_rows": (_I, [_I64]),
     "wz_fp8_wire_pack": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "wz_sparse_attn_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "wz_sparse_attn": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P]),

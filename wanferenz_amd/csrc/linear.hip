@@ -219,15 +219,33 @@ __global__ __launch_bounds__(W * 64, MINW) void fp8_gemv_kernel(const void* __re
 // The same block amax, scale and rounding as act_quant, and the ring kernel's
 // K split, so both kernels give the same bits.  Four waves sum the W
 // K-partials of the 16 x 16 tile in wave order.
-template <int W, int NKB, int XP, bool QA, bool AP2, bool BP2>
+//   NORM: x is the bf16 input of RMSNorm (fp32 weight nw [K], eps), first the
+//   residual step x + xb when xb is given (written to hsum by workgroup 0);
+//   the norm output is quantised into LDS as above.  Row r is taken by NWR
+//   waves whose thread t = 64 nw + lane holds chunks t + 256 j: the mapping,
+//   sequential sum of squares, xor butterfly and partial order of
+//   rmsnorm_quant_kernel, so the codes are that kernel's bit for bit.
+template <int W, int NKB>
+struct GvNorm {
+  static constexpr int NJ = (W * NKB + 15) / 16;                               // chunks per thread
+  static constexpr int NWR = (W * NKB + 3) / 4 < 4 ? (W * NKB + 3) / 4 : 4;  // waves per row
+  static constexpr int ROWS = W / NWR;                                          // rows per launch
+};
+
+template <int W, int NKB, int XP, bool QA, bool AP2, bool BP2, bool NORM>
 __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restrict__ x, const void* __restrict__ xs,
                                                            int a_kind, const uint8_t* __restrict__ wp,
                                                            const void* __restrict__ w_s,
                                                            const uint16_t* __restrict__ res, uint16_t* __restrict__ y,
                                                            uint16_t* __restrict__ y_hi, int n_split, int M, int N,
-                                                           int K) {
+                                                           int K, const float* __restrict__ nw, float eps,
+                                                           const uint16_t* __restrict__ xb,
+                                                           uint16_t* __restrict__ hsum) {
   static_assert(W >= 4, "the epilogue uses four waves");
+  static_assert(!(NORM && QA), "the norm path starts from bf16 rows");
+  using NP = GvNorm<W, NKB>;
   __shared__ float red[W * 4 * kWave];
+  __shared__ float part[NORM ? NP::ROWS : 1][4];
   extern __shared__ __align__(16) uint8_t gv_lds[];  // !QA: e4m3 rows [M][K + 16], then (e8m0, scale) per pair
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = lane & 15, g = lane >> 4;
@@ -235,7 +253,8 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
   const int ldk = K + 16;
 
   AOp a[NKB];
-  uint4 xr[QA ? 1 : XP];
+  uint4 xr[QA || NORM ? 1 : XP];
+  v4i nv[NORM ? NP::NJ : 1], nbv[NORM ? NP::NJ : 1], nwv[NORM ? NP::NJ : 1][2];
   const int P = M * KB;
   if constexpr (QA) {
     const int xrow = nl < M ? nl : M - 1;  // rows past M repeat row M - 1; their outputs are dropped
@@ -245,6 +264,16 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
                            : static_cast<const void*>(static_cast<const float*>(xs) + int64_t(xrow) * KB);
 #pragma unroll
     for (int q = 0; q < NKB; ++q) a[q] = a_from_fp8_row(row, srow, kb0 + q, g, a_kind);
+  } else if constexpr (NORM) {
+    const int nr = wave / NP::NWR, rr = nr < M ? nr : M - 1, t = (wave % NP::NWR) * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < NP::NJ; ++j) {
+      const int64_t o = int64_t(rr) * K + (t + 256 * j) * 8;
+      nv[j] = load16(static_cast<const uint16_t*>(x) + o);
+      nbv[j] = load16((xb ? xb : static_cast<const uint16_t*>(x)) + o);  // unconditional: see below
+      nwv[j][0] = load16(nw + (t + 256 * j) * 8);
+      nwv[j][1] = load16(nw + (t + 256 * j) * 8 + 4);
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < XP; ++j) {
@@ -270,9 +299,72 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
     fp8_wscale(w_s, int64_t(item >> 3) * KB + kb0 + q, BP2 ? WZ_WSCALE_E8M0 : WZ_WSCALE_F32, se[q], sf[q]);
   __builtin_amdgcn_sched_barrier(0);
 
-  if constexpr (!QA) {
+  if constexpr (NORM) {
     uint8_t* xq = gv_lds;
     int2* xsc = reinterpret_cast<int2*>(gv_lds + M * ldk);
+    const int nr = wave / NP::NWR, nwi = wave % NP::NWR, t = nwi * 64 + lane;
+    // the addend's loads stay ahead of the weight loads: used only under the
+    // branch below, they would otherwise be sunk into it, behind the weights
+#pragma unroll
+    for (int j = 0; j < NP::NJ; ++j) asm volatile("" ::"v"(nbv[j]));
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NP::NJ; ++j) {
+      if (xb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = bf16lo(uint32_t(nv[j][i])) + bf16lo(uint32_t(nbv[j][i]));
+          const float hi = bf16hi(uint32_t(nv[j][i])) + bf16hi(uint32_t(nbv[j][i]));
+          nv[j][i] = int(uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a0 = bf16lo(uint32_t(nv[j][i])), b0 = bf16hi(uint32_t(nv[j][i]));
+        ss += a0 * a0;
+        ss += b0 * b0;
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, kWave);
+    if (lane == 0) part[nr][nwi] = ss;
+    __syncthreads();
+    {
+      const float* pp = part[nr];
+      const float p2 = NP::NWR > 2 ? pp[2] : 0.0f, p3 = NP::NWR > 3 ? pp[3] : 0.0f;
+      const float var = ((pp[0] + pp[1]) + (p2 + p3)) / float(K);
+      const float rs = 1.0f / sqrtf(var + eps);
+#pragma unroll
+      for (int j = 0; j < NP::NJ; ++j) {
+        const int c = t + 256 * j;
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float w0 = __int_as_float(nwv[j][i >> 1][(i & 1) * 2]);
+          const float w1 = __int_as_float(nwv[j][i >> 1][(i & 1) * 2 + 1]);
+          f[2 * i] = bf16_round(w0 * (bf16lo(uint32_t(nv[j][i])) * rs));
+          f[2 * i + 1] = bf16_round(w1 * (bf16hi(uint32_t(nv[j][i])) * rs));
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = absmax(amax, f[i]);
+        amax = row16_absmax(amax);
+        const ActScale sc = act_scale(amax, AP2);
+        const uint32_t q0 = pack_fp8x4(quant_div(f[0], sc, AP2), quant_div(f[1], sc, AP2),
+                                       quant_div(f[2], sc, AP2), quant_div(f[3], sc, AP2));
+        const uint32_t q1 = pack_fp8x4(quant_div(f[4], sc, AP2), quant_div(f[5], sc, AP2),
+                                       quant_div(f[6], sc, AP2), quant_div(f[7], sc, AP2));
+        if (nr < M) {
+          *reinterpret_cast<uint2*>(xq + nr * ldk + c * 8) = make_uint2(q0, q1);
+          if ((lane & 15) == 0) xsc[nr * KB + c / 16] = make_int2(AP2 ? sc.e8m0 : kE8m0One, __float_as_int(sc.s));
+        }
+      }
+    }
+  }
+  if constexpr (NORM || !QA) {
+    uint8_t* xq = gv_lds;
+    int2* xsc = reinterpret_cast<int2*>(gv_lds + M * ldk);
+    if constexpr (!NORM) {
     // each lane's amax of its eight elements, for every pass: the x loads
     // are used here, ahead of the passes' branches, so none of them is sunk
     // into a branch behind the weight loads (its wait would drain those)
@@ -303,6 +395,7 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
           if (nl == 0) xsc[pr] = make_int2(AP2 ? sc.e8m0 : kE8m0One, __float_as_int(sc.s));
         }
       }
+    }
     }
     __syncthreads();
 #pragma unroll
@@ -338,6 +431,15 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
       } else {
         y_hi[int64_t(row) * (N - n_split) + (col - n_split)] = f32_to_bf16(v);
       }
+    }
+  }
+  if constexpr (NORM) {
+    // the residual step's sum, by workgroup 0, last: stores count in vmcnt, so
+    // issued earlier they would make the quantisation's waits cover the weights
+    const int nr = wave / NP::NWR, t = (wave % NP::NWR) * 64 + lane;
+    if (xb && hsum && blockIdx.x == 0 && nr < M) {
+#pragma unroll
+      for (int j = 0; j < NP::NJ; ++j) *reinterpret_cast<v4i*>(hsum + int64_t(nr) * K + (t + 256 * j) * 8) = nv[j];
     }
   }
 }
@@ -487,8 +589,8 @@ static int launch_gemv1(const void* x, const void* xs, int a_kind, const uint8_t
   const bool bp = w_kind == WZ_WSCALE_E8M0;
   const size_t lds = QA ? 0 : gemv1_lds_bytes(M, K);
 #define WZ_GV1(AP, BP)                                                                                        \
-  WZ_LAUNCH("fp8_gemv1", stream, (fp8_gemv1_kernel<W, NKB, XP, QA, AP, BP>), grid, block, lds, x, xs, a_kind, w, \
-            w_s, res, y, y_hi, int(n_split), int(M), int(N), int(K))
+  WZ_LAUNCH("fp8_gemv1", stream, (fp8_gemv1_kernel<W, NKB, XP, QA, AP, BP, false>), grid, block, lds, x, xs, a_kind, \
+            w, w_s, res, y, y_hi, int(n_split), int(M), int(N), int(K), nullptr, 0.0f, nullptr, nullptr)
   if (pow2) {
     if (bp) WZ_GV1(true, true); else WZ_GV1(true, false);
   } else {
@@ -686,4 +788,99 @@ extern "C" int wz_fp4_gemm_packed(const void* a_e4m3, const void* a_s, const voi
   return launch_dense_fp4(static_cast<const uint8_t*>(w_packed), static_cast<const uint32_t*>(w_packed_s),
                           static_cast<const uint8_t*>(a_e4m3), xs, act_scale_kind != WZ_SCALE_F32,
                           static_cast<uint16_t*>(c_bf16), M, N, K, stream);
+}
+
+namespace wz {
+
+// RMSNorm (+ the residual step) fused into the one-tile GEMV's x path.
+template <int W, int NKB>
+static int launch_norm_gemv1(const void* x, const uint16_t* b, const float* nw, float eps, uint16_t* hsum,
+                             const uint8_t* w, const void* w_s, int w_kind, uint16_t* y, uint16_t* y_hi,
+                             int64_t n_split, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream) {
+  if (M > GvNorm<W, NKB>::ROWS)
+    return set_error(WZ_EINVAL, "fp8_norm_linear_packed: M=%lld rows exceed the %d the fused norm serves at K=%lld",
+                     (long long)M, GvNorm<W, NKB>::ROWS, (long long)K);
+  const dim3 grid(unsigned(N / 16)), block(W * 64);
+  const size_t lds = gemv1_lds_bytes(M, K);
+  const bool bp = w_kind == WZ_WSCALE_E8M0;
+#define WZ_NG1(AP, BP)                                                                                          \
+  WZ_LAUNCH("fp8_norm_gemv1", stream, (fp8_gemv1_kernel<W, NKB, 1, false, AP, BP, true>), grid, block, lds, x, nullptr, \
+            0, w, w_s, nullptr, y, y_hi, int(n_split), int(M), int(N), int(K), nw, eps, b, hsum)
+  if (pow2) {
+    if (bp) WZ_NG1(true, true); else WZ_NG1(true, false);
+  } else {
+    if (bp) WZ_NG1(false, true); else WZ_NG1(false, false);
+  }
+#undef WZ_NG1
+  return check_launch("fp8_norm_gemv1");
+}
+
+template <int W, int NKB, int XP>
+static int norm_rows(int) { return GvNorm<W, NKB>::ROWS; }
+
+}  // namespace wz
+
+extern "C" int wz_fp8_norm_linear_max_rows(int64_t K) {
+  using namespace wz;
+#define WZ_NR(...) return norm_rows<__VA_ARGS__>(0)
+  switch (K) {
+    case 1024: WZ_NR(WZ_GV1_K1024);
+    case 2048: WZ_NR(WZ_GV1_K2048);
+    case 4096: WZ_NR(WZ_GV1_K4096);
+    case 8192: WZ_NR(WZ_GV1_K8192);
+    default: return 0;
+  }
+#undef WZ_NR
+}
+
+extern "C" int wz_fp8_norm_linear_packed_pair(const void* x_bf16, const void* b_bf16, const float* norm_weight,
+                                              float eps, void* sum_bf16, const void* w_packed, const void* w_s,
+                                              void* c0_bf16, int64_t N0, void* c1_bf16, int64_t M, int64_t N,
+                                              int64_t K, int act_scale_kind, int w_scale_kind, hipStream_t stream) {
+  using namespace wz;
+  const char* name = "fp8_norm_linear_packed_pair";
+  if (M < 0 || N <= 0 || N % 16 || N > (1 << 30) || !gemv_shape_ok(K))
+    return set_error(WZ_EINVAL, "%s: bad shape M=%lld N=%lld K=%lld (K in 1024, 2048, 4096, 8192)", name,
+                     (long long)M, (long long)N, (long long)K);
+  if (c1_bf16 ? (N0 <= 0 || N0 >= N || N0 % 128) : N0 != N)
+    return set_error(WZ_EINVAL, "%s: split N0=%lld must be a multiple of 128 inside N=%lld (N0 = N without c1)",
+                     name, (long long)N0, (long long)N);
+  if (act_scale_kind < WZ_SCALE_F32 || act_scale_kind > WZ_SCALE_UE8M0_F32 ||
+      (w_scale_kind != WZ_WSCALE_F32 && w_scale_kind != WZ_WSCALE_E8M0))
+    return set_error(WZ_EINVAL, "%s: bad scale kinds %d/%d", name, act_scale_kind, w_scale_kind);
+  if (sum_bf16 && !b_bf16) return set_error(WZ_EINVAL, "%s: a sum output needs the addend b", name);
+  if (M == 0) return WZ_OK;
+  if (!x_bf16 || !norm_weight || !w_packed || !w_s || !c0_bf16) return set_error(WZ_EINVAL, "%s: null pointer", name);
+  // workgroup 0 writes the sum while the others read x and b; every workgroup
+  // writes its outputs while others may still read x, b
+  const size_t xbytes = size_t(M) * size_t(K) * 2;
+  const size_t y0bytes = size_t(M) * size_t(N0) * 2, y1bytes = size_t(M) * size_t(N - N0) * 2;
+  auto meets = [](const void* a, size_t na, const void* b, size_t nb) {
+    const char *pa = static_cast<const char*>(a), *pb = static_cast<const char*>(b);
+    return pa < pb + nb && pb < pa + na;
+  };
+  const void* ins[2] = {x_bf16, b_bf16};
+  for (const void* in : ins) {
+    if (!in) continue;
+    if ((sum_bf16 && meets(sum_bf16, xbytes, in, xbytes)) || meets(c0_bf16, y0bytes, in, xbytes) ||
+        (c1_bf16 && meets(c1_bf16, y1bytes, in, xbytes)))
+      return set_error(WZ_EINVAL, "%s: an output overlaps an input", name);
+  }
+  const uint8_t* w = static_cast<const uint8_t*>(w_packed);
+  const uint16_t* b = static_cast<const uint16_t*>(b_bf16);
+  uint16_t *y0 = static_cast<uint16_t*>(c0_bf16), *y1 = static_cast<uint16_t*>(c1_bf16),
+           *hs = static_cast<uint16_t*>(sum_bf16);
+  const bool pow2 = act_scale_kind != WZ_SCALE_F32;
+#define WZ_NL_(W_, NKB_, XP_)                                                                                  \
+  return launch_norm_gemv1<W_, NKB_>(x_bf16, b, norm_weight, eps, hs, w, w_s, w_scale_kind, y0, y1, N0, M, N, K, \
+                                     pow2, stream)
+#define WZ_NL(...) WZ_NL_(__VA_ARGS__)
+  switch (K) {
+    case 1024: WZ_NL(WZ_GV1_K1024);
+    case 2048: WZ_NL(WZ_GV1_K2048);
+    case 4096: WZ_NL(WZ_GV1_K4096);
+    default: WZ_NL(WZ_GV1_K8192);
+  }
+#undef WZ_NL
+#undef WZ_NL_
 }

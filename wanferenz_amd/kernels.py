@@ -396,6 +396,40 @@ class PackedFp8Pair:
                0 if ws is None else ws.numel(), N.stream_handle(q.device))
         return y0, y1
 
+    def norm_gemm(self, x, weight, eps=1e-6, b=None, sum_out=None, out=None, scale_fmt="ue8m0",
+                  scale_dtype=_E8M0):
+        """``gemm(*rms_norm_quant(x, weight, eps))``, or with ``b`` the residual step
+        first (``add_rms_norm_quant(x, b, ...)``, h written to ``sum_out``), in one
+        launch (wz_fp8_norm_linear_packed_pair): the same codes, so the same outputs
+        bit for bit.  At most ``norm_linear_rows(K)`` rows."""
+        assert x.is_contiguous() and weight.is_contiguous() and x.size(-1) == self.K
+        _require_cuda(x, weight)
+        if x.dtype != torch.bfloat16 or weight.dtype != torch.float32 or weight.numel() != self.K:
+            raise TypeError("norm_gemm: x must be bf16 [..., K] and weight float32 [K]")
+        if b is not None:
+            assert b.is_contiguous() and b.shape == x.shape and b.dtype == torch.bfloat16
+            _require_cuda(b)
+        elif sum_out is not None:
+            raise ValueError("norm_gemm: sum_out needs b")
+        M = x.numel() // self.K
+        kind = _act_kind(scale_fmt, scale_dtype)
+        lead = x.size()[:-1]
+        if out is None:
+            out = (torch.empty(*lead, self.N0, dtype=torch.bfloat16, device=x.device),
+                   torch.empty(*lead, self.N1, dtype=torch.bfloat16, device=x.device))
+        if b is not None and sum_out is None:
+            sum_out = torch.empty_like(x)
+        y0, y1 = out
+        N.call("wz_fp8_norm_linear_packed_pair", N.ptr(x), None if b is None else N.ptr(b), N.ptr(weight),
+               float(eps), None if sum_out is None else N.ptr(sum_out), N.ptr(self.packed), N.ptr(self.scale),
+               N.ptr(y0), self.N0, N.ptr(y1), M, self.N, self.K, kind, self.w_kind, N.stream_handle(x.device))
+        return (y0, y1) if b is None else (sum_out, y0, y1)
+
+
+def norm_linear_rows(K: int) -> int:
+    """Rows the fused norm + FP8 projections (``PackedFp8Pair.norm_gemm``) serve at K."""
+    return int(N.lib().wz_fp8_norm_linear_max_rows(int(K)))
+
 
 def rms_norm(x, weight, eps=1e-6, out=None):
     """RMSNorm.forward (architecture.py:217-230): bf16(weight * (x * rsqrt(mean(x^2) + eps))),

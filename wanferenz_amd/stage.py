@@ -26,12 +26,15 @@ Per block, with h the [T, D] residual stream (bf16):
     e  = moe(m)
     (after the last block: h = h1 + e)
 
-Each FP8 input is produced quantised by the norm that precedes it
-(rms_norm_quant), the two projections that read one input run as one launch
-(wq_a with wkv, wq_b with the indexer's wq_b: kernels.PackedFp8Pair), the
-residual add of the attention side sits in wo_b's epilogue and that of the MoE
-side in the next block's norm.  Every buffer is allocated once, so a step is a
-fixed sequence of launches.
+The two projections that read one input run as one launch (wq_a with wkv,
+wq_b with the indexer's wq_b: kernels.PackedFp8Pair), and the norm that feeds
+them (attn_norm with the previous block's MoE residual, q_norm) runs inside
+that launch (PackedFp8Pair.norm_gemm: the rms_norm_quant codes, bit for bit)
+when T fits its rows (T <= 4); otherwise each FP8 input is produced quantised
+by the norm that precedes it (rms_norm_quant).  The residual add of the
+attention side sits in wo_b's epilogue and that of the MoE side in the next
+block's norm.  Every buffer is allocated once, so a step is a fixed sequence of
+launches.
 """
 
 from __future__ import annotations
@@ -101,7 +104,7 @@ class DecodeStage:
     """A stack of StageBlocks at a fixed token count T; ``step`` runs it eagerly,
     ``capture`` records one step as a graph, ``replay`` runs the graph."""
 
-    def __init__(self, blocks: Sequence[StageBlock], T: int, eps: float = 1e-6):
+    def __init__(self, blocks: Sequence[StageBlock], T: int, eps: float = 1e-6, fused_norms: bool = True):
         self.blocks: List[StageBlock] = list(blocks)
         self.T, self.eps = T, eps
         b0 = self.blocks[0]
@@ -130,6 +133,9 @@ class DecodeStage:
             for lin in (b.qa_kv, b.q_idx, b.wo_b):
                 lin.reserve(T)
             b.moe.reserve(T)
+        # the norms ride in the projections' launches when T fits the fused path
+        self.fused_norms = fused_norms and all(
+            T <= kernels.norm_linear_rows(lin.K) for b in self.blocks for lin in (b.qa_kv, b.q_idx))
         self.graph = None
 
     def _run(self, routing=None, trace=None):
@@ -138,16 +144,31 @@ class DecodeStage:
         nxt = iter(self.h * (2 * len(self.blocks)))
         for i, b in enumerate(self.blocks):
             h_in, e_in = (None, None) if trace is None else (h.clone(), None if i == 0 else self.e.clone())
-            if i == 0:
-                kernels.rms_norm_quant(h, b.attn_norm, eps, out=self.hq)
+            if self.fused_norms:
+                # attn_norm (with the previous block's MoE residual) and q_norm run
+                # inside the projections' launches, on the codes the unfused norms
+                # give; a trace records those codes from the unfused kernels
+                if i == 0:
+                    b.qa_kv.norm_gemm(h, b.attn_norm, eps, out=(self.qa, self.kv))
+                else:
+                    hs = next(nxt)
+                    b.qa_kv.norm_gemm(h, b.attn_norm, eps, b=self.e, sum_out=hs, out=(self.qa, self.kv))
+                    h = hs
+                b.q_idx.norm_gemm(self.qa, b.q_norm, eps, out=(self.q, self.iq))
+                if trace is not None:
+                    kernels.rms_norm_quant(h, b.attn_norm, eps, out=self.hq)
+                    kernels.rms_norm_quant(self.qa, b.q_norm, eps, out=self.qq)
             else:
-                # the previous block's MoE residual, fused into this block's norm
-                hs = next(nxt)
-                kernels.add_rms_norm_quant(h, self.e, b.attn_norm, eps, sum_out=hs, out=self.hq)
-                h = hs
-            b.qa_kv.gemm(*self.hq, out=(self.qa, self.kv))
-            kernels.rms_norm_quant(self.qa, b.q_norm, eps, out=self.qq)
-            b.q_idx.gemm(*self.qq, out=(self.q, self.iq))
+                if i == 0:
+                    kernels.rms_norm_quant(h, b.attn_norm, eps, out=self.hq)
+                else:
+                    # the previous block's MoE residual, fused into this block's norm
+                    hs = next(nxt)
+                    kernels.add_rms_norm_quant(h, self.e, b.attn_norm, eps, sum_out=hs, out=self.hq)
+                    h = hs
+                b.qa_kv.gemm(*self.hq, out=(self.qa, self.kv))
+                kernels.rms_norm_quant(self.qa, b.q_norm, eps, out=self.qq)
+                b.q_idx.gemm(*self.qq, out=(self.q, self.iq))
             h1 = next(nxt)
             b.wo_b(self.iq, out=h1, residual=h)
             kernels.rms_norm(h1, b.ffn_norm, eps, out=self.m)
