@@ -151,9 +151,13 @@ def test_fp4_gemm_exact(gpu, M, N, K):
 
 
 @pytest.mark.parametrize("act_fmt", ["ue8m0", None])
-@pytest.mark.parametrize("M,N,K", [(20, 256, 1024), (130, 128, 2048), (200, 384, 4096), (64, 16, 512)])
+@pytest.mark.parametrize("M,N,K", [(20, 256, 1024), (130, 128, 2048), (200, 384, 4096), (64, 16, 512),
+                                   (300, 256, 1024), (512, 512, 2048), (256, 768, 1536), (384, 512, 4096)])
 def test_fp4_gemm_packed_random(gpu, act_fmt, M, N, K):
-    """fp4_gemm on the packed weight (the tile GEMM of the prefill) against the oracle."""
+    """fp4_gemm on the packed weight against the oracle: the prefill tile GEMM, and
+    at M >= 256 with N a multiple of 256 and power-of-two activation scales the
+    128 x 256 big-tile kernel (ragged M; K = 1536 leaves the last scale dword half
+    used)."""
     xb = _x(M + 5 * N + K, M, K)
     sd = torch.float8_e8m0fnu if act_fmt else torch.float32
     x = bf16_tensor(xb, gpu)
@@ -168,9 +172,11 @@ def test_fp4_gemm_packed_random(gpu, act_fmt, M, N, K):
     assert (got == ref).mean() > 0.9, (got == ref).mean()
 
 
-@pytest.mark.parametrize("M,N,K", [(17, 128, 1024), (100, 256, 2048), (64, 128, 4096)])
+@pytest.mark.parametrize("M,N,K", [(17, 128, 1024), (100, 256, 2048), (64, 128, 4096), (260, 256, 2048),
+                                   (512, 512, 1024)])
 def test_fp4_gemm_packed_exact(gpu, M, N, K):
-    """Small codes and unit scales through the packed tile GEMM: bit-exact bf16."""
+    """Small codes and unit scales through the packed tile GEMM (and the big-tile
+    kernel at M >= 256): bit-exact bf16."""
     a_codes = _exact_codes(M * K + 3, M * K, [0x00, 0x30, 0xB0, 0x38, 0xB8, 0x3C, 0xBC, 0x40, 0xC0]).reshape(M, K)
     w = synth.fill_u8(synth.stream_key(N + 3, 7), 0, N * K // 2).reshape(N, K // 2)
     ws = np.full((N, K // 32), 127, np.uint8)
