@@ -56,7 +56,8 @@ def _dequant(v: torch.Tensor, s: torch.Tensor, block: int) -> torch.Tensor:
 def unpack_fp4(b: torch.Tensor) -> torch.Tensor:
     """torch_ops.py:84-92: packed e2m1 bytes [N, K/2] -> float32 [N, K], low nibble first."""
     u = b.view(torch.uint8)
-    return torch.stack([_FP4_TABLE[(u & 0x0F).long()], _FP4_TABLE[(u >> 4).long()]], dim=-1).flatten(-2)
+    t = _FP4_TABLE.to(u.device)
+    return torch.stack([t[(u & 0x0F).long()], t[(u >> 4).long()]], dim=-1).flatten(-2)
 
 
 def fp8_gemm(a, a_s, w_codes, w_s, out_dtype=torch.bfloat16) -> torch.Tensor:

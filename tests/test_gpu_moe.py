@@ -272,6 +272,35 @@ def test_moe_prefill_oracle_cases(gpu, name):
     print(f"{name}: rel {rel:.2e} cos {cos:.8f} bit-equal {np.mean(got == ref.y):.4f} near-ties {near}")
 
 
+def _torch_oracle_rows(cfg, w, xb, g, dev):
+    """Every row of the layer by the torch float32 restatement of the reference CPU
+    path (oracle/torch_ref.py: act_quant, dequantised fp4/fp8 GEMMs, clamp-SwiGLU,
+    the non-accumulating y[idx] += per expert, then the shared expert), run on the
+    device over the numpy oracle's exact routing ``g``, the weights read back from
+    the layer's reference-layout bank."""
+    from oracle import torch_ref as tr
+
+    I, D = cfg.inter, cfg.dim
+
+    def e8m0(t):
+        return torch.ldexp(torch.ones(t.shape, device=dev), t.to(torch.int32).float() - 127.0)
+
+    x = torch.from_numpy(from_bf16_bits(xb).reshape(-1, D)).to(dev).to(torch.bfloat16)
+    idx = torch.from_numpy(g.indices).to(dev)
+    wts = torch.from_numpy(g.weights).to(dev)
+    y = torch.zeros(x.shape, dtype=torch.float32, device=dev)
+    for e in sorted(set(g.indices.ravel().tolist())):
+        w13, s13 = w.w13[e], e8m0(w.w13_s[e])
+        ws = (tr.QLinear("fp4", w13[:I], s13[:I]), tr.QLinear("fp4", w13[I:], s13[I:]),
+              tr.QLinear("fp4", w.w2[e], e8m0(w.w2_s[e])))
+        rows, slot = torch.where(idx == e)
+        y[rows] += tr.expert_forward(ws, x[rows], wts[rows, slot, None], cfg.swiglu_limit, True).float()
+    shared = tuple(tr.QLinear("fp8", a, e8m0(b)) for a, b in
+                   ((w.sh_w1, w.sh_w1_s), (w.sh_w3, w.sh_w3_s), (w.sh_w2, w.sh_w2_s)))
+    y += tr.expert_forward(shared, x, None, cfg.swiglu_limit, True).float()
+    return f32_of_bf16(y.to(torch.bfloat16))
+
+
 def _decode_chunks(moe, x, chunk=16):
     return torch.cat([moe.forward(x[i:i + chunk]) for i in range(0, x.size(0), chunk)])
 
@@ -281,9 +310,10 @@ def _decode_chunks(moe, x, chunk=16):
 def test_v4_prefill_parity(v4_layer, T, bias):
     """Prefill at the V4 shape; "zipf" is the calibrated Zipf(1.1) gate bias of the
     prefill workload (wanferenz_amd/zipf_v4.json).  All routing is checked in full;
-    the outputs of 16 sampled rows (including rows of the most loaded expert)
-    against the oracle, and every row against the decode path run over 16-token
-    chunks."""
+    every output row against the torch float32 restatement of the reference's CPU
+    path (on the device, over the oracle's exact routing), 16 sampled rows
+    (including rows of the most loaded expert) against the numpy oracle, and every
+    row against the decode path run over 16-token chunks."""
     import dataclasses
     cfg, w, host, moe = v4_layer
     b = host["gate_bias"]
@@ -312,12 +342,17 @@ def test_v4_prefill_parity(v4_layer, T, bias):
     ref = om.moe_forward(p, from_bf16_bits(xs))
     rel, cos = om.max_rel_err(got[rows], ref.y), om.cosine(got[rows], ref.y)
     assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    # every row against the torch restatement of the reference path
+    full = _torch_oracle_rows(cfg, w, xb, g, x.device)
+    rel_t, cos_t = om.max_rel_err(got, full), om.cosine(got, full)
+    assert rel_t <= TOL_REL and cos_t >= TOL_COS, (rel_t, cos_t)
     # every row against the decode path on 16-token chunks
     dec = f32_of_bf16(_decode_chunks(moe, x))
     rel_d, cos_d = om.max_rel_err(got, dec), om.cosine(got, dec)
     assert rel_d <= TOL_REL and cos_d >= TOL_COS, (rel_d, cos_d)
     print(f"V4 prefill T={T} ({bias} bias, experts hit {int((counts > 0).sum())}, max rows "
-          f"{int(counts.max())}): {len(rows)} sampled rows vs oracle rel {rel:.2e} cos {cos:.8f}; vs decode "
+          f"{int(counts.max())}): all rows vs torch oracle rel {rel_t:.2e} cos {cos_t:.8f} bit-equal "
+          f"{np.mean(got == full):.4f}; {len(rows)} sampled rows vs oracle rel {rel:.2e} cos {cos:.8f}; vs decode "
           f"rel {rel_d:.2e} cos {cos_d:.8f} bit-equal {np.mean(got == dec):.4f}; near-ties {near}")
 
 
