@@ -359,15 +359,16 @@ def test_fp8_linear_projection_shapes(gpu, w_fp32, N, K, M):
 @pytest.mark.parametrize("M,N,K", [(1, 256, 4096), (5, 512, 1024), (16, 128, 2048), (40, 256, 4096),
                                    (3, 128, 1536), (1, 512, 8192), (16, 384, 8192), (2, 4096, 1024),
                                    (4, 256, 4096), (9, 256, 4096), (12, 128, 1024), (5, 256, 8192),
-                                   (6, 256, 8192)])
+                                   (6, 256, 8192), (8, 256, 8192), (12, 128, 4096)])
 def test_fp8_linear_packed_exact(gpu, M, N, K):
     """x in {0, +-0.5, +-1, +-1.5} with one 2.0 per 128-block quantises exactly (ue8m0
     scale 2^-7), weight codes of the same values with unit scales: every partial sum
     is exact in fp32, so the packed linear must equal the oracle bit for bit, on the
     GEMV path (M <= 16) and the quantise + tile GEMM path (M = 40, K = 1536).  The
     one-tile GEMV quantises x in LDS in 1, 2, 4 or 8 passes per wave by M x K / 128
-    (M = 1, 4, 12, 9 / 5 at K = 4096 / 8192); M = 6 and 16 at K = 8192 exceed its LDS
-    and run the ring kernel."""
+    (M = 1, 4, 12, 9 / 5 at K = 4096 / 8192); M = 6, 8 at K = 8192 and 12 at 4096 hold
+    more than 64 KB of LDS; M = 16 at K = 8192 needs more passes and runs the ring
+    kernel."""
     from oracle.numerics import bf16_bits
 
     vals = np.array([0.0, 0.5, -0.5, 1.0, -1.0, 1.5, -1.5], np.float32)

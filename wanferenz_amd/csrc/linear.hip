@@ -447,6 +447,19 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
 // dynamic LDS of the one-tile kernel's bf16 path: e4m3 rows + per-pair scales
 static size_t gemv1_lds_bytes(int64_t M, int64_t K) { return size_t(M) * size_t(K + 16) + size_t(M) * size_t(K / 128) * 8; }
 
+// LDS a workgroup may hold on gfx950 (160 KB); dynamic LDS past 64 KB is
+// requested per kernel once (hipFuncAttributeMaxDynamicSharedMemorySize).
+constexpr size_t kLdsMax = 160 * 1024;
+template <typename F>
+static int allow_lds(F* kernel, size_t bytes, int& granted) {
+  if (bytes <= 64 * 1024 || int(bytes) <= granted) return 0;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          int(bytes)) != hipSuccess)
+    return set_error(WZ_ELAUNCH, "fp8 gemv: %zu bytes of LDS refused", bytes);
+  granted = int(bytes);
+  return 0;
+}
+
 template <int W, int NKB, int NB, int MINW, bool XF, bool QA>
 static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
                        uint16_t* y, int64_t M, int64_t N, int64_t K, bool pow2, hipStream_t stream);
@@ -589,8 +602,12 @@ static int launch_gemv1(const void* x, const void* xs, int a_kind, const uint8_t
   const bool bp = w_kind == WZ_WSCALE_E8M0;
   const size_t lds = QA ? 0 : gemv1_lds_bytes(M, K);
 #define WZ_GV1(AP, BP)                                                                                        \
-  WZ_LAUNCH("fp8_gemv1", stream, (fp8_gemv1_kernel<W, NKB, XP, QA, AP, BP, false>), grid, block, lds, x, xs, a_kind, \
-            w, w_s, res, y, y_hi, int(n_split), int(M), int(N), int(K), nullptr, 0.0f, nullptr, nullptr)
+  do {                                                                                                          \
+    static int granted = 0;                                                                                     \
+    if (int rc = allow_lds(fp8_gemv1_kernel<W, NKB, XP, QA, AP, BP, false>, lds, granted)) return rc;              \
+    WZ_LAUNCH("fp8_gemv1", stream, (fp8_gemv1_kernel<W, NKB, XP, QA, AP, BP, false>), grid, block, lds, x, xs, a_kind, w, \
+              w_s, res, y, y_hi, int(n_split), int(M), int(N), int(K), nullptr, 0.0f, nullptr, nullptr);         \
+  } while (0)
   if (pow2) {
     if (bp) WZ_GV1(true, true); else WZ_GV1(true, false);
   } else {
@@ -626,7 +643,7 @@ static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, con
   // the bf16 path quantises M x K / 128 pairs in passes of four per wave, the
   // fewest of 1, 2, 4, 8 passes that cover them (at most the third value of
   // each WZ_GV1_K*), and holds them in LDS
-  auto fits1 = [&](int W_, int XP_) { return M * (K / 128) <= 4 * W_ * XP_ && gemv1_lds_bytes(M, K) + size_t(W_) * 1024 <= 64 * 1024; };
+  auto fits1 = [&](int W_, int XP_) { return M * (K / 128) <= 4 * W_ * XP_ && gemv1_lds_bytes(M, K) + size_t(W_) * 1024 <= kLdsMax; };
   if (N / 16 <= WZ_GV1_MAX_TILES) {
 #define WZ_G1_(W_, NKB_, XP_)                                                                                 \
   if (qa) return launch_gemv1<W_, NKB_, 1, true>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream); \
@@ -804,8 +821,12 @@ static int launch_norm_gemv1(const void* x, const uint16_t* b, const float* nw, 
   const size_t lds = gemv1_lds_bytes(M, K);
   const bool bp = w_kind == WZ_WSCALE_E8M0;
 #define WZ_NG1(AP, BP)                                                                                          \
-  WZ_LAUNCH("fp8_norm_gemv1", stream, (fp8_gemv1_kernel<W, NKB, 1, false, AP, BP, true>), grid, block, lds, x, nullptr, \
-            0, w, w_s, nullptr, y, y_hi, int(n_split), int(M), int(N), int(K), nw, eps, b, hsum)
+  do {                                                                                                          \
+    static int granted = 0;                                                                                     \
+    if (int rc = allow_lds(fp8_gemv1_kernel<W, NKB, 1, false, AP, BP, true>, lds, granted)) return rc;             \
+    WZ_LAUNCH("fp8_norm_gemv1", stream, (fp8_gemv1_kernel<W, NKB, 1, false, AP, BP, true>), grid, block, lds, x, nullptr, 0, \
+              w, w_s, nullptr, y, y_hi, int(n_split), int(M), int(N), int(K), nw, eps, b, hsum);               \
+  } while (0)
   if (pow2) {
     if (bp) WZ_NG1(true, true); else WZ_NG1(true, false);
   } else {
