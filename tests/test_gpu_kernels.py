@@ -529,6 +529,54 @@ def test_fp8_pair_equals_two_linears(gpu, M, N0, N1, K):
     assert torch.equal(y0, l0.gemm(q, qs)) and torch.equal(y1, l1.gemm(q, qs))
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 4096), (4, 256, 8192), (8, 512, 1024), (16, 128, 2048),
+                                   (3, 40960, 1024)])
+def test_fp8_linear_packed_float_act_scales(gpu, M, N, K):
+    """The packed linear with non-power-of-two activation scales (scale_fmt None:
+    amax / 448 as float32, applied on the VALU per K-block), on the one-tile GEMV
+    (its LDS quantisation) and the ring kernel (N = 40960), against the oracle's
+    act_quant(round_pow2=False) and fp8_gemm."""
+    from wanferenz_amd import stage
+
+    w, ws = stage.synthetic_linear(N, K, N + K + 11, gpu, fp32_scales=True)
+    xb = _x(M * 11 + K, M, K)
+    lin = kernels.PackedFp8Linear(w, ws, None)
+    got = f32_of_bf16(lin(bf16_tensor(xb, gpu).view(M, K)))
+    rq, rs = om.act_quant(from_bf16_bits(xb), 128, False)
+    rows = np.arange(min(N, 1024))
+    ref = om.fp8_gemm(rq, rs, bytes8(w[:rows.size]).reshape(rows.size, K), ws[: (rows.size + 127) // 128].cpu().numpy())
+    rel, cos = _close(got[:, rows], ref)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+
+
+@pytest.mark.parametrize("with_b", [False, True])
+@pytest.mark.parametrize("M,K", [(4, 4096), (3, 1024)])
+def test_fused_norm_pair_float_act_scales(gpu, with_b, M, K):
+    """norm_gemm with non-power-of-two activation scales (scale_fmt None, float32
+    scales) = rms_norm_quant / add_rms_norm_quant with the same scales, then the
+    pair's GEMV, bit for bit."""
+    from wanferenz_amd import stage
+
+    w0, s0 = stage.synthetic_linear(256, K, K + 21, gpu, fp32_scales=True)
+    w1, s1 = stage.synthetic_linear(128, K, K + 22, gpu, fp32_scales=True)
+    pair = kernels.PackedFp8Pair(w0, s0, w1, s1, None)
+    x = bf16_tensor(_x(M * 7 + K, M, K), gpu).view(M, K)
+    nw = torch.from_numpy(np.linspace(0.25, 2.0, K, dtype=np.float32)).to(gpu)
+    f32 = dict(scale_fmt=None, scale_dtype=torch.float32)
+    if with_b:
+        b = bf16_tensor(_x(M * 9 + K, M, K), gpu).view(M, K)
+        h, q, qs = kernels.add_rms_norm_quant(x, b, nw, 1e-6, **f32)
+        hf, y0, y1 = pair.norm_gemm(x, nw, 1e-6, b=b, **f32)
+        torch.cuda.synchronize()
+        assert torch.equal(hf, h)
+    else:
+        q, qs = kernels.rms_norm_quant(x, nw, 1e-6, **f32)
+        y0, y1 = pair.norm_gemm(x, nw, 1e-6, **f32)
+    r0, r1 = pair.gemm(q, qs)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, r0) and torch.equal(y1, r1)
+
+
 @pytest.mark.parametrize("with_b", [False, True])
 @pytest.mark.parametrize("M,N0,N1,K,wfp32", [(4, 1024, 512, 4096, False), (1, 1024, 512, 4096, True),
                                               (3, 32768, 8192, 1024, False), (4, 256, 128, 1024, True),
