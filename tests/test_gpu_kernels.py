@@ -549,6 +549,29 @@ def test_fp8_linear_packed_float_act_scales(gpu, M, N, K):
     assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
 
 
+def test_pair_outputs_are_checked(gpu):
+    """Outputs of the wrong size, dtype or layout are refused before any launch."""
+    from wanferenz_amd import stage
+
+    w0, s0 = stage.synthetic_linear(256, 1024, 31, gpu, fp32_scales=False)
+    w1, s1 = stage.synthetic_linear(128, 1024, 32, gpu, fp32_scales=False)
+    pair = kernels.PackedFp8Pair(w0, s0, w1, s1)
+    x = bf16_tensor(_x(5, 4, 1024), gpu).view(4, 1024)
+    nw = torch.ones(1024, dtype=torch.float32, device=gpu)
+    y0 = torch.empty(4, 256, dtype=torch.bfloat16, device=gpu)
+    y1 = torch.empty(4, 128, dtype=torch.bfloat16, device=gpu)
+    for bad in ((y0[:1], y1), (y0, y1.float()), (y0.t(), y1)):
+        with pytest.raises(ValueError):
+            pair.norm_gemm(x, nw, out=bad)
+    with pytest.raises(ValueError):
+        pair.norm_gemm(x, nw, b=x.clone(), sum_out=torch.empty(2, 1024, dtype=torch.bfloat16, device=gpu))
+    q, qs = kernels.rms_norm_quant(x, nw)
+    with pytest.raises(ValueError):
+        pair.gemm(q, qs, out=(y0[:2], y1))
+    pair.norm_gemm(x, nw, out=(y0, y1))
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("with_b", [False, True])
 @pytest.mark.parametrize("M,K", [(4, 4096), (3, 1024)])
 def test_fused_norm_pair_float_act_scales(gpu, with_b, M, K):

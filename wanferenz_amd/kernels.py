@@ -380,16 +380,22 @@ class PackedFp8Pair:
             self._ws = torch.empty(need, dtype=torch.uint8, device=self.packed.device)
         return self
 
+    def _outs(self, lead, M, out, device):
+        if out is None:
+            return (torch.empty(*lead, self.N0, dtype=torch.bfloat16, device=device),
+                    torch.empty(*lead, self.N1, dtype=torch.bfloat16, device=device))
+        for y, n in zip(out, (self.N0, self.N1)):
+            if y.dtype != torch.bfloat16 or not y.is_contiguous() or y.numel() != M * n or y.device != device:
+                raise ValueError(f"PackedFp8Pair: an output must be a contiguous bf16 tensor of {M}x{n} "
+                                 f"elements on {device}, got {y.dtype} {tuple(y.shape)} on {y.device}")
+        return out
+
     def gemm(self, q, q_s, out=None):
         assert q.is_contiguous() and q_s.is_contiguous() and q.size(-1) == self.K
         _require_cuda(q, q_s)
         M = q.numel() // self.K
         self.reserve(M, q_s.dtype)
-        lead = q.size()[:-1]
-        if out is None:
-            out = (torch.empty(*lead, self.N0, dtype=torch.bfloat16, device=q.device),
-                   torch.empty(*lead, self.N1, dtype=torch.bfloat16, device=q.device))
-        y0, y1 = out
+        y0, y1 = self._outs(q.size()[:-1], M, out, q.device)
         ws = self._ws
         N.call("wz_fp8_gemm_packed_pair", N.ptr(q), N.ptr(q_s), N.ptr(self.packed), N.ptr(self.scale), N.ptr(y0),
                self.N0, N.ptr(y1), M, self.N, self.K, _scale_kind_of(q_s), self.w_kind, N.ptr(ws),
@@ -413,13 +419,12 @@ class PackedFp8Pair:
             raise ValueError("norm_gemm: sum_out needs b")
         M = x.numel() // self.K
         kind = _act_kind(scale_fmt, scale_dtype)
-        lead = x.size()[:-1]
-        if out is None:
-            out = (torch.empty(*lead, self.N0, dtype=torch.bfloat16, device=x.device),
-                   torch.empty(*lead, self.N1, dtype=torch.bfloat16, device=x.device))
+        y0, y1 = self._outs(x.size()[:-1], M, out, x.device)
         if b is not None and sum_out is None:
             sum_out = torch.empty_like(x)
-        y0, y1 = out
+        if sum_out is not None and (sum_out.dtype != torch.bfloat16 or not sum_out.is_contiguous()
+                                    or sum_out.numel() != x.numel() or sum_out.device != x.device):
+            raise ValueError("norm_gemm: sum_out must be a contiguous bf16 tensor of x's size on x's device")
         N.call("wz_fp8_norm_linear_packed_pair", N.ptr(x), None if b is None else N.ptr(b), N.ptr(weight),
                float(eps), None if sum_out is None else N.ptr(sum_out), N.ptr(self.packed), N.ptr(self.scale),
                N.ptr(y0), self.N0, N.ptr(y1), M, self.N, self.K, kind, self.w_kind, N.stream_handle(x.device))
