@@ -301,54 +301,55 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
 
 // --------------------------------------------------------------- combine ----
 
-// One workgroup per (token, 2048 columns).  The token's pair rows are put in
-// ascending permuted position (= ascending expert id) once, by its first wave,
-// in LDS; a repeated expert of a hash-routed token counts once, by its last
-// slot (the row a decode step computes; architecture.py:790 index_put keeps
-// the last write).  Each thread then requests its 8 columns of all KMAX rows
-// at once (rows past k repeat the last one and are not added) and sums them
-// in that order, then adds the shared expert's row.
+// One workgroup per (token, 2048 columns).  The token's slots are ordered by
+// their permuted position (= ascending expert id) by every wave alike: the
+// positions and experts are the same across the workgroup, so each wave reads
+// them once and a fixed exchange network sorts them in scalar registers (no
+// shuffle, LDS or barrier in front of the row loads).  A repeated expert of a hash-routed token
+// counts once, by its last slot (the row a decode step computes;
+// architecture.py:790 index_put keeps the last write): a row is skipped when
+// the next in position order has the same expert.  Each thread requests its 8
+// columns of all KMAX rows at once (rows past k repeat the first one and are
+// not added) and sums them in that order, then adds the shared expert's row.
 template <int KMAX>
 __global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int D, uint16_t* __restrict__ y) {
-  __shared__ int s_p[KMAX];
-  __shared__ int s_use[KMAX];
   const int t = blockIdx.y;
   const int c = blockIdx.x * 256 + threadIdx.x;  // 8-column chunk
   const int P = gridDim.y * k;
-  if (threadIdx.x < 64) {
-    const int j = threadIdx.x;
-    const int p = j < k ? clampi(ws.pos[int64_t(t) * k + j], 0, P - 1) : 0x7FFFFFFF;
-    const int e = j < k ? ws.idx[int64_t(t) * k + j] : -1;
-    int rank = 0;  // positions are distinct: rank = slots with a lower position
+  // lane j < k reads slot j (one vector load per array, one wait), then each
+  // slot is read out of its lane into a scalar register
+  const int lane = threadIdx.x & 63, jl = lane < k ? lane : 0;
+  const int pl = clampi(ws.pos[int64_t(t) * k + jl], 0, P - 1);
+  const int el = ws.idx[int64_t(t) * k + jl];
+  int ps[KMAX], es[KMAX];
 #pragma unroll
-    for (int jj = 0; jj < KMAX; ++jj) rank += __shfl(p, jj, kWave) < p ? 1 : 0;
-    // the slot ranked just above (same expert there: skip this one)
-    int e_next = -2;
-#pragma unroll
-    for (int jj = 0; jj < KMAX; ++jj) {
-      const int pj = __shfl(p, jj, kWave), ej = __shfl(e, jj, kWave);
-      int rj = 0;
-#pragma unroll
-      for (int q = 0; q < KMAX; ++q) rj += __shfl(p, q, kWave) < pj ? 1 : 0;
-      if (jj < k && rj == rank + 1) e_next = ej;
-    }
-    if (j < k) {
-      s_p[rank] = p;
-      s_use[rank] = e_next == e ? 0 : 1;
-    }
+  for (int j = 0; j < KMAX; ++j) {
+    ps[j] = j < k ? __builtin_amdgcn_readlane(pl, j) : 0x7FFFFFFF;
+    es[j] = j < k ? __builtin_amdgcn_readlane(el, j) : -1;
   }
-  __syncthreads();
+#pragma unroll
+  for (int a = 0; a < KMAX - 1; ++a)
+#pragma unroll
+    for (int i = 0; i + 1 < KMAX - a; ++i)
+      if (ps[i] > ps[i + 1]) {
+        const int tp = ps[i], te = es[i];
+        ps[i] = ps[i + 1];
+        es[i] = es[i + 1];
+        ps[i + 1] = tp;
+        es[i + 1] = te;
+      }
   if (c * 8 >= D) return;
   v4i v[KMAX];
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r) v[r] = load16(ws.out2 + int64_t(s_p[min(r, k - 1)]) * D + c * 8);
+  for (int r = 0; r < KMAX; ++r) v[r] = load16(ws.out2 + int64_t(r < k ? ps[r] : ps[0]) * D + c * 8);
   const v4i sv = load16(ws.sh_out + int64_t(t) * D + c * 8);
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
 #pragma unroll
   for (int r = 0; r < KMAX; ++r) {
-    if (r < k && s_use[r]) {
+    const bool use = r < k && !(r + 1 < k && es[r + 1] == es[r]);
+    if (use) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         acc[2 * i] += bf16lo(uint32_t(v[r][i]));
