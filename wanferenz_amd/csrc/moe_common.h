@@ -181,6 +181,25 @@ __device__ __forceinline__ uint32_t wave_max_all_u32(uint32_t v) {
 
 __device__ __forceinline__ uint32_t wave_min_all_u32(uint32_t v) { return ~wave_max_all_u32(~v); }
 
+// wave_argmax's winner in every lane with no LDS round trip, for a full wave
+// and non-negative indices.  With no NaN value in the wave, cand_better is a
+// total order (value, with -0 == +0, then the lower index), so the winner is
+// the lane with the largest order-preserving key of its value (zeros keyed
+// alike) and, among the lanes holding that key, the lowest index: two
+// all-lane DPP maxima, the second over the complemented indices.  The value
+// returned is the key's float (+0 for a zero winner).  A NaN anywhere in the
+// wave takes the shuffle butterfly, unchanged.
+__device__ __forceinline__ Cand wave_argmax_dpp(Cand c) {
+  if (__ballot(c.v != c.v) != 0ull) return wave_argmax(c);
+  const uint32_t key = c.v == 0.0f ? 0x80000000u : f32_key(c.v);
+  const uint32_t km = wave_max_all_u32(key);
+  const uint32_t im = wave_max_all_u32(key == km ? ~uint32_t(c.i) : 0u);
+  Cand r;
+  r.v = __uint_as_float((km & 0x80000000u) ? (km & 0x7FFFFFFFu) : ~km);
+  r.i = int(~im);
+  return r;
+}
+
 // Agent-scope arrival counter: returns true in the last of `n` arrivals and
 // resets the counter for the next launch.
 __device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t n) {

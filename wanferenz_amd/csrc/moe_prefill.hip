@@ -404,7 +404,7 @@ __global__ __launch_bounds__(kRefineWaves * 64, 2) void topk_refine_kernel(
         const int e = lane + 64 * i;
         if (e < E && !((taken >> i) & 1u)) best = cand_better(best, Cand{lo[i], e});
       }
-      best = wave_argmax(best);
+      best = wave_argmax_dpp(best);
       theta = best.v;
       if ((best.i & 63) == lane) taken |= 1u << (best.i >> 6);
     }
@@ -456,7 +456,7 @@ __global__ __launch_bounds__(kRefineWaves * 64, 2) void topk_refine_kernel(
         const int e = lane + 64 * i;
         if (e < E && !((taken >> i) & 1u) && kx[i] != -INFINITY) best = cand_better(best, Cand{kx[i], e});
       }
-      best = wave_argmax(best);
+      best = wave_argmax_dpp(best);
       const int bi = clampi(best.i, 0, E - 1);
       float sv = 0.0f;
 #pragma unroll
