@@ -203,7 +203,7 @@ def _fp8_param(N, K, gpu, seed):
 
 
 @pytest.mark.parametrize("name", list(V4_PROJECTIONS))
-@pytest.mark.parametrize("M", [1, 4, 40])
+@pytest.mark.parametrize("M", [1, 4, 17, 32, 40])
 def test_installed_linear_runs_the_packed_path(gpu, lin_mod, name, M):
     """linear(x, W) and act_quant + fp8_gemm through the installed bindings, on a
     weight Parameter: both run on the packed copy made at first use, agree bit
@@ -211,19 +211,26 @@ def test_installed_linear_runs_the_packed_path(gpu, lin_mod, name, M):
     blocks of the output."""
     N, K = V4_PROJECTIONS[name]
     w = _fp8_param(N, K, gpu, N + 3 * K)
+    nb = N // 128
+    blocks = sorted({0, nb // 2, nb - 1})
+    rows = np.concatenate([np.arange(b * 128, b * 128 + 128) for b in blocks])
+    # the row-major bytes, read before the first call packs the weight in place
+    wsub = w.detach().view(torch.uint8)[torch.from_numpy(rows).to(gpu)].cpu().numpy()
+    ssub = e8m0_decode(w.scale.detach().view(torch.uint8)[blocks].cpu().numpy())
     xb = synth.normal_bf16(synth.stream_key(M + N, synth.S_FP8_X), (M, K), 1.0)
     x = bf16_tensor(xb, gpu)
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(gpu)
     y = lin_mod.linear(x, w)
-    assert getattr(w, "_wz_packed", None) is not None
+    torch.cuda.synchronize()
+    # one copy of the projection: the tiles sit in the Parameter's own storage
+    assert kernels.is_packed(w) and tuple(w.shape) == (N, K) and w.dtype == torch.float8_e4m3fn
+    assert w.untyped_storage().nbytes() == N * K
+    assert torch.cuda.memory_allocated(gpu) - before < N * K // 2
     q, s = lin_mod.act_quant(x, 128, lin_mod.scale_fmt, lin_mod.scale_dtype)
     y2 = lin_mod.fp8_gemm(q, s, w, w.scale, lin_mod.scale_dtype)
     torch.cuda.synchronize()
     assert torch.equal(y, y2)
-    nb = N // 128
-    blocks = sorted({0, nb // 2, nb - 1})
-    rows = np.concatenate([np.arange(b * 128, b * 128 + 128) for b in blocks])
-    wsub = w.detach().view(torch.uint8)[torch.from_numpy(rows).to(gpu)].cpu().numpy()
-    ssub = e8m0_decode(w.scale.detach().view(torch.uint8)[blocks].cpu().numpy())
     rq, rs = om.act_quant(from_bf16_bits(xb), 128, True)
     ref = om.fp8_gemm(rq, rs, wsub, ssub)
     got = f32_of_bf16(y)[:, rows]
@@ -261,3 +268,95 @@ def test_packed_copy_follows_the_weight(gpu, lin_mod):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, y1)
+
+
+def test_packed_weight_unpacks_and_rejects_bad_operands(gpu, lin_mod):
+    """unpack_fp8_in_place restores the row-major bytes exactly; a packed weight
+    refuses the calls the replaced binding would have served on row-major bytes
+    (fp32 input); uninstall(mod, model) unpacks every packed weight."""
+    N, K = 1024, 4096
+    w = _fp8_param(N, K, gpu, 21)
+    orig = w.detach().view(torch.uint8).clone()
+    x = bf16_tensor(synth.normal_bf16(synth.stream_key(9, synth.S_FP8_X), (3, K), 1.0), gpu)
+    y = lin_mod.linear(x, w)
+    assert kernels.is_packed(w) and not torch.equal(w.detach().view(torch.uint8), orig)
+    with pytest.raises(TypeError):
+        lin_mod.linear(x.float(), w)
+    with pytest.raises(ValueError):
+        lin_mod.linear(x[:, :1024].contiguous(), w)
+    assert kernels.unpack_fp8_in_place(w) and not kernels.is_packed(w)
+    assert torch.equal(w.detach().view(torch.uint8), orig)
+    assert torch.equal(lin_mod.linear(x, w), y)
+    model = torch.nn.Module()
+    model.w = w
+    kernels.pack_fp8_weights(model)
+    assert kernels.is_packed(w)
+    kernels.uninstall(lin_mod, model)
+    kernels.install(lin_mod)
+    assert not kernels.is_packed(w) and torch.equal(w.detach().view(torch.uint8), orig)
+
+
+def test_pack_fp8_weights_leaves_moe_layers_to_the_moe_packer(gpu, mod):
+    """pack_fp8_weights skips the MoE's shared expert; and a shared expert packed in
+    place by the FP8 linear path before the MoE layer is built is turned back
+    before the bank packer reads it, so the layer still matches the golden vectors."""
+    case = CASES["toy_t4"]
+    inp = make_inputs(case)
+    moe = mm.moe_from_case(case, inp, gpu)
+    model = torch.nn.Module()
+    model.ffn = moe
+    assert kernels.pack_fp8_weights(model) == 0
+    assert not kernels.is_packed(moe.shared_experts.w1.weight)
+    # the shared expert's linears run through the installed FP8 path first
+    for lin in (moe.shared_experts.w1, moe.shared_experts.w3, moe.shared_experts.w2):
+        assert kernels._packed_of(lin.weight) is not None and kernels.is_packed(lin.weight)
+    wm.install(mod)
+    x = bf16_tensor(inp.x, gpu).view(1, case.T, case.dim)
+    ids = torch.from_numpy(inp.input_ids).to(gpu).view(1, case.T)
+    y = mod.MoE.forward(moe, x, ids)
+    torch.cuda.synchronize()
+    got = f32_of_bf16(y.view(case.T, case.dim))
+    gold = from_bf16_bits(np.load(f"tests/golden/{case.name}.npz")["y_bf16"])
+    rel, cos = om.max_rel_err(got, gold), om.cosine(got, gold)
+    assert rel <= 1e-2 and cos >= 0.9999, (rel, cos)
+    # released: no packed-tile record is left on the emptied parameters
+    assert not hasattr(moe.shared_experts.w1.weight, "_wz_packed")
+
+
+@pytest.mark.parametrize("name", ["toy_t4", "top6_t8", "toy_t1"])
+def test_drafter_moe_bound_per_instance(gpu, mod, name):
+    """install_drafter binds the HIP layer on each non-hash MTP block's MoE as an
+    instance attribute (expert_bank.install_drafter, expert_bank.py:167-191), so the
+    drafter's MoE never reaches the class-level forward or a grouped-GEMM kernel of
+    the reference; the output matches the reference's golden vectors.  A hash-routed
+    block is left alone, as the reference leaves it."""
+    case = CASES[name]
+    inp = make_inputs(case)
+    moe = mm.moe_from_case(case, inp, gpu)
+    hcase = CASES["hash_t3"]
+    hmoe = mm.moe_from_case(hcase, make_inputs(hcase), gpu)
+    hmoe.layer_id = 1
+    tail = types.SimpleNamespace(mtp=[types.SimpleNamespace(ffn=moe), types.SimpleNamespace(ffn=hmoe)])
+    assert wm.install_drafter(tail, mod) == 0  # V4_DSPARK_MOE is not set
+    assert wm.install_drafter(tail, mod, force=True) == 1
+    assert wm.install_drafter(tail, mod, force=True) == 0  # already bound
+    assert "forward" in moe.__dict__ and "forward" not in hmoe.__dict__
+    x = bf16_tensor(inp.x, gpu).view(1, case.T, case.dim)
+    ids = torch.from_numpy(inp.input_ids).to(gpu).view(1, case.T)
+    y = moe(x, ids)  # nn.Module.__call__ finds the instance binding, as the model's block does
+    torch.cuda.synchronize()
+    assert moe.ref_calls == 0 and getattr(moe, "_draft_steps", 0) == 1
+    got = f32_of_bf16(y.view(case.T, case.dim))
+    gold = from_bf16_bits(np.load(f"tests/golden/{name}.npz")["y_bf16"])
+    rel, cos = om.max_rel_err(got, gold), om.cosine(got, gold)
+    assert rel <= 1e-2 and cos >= 0.9999, (rel, cos)
+    assert wm.drafter_coverage(tail) == {0: (1, {}), 1: (0, {})}
+    # a layer the HIP path cannot serve declines to the class-level forward, tallied
+    mod.world_size = 2
+    try:
+        yd = moe(x, ids)
+    finally:
+        mod.world_size = 1
+    assert moe.ref_calls == 1 and float(yd.flatten()[0]) == mm.SENTINEL
+    assert moe._draft_declined == {"world_size>1": 1}
+    assert wm.uninstall_drafter(tail) == 1 and "forward" not in moe.__dict__

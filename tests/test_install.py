@@ -175,3 +175,75 @@ def test_kernels_refuse_cpu_tensors():
     s = torch.zeros(2, 1, dtype=torch.float32)
     with pytest.raises(RuntimeError, match="GPU only"):
         kernels.fp8_gemm(a, s, a, torch.ones(1, 1))
+
+
+def test_installed_linear_rejects_mismatched_fp8_operands_before_launch():
+    """An FP8 weight whose K or block-scale grid does not match x raises ValueError
+    in linear() before any packing or launch (the packed kernels read K and the
+    scale grid from these; a wider x would read past the weight)."""
+    m = types.ModuleType("model_linear_fp8")
+    m.block_size, m.scale_fmt, m.scale_dtype = 128, "ue8m0", torch.float8_e8m0fnu
+
+    def unused(*a, **k):
+        raise AssertionError("the replaced binding was called")
+
+    m.linear = unused
+    kernels.install(m)
+    try:
+        w = torch.nn.Parameter(torch.zeros(256, 512, dtype=torch.uint8).view(torch.float8_e4m3fn),
+                               requires_grad=False)
+        w.scale = torch.nn.Parameter(torch.zeros(2, 4, dtype=torch.uint8).view(torch.float8_e8m0fnu),
+                                     requires_grad=False)
+        for K in (640, 384):
+            with pytest.raises(ValueError, match="K="):
+                m.linear(torch.zeros(3, K, dtype=torch.bfloat16), w)
+        w.scale = torch.nn.Parameter(torch.zeros(2, 3, dtype=torch.uint8).view(torch.float8_e8m0fnu),
+                                     requires_grad=False)
+        with pytest.raises(ValueError, match="block scales"):
+            m.linear(torch.zeros(3, 512, dtype=torch.bfloat16), w)
+        assert not hasattr(w, "_wz_packed")
+    finally:
+        kernels.uninstall(m)
+
+
+def _pack_statement(w: torch.Tensor) -> torch.Tensor:
+    """The FP8 tile layout wz_fp8_pack writes (pack.hip, mode 3): [N/16][K/128][2 halves]
+    [64 lanes][16 B], lane l = 16 g + r of half h holding row r, K [64 h + 16 g, +16);
+    written out here element by element."""
+    N_, K = w.shape
+    out = torch.empty(N_ * K, dtype=torch.uint8)
+    u = w.view(torch.uint8)
+    i = 0
+    for nt in range(N_ // 16):
+        for kb in range(K // 128):
+            for h in range(2):
+                for ln in range(64):
+                    r, g = ln & 15, ln >> 4
+                    c = kb * 128 + 64 * h + 16 * g
+                    out[i:i + 16] = u[nt * 16 + r, c:c + 16]
+                    i += 16
+    return out
+
+
+def test_unpack_in_place_inverts_the_tile_layout():
+    """unpack_fp8_in_place restores the row-major bytes from the packed tiles (CPU
+    tensors: the permutation is torch's, no kernel)."""
+    g = torch.Generator().manual_seed(3)
+    rowmajor = torch.randint(0, 256, (32, 256), generator=g, dtype=torch.uint8)
+    p = torch.nn.Parameter(_pack_statement(rowmajor).view(32, 256).view(torch.float8_e4m3fn), requires_grad=False)
+    assert kernels.unpack_fp8_in_place(p) is False  # not marked packed: left alone
+    p._wz_packed = (p.data_ptr(), p._version)
+    assert kernels.is_packed(p)
+    assert kernels.unpack_fp8_in_place(p) is True
+    assert torch.equal(p.detach().view(torch.uint8), rowmajor) and not kernels.is_packed(p)
+
+
+def test_drafter_install_needs_the_flag_and_skips_hash_layers():
+    """install_drafter binds nothing unless V4_DSPARK_MOE is set (or forced), and never
+    a hash-routed block's MoE (expert_bank.py:167-191)."""
+    hmoe = mm.MoE(0, 256, 128, 8, 2, hash_layer=True)
+    tail = types.SimpleNamespace(mtp=[types.SimpleNamespace(ffn=hmoe), types.SimpleNamespace(ffn=None)])
+    assert wm.install_drafter(tail, types.ModuleType("m")) == 0
+    assert wm.install_drafter(tail, types.ModuleType("m"), force=True) == 0
+    assert "forward" not in hmoe.__dict__
+    assert wm.uninstall_drafter(tail) == 0

@@ -97,41 +97,85 @@ def act_quant(x, block_size=128, scale_fmt=None, scale_dtype=torch.float32, inpl
 
 
 # Pack FP8 weight Parameters into the GEMV tile format on their first use outside
-# graph capture (fp8_gemm / linear keep the packed copy on the Parameter).
+# graph capture, in their own storage (fp8_gemm / linear then read the tiles).
 PACK_FP8_WEIGHTS = True
 
 
-def _packed_of(b):
-    """The packed copy of FP8 weight ``b`` ([N, K] e4m3 Parameter), packing it once.
+def _tile_view(b) -> torch.Tensor:
+    return b.detach().view(torch.uint8).view(-1)
 
-    The copy is kept on the Parameter (``b._wz_packed``) with the storage
-    address and version it was made from, and remade when either changes.
-    Returns None where the tile format does not apply (N % 16, K % 128), for
-    tensors that are not Parameters (no place to keep a copy), or while a graph
-    is being captured and no current copy exists."""
+
+def is_packed(b) -> bool:
+    """True when FP8 weight ``b`` holds the packed tiles (wz_fp8_pack's format) in
+    its own storage: packed at this address and not written since."""
+    got = getattr(b, "_wz_packed", None)
+    return got is not None and got == (b.data_ptr(), b._version)
+
+
+def _packed_of(b):
+    """The packed tiles of FP8 weight ``b`` ([N, K] e4m3 Parameter), packing it once.
+
+    The tiles hold the same N*K bytes as the row-major weight, so they are
+    written over it: the Parameter keeps its shape, dtype and storage, and the
+    model holds one copy of each projection (the reference's decode retile reads
+    its weights in place as well, fp8_vector.py:316-351).  ``b._wz_packed``
+    records the storage address and version the tiles were written at; a later
+    write into the Parameter (a checkpoint load bumps its version) holds
+    row-major bytes again, and the next call repacks.  Returns None where the
+    tile format does not apply (N % 16, K % 128, a CPU or non-contiguous
+    tensor), for tensors that are not Parameters, or while a graph is being
+    captured and the weight is not packed yet; the caller then reads the
+    row-major bytes."""
     if not PACK_FP8_WEIGHTS or not isinstance(b, torch.nn.Parameter) or b.dim() != 2:
         return None
     Nn, K = b.shape
-    if Nn % 16 or K % 128 or b.dtype not in (_E4M3, torch.uint8):
+    if Nn % 16 or K % 128 or b.dtype not in (_E4M3, torch.uint8) or not b.is_cuda:
         return None
-    key = (b.data_ptr(), b._version)
-    got = getattr(b, "_wz_packed", None)
-    if got is not None and got[0] == key:
-        return got[1]
-    if torch.cuda.is_current_stream_capturing():
+    if is_packed(b):
+        return _tile_view(b)
+    if torch.cuda.is_current_stream_capturing() or not b.is_contiguous():
         return None
-    packed = torch.empty(Nn * K, dtype=torch.uint8, device=b.device)
-    N.call("wz_fp8_pack", N.ptr(b), Nn, K, N.ptr(packed), N.stream_handle(b.device))
-    b._wz_packed = (key, packed)
-    return packed
+    tmp = torch.empty(Nn * K, dtype=torch.uint8, device=b.device)
+    N.call("wz_fp8_pack", N.ptr(b), Nn, K, N.ptr(tmp), N.stream_handle(b.device))
+    # .data: the copy is not an autograd write, so the version stays the one recorded
+    b.data.view(torch.uint8).view(-1).copy_(tmp)
+    b._wz_packed = (b.data_ptr(), b._version)
+    return _tile_view(b)
+
+
+def unpack_fp8_in_place(b) -> bool:
+    """Turn a weight packed by :func:`_packed_of` back into row-major bytes (for a
+    consumer that reads the reference layout, e.g. the MoE bank packer).  The
+    tile of 16 rows x 128 K is two 1-KB halves; lane l = 16 g + r of half h holds
+    row r, K [64 h + 16 g, +16).  Returns whether anything was done."""
+    if not is_packed(b):
+        return False
+    Nn, K = b.shape
+    t = _tile_view(b).view(Nn // 16, K // 128, 2, 4, 16, 16)
+    rows = t.permute(0, 4, 1, 2, 3, 5).contiguous().view(-1)
+    b.data.view(torch.uint8).view(-1).copy_(rows)
+    del b._wz_packed
+    return True
+
+
+def _moe_param_ids(module) -> set:
+    """ids of the parameters inside MoE layers (modules with experts and a shared
+    expert): the MoE packer turns those into its own banks."""
+    out = set()
+    for m in module.modules():
+        if hasattr(m, "experts") and hasattr(m, "shared_experts"):
+            out.update(id(p) for p in m.parameters())
+    return out
 
 
 def pack_fp8_weights(module) -> int:
-    """Pack every FP8 weight Parameter of ``module`` now (before a graph capture,
-    so captured steps find the packed copies); returns how many were packed."""
+    """Pack every FP8 weight Parameter of ``module`` in place now (before a graph
+    capture, so captured steps find the packed tiles); returns how many are packed.
+    The MoE layers' weights are left to the MoE packer (moe.prepare)."""
+    skip = _moe_param_ids(module)
     n = 0
     for p in module.parameters():
-        if p.dtype == _E4M3 and p.is_cuda and _packed_of(p) is not None:
+        if p.dtype == _E4M3 and p.is_cuda and id(p) not in skip and _packed_of(p) is not None:
             n += 1
     return n
 
@@ -583,10 +627,13 @@ def linear(x, weight, bias=None):
     else F.linear, as in the reference."""
     assert bias is None
     mod = _LINEAR_MOD
+    if weight.dtype == _E4M3:
+        _check_fp8_operands(x, weight)
     if weight.dtype == _E4M3 and x.dtype == torch.bfloat16 and getattr(mod, "block_size", 128) == 128:
         packed = _packed_of(weight)
-        if packed is not None and x.is_contiguous():
+        if packed is not None:
             _require_cuda(x)
+            x = x.contiguous()
             scale_fmt = getattr(mod, "scale_fmt", None)
             K = x.size(-1)
             M = x.numel() // K
@@ -598,7 +645,27 @@ def linear(x, weight, bias=None):
             N.call("wz_fp8_linear_packed", N.ptr(x), N.ptr(packed), N.ptr(weight.scale), N.ptr(y), M, Nn, K,
                    akind, _wscale_kind_of(weight.scale), N.ptr(ws), need, N.stream_handle(x.device))
             return _finish(y)
+    if weight.dtype == _E4M3 and is_packed(weight):
+        # the replaced binding would read the tiles as row-major bytes
+        raise TypeError(f"linear: the FP8 weight is packed in place; its input must be bf16 (got {x.dtype}) "
+                        f"with 128-element quantisation blocks (got {getattr(mod, 'block_size', 128)})")
     return _REF["linear"](x, weight, bias)
+
+
+def _check_fp8_operands(x, weight):
+    """The shapes linear() on an FP8 weight needs (architecture.py:158-168): x
+    [..., K] against weight [N, K] and its block scales [ceil(N/128), ceil(K/128)].
+    The packed kernels read K and the scale grid from these, so a mismatch would
+    read past the weight; it raises here, before any launch, as the reference's
+    fp8_gemm rejects it."""
+    Nn, K = weight.shape
+    if x.size(-1) != K:
+        raise ValueError(f"linear: x has K={x.size(-1)}, the FP8 weight [{Nn}, {K}] needs K={K}")
+    s = getattr(weight, "scale", None)
+    want = ((Nn + 127) // 128, (K + 127) // 128)
+    if s is None or tuple(s.shape) != want:
+        raise ValueError(f"linear: the FP8 weight [{Nn}, {K}] needs block scales {list(want)}, "
+                         f"got {None if s is None else list(s.shape)}")
 
 
 fp8_gemm._v4_hip_fp8_gemm = True
@@ -621,8 +688,9 @@ def install(mod, model=None) -> bool:
 
     Idempotent via the marker attributes; the replaced functions are kept in
     ``_REF`` (the reference's _REF_FP8_GEMM pattern, fp8_vector.py:472-491).
-    With ``model`` given, its FP8 weights are packed now (pack_fp8_weights), so a
-    graph captured afterwards runs the packed GEMV from the first step.
+    With ``model`` given, its FP8 weights are packed in place now
+    (pack_fp8_weights), so a graph captured afterwards runs the packed GEMV from
+    the first step and the model holds one copy of each projection.
     """
     global _LINEAR_MOD
     took = False
@@ -642,8 +710,13 @@ def install(mod, model=None) -> bool:
     return took
 
 
-def uninstall(mod) -> bool:
-    """Restore the functions install() replaced on ``mod``."""
+def uninstall(mod, model=None) -> bool:
+    """Restore the functions install() replaced on ``mod``.  The restored bindings
+    read FP8 weights row-major, so with ``model`` given every weight packed in
+    place is turned back (unpack_fp8_in_place) first."""
+    if model is not None:
+        for p in model.parameters():
+            unpack_fp8_in_place(p)
     took = False
     for name, fn in _installed():
         if getattr(mod, name, None) is fn and name in _REF:

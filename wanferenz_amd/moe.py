@@ -23,12 +23,14 @@ Two ways in:
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass, field
 from typing import Optional
 
 import torch
 
 from . import _native as N
+from . import kernels
 
 SCORE_FUNCS = {"softmax": N.WZ_SCORE_SOFTMAX, "sigmoid": N.WZ_SCORE_SIGMOID,
                "sqrtsoftplus": N.WZ_SCORE_SQRTSOFTPLUS}
@@ -417,6 +419,9 @@ def _release(params):
         if key not in empty:
             empty[key] = torch.empty(0, dtype=p.dtype, device=p.device)
         p.data = empty[key]
+        # a packed-tile record of the FP8 linear path (kernels._packed_of) names
+        # storage that is gone
+        p.__dict__.pop("_wz_packed", None)
 
 
 def hip_moe_of(moe, mod=None, release: Optional[bool] = None) -> Optional[HipMoE]:
@@ -458,13 +463,21 @@ def hip_moe_of(moe, mod=None, release: Optional[bool] = None) -> Optional[HipMoE
     def scale(lin):
         return lin.scale.detach() if lin.scale.dtype == torch.float32 else _bytes(lin.scale)
 
-    shared = (_bytes(sh.w1.weight), scale(sh.w1), _bytes(sh.w3.weight), scale(sh.w3), _bytes(sh.w2.weight),
-              scale(sh.w2))
     with torch.no_grad():
+        # the shared expert's linears may have run through the installed FP8 path,
+        # which packs weights in their own storage; the bank packer reads row-major
+        for lin in (sh.w1, sh.w3, sh.w2):
+            kernels.unpack_fp8_in_place(lin.weight)
+        shared = (_bytes(sh.w1.weight), scale(sh.w1), _bytes(sh.w3.weight), scale(sh.w3), _bytes(sh.w2.weight),
+                  scale(sh.w2))
         h = HipMoE.from_experts(
             cfg, gate.weight.detach(), None if gate.bias is None else gate.bias.detach(), expert, shared,
             tid2eid=gate.tid2eid.detach() if getattr(gate, "hash", False) else None)
         if release:
+            # the pack kernels read the module's storage on the current stream; the
+            # caching allocator may hand freed blocks to another stream (the
+            # reference warms its graphs up on a side stream), so they finish first
+            torch.cuda.current_stream(gate.weight.device).synchronize()
             # the reference's relayout may have left a bank the experts' views point into
             moe._grouped_bank = None
             _release([getattr(getattr(moe.experts[e], kind), "weight") for e in range(lo, hi)
@@ -543,6 +556,101 @@ def uninstall(mod) -> bool:
     mod.MoE.forward = _REF_FORWARD
     _REF_FORWARD = None
     return True
+
+
+# ------------------------------------------------------------- the drafter ----
+#
+# The DSpark drafter's MTP blocks get their MoE forward bound per instance
+# (decoding/expert_bank.py:167-191, called from decoding/dspark.py:450-452 when
+# V4_DSPARK_MOE is set): an instance attribute, which a class-level
+# MoE.forward replacement never reaches.  install_drafter binds the HIP layer
+# the same way, so the drafter's MoE runs here instead of the reference's
+# TileLang grouped kernel (expert_bank.py:38-60).
+
+V4_DSPARK_MOE = os.environ.get("V4_DSPARK_MOE", "0") not in ("", "0")
+
+
+def _draft_decline(self, why, x, input_ids):
+    """The reference drafter's decline (expert_bank.py:99-105): tally the reason,
+    run the class-level forward."""
+    tally = getattr(self, "_draft_declined", None)
+    if tally is None:
+        tally = self._draft_declined = {}
+    tally[why] = tally.get(why, 0) + 1
+    return type(self).forward(self, x, input_ids)
+
+
+def hip_draft_forward(self, x, input_ids):
+    """Per-instance MoE forward of a drafter MTP block (expert_bank.draft_forward,
+    expert_bank.py:108-164): the same routing, experts, shared expert and combine
+    as MoE.forward, on the HIP layer.  The HIP layer serves every token count,
+    so the reference's width limits (T > 1, T * k <= its 32-row tile) do not
+    apply; what it cannot serve declines as the reference's does."""
+    if int(getattr(_DRAFT_MOD, "world_size", 1) or 1) > 1:
+        return _draft_decline(self, "world_size>1", x, input_ids)
+    if self.gate.hash:
+        return _draft_decline(self, "hash-routed", x, input_ids)
+    if self.experts_start_idx != 0 or self.experts_end_idx != self.n_routed_experts:
+        return _draft_decline(self, "partial-experts", x, input_ids)
+    h = hip_moe_of(self, _DRAFT_MOD)
+    if h is None:
+        return _draft_decline(self, "not-mxfp4-bank", x, input_ids)
+    y = h.forward(x, input_ids)
+    self._draft_steps = getattr(self, "_draft_steps", 0) + 1
+    return y
+
+
+hip_draft_forward._v4_hip_draft = True
+_DRAFT_MOD = None
+
+
+def install_drafter(dstail, mod=None, force: bool = False) -> int:
+    """Bind :func:`hip_draft_forward` on each non-hash MoE of ``dstail.mtp`` (the
+    reference's install_drafter, expert_bank.py:167-191): only when V4_DSPARK_MOE
+    is set, as there, unless ``force``.  ``mod`` is the model module (its
+    scale_fmt / scale_dtype / world_size; the reference takes partition.ref()).
+    Each bound layer is packed now (its expert weights released, as the
+    reference's relayout with preserve=False does).  Returns the number bound."""
+    global _DRAFT_MOD
+    if not (V4_DSPARK_MOE or force):
+        return 0
+    _DRAFT_MOD = mod or _MOD
+    took = 0
+    for blk in dstail.mtp:
+        moe = getattr(blk, "ffn", None)
+        if moe is None or moe.gate.hash:
+            continue
+        e0 = moe.experts[moe.experts_start_idx]
+        if e0.w1.weight.dtype != torch.float4_e2m1fn_x2 and getattr(moe, "_hip_moe", None) is None:
+            continue
+        if getattr(moe.forward, "_v4_hip_draft", False):
+            continue
+        if hip_moe_of(moe, _DRAFT_MOD) is None:
+            continue
+        moe.forward = hip_draft_forward.__get__(moe, type(moe))
+        took += 1
+    return took
+
+
+def uninstall_drafter(dstail) -> int:
+    """Remove the per-instance binding (the class-level forward is used again)."""
+    n = 0
+    for blk in dstail.mtp:
+        moe = getattr(blk, "ffn", None)
+        if moe is not None and getattr(moe.__dict__.get("forward"), "_v4_hip_draft", False):
+            del moe.forward
+            n += 1
+    return n
+
+
+def drafter_coverage(dstail) -> dict:
+    """Per-layer (steps served, declines by reason) of the drafter's MoEs
+    (expert_bank.coverage, expert_bank.py:194-203)."""
+    out = {}
+    for blk in dstail.mtp:
+        moe = blk.ffn
+        out[moe.layer_id] = (getattr(moe, "_draft_steps", 0), dict(getattr(moe, "_draft_declined", {})))
+    return out
 
 
 def coverage(module) -> dict:
