@@ -320,7 +320,7 @@ PROJ_SHAPES = [(4096, 1024), (1024, 4096), (4096, 4096), (16384, 4096),
 
 @pytest.mark.parametrize("w_fp32", [True, False])
 @pytest.mark.parametrize("N,K", PROJ_SHAPES)
-@pytest.mark.parametrize("M", [1, 8, 128])
+@pytest.mark.parametrize("M", [1, 4, 8, 17, 32, 128])
 def test_fp8_linear_projection_shapes(gpu, w_fp32, N, K, M):
     """fp8_linear (act_quant fused) at the dense projection shapes, weights generated on
     the device by the same hash stream as the host generator; the oracle checks three

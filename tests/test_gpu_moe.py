@@ -301,6 +301,45 @@ def _torch_oracle_rows(cfg, w, xb, g, dev):
     return f32_of_bf16(y.to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("T", [12, 16, 17, 24, 32])
+def test_v4_multi_token_parity(v4_layer, T):
+    """The multi-token widths of the reference's decode paths (expert_batch.py:14-53
+    serves T in [2, 32], the drafter T * k <= 32, expert_bank.py:108-164) at the
+    V4 shape, each against the oracle directly: routing of every token bit-exact
+    (the exported tables too), every output row against the torch float32
+    restatement of the reference's CPU path over the oracle's routing, and four
+    rows (the first, the last and two of the most loaded expert's) against the
+    numpy oracle."""
+    cfg, w, host, moe = v4_layer
+    xb = synth.normal_bf16(synth.stream_key(300 + T, synth.S_X), (T, cfg.dim), 1.0)
+    x = bf16_tensor(xb, "cuda")
+    b = host["gate_bias"]
+    g = om.gate(from_bf16_bits(xb), from_bf16_bits(host["gate_w"]), b, cfg.topk, cfg.score_func, cfg.route_scale)
+    near = check_routing(moe, x, None, g, cfg.n_experts)
+    rw = torch.empty(T, cfg.topk, dtype=torch.float32, device="cuda")
+    ri = torch.empty(T, cfg.topk, dtype=torch.int64, device="cuda")
+    y = moe.forward(x, routing_out=(rw, ri))
+    if not near:
+        assert np.array_equal(ri.cpu().numpy(), g.indices)
+        wd = np.abs(rw.cpu().numpy() - g.weights)
+        assert (wd <= 4 * np.spacing(np.abs(g.weights).astype(np.float32))).all(), wd.max()
+    got = f32_of_bf16(y)
+    full = _torch_oracle_rows(cfg, w, xb, g, x.device)
+    rel_t, cos_t = om.max_rel_err(got, full), om.cosine(got, full)
+    assert rel_t <= TOL_REL and cos_t >= TOL_COS, (rel_t, cos_t)
+    counts = np.bincount(g.indices.ravel(), minlength=cfg.n_experts)
+    hot_rows = np.nonzero((g.indices == int(counts.argmax())).any(1))[0]
+    rows = sorted({0, T - 1} | set(hot_rows[:2].tolist()))
+    gs = om.gate(from_bf16_bits(xb[rows]), from_bf16_bits(host["gate_w"]), b, cfg.topk, cfg.score_func,
+                 cfg.route_scale)
+    p = _oracle_params_from_device(cfg, w, host, sorted(set(gs.indices.ravel().tolist())))
+    ref = om.moe_forward(p, from_bf16_bits(xb[rows]))
+    rel, cos = om.max_rel_err(got[rows], ref.y), om.cosine(got[rows], ref.y)
+    assert rel <= TOL_REL and cos >= TOL_COS, (rel, cos)
+    print(f"V4 T={T}: all rows vs torch oracle rel {rel_t:.2e} cos {cos_t:.8f} bit-equal {np.mean(got == full):.4f};"
+          f" rows {rows} vs oracle rel {rel:.2e} cos {cos:.8f}; near-ties {near}")
+
+
 def _decode_chunks(moe, x, chunk=16):
     return torch.cat([moe.forward(x[i:i + chunk]) for i in range(0, x.size(0), chunk)])
 

@@ -30,26 +30,55 @@ def _close(got, ref):
     return om.max_rel_err(got, ref), om.cosine(got, ref)
 
 
-def _oracle_linear_q(q, qs, n, k, seed):
-    """The oracle's fp8_gemm of pre-quantised activations (the stage's own codes)."""
+def _oracle_linear_q(q, qs, n, k, seed, blocks=None):
+    """The oracle's fp8_gemm of pre-quantised activations (the stage's own codes);
+    with ``blocks``, only those 128-row blocks of the weight (their output columns)."""
     w, s = stage.synthetic_linear(n, k, seed, "cuda", fp32_scales=False)
-    return om.fp8_gemm(q, qs, bytes8(w), e8m0_decode(bytes8(s).reshape(s.shape)))
+    if blocks is None:
+        return om.fp8_gemm(q, qs, bytes8(w), e8m0_decode(bytes8(s).reshape(s.shape)))
+    rows = torch.from_numpy(np.concatenate([np.arange(b * 128, b * 128 + 128) for b in blocks])).to(w.device)
+    return om.fp8_gemm(q, qs, bytes8(w.view(torch.uint8)[rows]), e8m0_decode(bytes8(s).reshape(s.shape)[blocks]))
 
 
-def test_stage_ops_match_oracle(gpu):
-    """Two toy blocks (D 1024, 16 experts top-2; q_lora 256, head_dim 128, q width 2048,
-    indexer width 1024): wq_a, wkv and wo_b (K = 1024) run the GEMV, wq_b and the
-    indexer (K = 256) the tile GEMM; wo_b carries the residual in its epilogue and the
-    second block's norm carries the first block's MoE residual.  Every op of every
-    block is checked against the oracle fed the stage's own input to that op, since
-    each FP8 re-quantisation turns a one-ulp bf16 difference upstream into an e4m3
-    rounding flip downstream: residual adds bit-exact, the fused norm + act_quant
-    equal to the oracle's act_quant of the oracle's norm except where a one-ulp norm
-    difference moves a code, projections and the MoE to the bf16 tolerance, the
-    routing of each MoE the oracle's on the stage's input."""
-    cfg = MoEConfig(1024, 512, 16, 2, "sqrtsoftplus", 1.5, 10.0, N.WZ_SCALE_UE8M0, N.WZ_WSCALE_E8M0)
-    T, D = 4, 1024
-    dims = dict(q_lora=256, head_dim=128, q_width=2048, idx_width=1024)
+def _cols(blocks):
+    return slice(None) if blocks is None else np.concatenate([np.arange(b * 128, b * 128 + 128) for b in blocks])
+
+
+def _some_blocks(n, sample):
+    nb = n // 128
+    return sorted({0, nb // 2, nb - 1}) if sample else None
+
+
+STAGE_SHAPES = {
+    # D, MoE (E, top-k, I), attention widths; "sample": projections checked on three
+    # 128-column blocks of the output (first, middle, last)
+    "toy": dict(cfg=(1024, 512, 16, 2), dims=dict(q_lora=256, head_dim=128, q_width=2048, idx_width=1024),
+                sample=False),
+    "v4": dict(cfg=(4096, 2048, 256, 6), dims=dict(q_lora=1024, head_dim=512, q_width=32768, idx_width=8192),
+               sample=True),
+}
+
+
+@pytest.mark.parametrize("shape", list(STAGE_SHAPES))
+def test_stage_ops_match_oracle(gpu, shape):
+    """Two blocks of the stage, every op checked against the oracle fed the stage's
+    own input to that op, since each FP8 re-quantisation turns a one-ulp bf16
+    difference upstream into an e4m3 rounding flip downstream.  "toy": D 1024, 16
+    experts top-2; q_lora 256, head_dim 128, q width 2048, indexer width 1024 (wq_a,
+    wkv and wo_b at K = 1024 run the GEMV, wq_b and the indexer at K = 256 the tile
+    GEMM).  "v4": the V4-Flash shapes (D 4096, 256 MXFP4 experts top-6, wq_a 1024 x
+    4096, wkv 512 x 4096, wq_b 32768 x 1024, indexer wq_b 8192 x 1024, wo_b 4096 x
+    8192).  wo_b carries the residual in its epilogue and the second block's norm
+    carries the first block's MoE residual.  Residual adds bit-exact, the fused norm
+    + act_quant equal to rms_norm then act_quant on the device and to the oracle's
+    act_quant of that row, the norms within one bf16 ulp of the oracle's,
+    projections and the MoE to the bf16 tolerance, the routing of each MoE the
+    oracle's on the stage's input."""
+    spec = STAGE_SHAPES[shape]
+    D, I_, E_, k_ = spec["cfg"]
+    dims, sample = spec["dims"], spec["sample"]
+    cfg = MoEConfig(D, I_, E_, k_, "sqrtsoftplus", 1.5, 10.0, N.WZ_SCALE_UE8M0, N.WZ_WSCALE_E8M0)
+    T = 4
     layers = [synth.synthetic_moe(cfg, seed=0, layer=l, device=gpu) for l in range(2)]
     blocks = [stage.synthetic_block(HipMoE(cfg, w, max_tokens=T), D, seed=l, device=gpu, **dims)
               for l, (w, _) in enumerate(layers)]
@@ -94,15 +123,21 @@ def test_stage_ops_match_oracle(gpu):
             assert np.array_equal(g["h"], bf16_round((g["h_in"] + g["e_in"]).astype(np.float32)))
         hq, hs = dq(tr["hq"]), e8m0_decode(dq(tr["hs"]))
         norm_quant("attn_norm", tr["hq"], tr["hs"], tr["h"], b.attn_norm)
-        close("wq_a", g["qa"], _oracle_linear_q(hq, hs, ql, D, l * 16 + 0))
-        close("wkv", g["kv"], _oracle_linear_q(hq, hs, dims["head_dim"], D, l * 16 + 1))
+        bl = _some_blocks(ql, sample)
+        close("wq_a", g["qa"][:, _cols(bl)], _oracle_linear_q(hq, hs, ql, D, l * 16 + 0, bl))
+        bl = _some_blocks(dims["head_dim"], sample)
+        close("wkv", g["kv"][:, _cols(bl)], _oracle_linear_q(hq, hs, dims["head_dim"], D, l * 16 + 1, bl))
         qq, qs = dq(tr["qq"]), e8m0_decode(dq(tr["qs"]))
         norm_quant("q_norm", tr["qq"], tr["qs"], tr["qa"], b.q_norm)
-        close("wq_b", g["q"], _oracle_linear_q(qq, qs, qw, ql, l * 16 + 2))
-        close("idx_wq_b", g["iq"], _oracle_linear_q(qq, qs, idw, ql, l * 16 + 3))
+        bl = _some_blocks(qw, sample)
+        close("wq_b", g["q"][:, _cols(bl)], _oracle_linear_q(qq, qs, qw, ql, l * 16 + 2, bl))
+        bl = _some_blocks(idw, sample)
+        close("idx_wq_b", g["iq"][:, _cols(bl)], _oracle_linear_q(qq, qs, idw, ql, l * 16 + 3, bl))
         rq, rs = om.act_quant(g["iq"], 128, True)
-        wo = _oracle_linear_q(rq, rs, D, idw, l * 16 + 4)
-        close("wo_b + residual", g["h1"], bf16_round((g["h"] + wo).astype(np.float32)))
+        bl = _some_blocks(D, sample)
+        wo = _oracle_linear_q(rq, rs, D, idw, l * 16 + 4, bl)
+        c = _cols(bl)
+        close("wo_b + residual", g["h1"][:, c], bf16_round((g["h"][:, c] + wo).astype(np.float32)))
         one_ulp("ffn_norm", g["m"], om.rmsnorm(g["h1"], b.ffn_norm.cpu().numpy()))
         gate = om.gate(g["m"], from_bf16_bits(host["gate_w"]), host["gate_bias"], cfg.topk, cfg.score_func,
                        cfg.route_scale)

@@ -50,3 +50,46 @@ def test_missing_and_malformed_tensors(tmp_path):
     save_file(st, f)
     with pytest.raises(loader.CheckpointError, match="MXFP4"):
         loader.load_moe_layer(path, 0, device="cpu")
+
+
+def _pattern(name: str, layer: int) -> str:
+    import re
+
+    return re.sub(r"experts\.\d+\.", "experts.<e>.", name.replace(f"layers.{layer}.", "layers.<L>."))
+
+
+@pytest.mark.parametrize("label,name", [("routed", "toy_t4"), ("hash", "hash_t3")])
+def test_names_are_the_reference_converters(tmp_path, monkeypatch, label, name):
+    """The tensor names the loader reads for one block are the reference's: the names
+    of its own MoE module's state_dict under layers.<L>.ffn., which its converter's
+    _rename produces from the Hugging Face names (tests/golden/ckpt_names.json,
+    written by tests/golden/make_names.py from the reference).  Checked as patterns
+    (expert index and layer abstracted): the names read == the fixture's, and the
+    fixture's HF names carry the renames conversion.py:15-29 undoes."""
+    import json
+    import os
+
+    fx = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "ckpt_names.json")))["layers"][label]
+    want = {_pattern(n, fx["layer"]) for n in fx["names"]}
+    for conv, hf in fx["names"].items():
+        assert hf.startswith("model.") and ".mlp." in hf and ".ffn." in conv
+        assert conv.endswith(".scale") == hf.endswith(".weight_scale_inv")
+        assert conv.endswith("gate.bias") == hf.endswith("gate.e_score_correction_bias")
+    case = CASES[name]
+    inp = make_inputs(case)
+    layer = 3
+    path = write_case_checkpoint(case, inp, str(tmp_path / name), layer=layer)
+    read = set()
+    orig = loader.Checkpoint.get
+
+    def get(self, n):
+        read.add(n)
+        return orig(self, n)
+
+    monkeypatch.setattr(loader.Checkpoint, "get", get)
+    loader.load_moe_layer(path, layer, device="cpu")
+    got = {_pattern(n, layer) for n in read}
+    assert got == want, (sorted(got ^ want))
+    # every expert's names are read, and nothing outside this block's ffn
+    assert all(n.startswith(f"layers.{layer}.ffn.") for n in read)
+    assert len(read) == len(want) - 6 + 6 * case.n_experts
