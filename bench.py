@@ -21,20 +21,6 @@ Printed JSON line (one):
               live: the stage replayed alone for all layers from a captured
               graph, HIP events on the replay stream (stage_times)
   stage_us    the same per-launch measurement for every stage of the layer
-  cpu_baseline the torch float32 restatement of the reference CPU path
-              (oracle/torch_ref.py) on layer 0: all cores (<= 16) at T tokens and
-              one core at T = 1, median of 10 after 3 warm-ups, CPU model, the HIP
-              layer's agreement on the same tokens and the near-tie tokens
-  per_T       the same layer measured at T = 1, 2, 4, 8
-  prefill     the same layer at T = 128, 512, 2048 with the calibrated Zipf(1.1)
-              gate bias (beta in wanferenz_amd/zipf_v4.json; the fitted exponent
-              of each batch's routing is reported): µs/layer, tokens/s,
-              algorithmic HBM GB/s, and MFMA utilisation = 6*D*I*(T*k + T) flops /
-              time against the dense FP8 (5.0 PFLOP/s, the rate of an e4m3 x e2m1
-              scaled MFMA) and FP4 (10.1 PFLOP/s) peaks
-  prefill_hot_experts  T = 2048 with every token on experts 0..5 (2048 rows
-              each): the w13 / w2 launches' MFMA rate on full tiles
-  fp4_gemm_m2048  one expert's w1|w3 and w2 GEMMs alone at M = 2048 (wz_fp4_gemm)
   fp8_gemv    the FP8 linear at the dense projection shapes (packed and row-major)
   grouped_fp4 the grouped MXFP4 GEMM of the banked decode path (6 experts' w1|w3, w2)
   sparse_attn sparse attention at 64 heads of 512, topk 640: decode B = 1, 4, 8
@@ -42,6 +28,25 @@ Printed JSON line (one):
               utilisation)
   decode_stage 12 V4 blocks (fused norms, the five FP8 attention-side projections,
               residuals, MoE) in one graph per step
+  prefill_detail  the layer at T = 128, 512, 2048 with the calibrated Zipf(1.1)
+              gate bias (beta in wanferenz_amd/zipf_v4.json; the fitted exponent
+              of each batch's routing is reported): µs/layer, tokens/s,
+              algorithmic HBM GB/s, and MFMA utilisation = 6*D*I*(T*k + T) flops /
+              time against the dense FP8 (5.0 PFLOP/s, the rate of an e4m3 x e2m1
+              scaled MFMA) and FP4 (10.1 PFLOP/s) peaks
+  prefill_hot_experts  T = 2048 with every token on experts 0..5 (2048 rows
+              each): the w13 / w2 launches' MFMA rate on full tiles
+  fp4_gemm_m2048  one expert's w1|w3 and w2 GEMMs alone at M = 2048
+  per_T_stage_us  the per-launch stage times of the decode sweep
+The last three keys hold the whole metric in scalars:
+  cpu_baseline the torch float32 restatement of the reference CPU path
+              (oracle/torch_ref.py) on layer 0 at T tokens, all cores (<= 16) and
+              one core on the same tokens, median of 6 after 2 warm-ups, CPU
+              model, the HIP layer's agreement on the same tokens, near-tie tokens
+  prefill     the prefill half flat: T = 2048 µs/layer, HBM fraction and MFMA
+              rate, T = 128 / 512, the hot-expert tiles, the M = 2048 GEMMs and the
+              committed MFMA-busy counters
+  per_T       the decode layer at T = 1, 2, 4, 8 (µs/layer, HBM fraction)
 """
 
 from __future__ import annotations
@@ -690,12 +695,13 @@ def _torch_layer(moe, used):
 
 def cpu_baseline(layers, cfg, T, dev):
     """The torch float32 restatement of the reference CPU path (oracle/torch_ref.py,
-    op for op after torch_ops.py and architecture.py) on layer 0 of the benchmark:
-    all cores (at most 16, the box's CPU share) on the T-token step, and one core
-    (the reference's OMP_NUM_THREADS=1) on a 1-token step; 3 warm-up runs, then the
-    median of 10.  Each run dequantises the weights it multiplies, as the reference
-    CPU path does.  The same inputs go through the HIP layer: expert indices must
-    match, outputs within 1e-2 relative / 0.9999 cosine; near-tie tokens are listed."""
+    op for op after torch_ops.py and architecture.py) on layer 0 of the benchmark,
+    on the T-token step: all cores (at most 16, the box's CPU share) and one core
+    (the reference's OMP_NUM_THREADS=1) on the same tokens; 2 warm-up runs, then
+    the median of 6.  Each run dequantises the weights it multiplies, as the
+    reference CPU path does.  The same inputs go through the HIP layer: expert
+    indices must match, outputs within 1e-2 relative / 0.9999 cosine; near-tie
+    tokens are listed.  The result is flat (scalars) first, the two legs after."""
     import torch
 
     from oracle import torch_ref as tr
@@ -703,48 +709,100 @@ def cpu_baseline(layers, cfg, T, dev):
 
     moe, _ = layers[0]
     n_all = max(1, min(16, len(os.sched_getaffinity(0))))
-    res = {"cpu_model": _cpu_model()}
+    legs = {}
     prev_threads, prev_dtype = torch.get_num_threads(), torch.get_default_dtype()
     torch.set_default_dtype(torch.bfloat16)
     try:
-        for leg, Tl, nt in (("all_cores", T, n_all), ("one_core", 1, 1)):
-            bits = synth.normal_bf16(synth.stream_key(1000, synth.layer_stream(0, synth.S_X)), (Tl, D), 1.0)
-            xc = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
-            _, idx_c, scores = tr.gate_forward(xc, moe.weights.gate_w.cpu(), moe.weights.gate_bias.cpu(), K_TOP,
-                                               "sqrtsoftplus", 1.5)
-            used = sorted(set(idx_c.flatten().tolist()))
-            p = _torch_layer(moe, used)
+        bits = synth.normal_bf16(synth.stream_key(1000, synth.layer_stream(0, synth.S_X)), (T, D), 1.0)
+        xc = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+        _, idx_c, scores = tr.gate_forward(xc, moe.weights.gate_w.cpu(), moe.weights.gate_bias.cpu(), K_TOP,
+                                           "sqrtsoftplus", 1.5)
+        used = sorted(set(idx_c.flatten().tolist()))
+        p = _torch_layer(moe, used)
+        # the HIP layer on the same tokens
+        out = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
+        moe.forward(xc.to(dev), out=out)
+        _, idx_g, _, _, _ = moe.route(xc.to(dev))
+        torch.cuda.synchronize()
+        nbytes = layer_bytes(len(used), T)
+        for leg, nt in (("all_cores", n_all), ("one_core", 1)):
             torch.set_num_threads(nt)
             times = []
-            for i in range(13):
+            for i in range(8):
                 t0 = time.perf_counter()
                 y_c, _, idx_c = tr.moe_forward(p, xc)
                 times.append(time.perf_counter() - t0)
-            med = float(np.median(times[3:]))
-            # the HIP layer on the same tokens
-            out = torch.empty(Tl, D, dtype=torch.bfloat16, device=dev)
-            moe.forward(xc.to(dev), out=out)
-            _, idx_g, _, _, _ = moe.route(xc.to(dev))
-            torch.cuda.synchronize()
+            med = float(np.median(times[2:]))
             yg, yc = out.float().cpu().numpy(), y_c.float().numpy()
-            rel = float(np.abs(yg - yc).max() / max(np.abs(yc).max(), 1e-30))
-            cos = float((yg * yc).sum() / max(np.linalg.norm(yg) * np.linalg.norm(yc), 1e-30))
-            nbytes = layer_bytes(len(used), Tl)
-            res[leg] = {"T": Tl, "threads": nt, "us_per_layer": round(med * 1e6, 1),
-                        "tokens_per_s": round(Tl / med, 2), "GB_s": round(nbytes / med / 1e9, 4),
-                        "runs": len(times) - 3, "warmup": 3, "distinct_experts": len(used),
-                        "indices_match": bool(torch.equal(idx_g.cpu().long(), idx_c.long())),
-                        "max_rel_err": round(rel, 6), "cosine": round(cos, 7),
-                        "near_tie_tokens": tr.near_ties(scores, K_TOP)}
+            legs[leg] = {"threads": nt, "us_per_layer": round(med * 1e6, 1), "tokens_per_s": round(T / med, 2),
+                         "GB_s": round(nbytes / med / 1e9, 4), "runs": len(times) - 2, "warmup": 2,
+                         "max_rel_err": round(float(np.abs(yg - yc).max() / max(np.abs(yc).max(), 1e-30)), 6),
+                         "cosine": round(float((yg * yc).sum() / max(np.linalg.norm(yg) * np.linalg.norm(yc),
+                                                                    1e-30)), 7),
+                         "indices_match": bool(torch.equal(idx_g.cpu().long(), idx_c.long()))}
     finally:
         torch.set_num_threads(prev_threads)
         torch.set_default_dtype(prev_dtype)
-    a = res["all_cores"]
-    res.update({"value": a["GB_s"], "unit": "GB/s", "cores": a["threads"], "kind": "port",
-                "sample": f"one V4 MoE layer (layer 0 of the benchmark, T={a['T']}, U={a['distinct_experts']}) "
-                          f"through the torch float32 restatement of the reference CPU path on "
-                          f"{a['threads']} threads: median of 10 after 3 warm-ups; one_core: T=1, 1 thread"})
-    return res
+    a, o = legs["all_cores"], legs["one_core"]
+    return {"value": a["GB_s"], "unit": "GB/s", "cores": a["threads"], "kind": "port",
+            "sample": f"one V4 MoE layer (layer 0 of the benchmark, T={T}, U={len(used)}) through the torch "
+                      f"float32 restatement of the reference CPU path, {a['threads']} threads and 1 thread on "
+                      f"the same tokens: median of 6 after 2 warm-ups each",
+            "cpu_model": _cpu_model(), "T": T, "distinct_experts": len(used),
+            "us_per_layer": a["us_per_layer"], "tokens_per_s": a["tokens_per_s"],
+            "one_core_us_per_layer": o["us_per_layer"], "one_core_GB_s": o["GB_s"],
+            "one_core_tokens_per_s": o["tokens_per_s"],
+            "indices_match": a["indices_match"] and o["indices_match"],
+            "max_rel_err": max(a["max_rel_err"], o["max_rel_err"]), "cosine": min(a["cosine"], o["cosine"]),
+            "near_tie_tokens": len(tr.near_ties(scores, K_TOP)),
+            "legs": legs}
+
+
+def committed_mfma_busy():
+    """MFMA busy (%) of the prefill w1/w3 and w2 launches at T = 2048 from the committed
+    rocprofv3 counter summary: the calibrated Zipf batch, then the hot-expert batch."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", "moe_prefill_T2048_mfma_pmc.md")
+    if not os.path.exists(path):
+        return {}
+    rows = re.findall(r"^\| `(\w+)<([^>]*)>` \|(?:[^|]*\|){4} ([\d.]+) % \|", open(path).read(), re.M)
+    if len(rows) < 4:
+        return {}
+    return {"counter_mfma_busy_w13_zipf": float(rows[0][2]), "counter_mfma_busy_w2_zipf": float(rows[1][2]),
+            "counter_mfma_busy_w13_hot": float(rows[2][2]), "counter_mfma_busy_w2_hot": float(rows[3][2]),
+            "counter_source": "profiles/moe_prefill_T2048_mfma_pmc.md (SQ_VALU_MFMA_BUSY_CYCLES)"}
+
+
+def flat_prefill(detail, hot, gemm):
+    """The prefill half of the metric as one flat block of scalars: T = 2048 with the
+    calibrated skew (µs per layer, HBM fraction, MFMA rate), the other T, the hot-expert
+    tiles, one expert's GEMMs at M = 2048, and the committed counter figures."""
+    out = {}
+    if "2048" in detail:
+        d = detail["2048"]
+        out.update({"T": 2048, "us_per_layer": d["us_per_layer"], "tokens_per_s": d["tokens_per_s"],
+                    "GB_s": d["GB_s"], "hbm_frac": d["hbm_frac"], "TFLOP_s": d["TFLOP_s"],
+                    "mfma_frac_fp4_peak": d["mfma_frac_fp4"], "mfma_frac_fp8_rate": d["mfma_frac_fp8"],
+                    "zipf_exponent": d["zipf_exponent"], "max_expert_rows": d["max_expert_rows"]})
+    for T, d in detail.items():
+        if T != "2048":
+            out[f"T{T}_us_per_layer"] = d["us_per_layer"]
+            out[f"T{T}_hbm_frac"] = d["hbm_frac"]
+    if hot:
+        out["hot_us_per_layer"] = hot["us_per_layer"]
+        for st in ("w13", "w2"):
+            out[f"hot_{st}_TFLOP_s"] = hot[st]["TFLOP_s"]
+            out[f"hot_{st}_mfma_frac_fp8_rate"] = hot[st]["mfma_frac_fp8_rate"]
+            out[f"hot_{st}_mfma_frac_fp4_peak"] = hot[st]["mfma_frac_fp4_peak"]
+    if gemm:
+        for st in ("w13", "w2"):
+            g = gemm[st]["packed"]
+            out[f"m2048_{st}_us"] = g["us"]
+            out[f"m2048_{st}_mfma_frac_fp8_rate"] = g["mfma_frac_fp8_rate"]
+            out[f"m2048_{st}_mfma_frac_fp4_peak"] = g["mfma_frac_fp4_peak"]
+    out.update(committed_mfma_busy())
+    return out
 
 
 def main():
@@ -801,8 +859,8 @@ def main():
                      "mean_us": round(w13_us, 2)},
         "stage_us": {k: round(v, 2) for k, v in kt.items()},
     }
+    sweep = {}
     if not args.no_sweep:
-        sweep = {}
         for Ts in (1, 2, 4, 8):
             r = main_run if Ts == T else measure_T(layers, Ts, 120, 12, dev, Ts)
             v = r["total_bytes"] / r["secs"] / 1e9
@@ -811,16 +869,16 @@ def main():
                               "hbm_frac": round(v / HBM_PEAK_GBS, 4),
                               "mean_U": round(float(np.mean(r["Us"])), 1),
                               "stage_us": {k: round(x, 2) for k, x in r["kernels"].items()}}
-        out["per_T"] = sweep
+    detail, hot, gemm = {}, None, None
     if args.prefill:
         Ts = [int(t) for t in args.prefill.split(",") if t]
         legs = set(args.prefill_legs.split(","))
         if "zipf" in legs:
-            out["prefill"] = measure_prefill(layers[:max(1, args.prefill_layers)], Ts, dev)
+            detail = measure_prefill(layers[:max(1, args.prefill_layers)], Ts, dev)
         if "hot" in legs:
-            out["prefill_hot_experts"] = measure_hot_experts(layers[:max(1, args.prefill_layers)], dev)
+            hot = measure_hot_experts(layers[:max(1, args.prefill_layers)], dev)
         if "gemm" in legs:
-            out["fp4_gemm_m2048"] = measure_fp4_gemm_2048(dev)
+            gemm = measure_fp4_gemm_2048(dev)
     if not args.no_gemv:
         out["fp8_gemv"] = measure_gemv(dev)
         out["grouped_fp4"] = measure_grouped_fp4(dev)
@@ -828,8 +886,23 @@ def main():
         out["sparse_attn"] = measure_attn(dev)
     if not args.no_stage:
         out["decode_stage"] = measure_stage(layers, dev, T=args.T)
+    if detail:
+        out["prefill_detail"] = detail
+    if hot:
+        out["prefill_hot_experts"] = hot
+    if gemm:
+        out["fp4_gemm_m2048"] = gemm
+    # the last keys of the line: the CPU baseline, the flat prefill block and the
+    # decode sweep, so a reader of the line's tail finds the whole metric there
+    if sweep:
+        out["per_T_stage_us"] = {k: v["stage_us"] for k, v in sweep.items()}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(layers, cfg, T, dev)
+    if detail or hot or gemm:
+        out["prefill"] = flat_prefill(detail, hot, gemm)
+    if sweep:
+        out["per_T"] = {k: {"us_per_layer": v["us_per_layer"], "hbm_frac": v["hbm_frac"], "GB_s": v["GB_s"],
+                            "mean_U": v["mean_U"]} for k, v in sweep.items()}
     print(json.dumps(out), flush=True)
 
 
