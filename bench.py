@@ -274,7 +274,7 @@ def measure_T(layers, T, steps, warmup, dev, salt):
 # wo_b and the indexer's wq_b (fp8_vector.py:505-510; wq_a is 1024 x 4096)
 GEMV_SHAPES = ((4096, 1024), (1024, 4096), (4096, 4096), (16384, 4096), (512, 4096), (32768, 1024), (4096, 8192),
                (8192, 1024))
-GEMV_TS = (1, 4, 8, 128)
+GEMV_TS = (1, 4, 8, 16, 32, 128)
 GEMV_ROTATE_BYTES = 640 << 20   # weight copies per shape: more than the 256 MB Infinity Cache
 
 

@@ -359,7 +359,9 @@ def test_fp8_linear_projection_shapes(gpu, w_fp32, N, K, M):
 @pytest.mark.parametrize("M,N,K", [(1, 256, 4096), (5, 512, 1024), (16, 128, 2048), (40, 256, 4096),
                                    (3, 128, 1536), (1, 512, 8192), (16, 384, 8192), (2, 4096, 1024),
                                    (4, 256, 4096), (9, 256, 4096), (12, 128, 1024), (5, 256, 8192),
-                                   (6, 256, 8192), (8, 256, 8192), (12, 128, 4096)])
+                                   (6, 256, 8192), (8, 256, 8192), (12, 128, 4096), (24, 256, 1024),
+                                   (33, 256, 8192), (64, 256, 4096), (130, 384, 1024), (200, 128, 2048),
+                                   (257, 128, 1536)])
 def test_fp8_linear_packed_exact(gpu, M, N, K):
     """x in {0, +-0.5, +-1, +-1.5} with one 2.0 per 128-block quantises exactly (ue8m0
     scale 2^-7), weight codes of the same values with unit scales: every partial sum
@@ -485,7 +487,7 @@ def test_add_rms_norm_quant_is_add_then_norm_quant(gpu, T, D):
 
 
 @pytest.mark.parametrize("M,N,K", [(4, 4096, 8192), (1, 1024, 4096), (16, 512, 1024), (40, 256, 1024),
-                                   (3, 128, 1536)])
+                                   (3, 128, 1536), (24, 1024, 1024), (33, 1024, 4096), (128, 4096, 4096)])
 def test_fp8_linear_residual_epilogue(gpu, M, N, K):
     """y = residual + linear(x): the GEMV epilogue (M <= 16, K in the GEMV set) and the
     tile GEMM followed by an add both give bf16(bf16(linear(x)) + residual), i.e. the
@@ -513,7 +515,8 @@ def test_fp8_linear_residual_epilogue(gpu, M, N, K):
 
 
 @pytest.mark.parametrize("M,N0,N1,K", [(4, 1024, 512, 4096), (4, 32768, 8192, 1024), (1, 256, 128, 8192),
-                                        (24, 256, 384, 1024), (3, 128, 48, 256)])
+                                        (24, 256, 384, 1024), (3, 128, 48, 256), (40, 1024, 512, 4096),
+                                        (128, 32768, 8192, 1024), (17, 256, 384, 8192)])
 def test_fp8_pair_equals_two_linears(gpu, M, N0, N1, K):
     """Two stacked projections in one launch give each projection's own output bit
     for bit (GEMV path at M <= 16 and K in its set, the two tile GEMMs otherwise)."""
@@ -530,7 +533,7 @@ def test_fp8_pair_equals_two_linears(gpu, M, N0, N1, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1024, 4096), (4, 256, 8192), (8, 512, 1024), (16, 128, 2048),
-                                   (3, 40960, 1024)])
+                                   (3, 40960, 1024), (24, 512, 1024), (40, 1024, 4096), (128, 512, 8192)])
 def test_fp8_linear_packed_float_act_scales(gpu, M, N, K):
     """The packed linear with non-power-of-two activation scales (scale_fmt None:
     amax / 448 as float32, applied on the VALU per K-block), on the one-tile GEMV
@@ -733,3 +736,38 @@ def test_wire_pack_non_finite_rows(gpu):
     rq, rs = om.wire_pack(from_bf16_bits(xb))
     assert _same_codes(bytes8(q), rq)
     assert np.array_equal(f32_of_bf16(sc), rs, equal_nan=True)
+
+
+# the M values the reference's invariance probe covers (fp8_vector.py:235-252),
+# either side of each switch between kernels (16 | 17, 32 | 33), and a prefill width
+INVARIANT_M = [1, 4, 8, 16, 17, 24, 32, 33, 64, 128]
+
+
+@pytest.mark.parametrize("w_fp32", [False, True])
+@pytest.mark.parametrize("act", ["ue8m0", "float"])
+@pytest.mark.parametrize("N,K", PROJ_SHAPES)
+def test_fp8_linear_batch_invariant(gpu, w_fp32, act, N, K):
+    """A row's output does not depend on how many rows share the call: the packed
+    linear at M = 1 .. 128 (one-tile GEMV, ring GEMV and tile GEMM, whichever serves
+    each M) gives every row the bits it has at M = 128, torch.equal as the reference
+    requires before it enables its decode GEMV (fp8_vector.py:235-252).  Both weight
+    scale kinds, power-of-two and float activation scales, bf16 input (act_quant
+    fused) and pre-quantised input (fp8_gemm on the packed weight)."""
+    from wanferenz_amd import stage
+
+    w, ws = stage.synthetic_linear(N, K, N + 5 * K, gpu, fp32_scales=w_fp32)
+    lin = kernels.PackedFp8Linear(w, ws, "ue8m0" if act == "ue8m0" else None)
+    Mmax = max(INVARIANT_M)
+    x = bf16_tensor(_x(N + K + 3, Mmax, K), gpu).view(Mmax, K)
+    ref = lin(x)
+    sdt = torch.float8_e8m0fnu if act == "ue8m0" else torch.float32
+    q, qs = kernels.act_quant(x, 128, "ue8m0" if act == "ue8m0" else None, sdt)
+    ref_q = lin.gemm(q, qs)
+    torch.cuda.synchronize()
+    assert torch.equal(ref, ref_q)
+    for M in INVARIANT_M[:-1]:
+        y = lin(x[:M].contiguous())
+        yq = lin.gemm(q[:M].contiguous(), qs[:M].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref[:M]), f"M={M}: bf16 input differs from M={Mmax}"
+        assert torch.equal(yq, ref[:M]), f"M={M}: pre-quantised input differs from M={Mmax}"

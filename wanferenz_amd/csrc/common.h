@@ -206,6 +206,30 @@ __device__ __forceinline__ uint32_t lds_addr(X* p) {
   return uint32_t(uintptr_t((__attribute__((address_space(3))) X*)p));
 }
 
+// Workgroups are dispatched to the XCDs round-robin (block b to XCD b % 8),
+// each XCD with its own L2.  xcd_runs renumbers the blocks [d0, d0 + n) so
+// that each XCD takes runs of 64 consecutive logical blocks (as many as its
+// CUs hold at once at two per CU): blocks that share operands, placed next to
+// each other in the logical order, then meet in one L2.  Run j goes to XCD
+// j % 8; the last, partial round of 8 runs is split contiguously.  A bijection
+// on [d0, d0 + n) for any n (checked exhaustively on the CPU), so only
+// locality depends on the dispatch order.
+__device__ __forceinline__ int xcd_runs(int b, int d0, int n) {
+  constexpr int kXcds = 8, kRun = 64;
+  const int x = b % kXcds;
+  const int fx = d0 + ((x - d0) & (kXcds - 1));  // first routed block on XCD x
+  const int k = (b - fx) / kXcds;                // b's place among them
+  const int full = n / (kXcds * kRun);           // complete rounds of 8 runs
+  if (k < full * kRun) return ((k / kRun) * kXcds + x) * kRun + k % kRun;
+  int before = 0;  // blocks of the last round on the XCDs ahead of x
+  for (int y = 0; y < x; ++y) {
+    const int fy = d0 + ((y - d0) & (kXcds - 1));
+    before += (fy < d0 + n ? (d0 + n - fy + kXcds - 1) / kXcds : 0) - full * kRun;
+  }
+  return full * kXcds * kRun + before + (k - full * kRun);
+}
+
+
 }  // namespace wz
 
 // Error reporting (errors.hip) and optional launch timing (prof.hip).

@@ -29,8 +29,12 @@ int launch_dense_fp8(const uint8_t* wp, const void* w_s, int w_kind, const uint8
                      bool a_pow2, uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 int launch_dense_fp4(const uint8_t* wp, const uint32_t* wp_s, const uint8_t* xq, const float* xs, bool a_pow2,
                      uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+bool tile_gemm_fits(int64_t M, int64_t N, int64_t K);
+int launch_tile_gemm(const uint8_t* xq, const float* xs, bool a_pow2, const uint8_t* wp, const void* w_s, int w_kind,
+                     const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
+                     int64_t K, hipStream_t stream);
 
-constexpr int kGvMaxM = 16;
+constexpr int kGvMaxM = 32;
 
 // GEMV shapes: W waves per workgroup, wave w owns K-blocks [w NKB, (w+1) NKB)
 // of every 16-column tile, NB tiles in flight per workgroup (a ring of
@@ -57,6 +61,19 @@ constexpr int kGvMaxM = 16;
 
 static bool gemv_shape_ok(int64_t K) { return K == 1024 || K == 2048 || K == 4096 || K == 8192; }
 
+static bool gemv_serves(bool qa, int64_t M, int64_t N, int64_t K);
+static int gemv_nkb(int64_t K);
+
+// K-blocks per slice of the summation order every FP8 linear path shares (the
+// tile GEMM follows it): the K range one GEMV wave owns, or the whole K where
+// no GEMV serves it.
+int gemv_slice_blocks(int64_t K) { return gemv_shape_ok(K) ? gemv_nkb(K) : int(K / 128); }
+
+// Pre-quantised rows on the M-tiled one-tile GEMV: up to 32 rows where the
+// tiles fit the one-tile kernel's range; wider rows and wider N on the tile
+// GEMM.
+static bool gemv_mt_serves(int64_t M, int64_t N, int64_t K);
+
 template <int NKB>
 struct GvBuf {
   v8i w[NKB];
@@ -66,13 +83,14 @@ struct GvBuf {
 
 // QA: x is pre-quantised e4m3 [M, K] with block scales xs [M, K/128] of kind
 // a_kind (fp8_gemm's a, a_s); otherwise x is bf16 and act_quant is fused.
+// RT row tiles of 16 (M <= 16 RT): each weight tile feeds RT MFMAs per K-block.
 // Workgroup b takes tiles b, b + G, ... (n_my of them); tile j sits in ring
 // slot j % NB, and slot s is refilled with tile j + NB as soon as tile j's
 // MFMAs have issued, so NB tiles stay in flight.  The W K-partials of a tile
 // meet in LDS and are summed in wave order.  AP2 / BP2: power-of-two
 // activation / e8m0 weight scales (compile-time, so the scaled MFMA chains
 // without a runtime branch around it).
-template <int W, int NKB, int NB, int MINW, bool XF, bool QA, bool AP2, bool BP2>
+template <int W, int NKB, int NB, int MINW, bool XF, bool QA, bool AP2, bool BP2, int RT>
 __global__ __launch_bounds__(W * 64, MINW) void fp8_gemv_kernel(const void* __restrict__ x, const void* __restrict__ xs,
                                                          int a_kind, const uint8_t* __restrict__ wp,
                                                          const void* __restrict__ w_s, int w_kind,
@@ -102,33 +120,39 @@ __global__ __launch_bounds__(W * 64, MINW) void fp8_gemv_kernel(const void* __re
     for (int q = 0; q < NKB; ++q) fp8_wscale(w_s, int64_t(item >> 3) * KB + kb0 + q, wkind, b.se[q], b.sf[q]);
   };
 
-  // this wave's K slice of the (<= 16) token rows, quantised once.  XF: the
+  // this wave's K slice of the (<= 16 RT) token rows, quantised once.  XF: the
   // bf16 rows are requested, then the first tile's weights, and the
   // quantisation runs while those are in flight (the x loads, issued first,
   // return first); otherwise the rows are quantised before any weight request.
-  AOp a[NKB];
-  ARaw xr[QA || !XF ? 1 : NKB];
-  if constexpr (QA) {
-    const uint8_t* xrow = nl < M ? static_cast<const uint8_t*>(x) + int64_t(nl) * K : nullptr;
-    const void* srow = a_kind == WZ_SCALE_UE8M0
-                           ? static_cast<const void*>(static_cast<const uint8_t*>(xs) + int64_t(nl) * KB)
-                           : static_cast<const void*>(static_cast<const float*>(xs) + int64_t(nl) * KB);
+  AOp a[RT][NKB];
+  ARaw xr[RT][QA || !XF ? 1 : NKB];
 #pragma unroll
-    for (int q = 0; q < NKB; ++q) a[q] = a_from_fp8(xrow, srow, kb0 + q, g, a_kind);
-  } else {
-    const uint16_t* xrow = nl < M ? static_cast<const uint16_t*>(x) + int64_t(nl) * K : nullptr;
+  for (int rt = 0; rt < RT; ++rt) {
+    const int r = rt * 16 + nl;
+    if constexpr (QA) {
+      const uint8_t* xrow = r < M ? static_cast<const uint8_t*>(x) + int64_t(r) * K : nullptr;
+      const void* srow = a_kind == WZ_SCALE_UE8M0
+                             ? static_cast<const void*>(static_cast<const uint8_t*>(xs) + int64_t(r) * KB)
+                             : static_cast<const void*>(static_cast<const float*>(xs) + int64_t(r) * KB);
 #pragma unroll
-    for (int q = 0; q < NKB; ++q) {
-      if constexpr (XF)
-        xr[q] = a_load_bf16(xrow, kb0 + q, g);
-      else
-        a[q] = a_from_bf16(xrow, kb0 + q, g, AP2);
+      for (int q = 0; q < NKB; ++q) a[rt][q] = a_from_fp8(xrow, srow, kb0 + q, g, a_kind);
+    } else {
+      const uint16_t* xrow = r < M ? static_cast<const uint16_t*>(x) + int64_t(r) * K : nullptr;
+#pragma unroll
+      for (int q = 0; q < NKB; ++q) {
+        if constexpr (XF)
+          xr[rt][q] = a_load_bf16(xrow, kb0 + q, g);
+        else
+          a[rt][q] = a_from_bf16(xrow, kb0 + q, g, AP2);
+      }
     }
   }
   auto quant_x = [&]() {
     if constexpr (!QA && XF) {
 #pragma unroll
-      for (int q = 0; q < NKB; ++q) a[q] = a_quant_bf16(xr[q], AP2);
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int q = 0; q < NKB; ++q) a[rt][q] = a_quant_bf16(xr[rt][q], AP2);
     }
   };
   // keeps the weight requests below the quantisation: hoisted above it, they
@@ -137,29 +161,39 @@ __global__ __launch_bounds__(W * 64, MINW) void fp8_gemv_kernel(const void* __re
 
   auto process = [&](const GvBuf<NKB>& b, int j) {
     const int item = first + j * G;
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    v4f acc[RT];
 #pragma unroll
-    for (int q = 0; q < NKB; ++q) mma_step<kFmtFp8, kFmtFp8>(acc, a[q], b.w[q], b.se[q], b.sf[q], a_pow2, bp, lane);
-    float* r = red[j & 1];
+    for (int rt = 0; rt < RT; ++rt) {
+      acc[rt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[(wave * 4 + i) * kWave + lane] = acc[i];
-    __syncthreads();
-    if (wave == 0) {
+      for (int q = 0; q < NKB; ++q)
+        mma_step<kFmtFp8, kFmtFp8>(acc[rt], a[rt][q], b.w[q], b.se[q], b.sf[q], a_pow2, bp, lane);
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v = r[i * kWave + lane];
+    for (int rt = 0; rt < RT; ++rt) {
+      // rounds alternate between the two buffers: a round's writes follow the
+      // barrier that wave 0 passes only after reading the previous round
+      float* r = red[(j * RT + rt) & 1];
 #pragma unroll
-        for (int w = 1; w < W; ++w) v += r[(w * 4 + i) * kWave + lane];
-        const int row = g * 4 + i;
-        const int col = item * 16 + nl;
-        if (row < M && col < n_split) {
-          const int64_t o = int64_t(row) * n_split + col;
-          // res: the residual stream, y = x + linear(..): the product rounded
-          // to bf16, then the fp32 sum rounded once (a bf16 tensor add)
-          y[o] = f32_to_bf16(res ? bf16_round(v) + __uint_as_float(uint32_t(res[o]) << 16) : v);
-        } else if (row < M) {
-          // columns past n_split: the second of two stacked weights, its own buffer
-          y_hi[int64_t(row) * (N - n_split) + (col - n_split)] = f32_to_bf16(v);
+      for (int i = 0; i < 4; ++i) r[(wave * 4 + i) * kWave + lane] = acc[rt][i];
+      __syncthreads();
+      if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = r[i * kWave + lane];
+#pragma unroll
+          for (int w = 1; w < W; ++w) v += r[(w * 4 + i) * kWave + lane];
+          const int row = rt * 16 + g * 4 + i;
+          const int col = item * 16 + nl;
+          if (row < M && col < n_split) {
+            const int64_t o = int64_t(row) * n_split + col;
+            // res: the residual stream, y = x + linear(..): the product rounded
+            // to bf16, then the fp32 sum rounded once (a bf16 tensor add)
+            y[o] = f32_to_bf16(res ? bf16_round(v) + __uint_as_float(uint32_t(res[o]) << 16) : v);
+          } else if (row < M) {
+            // columns past n_split: the second of two stacked weights, its own buffer
+            y_hi[int64_t(row) * (N - n_split) + (col - n_split)] = f32_to_bf16(v);
+          }
         }
       }
     }
@@ -232,7 +266,7 @@ struct GvNorm {
   static constexpr int ROWS = W / NWR;                                          // rows per launch
 };
 
-template <int W, int NKB, int XP, bool QA, bool AP2, bool BP2, bool NORM>
+template <int W, int NKB, int XP, bool QA, bool AP2, bool BP2, bool NORM, int RT>
 __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restrict__ x, const void* __restrict__ xs,
                                                            int a_kind, const uint8_t* __restrict__ wp,
                                                            const void* __restrict__ w_s,
@@ -240,30 +274,46 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
                                                            uint16_t* __restrict__ y_hi, int n_split, int M, int N,
                                                            int K, const float* __restrict__ nw, float eps,
                                                            const uint16_t* __restrict__ xb,
-                                                           uint16_t* __restrict__ hsum) {
+                                                           uint16_t* __restrict__ hsum, int n_mt) {
   static_assert(W >= 4, "the epilogue uses four waves");
   static_assert(!(NORM && QA), "the norm path starts from bf16 rows");
+  static_assert(!(NORM && RT > 1), "the norm path serves up to 16 rows");
+  static_assert(QA || RT <= 2, "the bf16 paths serve up to 32 rows");
   using NP = GvNorm<W, NKB>;
-  __shared__ float red[W * 4 * kWave];
   __shared__ float part[NORM ? NP::ROWS : 1][4];
-  extern __shared__ __align__(16) uint8_t gv_lds[];  // !QA: e4m3 rows [M][K + 16], then (e8m0, scale) per pair
+  // !QA: e4m3 rows [M][K + 16], then (e8m0, scale) per pair; afterwards (and
+  // always with QA) the W K-partials of the RT 16 x 16 tiles, [RT][W][4][64]
+  extern __shared__ __align__(16) uint8_t gv_lds[];
+  float* red = reinterpret_cast<float*>(gv_lds);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = lane & 15, g = lane >> 4;
-  const int KB = K / 128, kb0 = wave * NKB, item = blockIdx.x;
+  const int KB = K / 128, kb0 = wave * NKB;
+  // QA with n_mt > 1: workgroup b takes (tile, M-tile of 16 RT rows) t =
+  // xcd_runs(b), so the M-tiles of one weight tile run on one XCD together and
+  // read its tiles from that L2; otherwise tile b over rows 0 ..
+  int item = blockIdx.x, m0 = 0;
+  if (QA && n_mt > 1) {
+    const int t = xcd_runs(int(blockIdx.x), 0, (N / 16) * n_mt);
+    item = t / n_mt;
+    m0 = (t - item * n_mt) * 16 * RT;
+  }
   const int ldk = K + 16;
 
-  AOp a[NKB];
+  AOp a[RT][NKB];
   uint4 xr[QA || NORM ? 1 : XP];
   v4i nv[NORM ? NP::NJ : 1], nbv[NORM ? NP::NJ : 1], nwv[NORM ? NP::NJ : 1][2];
   const int P = M * KB;
   if constexpr (QA) {
-    const int xrow = nl < M ? nl : M - 1;  // rows past M repeat row M - 1; their outputs are dropped
-    const uint8_t* row = static_cast<const uint8_t*>(x) + int64_t(xrow) * K;
-    const void* srow = a_kind == WZ_SCALE_UE8M0
-                           ? static_cast<const void*>(static_cast<const uint8_t*>(xs) + int64_t(xrow) * KB)
-                           : static_cast<const void*>(static_cast<const float*>(xs) + int64_t(xrow) * KB);
 #pragma unroll
-    for (int q = 0; q < NKB; ++q) a[q] = a_from_fp8_row(row, srow, kb0 + q, g, a_kind);
+    for (int rt = 0; rt < RT; ++rt) {
+      const int r = m0 + rt * 16 + nl, xrow = r < M ? r : M - 1;  // rows past M repeat row M - 1; dropped
+      const uint8_t* row = static_cast<const uint8_t*>(x) + int64_t(xrow) * K;
+      const void* srow = a_kind == WZ_SCALE_UE8M0
+                             ? static_cast<const void*>(static_cast<const uint8_t*>(xs) + int64_t(xrow) * KB)
+                             : static_cast<const void*>(static_cast<const float*>(xs) + int64_t(xrow) * KB);
+#pragma unroll
+      for (int q = 0; q < NKB; ++q) a[rt][q] = a_from_fp8_row(row, srow, kb0 + q, g, a_kind);
+    }
   } else if constexpr (NORM) {
     const int nr = wave / NP::NWR, rr = nr < M ? nr : M - 1, t = (wave % NP::NWR) * 64 + lane;
 #pragma unroll
@@ -399,31 +449,43 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
     }
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < NKB; ++q) {
-      a[q] = a_zero();
-      if (nl < M) {
-        const uint8_t* pa = xq + nl * ldk + (kb0 + q) * 128 + g * 16;
-        const uint4 lo = *reinterpret_cast<const uint4*>(pa), hi = *reinterpret_cast<const uint4*>(pa + 64);
-        a[q].v = v8i{int(lo.x), int(lo.y), int(lo.z), int(lo.w), int(hi.x), int(hi.y), int(hi.z), int(hi.w)};
-        const int2 s2 = xsc[nl * KB + kb0 + q];
-        a[q].se8 = s2.x;
-        a[q].sf = __int_as_float(s2.y);
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int q = 0; q < NKB; ++q) {
+        const int r = rt * 16 + nl;
+        a[rt][q] = a_zero();
+        if (r < M) {
+          const uint8_t* pa = xq + r * ldk + (kb0 + q) * 128 + g * 16;
+          const uint4 lo = *reinterpret_cast<const uint4*>(pa), hi = *reinterpret_cast<const uint4*>(pa + 64);
+          a[rt][q].v = v8i{int(lo.x), int(lo.y), int(lo.z), int(lo.w), int(hi.x), int(hi.y), int(hi.z), int(hi.w)};
+          const int2 s2 = xsc[r * KB + kb0 + q];
+          a[rt][q].se8 = s2.x;
+          a[rt][q].sf = __int_as_float(s2.y);
+        }
       }
-    }
   }
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  v4f acc[RT];
 #pragma unroll
-  for (int q = 0; q < NKB; ++q) mma_step<kFmtFp8, kFmtFp8>(acc, a[q], w[q], se[q], sf[q], AP2, BP2, lane);
-
+  for (int rt = 0; rt < RT; ++rt) {
+    acc[rt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * kWave + lane] = acc[i];
+    for (int q = 0; q < NKB; ++q) mma_step<kFmtFp8, kFmtFp8>(acc[rt], a[rt][q], w[q], se[q], sf[q], AP2, BP2, lane);
+  }
+  // the partials go where the x rows were: every wave has its A fragments
+  if constexpr (NORM || !QA) __syncthreads();
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[((rt * W + wave) * 4 + i) * kWave + lane] = acc[rt][i];
   __syncthreads();
-  if (wave < 4) {
-    const int i = wave, row = g * 4 + i;
+  // (row tile, row of the four a lane holds) pairs, one per wave: wave order sums
+  for (int pi = wave; pi < 4 * RT; pi += W) {
+    const int rt = pi >> 2, i = pi & 3, row = m0 + rt * 16 + g * 4 + i;
+    const float* rr = red + rt * W * 4 * kWave;
     if (row < M) {
-      float v = red[i * kWave + lane];
+      float v = rr[i * kWave + lane];
 #pragma unroll
-      for (int ww = 1; ww < W; ++ww) v += red[(ww * 4 + i) * kWave + lane];
+      for (int ww = 1; ww < W; ++ww) v += rr[(ww * 4 + i) * kWave + lane];
       const int col = item * 16 + nl;
       if (col < n_split) {
         const int64_t o = int64_t(row) * n_split + col;
@@ -446,6 +508,11 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
 
 // dynamic LDS of the one-tile kernel's bf16 path: e4m3 rows + per-pair scales
 static size_t gemv1_lds_bytes(int64_t M, int64_t K) { return size_t(M) * size_t(K + 16) + size_t(M) * size_t(K / 128) * 8; }
+// ... and in total: that region, then the K-partials of RT row tiles in its place
+static size_t gemv1_dyn_bytes(bool qa, int64_t M, int64_t K, int W, int RT) {
+  const size_t red = size_t(RT) * size_t(W) * 4 * kWave * 4;
+  return qa ? red : std::max(gemv1_lds_bytes(M, K), red);
+}
 
 // LDS a workgroup may hold on gfx950 (160 KB); dynamic LDS past 64 KB is
 // requested per kernel once (hipFuncAttributeMaxDynamicSharedMemorySize).
@@ -467,6 +534,9 @@ static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t*
 static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s,
                          int w_kind, const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M,
                          int64_t N, int64_t K, bool pow2, hipStream_t stream);
+static int gemv_mt_dispatch(const void* xq, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
+                            const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
+                            int64_t K, bool pow2, hipStream_t stream);
 
 static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
@@ -481,10 +551,12 @@ extern "C" int wz_fp8_pack(const void* w_e4m3, int64_t N, int64_t K, void* packe
   return launch_pack_fp8(w_e4m3, N, K, packed, stream);
 }
 
+// No workspace where the GEMV serves every N (M <= 16); otherwise the act_quant
+// of x for the tile GEMM (M <= 32 may still run the GEMV, depending on N).
 extern "C" size_t wz_fp8_linear_workspace_bytes(int64_t M, int64_t K) {
   using namespace wz;
   if (M <= 0 || K <= 0) return 0;
-  if (M <= kGvMaxM && gemv_shape_ok(K)) return 0;
+  if (M <= 16 && gemv_shape_ok(K)) return 0;
   return align256(size_t(M) * size_t(K)) + size_t(M) * size_t(K / 128) * 4;
 }
 
@@ -519,7 +591,7 @@ static int linear_packed(const char* name, const void* x_bf16, const void* w_pac
     return set_error(WZ_EINVAL, "%s: the residual and the output overlap", name);
   const bool pow2 = act_scale_kind != WZ_SCALE_F32;
   uint16_t* y = static_cast<uint16_t*>(y_bf16);
-  if (M <= kGvMaxM && gemv_shape_ok(K))
+  if (gemv_serves(false, M, N, K))
     return gemv_dispatch(false, x_bf16, nullptr, 0, static_cast<const uint8_t*>(w_packed), w_s, w_scale_kind, res, y,
                          nullptr, N, M, N, K, pow2, stream);
   const size_t need = wz_fp8_linear_workspace_bytes(M, K);
@@ -530,9 +602,12 @@ static int linear_packed(const char* name, const void* x_bf16, const void* w_pac
   float* xs = reinterpret_cast<float*>(xq + align256(size_t(M) * size_t(K)));
   const int qkind = pow2 ? WZ_SCALE_UE8M0_F32 : WZ_SCALE_F32;
   if (int rc = launch_act_quant(x_bf16, M, K, xq, xs, qkind, stream)) return rc;
-  return add_residual(res, y, M, N,
-                      launch_dense_fp8(static_cast<const uint8_t*>(w_packed), w_s, w_scale_kind, xq, xs, pow2, y, M,
-                                       N, K, stream),
+  const uint8_t* wp = static_cast<const uint8_t*>(w_packed);
+  if (gemv_mt_serves(M, N, K))
+    return gemv_mt_dispatch(xq, xs, qkind, wp, w_s, w_scale_kind, res, y, nullptr, N, M, N, K, pow2, stream);
+  if (tile_gemm_fits(M, N, K))
+    return launch_tile_gemm(xq, xs, pow2, wp, w_s, w_scale_kind, res, y, nullptr, N, M, N, K, stream);
+  return add_residual(res, y, M, N, launch_dense_fp8(wp, w_s, w_scale_kind, xq, xs, pow2, y, M, N, K, stream),
                       stream);
 }
 
@@ -564,49 +639,59 @@ __global__ void e8m0_to_f32_kernel(const uint8_t* __restrict__ src, float* __res
 
 // Resident workgroups per CU of one GEMV instantiation (its registers and
 // LDS decide), asked once.  The grid is that many per CU, or one per tile.
-template <int W, int NKB, int NB, int MINW, bool XF, bool QA, bool AP2, bool BP2>
+template <int W, int NKB, int NB, int MINW, bool XF, bool QA, bool AP2, bool BP2, int RT>
 static int launch_gemv_k(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
                          const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
                          int64_t K, hipStream_t stream) {
   static const int per_cu = [] {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fp8_gemv_kernel<W, NKB, NB, MINW, XF, QA, AP2, BP2>, W * 64, 0) !=
-            hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fp8_gemv_kernel<W, NKB, NB, MINW, XF, QA, AP2, BP2, RT>,
+                                                     W * 64, 0) != hipSuccess ||
         n < 1)
       n = 1;
     return n;
   }();
   const dim3 grid(unsigned(std::min<int64_t>(N / 16, int64_t(per_cu) * cu_count())));
-  WZ_LAUNCH("fp8_gemv", stream, (fp8_gemv_kernel<W, NKB, NB, MINW, XF, QA, AP2, BP2>), grid, dim3(W * 64), 0, x, xs, a_kind,
-            w, w_s, w_kind, res, y, y_hi, int(n_split), int(M), int(N), int(K), AP2 ? 1 : 0);
+  WZ_LAUNCH("fp8_gemv", stream, (fp8_gemv_kernel<W, NKB, NB, MINW, XF, QA, AP2, BP2, RT>), grid, dim3(W * 64), 0, x,
+            xs, a_kind, w, w_s, w_kind, res, y, y_hi, int(n_split), int(M), int(N), int(K), AP2 ? 1 : 0);
   return check_launch("fp8_gemv");
 }
 
+template <int W, int NKB, int NB, int MINW, bool XF, bool QA, int RT>
+static int launch_gemv_rt(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
+                          const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
+                          int64_t K, bool pow2, hipStream_t stream) {
+  const bool bp = w_kind == WZ_WSCALE_E8M0;
+#define WZ_GVK(AP, BP) \
+  launch_gemv_k<W, NKB, NB, MINW, XF, QA, AP, BP, RT>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, stream)
+  if (pow2) return bp ? WZ_GVK(true, true) : WZ_GVK(true, false);
+  return bp ? WZ_GVK(false, true) : WZ_GVK(false, false);
+#undef WZ_GVK
+}
+
+// M <= 16 (one row tile): a second row tile's x slice and the ring do not
+// fit the registers of sixteen waves, so wider M goes to the tile GEMM
 template <int W, int NKB, int NB, int MINW, bool XF, bool QA>
 static int launch_gemv(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
                        const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
                        int64_t K, bool pow2, hipStream_t stream) {
-  const bool bp = w_kind == WZ_WSCALE_E8M0;
-  if (pow2)
-    return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, true>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, stream)
-              : launch_gemv_k<W, NKB, NB, MINW, XF, QA, true, false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, stream);
-  return bp ? launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, true>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, stream)
-            : launch_gemv_k<W, NKB, NB, MINW, XF, QA, false, false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, stream);
+  return launch_gemv_rt<W, NKB, NB, MINW, XF, QA, 1>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K,
+                                                      pow2, stream);
 }
 
-template <int W, int NKB, int XP, bool QA>
-static int launch_gemv1(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
-                        const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
-                        int64_t K, bool pow2, hipStream_t stream) {
+template <int W, int NKB, int XP, bool QA, int RT>
+static int launch_gemv1_rt(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
+                           const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
+                           int64_t K, bool pow2, hipStream_t stream) {
   const dim3 grid(unsigned(N / 16)), block(W * 64);
   const bool bp = w_kind == WZ_WSCALE_E8M0;
-  const size_t lds = QA ? 0 : gemv1_lds_bytes(M, K);
+  const size_t lds = gemv1_dyn_bytes(QA, M, K, W, RT);
 #define WZ_GV1(AP, BP)                                                                                        \
   do {                                                                                                          \
     static int granted = 0;                                                                                     \
-    if (int rc = allow_lds(fp8_gemv1_kernel<W, NKB, XP, QA, AP, BP, false>, lds, granted)) return rc;              \
-    WZ_LAUNCH("fp8_gemv1", stream, (fp8_gemv1_kernel<W, NKB, XP, QA, AP, BP, false>), grid, block, lds, x, xs, a_kind, w, \
-              w_s, res, y, y_hi, int(n_split), int(M), int(N), int(K), nullptr, 0.0f, nullptr, nullptr);         \
+    if (int rc = allow_lds(fp8_gemv1_kernel<W, NKB, XP, QA, AP, BP, false, RT>, lds, granted)) return rc;          \
+    WZ_LAUNCH("fp8_gemv1", stream, (fp8_gemv1_kernel<W, NKB, XP, QA, AP, BP, false, RT>), grid, block, lds, x, xs,  \
+              a_kind, w, w_s, res, y, y_hi, int(n_split), int(M), int(N), int(K), nullptr, 0.0f, nullptr, nullptr, 1); \
   } while (0)
   if (pow2) {
     if (bp) WZ_GV1(true, true); else WZ_GV1(true, false);
@@ -617,6 +702,45 @@ static int launch_gemv1(const void* x, const void* xs, int a_kind, const uint8_t
   return check_launch("fp8_gemv1");
 }
 
+template <int W, int NKB, int XP, bool QA>
+static int launch_gemv1(const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
+                        const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
+                        int64_t K, bool pow2, hipStream_t stream) {
+  if (M <= 16)
+    return launch_gemv1_rt<W, NKB, XP, QA, 1>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2,
+                                              stream);
+  return launch_gemv1_rt<W, NKB, XP, QA, 2>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2,
+                                            stream);
+}
+
+// Pre-quantised rows past the GEMV's 16 on the one-tile kernel, M-tiled: a
+// workgroup per (16-column tile, 16 RT rows), every load of its K range issued
+// at once, the same K split and wave-order sum as the GEMV (so the same bits).
+template <int W, int NKB, int RT>
+static int launch_gemv_mt(const void* xq, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
+                          const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
+                          int64_t K, bool pow2, hipStream_t stream) {
+  const int n_mt = int((M + 16 * RT - 1) / (16 * RT));
+  const dim3 grid(unsigned((N / 16) * n_mt)), block(W * 64);
+  const bool bp = w_kind == WZ_WSCALE_E8M0;
+  const size_t lds = gemv1_dyn_bytes(true, M, K, W, RT);
+#define WZ_GVM(AP, BP)                                                                                        \
+  do {                                                                                                          \
+    static int granted = 0;                                                                                     \
+    if (int rc = allow_lds(fp8_gemv1_kernel<W, NKB, 1, true, AP, BP, false, RT>, lds, granted)) return rc;         \
+    WZ_LAUNCH("fp8_gemv_mt", stream, (fp8_gemv1_kernel<W, NKB, 1, true, AP, BP, false, RT>), grid, block, lds, xq,   \
+              xs, a_kind, w, w_s, res, y, y_hi, int(n_split), int(M), int(N), int(K), nullptr, 0.0f, nullptr,     \
+              nullptr, n_mt);                                                                                   \
+  } while (0)
+  if (pow2) {
+    if (bp) WZ_GVM(true, true); else WZ_GVM(true, false);
+  } else {
+    if (bp) WZ_GVM(false, true); else WZ_GVM(false, false);
+  }
+#undef WZ_GVM
+  return check_launch("fp8_gemv_mt");
+}
+
 // GEMV shape per K for the one-tile kernel: (W, NKB) as the ring kernel's, so
 // both split K the same way and give the same bits.  It serves N / 16 tiles up
 // to WZ_GV1_MAX_TILES; above that the ring kernel's persistent workgroups
@@ -625,7 +749,7 @@ static int launch_gemv1(const void* x, const void* xs, int a_kind, const uint8_t
 #define WZ_GV1_MAX_TILES 512
 #endif
 #ifndef WZ_GV1_K1024
-#define WZ_GV1_K1024 8, 1, 4
+#define WZ_GV1_K1024 8, 1, 8
 #endif
 #ifndef WZ_GV1_K2048
 #define WZ_GV1_K2048 8, 2, 8
@@ -637,13 +761,94 @@ static int launch_gemv1(const void* x, const void* xs, int a_kind, const uint8_t
 #define WZ_GV1_K8192 16, 4, 8
 #endif
 
+template <int W, int NKB, int NB, int MINW, bool XF>
+constexpr int ring_nkb() { return NKB; }
+template <int W, int NKB, int XP>
+constexpr int one_nkb() { return NKB; }
+template <int W, int NKB, int XP>
+constexpr int one_w() { return W; }
+template <int W, int NKB, int XP>
+constexpr int one_xp() { return XP; }
+// the one-tile and ring kernels split K alike at every K, so they give the same bits
+static_assert(ring_nkb<WZ_GV_K1024>() == one_nkb<WZ_GV1_K1024>() && ring_nkb<WZ_GV_K2048>() == one_nkb<WZ_GV1_K2048>() &&
+                  ring_nkb<WZ_GV_K4096>() == one_nkb<WZ_GV1_K4096>() && ring_nkb<WZ_GV_K8192>() == one_nkb<WZ_GV1_K8192>(),
+              "GEMV kernels must share the K split");
+
+static int gemv_nkb(int64_t K) {
+  switch (K) {
+    case 1024: return ring_nkb<WZ_GV_K1024>();
+    case 2048: return ring_nkb<WZ_GV_K2048>();
+    case 4096: return ring_nkb<WZ_GV_K4096>();
+    default: return ring_nkb<WZ_GV_K8192>();
+  }
+}
+
+static bool gemv_mt_serves(int64_t M, int64_t N, int64_t K) {
+  return gemv_shape_ok(K) && M <= kGvMaxM && N / 16 <= WZ_GV1_MAX_TILES;
+}
+
+// Whether a GEMV kernel serves (M, N, K) from x as given: every M <= 16; M <= 32
+// on the one-tile kernel with two row tiles, where its tiles fit one launch and,
+// for bf16 x, the quantised rows fit its passes and LDS.  The rest quantises x
+// first and runs the M-tiled one-tile kernel.
+static bool gemv_serves(bool qa, int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || !gemv_shape_ok(K)) return false;
+  if (M <= 16) return true;
+  if (M > kGvMaxM || N / 16 > WZ_GV1_MAX_TILES) return false;
+  if (qa) return true;
+  int W = 0, XP = 0;
+  switch (K) {
+    case 1024: W = one_w<WZ_GV1_K1024>(); XP = one_xp<WZ_GV1_K1024>(); break;
+    case 2048: W = one_w<WZ_GV1_K2048>(); XP = one_xp<WZ_GV1_K2048>(); break;
+    case 4096: W = one_w<WZ_GV1_K4096>(); XP = one_xp<WZ_GV1_K4096>(); break;
+    default: W = one_w<WZ_GV1_K8192>(); XP = one_xp<WZ_GV1_K8192>(); break;
+  }
+  return M * (K / 128) <= 4 * W * XP && gemv1_dyn_bytes(false, M, K, W, 2) + 64 <= kLdsMax;
+}
+
+// Row tiles per workgroup of the M-tiled kernel at each K (registers: RT x
+// NKB A fragments beside the weights).
+#ifndef WZ_GVM_K1024
+#define WZ_GVM_K1024 4
+#endif
+#ifndef WZ_GVM_K2048
+#define WZ_GVM_K2048 4
+#endif
+#ifndef WZ_GVM_K4096
+#define WZ_GVM_K4096 4
+#endif
+#ifndef WZ_GVM_K8192
+#define WZ_GVM_K8192 2
+#endif
+
+static int gemv_mt_dispatch(const void* xq, const void* xs, int a_kind, const uint8_t* w, const void* w_s, int w_kind,
+                            const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N,
+                            int64_t K, bool pow2, hipStream_t stream) {
+#define WZ_MT_(W_, NKB_, XP_, RT_)                                                                          \
+  return launch_gemv_mt<W_, NKB_, RT_>(xq, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, \
+                                       stream)
+#define WZ_MT(...) WZ_MT_(__VA_ARGS__)
+  switch (K) {
+    case 1024: WZ_MT(WZ_GV1_K1024, WZ_GVM_K1024);
+    case 2048: WZ_MT(WZ_GV1_K2048, WZ_GVM_K2048);
+    case 4096: WZ_MT(WZ_GV1_K4096, WZ_GVM_K4096);
+    case 8192: WZ_MT(WZ_GV1_K8192, WZ_GVM_K8192);
+    default: return set_error(WZ_EINVAL, "fp8 gemv: no shape for K=%lld", (long long)K);
+  }
+#undef WZ_MT
+#undef WZ_MT_
+}
+
 static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s,
                          int w_kind, const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M,
                          int64_t N, int64_t K, bool pow2, hipStream_t stream) {
   // the bf16 path quantises M x K / 128 pairs in passes of four per wave, the
-  // fewest of 1, 2, 4, 8 passes that cover them (at most the third value of
-  // each WZ_GV1_K*), and holds them in LDS
-  auto fits1 = [&](int W_, int XP_) { return M * (K / 128) <= 4 * W_ * XP_ && gemv1_lds_bytes(M, K) + size_t(W_) * 1024 <= kLdsMax; };
+  // fewest of 1, 2, 4, 8, 16 passes that cover them (at most the third value
+  // of each WZ_GV1_K*), and holds them in LDS
+  const int rt = M <= 16 ? 1 : 2;
+  auto fits1 = [&](int W_, int XP_) {
+    return M * (K / 128) <= 4 * W_ * XP_ && gemv1_dyn_bytes(false, M, K, W_, rt) + 64 <= kLdsMax;
+  };
   if (N / 16 <= WZ_GV1_MAX_TILES) {
 #define WZ_G1_(W_, NKB_, XP_)                                                                                 \
   if (qa) return launch_gemv1<W_, NKB_, 1, true>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream); \
@@ -663,6 +868,7 @@ static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, con
 #undef WZ_G1
 #undef WZ_G1_
   }
+  if (M > 16) return set_error(WZ_EINVAL, "fp8 gemv: M=%lld rows need the one-tile kernel", (long long)M);
 #define WZ_GV(...)                                                                                          \
   return qa ? launch_gemv<__VA_ARGS__, true>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream)          \
             : launch_gemv<__VA_ARGS__, false>(x, xs, a_kind, w, w_s, w_kind, res, y, y_hi, n_split, M, N, K, pow2, stream)
@@ -681,15 +887,19 @@ static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, con
 extern "C" size_t wz_fp8_gemm_packed_workspace_bytes(int64_t M, int64_t K, int act_scale_kind) {
   using namespace wz;
   if (M <= 0 || K <= 0) return 0;
-  if (M <= kGvMaxM && gemv_shape_ok(K)) return 0;
+  if (M <= 16 && gemv_shape_ok(K)) return 0;  // the GEMV kernels read e8m0 scales as they are
   return act_scale_kind == WZ_SCALE_UE8M0 ? size_t(M) * size_t(K / 128) * 4 : 0;
 }
 
 namespace wz {
 
+// y_hi / n_split: two stacked weights, the columns from n_split on to their own
+// buffer (nullptr / N: one weight).
 static int gemm_packed(const char* name, const void* a_e4m3, const void* a_s, const void* w_packed, const void* w_s,
                        const uint16_t* res, void* c_bf16, int64_t M, int64_t N, int64_t K, int act_scale_kind,
-                       int w_scale_kind, void* ws, size_t ws_bytes, hipStream_t stream) {
+                       int w_scale_kind, void* ws, size_t ws_bytes, hipStream_t stream, uint16_t* y_hi = nullptr,
+                       int64_t n_split = -1) {
+  if (n_split < 0) n_split = N;
   if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 128)
     return set_error(WZ_EINVAL, "%s: bad shape M=%lld N=%lld K=%lld", name, (long long)M, (long long)N, (long long)K);
   if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30)) return set_error(WZ_EINVAL, "%s: dimension too large", name);
@@ -703,9 +913,14 @@ static int gemm_packed(const char* name, const void* a_e4m3, const void* a_s, co
   const bool pow2 = act_scale_kind != WZ_SCALE_F32;
   const uint8_t* w = static_cast<const uint8_t*>(w_packed);
   uint16_t* c = static_cast<uint16_t*>(c_bf16);
-  if (M <= kGvMaxM && gemv_shape_ok(K))
-    return gemv_dispatch(true, a_e4m3, a_s, act_scale_kind, w, w_s, w_scale_kind, res, c, nullptr, N, M, N, K, pow2,
-                         stream);
+  if (gemv_serves(true, M, N, K))
+    return gemv_dispatch(true, a_e4m3, a_s, act_scale_kind, w, w_s, w_scale_kind, res, c, y_hi, n_split, M, N, K,
+                         pow2, stream);
+  if (gemv_mt_serves(M, N, K))
+    return gemv_mt_dispatch(a_e4m3, a_s, act_scale_kind, w, w_s, w_scale_kind, res, c, y_hi, n_split, M, N, K, pow2,
+                            stream);
+  const bool tile = tile_gemm_fits(M, N, K);
+  if (y_hi && !tile) return set_error(WZ_EINVAL, "%s: a split output outside the tile GEMM's range", name);
   const float* xs = static_cast<const float*>(a_s);
   if (act_scale_kind == WZ_SCALE_UE8M0) {
     const size_t need = wz_fp8_gemm_packed_workspace_bytes(M, K, act_scale_kind);
@@ -718,10 +933,10 @@ static int gemm_packed(const char* name, const void* a_e4m3, const void* a_s, co
     if (int rc = check_launch("fp8_gemm_packed scales")) return rc;
     xs = static_cast<const float*>(ws);
   }
-  return add_residual(
-      res, c, M, N,
-      launch_dense_fp8(w, w_s, w_scale_kind, static_cast<const uint8_t*>(a_e4m3), xs, pow2, c, M, N, K, stream),
-      stream);
+  const uint8_t* xq = static_cast<const uint8_t*>(a_e4m3);
+  if (tile) return launch_tile_gemm(xq, xs, pow2, w, w_s, w_scale_kind, res, c, y_hi, n_split, M, N, K, stream);
+  return add_residual(res, c, M, N, launch_dense_fp8(w, w_s, w_scale_kind, xq, xs, pow2, c, M, N, K, stream),
+                      stream);
 }
 
 }  // namespace wz
@@ -752,7 +967,7 @@ extern "C" int wz_fp8_gemm_packed_pair(const void* a_e4m3, const void* a_s, cons
     return set_error(WZ_EINVAL, "fp8_gemm_packed_pair: split N0=%lld must be a multiple of 128 inside N=%lld",
                      (long long)N0, (long long)N);
   if (!c1_bf16) return set_error(WZ_EINVAL, "fp8_gemm_packed_pair: null pointer");
-  if (M > 0 && M <= kGvMaxM && gemv_shape_ok(K) && N % 16 == 0 && K % 128 == 0 && N <= (1 << 30) && K <= (1 << 30)) {
+  if (M > 0 && gemv_serves(true, M, N, K) && N % 16 == 0 && K % 128 == 0 && N <= (1 << 30) && K <= (1 << 30)) {
     if (act_scale_kind < WZ_SCALE_F32 || act_scale_kind > WZ_SCALE_UE8M0_F32 ||
         (w_scale_kind != WZ_WSCALE_F32 && w_scale_kind != WZ_WSCALE_E8M0))
       return set_error(WZ_EINVAL, "fp8_gemm_packed_pair: bad scale kinds %d/%d", act_scale_kind, w_scale_kind);
@@ -761,7 +976,11 @@ extern "C" int wz_fp8_gemm_packed_pair(const void* a_e4m3, const void* a_s, cons
                          nullptr, static_cast<uint16_t*>(c0_bf16), static_cast<uint16_t*>(c1_bf16), N0, M, N, K,
                          act_scale_kind != WZ_SCALE_F32, stream);
   }
-  // outside the GEMV: the two weights one after the other (the packed tiles of
+  if (gemv_mt_serves(M, N, K) || tile_gemm_fits(M, N, K))
+    // the M-tiled GEMV and the tile GEMM write the columns past N0 to the second buffer
+    return gemm_packed("fp8_gemm_packed_pair", a_e4m3, a_s, w_packed, w_s, nullptr, c0_bf16, M, N, K, act_scale_kind,
+                       w_scale_kind, ws, ws_bytes, stream, static_cast<uint16_t*>(c1_bf16), N0);
+  // outside both: the two weights one after the other (the packed tiles of
   // rows N0.. and their block-scale rows start where the first weight's end)
   if (int rc = gemm_packed("fp8_gemm_packed_pair", a_e4m3, a_s, w_packed, w_s, nullptr, c0_bf16, M, N0, K,
                            act_scale_kind, w_scale_kind, ws, ws_bytes, stream))
@@ -818,14 +1037,14 @@ static int launch_norm_gemv1(const void* x, const uint16_t* b, const float* nw, 
     return set_error(WZ_EINVAL, "fp8_norm_linear_packed: M=%lld rows exceed the %d the fused norm serves at K=%lld",
                      (long long)M, GvNorm<W, NKB>::ROWS, (long long)K);
   const dim3 grid(unsigned(N / 16)), block(W * 64);
-  const size_t lds = gemv1_lds_bytes(M, K);
+  const size_t lds = gemv1_dyn_bytes(false, M, K, W, 1);
   const bool bp = w_kind == WZ_WSCALE_E8M0;
 #define WZ_NG1(AP, BP)                                                                                          \
   do {                                                                                                          \
     static int granted = 0;                                                                                     \
-    if (int rc = allow_lds(fp8_gemv1_kernel<W, NKB, 1, false, AP, BP, true>, lds, granted)) return rc;             \
-    WZ_LAUNCH("fp8_norm_gemv1", stream, (fp8_gemv1_kernel<W, NKB, 1, false, AP, BP, true>), grid, block, lds, x, nullptr, 0, \
-              w, w_s, nullptr, y, y_hi, int(n_split), int(M), int(N), int(K), nw, eps, b, hsum);               \
+    if (int rc = allow_lds(fp8_gemv1_kernel<W, NKB, 1, false, AP, BP, true, 1>, lds, granted)) return rc;             \
+    WZ_LAUNCH("fp8_norm_gemv1", stream, (fp8_gemv1_kernel<W, NKB, 1, false, AP, BP, true, 1>), grid, block, lds, x, nullptr, 0, \
+              w, w_s, nullptr, y, y_hi, int(n_split), int(M), int(N), int(K), nw, eps, b, hsum, 1);            \
   } while (0)
   if (pow2) {
     if (bp) WZ_NG1(true, true); else WZ_NG1(true, false);

@@ -932,31 +932,12 @@ __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws,
   }
 }
 
-// Workgroups are dispatched to the XCDs round-robin (block b to XCD b % 8),
-// each XCD with its own L2.  The routed blocks [d0, d0 + n) are renumbered so
-// that each XCD takes runs of 64 consecutive (M-tile, N-block) pairs (as many
-// as its CUs hold at once, two per CU): an M-tile's N-blocks then share its
-// gathered activation rows in one L2, and the M-tiles of a group read the same
-// weight tiles there.  Run j goes to XCD j % 8, so the many runs of a hot
-// expert spread over every XCD instead of piling onto one (one XCD had held
-// all 368 blocks of the hottest expert of a T = 2048 batch and ended 25 %
-// after the first).  The last, partial round of 8 runs is split contiguously.
-// A bijection on [d0, d0 + n) for any n (checked exhaustively on the CPU), so
-// only locality depends on the dispatch order.
-__device__ __forceinline__ int xcd_runs(int b, int d0, int n) {
-  constexpr int kXcds = 8, kRun = 64;
-  const int x = b % kXcds;
-  const int fx = d0 + ((x - d0) & (kXcds - 1));  // first routed block on XCD x
-  const int k = (b - fx) / kXcds;                // b's place among them
-  const int full = n / (kXcds * kRun);           // complete rounds of 8 runs
-  if (k < full * kRun) return ((k / kRun) * kXcds + x) * kRun + k % kRun;
-  int before = 0;  // blocks of the last round on the XCDs ahead of x
-  for (int y = 0; y < x; ++y) {
-    const int fy = d0 + ((y - d0) & (kXcds - 1));
-    before += (fy < d0 + n ? (d0 + n - fy + kXcds - 1) / kXcds : 0) - full * kRun;
-  }
-  return full * kXcds * kRun + before + (k - full * kRun);
-}
+// The routed blocks [d0, d0 + n) run through xcd_runs (common.h): each XCD takes
+// runs of 64 consecutive (M-tile, N-block) pairs, so an M-tile's N-blocks share
+// its gathered activation rows in one L2 and the M-tiles of a group read the same
+// weight tiles there; the many runs of a hot expert spread over every XCD (one
+// XCD had held all 368 blocks of the hottest expert of a T = 2048 batch and
+// ended 25 % after the first).
 
 // (M-tile, N-block) of routed block r, r < n_mt * nblk: groups of gm M-tiles
 // take their N-blocks in parts of gn.  A window of consecutive blocks (the
