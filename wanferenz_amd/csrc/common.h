@@ -139,6 +139,16 @@ __device__ __forceinline__ float row16_absmax(float v) {
   return __uint_as_float(m);
 }
 
+// absmax of 8 bf16 values (16 bytes), as an f32: the packed 16-bit integer max
+// of the sign-cleared bits (absmax's order, NaN above inf), then widened.
+__device__ __forceinline__ float bf16x8_absmax(const v4i& w) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  auto a = [&](int i) { return __builtin_bit_cast(u16x2, uint32_t(w[i]) & 0x7FFF7FFFu); };
+  const u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(a(0), a(1)),
+                                            __builtin_elementwise_max(a(2), a(3)));
+  return __uint_as_float(uint32_t(m.x > m.y ? m.x : m.y) << 16);
+}
+
 // ---------------------------------------------------------------- MFMA -------
 
 template <int FMT_A, int FMT_B>

@@ -38,12 +38,12 @@ struct MoeWs {
   float* xs;           // [T, D/128] its block scales
   uint8_t* hq;         // decode: [U_max*T + T, I] e4m3 act_quant(h) (rows (u, t), then shared t)
   float* hs;           // [U_max*T + T, I/128]
-  uint16_t* h;         // [P, I] bf16 (general path) / [U_max*T, I] rows (u, t) (decode path)
+  uint16_t* h;         // [P, I] bf16 (a routed (expert, token) at its pair row), then sh_h
   int32_t* mt_u;       // prefill M-tile table: active expert of tile
   int32_t* mt_row0;    //   first pair row of tile
   int32_t* mt_n;       //   rows in tile (<= 128)
   int32_t* n_mt;       //   number of tiles
-  uint16_t* sh_h;      // [T, I] bf16
+  uint16_t* sh_h;      // [T, I] bf16, = h + P * I
   uint16_t* out2;      // [P, D] bf16
   uint16_t* sh_out;    // [T, D] bf16
   size_t bytes;
@@ -54,7 +54,6 @@ static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 static inline MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base) {
   const int64_t E = d->n_experts, k = d->topk, P = T * k, D = d->dim, I = d->inter;
   const int64_t UT = T <= kDecodeMaxT ? (P < E ? P : E) * T : 0;  // decode tables only
-  const int64_t HR = UT > P ? UT : P;
   size_t off = 0;
   MoeWs w;
   auto take = [&](size_t bytes) {
@@ -89,8 +88,9 @@ static inline MoeWs moe_ws_layout(const wz_moe_desc* d, int64_t T, uint8_t* base
   w.mt_row0 = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * MT));
   w.mt_n = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * MT));
   w.n_mt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 64));
-  w.h = reinterpret_cast<uint16_t*>(take(2 * size_t(HR) * I));
-  w.sh_h = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * I));
+  // h: P pair rows, then the T shared rows (sh_h), one contiguous image
+  w.h = reinterpret_cast<uint16_t*>(take(2 * size_t(P + T) * I));
+  w.sh_h = w.h ? w.h + size_t(P) * I : nullptr;
   w.out2 = reinterpret_cast<uint16_t*>(take(2 * size_t(P) * D));
   w.sh_out = reinterpret_cast<uint16_t*>(take(2 * size_t(T) * D));
   w.bytes = off;

@@ -631,19 +631,16 @@ __global__ __launch_bounds__(kDecThreads) void w13_decode_kernel(wz_moe_desc d, 
   if (wave == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (qrow[i] >= 0) {
-        const int t = g * 4 + i;
-        ws.h[(int64_t(u) * T + t) * I + ft * 16 + nl] =
-            f32_to_bf16(wrow[i] * swiglu(acc[0][i], acc[1][i], d.swiglu_limit));
-      }
+      if (qrow[i] >= 0 && qrow[i] < T * d.topk)
+        ws.h[int64_t(qrow[i]) * I + ft * 16 + nl] = f32_to_bf16(wrow[i] * swiglu(acc[0][i], acc[1][i], d.swiglu_limit));
     }
   }
 }
 
 // ----------------------------------------------------------------- hquant ---
 
-// Row r < u_max*T: h row (u, t), quantised only when routed; row u_max*T + t:
-// the shared expert's row t.
+// hq row r < u_max*T: (active expert u, token t), quantised from h's pair row
+// umap[r] only when routed; row u_max*T + t: the shared expert's row t.
 // Routed experts' w1/w3 for the decode batch on persistent workgroups.
 //
 // Work item = (active expert u, 16 intermediate features ft): 64 KB of packed
@@ -750,8 +747,8 @@ __global__ __launch_bounds__(kDecThreads) void w13_stream_kernel(wz_moe_desc d, 
           us += r[((w * 2 + 1) * 4 + i) * kWave + lane];
         }
         const int t = g * 4 + i;
-        if (t < T && b.q[i] >= 0)
-          ws.h[(int64_t(b.u) * T + t) * I + b.ft * 16 + nl] = f32_to_bf16(b.wt[i] * swiglu(gs, us, d.swiglu_limit));
+        if (t < T && b.q[i] >= 0 && b.q[i] < T * d.topk)
+          ws.h[int64_t(b.q[i]) * I + b.ft * 16 + nl] = f32_to_bf16(b.wt[i] * swiglu(gs, us, d.swiglu_limit));
       }
     }
   };
@@ -790,12 +787,13 @@ __global__ __launch_bounds__(kDecThreads) void w13_stream_kernel(wz_moe_desc d, 
   }
 }
 
-__global__ __launch_bounds__(kDecThreads) void hquant_kernel(MoeWs ws, int T, int I, int u_max, bool pow2) {
+__global__ __launch_bounds__(kDecThreads) void hquant_kernel(MoeWs ws, int T, int k, int I, int u_max, bool pow2) {
   const int r = blockIdx.x, UT = u_max * T;
   const uint16_t* src;
   if (r < UT) {
-    if (r / T >= min(ws.n_active[0], u_max) || ws.umap[r] < 0) return;
-    src = ws.h + int64_t(r) * I;
+    const int q = ws.umap[r];  // h holds the (expert, token) row at its pair row
+    if (r / T >= min(ws.n_active[0], u_max) || q < 0 || q >= T * k) return;
+    src = ws.h + int64_t(q) * I;
   } else {
     src = ws.sh_h + int64_t(r - UT) * I;
   }
@@ -906,27 +904,48 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
 
 // ------------------------------------------------- w2 (A rows in LDS) ---
 //
-// The jobs of w2_combine_kernel (shared expert as two K halves, then each
-// active routed expert over the full K; one workgroup per 16 output columns),
-// with the A operand read from LDS instead of registers.  The workgroup first
-// copies into LDS, with buffer loads straight to LDS, every e4m3 h row it can
-// need: one per routed (expert, token) pair, at its pair row q < P,
-// then the T shared rows.  A wave's registers then hold only weight tiles: the
-// NS = I / 128 one-KB tile slots of its job are all in flight at once, and
-// while it computes job j the tiles of its next job (j + 16) are requested
-// slot by slot into the registers just consumed.
+// One workgroup per 16 output columns, with the A operand read from LDS.
+//
+// * The shared expert (FP8) is split over the 16 waves by K-block (wave w:
+//   K-block w, 2 KB of tiles and its scale).  Nothing about it depends on the
+//   routing, so its loads are the kernel's first: they stream while the
+//   routing tables load.
+// * The workgroup copies into LDS, act_quant-ed (torch_ops.py:33-49), every
+//   e4m3 h row it can need: one per routed (expert, token) pair, at its pair
+//   row q < P, then the T shared rows.
+// * The routed experts are the jobs: wave w takes active experts w, w + 16,
+//   ... over the full K (MXFP4).  A wave's registers hold only weight tiles:
+//   the NS = I / 128 one-KB tile slots of its job are in flight at once, and
+//   while it computes job j the tiles of job j + 16 are requested slot by slot
+//   into the registers just consumed.
+// * Every load instruction runs in every wave: a wave with no job (or no next
+//   job) re-reads one KB of the bank, which its L1 serves, and h chunks past
+//   the image clamp to its last one.  Counted waits (s_waitcnt vmcnt) then stay
+//   exact; with the loads behind branches the compiler waited for a whole batch
+//   of tiles before the first h chunk could be quantised.
+// * The image is built in passes of 8 chunks per thread.  The last pass
+//   requests its h chunks before the first half of the first job's tiles, so
+//   quantising it waits for the chunks alone; earlier passes (V4: T > 4) run
+//   with no tile in flight.  Before, a later pass's chunks were requested
+//   after the first job's 16 tile slots and waited for them (at T = 8 the
+//   image was ready at 18.6 us, the tiles' batch at ~10 us).
 constexpr int kW2LdsBytes = 152 * 1024;
 
-// LDS bytes of w2_lds_kernel: A rows, their scales, umap, row sources, active
-// ids, the per-token combine lists, the pair outputs and the shared halves.
+// LDS bytes of w2_lds_kernel: A rows, their scales, umap, active ids and
+// first pair rows, the per-token combine lists, the pair outputs and the
+// shared expert's per-wave K-block partials.
 __host__ __device__ inline int64_t w2_lds_bytes(int64_t T, int64_t k, int64_t I, int64_t u_max) {
   const int64_t P = T * k, R = P + T, KB = I / 128;
   return ((R * I + 1023) & ~int64_t(1023)) + ((R * KB * 4 + 255) & ~int64_t(255)) +
-         4 * (u_max * T + P + 2 * u_max + P + T + P * 16 + 2 * T * 16);
+         4 * (u_max * T + 2 * u_max + P + T + P * 16 + kW2Waves * T * 16);
 }
 
-// POW2: activation scales are powers of two (they ride in the MFMA).
-template <int NS, bool POW2>
+// POW2: activation scales are powers of two (they ride in the MFMA).  NQ: h
+// chunks per thread and pass of the image (2, 4 or 8; the host picks the
+// smallest that holds the image in one pass, else 8).  PF: more than one pass,
+// the next pass's chunks requested before the current pass is quantised.
+// The registers the image does not take hold the first job's early tiles.
+template <int NS, bool POW2, int NQ, bool PF>
 __global__ __launch_bounds__(kW2Threads) void w2_lds_kernel(wz_moe_desc d, MoeWs ws, int T, int u_max,
                                                             uint16_t* __restrict__ y) {
   __shared__ __align__(1024) uint8_t smem[kW2LdsBytes];
@@ -939,132 +958,179 @@ __global__ __launch_bounds__(kW2Threads) void w2_lds_kernel(wz_moe_desc d, MoeWs
   const int a_bytes = (R * I + 1023) & ~1023, as_bytes = (R * KB * 4 + 255) & ~255;
   float* as_s = reinterpret_cast<float*>(smem + a_bytes);           // [R][KB] scales of the A rows
   int* um_s = reinterpret_cast<int*>(smem + a_bytes + as_bytes);    // [UT] umap
-  int* src_s = um_s + UT;                                   // [P] hq row of pair q, -1: none
-  int* act_s = src_s + P;                                   // [u_max] active expert ids
+  int* act_s = um_s + UT;                                   // [u_max] active expert ids
   int* uf_s = act_s + u_max;                                // [u_max] first routed pair of expert u
   int* tp_s = uf_s + u_max;                                 // [P] tok_pos
   int* tn_s = tp_s + P;                                     // [T] tok_n
   float* out_s = reinterpret_cast<float*>(tn_s + T);        // [P][16] routed pair outputs
-  float* sh_s = out_s + P * 16;                             // [2][T][16] shared K halves
+  float* sh_s = out_s + P * 16;                             // [16 waves][T][16] shared K-block partials
 
-  // ---- routing tables into LDS, and the inverse of umap (pair -> hq row) ----
-  const int n_act = min(ws.n_active[0], u_max);
-  for (int i = tid; i < UT; i += kW2Threads) um_s[i] = ws.umap[i];
-  for (int i = tid; i < u_max; i += kW2Threads) {
-    act_s[i] = clampi(ws.active[i], 0, E - 1);
-    uf_s[i] = P;
-  }
-  for (int i = tid; i < P; i += kW2Threads) {
-    src_s[i] = -1;
-    tp_s[i] = clampi(ws.tok_pos[i], 0, P - 1);
-  }
-  for (int i = tid; i < T; i += kW2Threads) tn_s[i] = clampi(ws.tok_n[i], 0, k);
-  __syncthreads();
-  for (int i = tid; i < UT; i += kW2Threads) {
-    const int q = um_s[i];
-    if (q >= 0 && q < P) {
-      src_s[q] = i;
-      atomicMin(&uf_s[i / T], q);
-    }
-  }
-  __syncthreads();
+  // Order of requests: the routing tables, the h rows of the image (two passes'
+  // worth), the shared expert's K-block; the first job's tiles only once the
+  // image is in LDS.  Loads complete in issue order and every CU serves a
+  // bounded number of them at once, so a load requested behind a batch of
+  // tiles waits for the batch: with the tiles requested first, the image was
+  // ready at 10 / 14 us (T = 1 / 4) instead of about 2.
 
-  // ---- jobs: 0 .. n_act - 1 routed expert u = job, then the shared expert's
-  // two K halves (so a shared half is always a wave's last job).  Slot s of
-  // any job is at tiles_of(job) + s KB: a shared K half is KB / 2 FP8 tiles of
-  // 2 KB, the same NS one-KB slots.  The shared halves' scales are read per
-  // K-block; scales_of gives them a harmless in-range address. ----
-  const int nj = n_act + 2;
-  auto tiles_of = [&](int job) {
-    return job < n_act
-               ? static_cast<const uint8_t*>(d.w2p) + (int64_t(act_s[job]) * DT + dt) * KB * 1024 + lane * 16
-               : static_cast<const uint8_t*>(d.sh2p) + (int64_t(dt) * KB + (job - n_act) * (KB / 2)) * 2048 +
-                     lane * 16;
+  // Buffer loads: a lane whose offset is past num_records reads zeros and
+  // makes no memory request, so every thread issues every load with no lane
+  // re-reading another's address.
+  auto rs_of = [](const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), short(0), bytes, 0x00020000);
   };
-  auto scales_of = [&](int job) {
-    return static_cast<const uint32_t*>(d.w2p_s) +
-           (job < n_act ? (int64_t(act_s[job]) * DT + dt) * KG * 64 : int64_t(0)) + lane;
+  auto bload_i32 = [&](__amdgpu_buffer_rsrc_t r) {
+    return __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(r, tid * 4, 0, 0));
   };
-  v4i w[NS];
-  uint32_t sc[KG];
-  int j = wave;
+  // ---- the routing tables: one load per thread and table (the host keeps
+  // u_max * T within one load per thread) ----
+  const int um_v = bload_i32(rs_of(ws.umap, UT * 4));
+  const int act_v = bload_i32(rs_of(ws.active, u_max * 4));
+  const int tp_v = bload_i32(rs_of(ws.tok_pos, P * 4));
+  const int tn_v = bload_i32(rs_of(ws.tok_n, T * 4));
+  const int nact_v = ws.n_active[0];
+
   // ---- A rows: act_quant (torch_ops.py:33-49, the arithmetic of quant_row)
-  // of the bf16 h row of every routed pair and of the T shared rows, into LDS
-  // as e4m3 codes and block scales.  A 16-lane group takes one 128-block (8
-  // elements per lane), kQ 16-byte chunks per thread in the first pass and 4
-  // in later ones.  The first pass's loads go out before this wave's first
-  // tiles, so its quantisation waits for them alone; later passes (T > 4 at
-  // the V4 shape) queue behind the tiles.  Then the first job's scales and tiles, and the
-  // MFMAs start as the tiles land. ----
-  constexpr int kQ = 8;
+  // of the bf16 h rows, into LDS as e4m3 codes and block scales.  The image is
+  // h's first R rows: row q < P is pair row q (the w1/w3 launch stores a
+  // routed (expert, token) at its pair row; a row no pair owns holds stale
+  // values and is never read as an operand), rows P .. P + T - 1 the shared
+  // rows (sh_h).  A 16-lane group takes one 128-block (8 elements per lane),
+  // kQ chunks per thread and pass; the next pass's chunks are requested before
+  // the current pass is quantised.  Chunks past the image are out of the
+  // buffer's range: zeros, no request, not stored. ----
   constexpr int CPR = I / 8;  // 16-byte chunks per row
+  constexpr int kQ = NQ;
   const int nch = R * CPR;
-  auto h_chunk = [&](int c) {  // a pair with no row (a repeated expert) reads shared row 0
-    const int cc = min(c, nch - 1), row = cc / CPR, off = (cc % CPR) * 8;
-    const int src = row < P ? src_s[row] : -1;
-    const uint16_t* base = row < P ? (src >= 0 ? ws.h + int64_t(src) * I : ws.sh_h) : ws.sh_h + int64_t(row - P) * I;
-    return load16(base + off);
+  const __amdgpu_buffer_rsrc_t h_rs = rs_of(ws.h, nch * 16);
+  // chunk c_base + tid; the whole offset in the lane's offset register (the
+  // range check covers that one, not the scalar offset)
+  auto h_chunk = [&](int c_base) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(h_rs, (c_base + tid) * 16, 0, 0));
   };
-  auto quant_pass = [&](int c0, const auto& hv) {
-    constexpr int n = sizeof(hv) / sizeof(hv[0]);
+  // Chunks wholly past the image are skipped (a wave-uniform test).  In a
+  // wave whose blocks are all finite the clamp to +-448 is left out: with a
+  // power-of-two scale s >= amax / 448, |x / s| <= 448 already.
+  auto quant_pass = [&](int c0, const v4i (&hv)[kQ]) {
 #pragma unroll
-    for (int i = 0; i < n; ++i) {
-      const int c = c0 + i * kW2Threads + tid;  // a 16-lane group: one 128-block of one row
+    for (int i = 0; i < kQ; ++i) {
+      const int cb = c0 + i * kW2Threads;
+      if (cb >= nch) continue;
+      const int c = cb + tid;
+      const float amax = row16_absmax(bf16x8_absmax(hv[i]));
+      const ActScale sc = act_scale(amax, POW2);
       float f[8];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         f[2 * q] = bf16lo(uint32_t(hv[i][q]));
         f[2 * q + 1] = bf16hi(uint32_t(hv[i][q]));
       }
-      float amax = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) amax = absmax(amax, f[e]);
-      amax = wave_absmax_xor(amax, 1);
-      amax = wave_absmax_xor(amax, 2);
-      amax = wave_absmax_xor(amax, 4);
-      amax = wave_absmax_xor(amax, 8);
-      const ActScale sc = act_scale(amax, POW2);
+      uint32_t lo, hi;
+      if (POW2 && __ballot(!is_finite_f32(amax)) == 0ull) {
+        lo = pack_fp8x4(f[0] * sc.inv, f[1] * sc.inv, f[2] * sc.inv, f[3] * sc.inv);
+        hi = pack_fp8x4(f[4] * sc.inv, f[5] * sc.inv, f[6] * sc.inv, f[7] * sc.inv);
+      } else {
+        lo = pack_fp8x4(quant_div(f[0], sc, POW2), quant_div(f[1], sc, POW2), quant_div(f[2], sc, POW2),
+                        quant_div(f[3], sc, POW2));
+        hi = pack_fp8x4(quant_div(f[4], sc, POW2), quant_div(f[5], sc, POW2), quant_div(f[6], sc, POW2),
+                        quant_div(f[7], sc, POW2));
+      }
       if (c < nch) {
         const int row = c / CPR, off = (c % CPR) * 8;
-        const uint32_t lo = pack_fp8x4(quant_div(f[0], sc, POW2), quant_div(f[1], sc, POW2),
-                                       quant_div(f[2], sc, POW2), quant_div(f[3], sc, POW2));
-        const uint32_t hi = pack_fp8x4(quant_div(f[4], sc, POW2), quant_div(f[5], sc, POW2),
-                                       quant_div(f[6], sc, POW2), quant_div(f[7], sc, POW2));
         *reinterpret_cast<uint2*>(smem + row * I + off) = make_uint2(lo, hi);
         if ((lane & 15) == 0) as_s[row * KB + off / 128] = sc.s;
       }
     }
   };
-  {
-    v4i hv[kQ];
+  v4i hv[kQ], hn[PF ? kQ : 1];
 #pragma unroll
-    for (int i = 0; i < kQ; ++i) hv[i] = h_chunk(i * kW2Threads + tid);
-    // the first job's tiles in two halves around the first pass (registers)
-    const uint8_t* base = j < nj ? tiles_of(j) : nullptr;
-    if (j < nj) {
-      const uint32_t* st = scales_of(j);
+  for (int i = 0; i < kQ; ++i) hv[i] = h_chunk(i * kW2Threads);
+  if constexpr (PF) {
 #pragma unroll
-      for (int c = 0; c < KG; ++c) sc[c] = st[c * 64];
-#pragma unroll
-      for (int s = 0; s < NS / 2; ++s) w[s] = load16_nt(base + s * 1024);
-    }
-    quant_pass(0, hv);
-    if (j < nj) {
-#pragma unroll
-      for (int s = NS / 2; s < NS; ++s) w[s] = load16_nt(base + s * 1024);
-    }
-    // later passes run with every tile slot live: 4 chunks per thread
-    for (int c0 = kQ * kW2Threads; c0 < nch; c0 += 4 * kW2Threads) {
-      v4i h4[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) h4[i] = h_chunk(c0 + i * kW2Threads + tid);
-      quant_pass(c0, h4);
-    }
+    for (int i = 0; i < kQ; ++i) hn[i] = h_chunk((kQ + i) * kW2Threads);
   }
-  // every thread's LDS writes are done (a bare barrier: __syncthreads' fence
-  // would also wait for the tiles)
+
+  // ---- the shared expert's K-block of this wave: tiles and block scale.
+  // Waves past KB re-read K-block KB - 1 and skip its MFMA.  Both scale kinds'
+  // loads are issued (the unused one reads the array's first element) and
+  // selected, so no load sits behind a branch. ----
+  const int kb_s = min(wave, KB - 1);
+  const uint8_t* sh_tile = static_cast<const uint8_t*>(d.sh2p) + (int64_t(dt) * KB + kb_s) * 2048 + lane * 16;
+  const v4i sw0 = load16_nt(sh_tile), sw1 = load16_nt(sh_tile + 1024);
+  const int sidx = (n0 >> 7) * KB + kb_s;
+  const bool sh_e8 = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  const uint8_t sh_b = static_cast<const uint8_t*>(d.sh_w2_s)[sh_e8 ? sidx : 0];
+  const float sh_f = static_cast<const float*>(d.sh_w2_s)[sh_e8 ? 0 : sidx];
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- routed job u: buffer resources over expert e's tiles and scales,
+  // empty (num_records 0: the loads return zeros without a memory request)
+  // when there is no such job, so a wave with no job issues the same
+  // instructions ----
+  auto tiles_rs = [&](int e, bool ok) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(static_cast<const uint8_t*>(d.w2p) + (int64_t(e) * DT + dt) * KB * 1024), short(0),
+        ok ? KB * 1024 : 0, 0x00020000);
+  };
+  auto scales_rs = [&](int e, bool ok) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(static_cast<const uint32_t*>(d.w2p_s) + (int64_t(e) * DT + dt) * KG * 64), short(0),
+        ok ? KG * 256 : 0, 0x00020000);
+  };
+  // 16 bytes per lane, non-temporal (read once)
+  auto bload16 = [&](__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, off, 2));
+  };
+  auto bload4 = [&](__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, off, 0));
+  };
+  // ---- the first job (active expert `wave`): its id read here (one
+  // wave-uniform word), its scales and first kPre tile slots requested before
+  // the image is quantised; the rest after ----
+  const int n_act = min(nact_v, u_max);
+  constexpr int kPre = PF ? (NS < 2 ? NS : 2) : NQ <= 2 ? NS : NQ <= 4 ? (NS < 12 ? NS : 12) : (NS < 8 ? NS : 8);
+  v4i w[NS];
+  uint32_t sc[KG];
+  const bool ok0 = wave < n_act;
+  const int e0 = __builtin_amdgcn_readfirstlane(clampi(ws.active[min(wave, u_max - 1)], 0, E - 1));
+  const __amdgpu_buffer_rsrc_t t_rs0 = tiles_rs(e0, ok0), s_rs0 = scales_rs(e0, ok0);
+#pragma unroll
+  for (int c = 0; c < KG; ++c) sc[c] = bload4(s_rs0, c * 256);
+#pragma unroll
+  for (int s = 0; s < kPre; ++s) w[s] = bload16(t_rs0, s * 1024);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- the tables into LDS ----
+  if (tid < UT) um_s[tid] = um_v;
+  if (tid < u_max) {
+    act_s[tid] = clampi(act_v, 0, E - 1);
+    uf_s[tid] = P;
+  }
+  if (tid < P) tp_s[tid] = clampi(tp_v, 0, P - 1);
+  if (tid < T) tn_s[tid] = clampi(tn_v, 0, k);
+  // ---- the image, pass by pass ----
+  quant_pass(0, hv);  // out of the loop, so its waits cover its own chunks alone
+  for (int c0 = kQ * kW2Threads; c0 < nch; c0 += kQ * kW2Threads) {
+    if constexpr (PF) {
+#pragma unroll
+      for (int i = 0; i < kQ; ++i) hv[i] = hn[i];
+#pragma unroll
+      for (int i = 0; i < kQ; ++i) hn[i] = h_chunk(c0 + (kQ + i) * kW2Threads);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kQ; ++i) hv[i] = h_chunk(c0 + i * kW2Threads);
+    }
+    quant_pass(c0, hv);
+  }
+  // Bare barriers: __syncthreads' fence would wait for the shared tiles.
   __builtin_amdgcn_s_waitcnt(lgkmcnt_only(0));
   asm volatile("s_barrier" : : : "memory");
+  // the first routed pair row of each expert
+  if (tid < UT && um_v >= 0 && um_v < P) atomicMin(&uf_s[tid / T], um_v);
+  __builtin_amdgcn_s_waitcnt(lgkmcnt_only(0));
+  asm volatile("s_barrier" : : : "memory");
+
+#pragma unroll
+  for (int s = kPre; s < NS; ++s) w[s] = bload16(t_rs0, s * 1024);
 
   // A operand of K-block kk from LDS row `row`
   auto a_lds = [&](int row, int kk) {
@@ -1080,48 +1146,36 @@ __global__ __launch_bounds__(kW2Threads) void w2_lds_kernel(wz_moe_desc d, MoeWs
     return a;
   };
 
-  // Keeps slot s's MFMA ahead of the load that refills slot s: without it the
-  // MFMAs (pure) sink to the end of the job and every old tile stays live.
-  auto pin = [](v4f& acc) { asm volatile("" : "+v"(acc) : : "memory"); };
   const int trow = min(nl, T - 1);
-  // shared expert, K half h = job - n_act (FP8: one MFMA per two slots); a
-  // wave's last job, so nothing is refilled.  bpw: e8m0 weight scales (else float)
-  auto shared_half = [&](auto bpw) {
-    constexpr bool kBp = decltype(bpw)::value;
-    const int h = j - n_act;
-    const int kb0 = h * (KB / 2), lrow = P + trow;
-    const int64_t sbase = int64_t(n0 >> 7) * KB;
+  // ---- the shared expert's K-block (FP8: one MFMA over its two slots) ----
+  {
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < NS; s += 2) {
-      const int kk = kb0 + s / 2;
-      int se;
-      float sf;
-      fp8_wscale(d.sh_w2_s, sbase + kk, kBp ? WZ_WSCALE_E8M0 : WZ_WSCALE_F32, se, sf);
-      const AOp a = a_lds(lrow, kk);
-      const v8i wb = v8i{w[s][0], w[s][1], w[s][2], w[s][3], w[s + 1][0], w[s + 1][1], w[s + 1][2], w[s + 1][3]};
-      mma_step<kFmtFp8, kFmtFp8>(acc, a, wb, se, sf, POW2, kBp, lane);
+    if (wave < KB) {
+      const AOp a = a_lds(P + trow, kb_s);
+      const v8i wb = v8i{sw0[0], sw0[1], sw0[2], sw0[3], sw1[0], sw1[1], sw1[2], sw1[3]};
+      mma_step<kFmtFp8, kFmtFp8>(acc, a, wb, sh_e8 ? int(sh_b) : kE8m0One, sh_e8 ? 1.0f : sh_f, POW2, sh_e8, lane);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (g * 4 + i < T) sh_s[(h * T + g * 4 + i) * 16 + nl] = acc[i];
-  };
-  // routed job j (expert u = j, full K); refill: request job j + 16's scales
-  // and tiles, slot s right after slot s's MFMA
-  auto routed = [&](auto refill) {
-    const int u = j;
+      if (g * 4 + i < T) sh_s[(wave * T + g * 4 + i) * 16 + nl] = acc[i];
+  }
+
+  // Keeps slot s's MFMA ahead of the load that refills slot s: without it the
+  // MFMAs (pure) sink to the end of the job and every old tile stays live.
+  auto pin = [](v4f& acc) { asm volatile("" : "+v"(acc) : : "memory"); };
+  // routed job u (expert u, full K); requests job u + 16's scales and tiles,
+  // slot s right after slot s's MFMA
+  for (int u = wave; u < n_act; u += kW2Waves) {
     const int q = um_s[u * T + trow], qf = uf_s[u];
     // a token not routed to u reads u's first routed row (its output row is
     // dropped below), so the wave reads few distinct LDS rows
     const int lrow = (q >= 0 && q < P) ? q : (qf < P ? qf : P + trow);
-    const uint8_t* nb = nullptr;
+    const int un = u + kW2Waves;
+    const int en = __builtin_amdgcn_readfirstlane(act_s[un < n_act ? un : 0]);
+    const __amdgpu_buffer_rsrc_t t_rs = tiles_rs(en, un < n_act), s_rs = scales_rs(en, un < n_act);
     uint32_t scn[KG];
-    if constexpr (decltype(refill)::value) {
-      const uint32_t* st = scales_of(j + kW2Waves);
 #pragma unroll
-      for (int c = 0; c < KG; ++c) scn[c] = st[c * 64];
-      nb = tiles_of(j + kW2Waves);
-    }
+    for (int c = 0; c < KG; ++c) scn[c] = bload4(s_rs, c * 256);
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -1130,12 +1184,10 @@ __global__ __launch_bounds__(kW2Threads) void w2_lds_kernel(wz_moe_desc d, MoeWs
       const v8i wb = v8i{w[s][0], w[s][1], w[s][2], w[s][3], 0, 0, 0, 0};
       mma_step<kFmtFp8, kFmtFp4>(acc, a, wb, es, 1.0f, POW2, true, lane);
       pin(acc);
-      if constexpr (decltype(refill)::value) w[s] = load16_nt(nb + s * 1024);
+      w[s] = bload16(t_rs, s * 1024);
     }
-    if constexpr (decltype(refill)::value) {
 #pragma unroll
-      for (int c = 0; c < KG; ++c) sc[c] = scn[c];
-    }
+    for (int c = 0; c < KG; ++c) sc[c] = scn[c];
     // each linear's output is bf16 (architecture.py:741)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1143,17 +1195,6 @@ __global__ __launch_bounds__(kW2Threads) void w2_lds_kernel(wz_moe_desc d, MoeWs
       const int qo = t < T ? um_s[u * T + t] : -1;
       if (qo >= 0 && qo < P) out_s[qo * 16 + nl] = bf16_round(acc[i]);
     }
-  };
-
-  // every job with a successor is routed (the shared halves come last)
-  for (; j + kW2Waves < nj; j += kW2Waves) routed(std::true_type{});
-  if (j < n_act) {
-    routed(std::false_type{});
-  } else if (j < nj) {
-    if (d.shared_w_scale_kind == WZ_WSCALE_E8M0)
-      shared_half(std::true_type{});
-    else
-      shared_half(std::false_type{});
   }
   __syncthreads();
   if (tid < 16 * T) {
@@ -1161,7 +1202,10 @@ __global__ __launch_bounds__(kW2Threads) void w2_lds_kernel(wz_moe_desc d, MoeWs
     const int n = tn_s[t];
     float acc = 0.0f;
     for (int jj = 0; jj < n; ++jj) acc += out_s[tp_s[t * k + jj] * 16 + col];
-    acc += bf16_round(sh_s[t * 16 + col] + sh_s[(T + t) * 16 + col]);
+    // the shared expert: its K-blocks' partials in K order, one bf16 output
+    float sh = 0.0f;
+    for (int w2 = 0; w2 < min(KB, kW2Waves); ++w2) sh += sh_s[(w2 * T + t) * 16 + col];
+    acc += bf16_round(sh);
     y[int64_t(t) * D + n0 + col] = f32_to_bf16(acc);
   }
 }
@@ -1421,13 +1465,16 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
   // T >= 6 and w2_combine_kernel below.  w2_lds_kernel quantises h itself.
   const int nkb2 = I / 512, kb2 = I / 128;
   // K-blocks of 2 .. 16 (16 only with power-of-two activation scales: the
-  // float-scale variant spills there) and the LDS image fits
+  // float-scale variant spills there), the LDS image fits, the (expert, token)
+  // map takes one load per thread, and the shared expert's w2 scale array
+  // holds at least one 4-byte word (both kinds' first elements are read)
   const bool p2 = d->act_scale_kind != WZ_SCALE_F32;
   const bool w2l = I % 128 == 0 && (kb2 == 2 || kb2 == 4 || kb2 == 8 || (kb2 == 16 && p2)) &&
-                   w2_lds_bytes(T, k, I, u_max) <= kW2LdsBytes;
+                   w2_lds_bytes(T, k, I, u_max) <= kW2LdsBytes && int64_t(u_max) * T <= kW2Threads &&
+                   (D / 128) * kb2 >= 4;
   if (!w2l && (only < 0 || only == WZ_STAGE_HQUANT)) {
     WZ_LAUNCH("moe_hquant", stream, hquant_kernel, dim3(unsigned(u_max * T + T)), dim3(kDecThreads), 0, w, int(T),
-              I, u_max, d->act_scale_kind != WZ_SCALE_F32);
+              k, I, u_max, d->act_scale_kind != WZ_SCALE_F32);
     if (int rc = check_launch("moe hquant")) return rc;
   }
   const bool w2s = !w2l && T >= 6 && I % 512 == 0 && (nkb2 == 1 || nkb2 == 2 || nkb2 == 4) && D % 64 == 0 &&
@@ -1436,15 +1483,25 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
     if (w2l) {
       const dim3 grid{unsigned(D / 16)};
       uint16_t* yo = static_cast<uint16_t*>(y);
-#define WZ_W2L(NS)                                                                                            \
-  do {                                                                                                        \
-    if (p2)                                                                                                   \
-      WZ_LAUNCH("moe_w2", stream, (w2_lds_kernel<NS, true>), grid, dim3(kW2Threads), 0, *d, w, int(T), u_max, yo); \
-    else                                                                                                      \
-      WZ_LAUNCH("moe_w2", stream, (w2_lds_kernel<NS, false>), grid, dim3(kW2Threads), 0, *d, w, int(T), u_max, yo); \
+      const int64_t cpt = (int64_t(T) * (k + 1) * (I / 8) + kW2Threads - 1) / kW2Threads;  // h chunks per thread
+#define WZ_W2L_P(NS, P2, NQ, PF) \
+  WZ_LAUNCH("moe_w2", stream, (w2_lds_kernel<NS, P2, NQ, PF>), grid, dim3(kW2Threads), 0, *d, w, int(T), u_max, yo)
+#define WZ_W2L(NS)                    \
+  do {                                \
+    if (p2)                           \
+      WZ_W2L_P(NS, true, 8, false);   \
+    else                              \
+      WZ_W2L_P(NS, false, 8, false);  \
   } while (0)
       if (kb2 == 16) {
-        WZ_LAUNCH("moe_w2", stream, (w2_lds_kernel<16, true>), grid, dim3(kW2Threads), 0, *d, w, int(T), u_max, yo);
+        if (cpt <= 2)
+          WZ_W2L_P(16, true, 2, false);
+        else if (cpt <= 4)
+          WZ_W2L_P(16, true, 4, false);
+        else if (cpt <= 8)
+          WZ_W2L_P(16, true, 8, false);
+        else
+          WZ_W2L_P(16, true, 8, true);
       } else if (kb2 == 8) {
         WZ_W2L(8);
       } else if (kb2 == 4) {
@@ -1453,6 +1510,7 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
         WZ_W2L(2);
       }
 #undef WZ_W2L
+#undef WZ_W2L_P
     } else if (w2s) {
       const int64_t items = int64_t(u_max) * (D / 64), cus = cu_count();
       const dim3 grid(unsigned(D / 64 + std::min<int64_t>(items, std::max<int64_t>(cus, std::min<int64_t>(2 * cus, items / 8)))));
