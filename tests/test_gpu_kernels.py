@@ -576,14 +576,15 @@ def test_pair_outputs_are_checked(gpu):
 
 
 @pytest.mark.parametrize("with_b", [False, True])
-@pytest.mark.parametrize("M,K", [(4, 4096), (3, 1024)])
-def test_fused_norm_pair_float_act_scales(gpu, with_b, M, K):
+@pytest.mark.parametrize("M,K,N0", [(4, 4096, 256), (3, 1024, 256), (3, 1024, 8192)])
+def test_fused_norm_pair_float_act_scales(gpu, with_b, M, K, N0):
     """norm_gemm with non-power-of-two activation scales (scale_fmt None, float32
     scales) = rms_norm_quant / add_rms_norm_quant with the same scales, then the
-    pair's GEMV, bit for bit."""
+    pair's GEMV, bit for bit; N0 = 8192 at K = 1024: more than 512 tiles (the
+    projection of the normed query latent is that wide)."""
     from wanferenz_amd import stage
 
-    w0, s0 = stage.synthetic_linear(256, K, K + 21, gpu, fp32_scales=True)
+    w0, s0 = stage.synthetic_linear(N0, K, K + 21, gpu, fp32_scales=True)
     w1, s1 = stage.synthetic_linear(128, K, K + 22, gpu, fp32_scales=True)
     pair = kernels.PackedFp8Pair(w0, s0, w1, s1, None)
     x = bf16_tensor(_x(M * 7 + K, M, K), gpu).view(M, K)

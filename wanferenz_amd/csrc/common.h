@@ -155,6 +155,12 @@ template <int FMT_A, int FMT_B>
 __device__ __forceinline__ v4f mfma_scaled(const v8i& a, const v8i& b, v4f c, int sa, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, 0, sa, 0, sb);
 }
+// The same with B's e8m0 scale byte OPB (0..3) of the dword sb: the MFMA
+// selects it, no shift or mask on the VALU.
+template <int FMT_A, int FMT_B, int OPB>
+__device__ __forceinline__ v4f mfma_scaled_bsel(const v8i& a, const v8i& b, v4f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, 0, sa, OPB, sb);
+}
 
 // ---------------------------------------------------------------- loads ------
 
@@ -207,6 +213,8 @@ __device__ __forceinline__ void load_lds_4(__amdgpu_buffer_rsrc_t rsrc, uint32_t
 // s_waitcnt immediate that waits for vmcnt <= n only (n < 64; gfx9 encoding:
 // vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// ... vmcnt <= n and lgkmcnt = 0.
+constexpr int vmcnt_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
 // ... and one that waits for lgkmcnt <= n only (n < 16).
 constexpr int lgkmcnt_only(int n) { return 15 | (3 << 14) | (7 << 4) | (n << 8); }
 

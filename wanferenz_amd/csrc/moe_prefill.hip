@@ -26,11 +26,6 @@ namespace wz {
 constexpr int kPM = kPrefillTileRows;  // pair rows per M-tile (64: the tile bodies then fit two
                                        // workgroups per CU, twice the weight bytes in flight)
 constexpr int kPThreads = 256;    // 4 waves
-// K-steps of weights and A rows in flight ahead of the one computed (kStages
-// + 1 LDS buffers hold the staged A tiles).  Three: four for w1/w3 measured
-// the same (T = 2048 994 vs 997 us) at 256 VGPRs, and w2 then lost its third
-// workgroup per CU.
-constexpr int stages_of(int) { return 3; }
 
 // ------------------------------------------------------------------- gate ---
 //
@@ -555,6 +550,25 @@ __device__ __forceinline__ bool tile_of(const MoeWs& ws, int mt, bool dense, int
 // in distinct banks; the rows' scales at as_s[(r / 16) * 64 + r % 16].
 __device__ __forceinline__ int a_swz(int row) { return (row >> 1) & 7; }
 
+// The K pipeline's four A buffers (rows and their scales), each its own LDS
+// array: the direct loads into them are the compiler's own buffer-to-LDS
+// builtin, so it counts them among the outstanding loads and, the arrays being
+// distinct objects, waits before a read of one buffer only for the loads into
+// that one.  K-step kb lives in buffer kb % 4 (the K loop is unrolled by four,
+// so every index is a constant).
+constexpr int kNBuf = 4;
+struct StageBufs {
+  uint8_t* a[kNBuf];
+  float* s[kNBuf];
+};
+typedef __attribute__((address_space(3))) void lds_void;
+// declares the four buffers (distinct LDS arrays) and a StageBufs L over them
+#define WZ_STAGE_BUFS(L)                                                                          \
+  __shared__ __align__(1024) uint8_t L##_a0[kPM * 128], L##_a1[kPM * 128], L##_a2[kPM * 128],      \
+      L##_a3[kPM * 128];                                                                          \
+  __shared__ __align__(16) float L##_s0[256], L##_s1[256], L##_s2[256], L##_s3[256];               \
+  const StageBufs L = {{L##_a0, L##_a1, L##_a2, L##_a3}, {L##_s0, L##_s1, L##_s2, L##_s3}}
+
 __device__ __forceinline__ AOp a_from_lds(const uint8_t* a_s, const float* as_s, int row, int g, bool pow2) {
   AOp a;
   const uint8_t* p = a_s + row * 128;
@@ -588,10 +602,11 @@ struct BTiles {
 // A wave owns NTW weight tiles of 16 output columns (routed w13: 4, i.e. 2
 // feature tiles x {w1, w3}; routed w2: 2 column tiles; shared FP8 tiles are
 // twice the bytes, so 2), and one A operand read from LDS feeds NTW MFMAs.
-// The K loop is software-pipelined kStages K-steps deep: while step kb
+// The K loop is software-pipelined three K-steps deep: while step kb
 // computes, the B tiles (registers) and the A rows (LDS, direct buffer loads
-// that need no registers) of steps kb+1 .. kb+kStages are in flight; A goes
-// through kNA = kStages + 1 LDS buffers with one barrier per step.
+// that need no registers) of steps kb+1 .. kb+3 are in flight; A goes through
+// the four StageBufs buffers and B through four register sets, with one
+// barrier per step.
 //
 // CHAIN: activation and weight scales are both powers of two, so they ride in
 // the MFMA's e8m0 scale operands and the accumulators chain over K; otherwise
@@ -602,8 +617,7 @@ struct BTiles {
 // the activation rows the N-blocks of an M-tile share.
 template <int MODE, bool CHAIN, int NM, bool KEEP>
 __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs& ws, int T, const TileRows& tr,
-                                               int nt, uint8_t (*a_s)[kPM * 128], float (*as_s)[256],
-                                               float (*am_s)[kPM]) {
+                                               int nt, const StageBufs& L, float (*am_s)[kPM]) {
   // DENSE: FP8 weights (the shared expert, an FP8 linear); DROWS: rows in
   // token order (no M-tile table)
   constexpr bool W13 = MODE < 2, DENSE = MODE == 1 || MODE == 3, DROWS = DENSE || MODE == 4;
@@ -612,7 +626,10 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
   // w2 2 (4 spilled registers at two workgroups per CU and measured 7 % slower);
   // FP8 shared tiles, twice the bytes, 2
   constexpr int NTW = (DENSE || MODE >= 2) ? 2 : 4;
-  constexpr int kStages = stages_of(MODE), kNA = kStages + 1;
+  // vector loads every K-step issues for certain: NTW weight tiles (fp4: a
+  // tile and its scale dword; FP8: two halves, the block scale possibly a
+  // scalar load) and the three direct A loads
+  constexpr int kStepLoads = 2 * NTW + 3;
   constexpr int CPW = W13 ? NTW / 2 : NTW;    // 16-column output tiles per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nl = lane & 15, g = lane >> 4;
@@ -665,14 +682,13 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
       W13 ? ws.xq : ws.hq, short(0), a_rows ? int(a_nrows * K) : 0, 0x00020000);
   const __amdgpu_buffer_rsrc_t s_rs = __builtin_amdgcn_make_buffer_rsrc(
       W13 ? ws.xs : ws.hs, short(0), a_rows ? int(a_nrows * KB * 4) : 0, 0x00020000);
-  const uint32_t a_lds = lds_addr(&a_s[0][0]), s_lds = lds_addr(&as_s[0][0]);
-  auto a_issue = [&](int kb) {
-    const uint32_t buf = uint32_t(kb % kNA);
+  // K-step kb into buffer buf (a constant wherever it is called)
+  auto a_issue = [&](int kb, int buf) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      load_lds_16(a_rs, __builtin_amdgcn_readfirstlane(a_lds + buf * (kPM * 128) + (2 * wave + i) * 1024), avo[i],
-                  uint32_t(kb) * 128u);
-    load_lds_4(s_rs, __builtin_amdgcn_readfirstlane(s_lds + (buf * 256 + wave * 64) * 4), svo, uint32_t(kb) * 4u);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_void*)(L.a[buf] + (2 * wave + i) * 1024), 16, int(avo[i]),
+                                               kb * 128, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rs, (lds_void*)(L.s[buf] + wave * 64), 4, int(svo), kb * 4, 0, 0);
   };
 
   auto wload = [](const uint8_t* p) { return KEEP ? load16(p) : load16_nt(p); };
@@ -737,83 +753,98 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
 #pragma unroll
     for (int m = 0; m < NM; ++m) acc[j][m] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int buf, const BTiles<NTW>& b, int kb) {
+  // K-step kb from buffer / register set buf = kb % 4
+  // (fp4 weights: the scale is byte buf of the packed dword, which the chained
+  // MFMA selects itself)
+  auto compute = [&](int buf, const BTiles<NTW>& b) {
     int e8[NTW];
 #pragma unroll
-    for (int j = 0; j < NTW; ++j) e8[j] = DENSE ? int(b.sw[j]) : int((b.sw[j] >> (8 * (kb & 3))) & 0xFFu);
+    for (int j = 0; j < NTW; ++j) e8[j] = DENSE || CHAIN ? int(b.sw[j]) : int((b.sw[j] >> (8 * buf)) & 0xFFu);
+    const int bsel = DENSE ? 0 : buf;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      const AOp a = a_from_lds(a_s[buf % kNA], as_s[buf % kNA], m * 16 + nl, g, CHAIN || a_pow2);
+      const AOp a = a_from_lds(L.a[buf], L.s[buf], m * 16 + nl, g, CHAIN || a_pow2);
 #pragma unroll
       for (int j = 0; j < NTW; ++j) {
         const v8i bv = DENSE ? v8i{b.lo[j][0], b.lo[j][1], b.lo[j][2], b.lo[j][3], b.hi[j][0], b.hi[j][1],
                                    b.hi[j][2], b.hi[j][3]}
                              : v8i{b.lo[j][0], b.lo[j][1], b.lo[j][2], b.lo[j][3], 0, 0, 0, 0};
-        if (CHAIN)
-          acc[j][m] = mfma_scaled<kFmtFp8, WF>(a.v, bv, acc[j][m], a.se8, e8[j]);
-        else
+        if (CHAIN) {
+          if (bsel == 0)
+            acc[j][m] = mfma_scaled_bsel<kFmtFp8, WF, 0>(a.v, bv, acc[j][m], a.se8, e8[j]);
+          else if (bsel == 1)
+            acc[j][m] = mfma_scaled_bsel<kFmtFp8, WF, 1>(a.v, bv, acc[j][m], a.se8, e8[j]);
+          else if (bsel == 2)
+            acc[j][m] = mfma_scaled_bsel<kFmtFp8, WF, 2>(a.v, bv, acc[j][m], a.se8, e8[j]);
+          else
+            acc[j][m] = mfma_scaled_bsel<kFmtFp8, WF, 3>(a.v, bv, acc[j][m], a.se8, e8[j]);
+        } else
           mma_step<kFmtFp8, WF>(acc[j][m], a, bv, e8[j], b.f[j], a_pow2, bp, lane);
       }
     }
   };
 
-  // Step kb (S = kStages): wait for B(kb) -- every register of it, so the wait
-  // covers the whole fetch -- then a barrier, compute from LDS buffer
-  // kb % (S + 1), then request B(kb + S) into the registers just used and
-  // A(kb + S) into the buffer read in step kb - 1 (every wave has passed this
-  // step's barrier, so none still reads it).  B(kb + S) goes out before
-  // A(kb + S), so A(kb) is
-  // the first load after B(kb): the compiler's wait for B(kb) counts only the
-  // loads it sees (the B fetches after it), every direct A load after B(kb)
-  // is among the loads it leaves outstanding too, and loads complete in
-  // order, so the oldest such loads -- A(kb) first -- have landed when it
-  // returns.  Every load is unconditional in the steady state, so those counts
-  // stay exact across the barriers.
-  auto b_touch = [](const BTiles<NTW>& b) {
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) {
-      asm volatile("" : : "v"(b.lo[j]), "v"(b.sw[j]));
-      if (DENSE) asm volatile("" : : "v"(b.hi[j]));
-      if (DENSE && !CHAIN) asm volatile("" : : "v"(b.f[j]));
-    }
-  };
-  auto step_sync = [&](const BTiles<NTW>& b) {
-    b_touch(b);
+  // Step kb (set / buffer i = kb % 4): wait until at most the loads of the
+  // (up to two) later K-steps already requested are outstanding -- loads
+  // complete in order, so B(kb) and this wave's rows of A(kb) have landed --
+  // then a barrier (every wave's rows of A(kb) are in LDS, and every wave has
+  // finished step kb - 1, whose buffer and register set are free), request
+  // K-step kb + 3 into them, and compute step kb.  The wait is the explicit
+  // one: the compiler's own waits for B(kb) and A(kb) come after the barrier.
+  // kStepLoads is a lower bound of each step's loads, so the count never
+  // lets one of step kb's loads still be outstanding.
+  // (lgkmcnt(0) too: this wave's LDS reads of step kb - 1 have returned
+  // before any wave may overwrite that buffer)
+  auto step_wait = [&](int ahead) {  // ahead: later K-steps requested (0..2)
+    __builtin_amdgcn_sched_barrier(0);
+    if (ahead >= 2)
+      __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(2 * kStepLoads));
+    else if (ahead == 1)
+      __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(kStepLoads));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0(0));
     asm volatile("s_barrier" : : : "memory");
   };
-  // the first kStages steps' loads, unconditionally (K-steps past the end
+  // the first three steps' loads, unconditionally (K-steps past the end
   // repeat the last one; nothing reads them): a load behind a branch would
   // leave the compiler unsure how many loads follow B(0) at the loop head, and
-  // it would drain them all there
-  BTiles<NTW> bt[kStages];
+  // it would drain them all there.  The fence after each step's loads keeps
+  // the compiler from merging the repeated fp4 scale-dword loads of steps 0..2
+  // (one dword holds four K-blocks' scales): every step then issues its
+  // kStepLoads, as the explicit waits count, and the loop head sees the same
+  // outstanding loads on entry as from the loop's own end.
+  BTiles<NTW> bt[kNBuf];
 #pragma unroll
-  for (int j = 0; j < kStages; ++j) {
+  for (int j = 0; j < kNBuf - 1; ++j) {
     b_fetch(bt[j], min(j, KB - 1));
-    a_issue(min(j, KB - 1));
+    a_issue(min(j, KB - 1), j);
+    asm volatile("" : : : "memory");
   }
   int kb = 0;
-  // steady state: every step refills (its K-step + kStages is in range)
-  for (; kb + 2 * kStages - 1 < KB; kb += kStages) {
+  // steady state: every step refills (its K-step + 3 is in range)
+  for (; kb + 7 <= KB; kb += kNBuf) {
 #pragma unroll
-    for (int i = 0; i < kStages; ++i) {
-      step_sync(bt[i]);
-      compute(kb + i, bt[i], kb + i);
+    for (int i = 0; i < kNBuf; ++i) {
+      step_wait(2);
+      b_fetch(bt[(i + 3) & 3], kb + i + 3);
+      a_issue(kb + i + 3, (i + 3) & 3);
       __builtin_amdgcn_sched_barrier(0);
-      b_fetch(bt[i], kb + i + kStages);
-      a_issue(kb + i + kStages);
+      compute(i, bt[i]);
     }
   }
-  // last K-steps
-  for (; kb < KB; kb += kStages) {
+  // last K-steps (kb is a multiple of four)
+  for (; kb < KB; kb += kNBuf) {
 #pragma unroll
-    for (int i = 0; i < kStages; ++i) {
-      if (kb + i >= KB) break;
-      step_sync(bt[i]);
-      compute(kb + i, bt[i], kb + i);
-      if (kb + i + kStages < KB) {
-        b_fetch(bt[i], kb + i + kStages);
-        a_issue(kb + i + kStages);
+    for (int i = 0; i < kNBuf; ++i) {
+      const int s = kb + i;
+      if (s >= KB) break;
+      step_wait(min(KB - 1 - s, 2));
+      if (s + 3 < KB) {
+        b_fetch(bt[(i + 3) & 3], s + 3);
+        a_issue(s + 3, (i + 3) & 3);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      compute(i, bt[i]);
     }
   }
 
@@ -911,24 +942,24 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
 // tiles of 16, so its MFMA loops carry no row branches.
 template <int MODE, bool CHAIN>
 __device__ __forceinline__ void gemm_tile(const wz_moe_desc& d, const MoeWs& ws, int T, int mt, int nt,
-                                          uint8_t (*a_s)[kPM * 128], float (*as_s)[256], float (*am_s)[kPM]) {
+                                          const StageBufs& L, float (*am_s)[kPM]) {
   TileRows tr;
   if (!tile_of(ws, mt, MODE == 1 || MODE == 3 || MODE == 4, T, T * d.topk, d.n_experts, tr)) return;
   static_assert(kPM == 64, "tile heights up to 4 row tiles");
   if (tr.keep) {
     if (tr.nrows <= 16)
-      gemm_tile_body<MODE, CHAIN, 1, true>(d, ws, T, tr, nt, a_s, as_s, am_s);
+      gemm_tile_body<MODE, CHAIN, 1, true>(d, ws, T, tr, nt, L, am_s);
     else if (tr.nrows <= 32)
-      gemm_tile_body<MODE, CHAIN, 2, true>(d, ws, T, tr, nt, a_s, as_s, am_s);
+      gemm_tile_body<MODE, CHAIN, 2, true>(d, ws, T, tr, nt, L, am_s);
     else
-      gemm_tile_body<MODE, CHAIN, 4, true>(d, ws, T, tr, nt, a_s, as_s, am_s);
+      gemm_tile_body<MODE, CHAIN, 4, true>(d, ws, T, tr, nt, L, am_s);
   } else {
     if (tr.nrows <= 16)
-      gemm_tile_body<MODE, CHAIN, 1, false>(d, ws, T, tr, nt, a_s, as_s, am_s);
+      gemm_tile_body<MODE, CHAIN, 1, false>(d, ws, T, tr, nt, L, am_s);
     else if (tr.nrows <= 32)
-      gemm_tile_body<MODE, CHAIN, 2, false>(d, ws, T, tr, nt, a_s, as_s, am_s);
+      gemm_tile_body<MODE, CHAIN, 2, false>(d, ws, T, tr, nt, L, am_s);
     else
-      gemm_tile_body<MODE, CHAIN, 4, false>(d, ws, T, tr, nt, a_s, as_s, am_s);
+      gemm_tile_body<MODE, CHAIN, 4, false>(d, ws, T, tr, nt, L, am_s);
   }
 }
 
@@ -964,19 +995,18 @@ __device__ __forceinline__ void tile_order(int r, int n_mt, int nblk, int gm, in
 template <bool W13, bool CR, bool CS>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void prefill_gemm_kernel(
     wz_moe_desc d, MoeWs ws, int T, int nblk, int nblk_dense, int dense_blocks, int gm, int gn) {
-  __shared__ __align__(1024) uint8_t a_s[stages_of(W13 ? 0 : 2) + 1][kPM * 128];
-  __shared__ __align__(16) float as_s[stages_of(W13 ? 0 : 2) + 1][256];
+  WZ_STAGE_BUFS(L);
   __shared__ float am_s[4][kPM];  // w1/w3 epilogue: each wave's row amax of its features
   const int b = blockIdx.x;
   if (b < dense_blocks) {
-    gemm_tile<W13 ? 1 : 3, CS>(d, ws, T, b / nblk_dense, b % nblk_dense, a_s, as_s, am_s);
+    gemm_tile<W13 ? 1 : 3, CS>(d, ws, T, b / nblk_dense, b % nblk_dense, L, am_s);
   } else {
     const int n = ws.n_mt[0] * nblk;  // routed blocks with work
     if (b - dense_blocks >= n) return;
     const int r = xcd_runs(b, dense_blocks, n);
     int mt, nt;
     tile_order(r, ws.n_mt[0], nblk, gm, gn, mt, nt);
-    gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, mt, nt, a_s, as_s, am_s);
+    gemm_tile<W13 ? 0 : 2, CR>(d, ws, T, mt, nt, L, am_s);
   }
 }
 
@@ -986,10 +1016,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
 template <bool CHAIN>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void dense_fp4_kernel(
     wz_moe_desc d, MoeWs ws, int M, int nblk) {
-  __shared__ __align__(1024) uint8_t a_s[stages_of(4) + 1][kPM * 128];
-  __shared__ __align__(16) float as_s[stages_of(4) + 1][256];
+  WZ_STAGE_BUFS(L);
   __shared__ float am_s[4][kPM];
-  gemm_tile<4, CHAIN>(d, ws, M, int(blockIdx.x) / nblk, int(blockIdx.x) % nblk, a_s, as_s, am_s);
+  gemm_tile<4, CHAIN>(d, ws, M, int(blockIdx.x) / nblk, int(blockIdx.x) % nblk, L, am_s);
 }
 
 int launch_act_quant(const void* x, int64_t rows, int64_t K, uint8_t* q, void* s, int kind, hipStream_t stream);
