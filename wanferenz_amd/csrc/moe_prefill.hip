@@ -26,6 +26,14 @@ namespace wz {
 constexpr int kPM = kPrefillTileRows;  // pair rows per M-tile (64: the tile bodies then fit two
                                        // workgroups per CU, twice the weight bytes in flight)
 constexpr int kPThreads = 256;    // 4 waves
+// 16-column weight tiles per wave of a tile-GEMM mode: 0 (routed w1/w3) 4, two
+// feature tiles x {w1, w3}; 1 and 3 (FP8 shared tiles, twice the bytes) 2;
+// 2 (routed w2) 2; 4 (a dense MXFP4 linear) 4.  Each A operand read from LDS
+// feeds NTW MFMAs, and the LDS reads of A bound the dense GEMM: at M = 2048
+// four tiles per wave took w1|w3 62.7 -> 55.2 us and w2 44.1 -> 40.9 us.  The
+// routed w2 keeps two: with the wider N-blocks a skewed T = 2048 batch has
+// half the workgroups and its w2 took 291 -> 301 us.
+constexpr int ntw_of(int mode) { return (mode == 0 || mode == 4) ? 4 : 2; }
 
 // ------------------------------------------------------------------- gate ---
 //
@@ -625,7 +633,7 @@ __device__ __forceinline__ void gemm_tile_body(const wz_moe_desc& d, const MoeWs
   // weight tiles per wave: routed w1/w3 4 (2 feature tiles x {w1, w3}); routed
   // w2 2 (4 spilled registers at two workgroups per CU and measured 7 % slower);
   // FP8 shared tiles, twice the bytes, 2
-  constexpr int NTW = (DENSE || MODE >= 2) ? 2 : 4;
+  constexpr int NTW = ntw_of(MODE);
   // vector loads every K-step issues for certain: NTW weight tiles (fp4: a
   // tile and its scale dword; FP8: two halves, the block scale possibly a
   // scalar load) and the three direct A loads
@@ -1041,7 +1049,7 @@ int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, 
   // column tiles of 16 per WG: routed w1/w3 4 waves x 2 feature tiles, routed w2
   // and the shared tiles 4 waves x 2
   const int nb13 = (I / 16 + 7) / 8, nb13d = (I / 16 + 3) / 4;
-  const int nb2 = (D / 16 + 7) / 8, nb2d = (D / 16 + 7) / 8;
+  const int nb2 = (D / 16 + 4 * ntw_of(2) - 1) / (4 * ntw_of(2)), nb2d = (D / 16 + 7) / 8;
   const bool cr = d->act_scale_kind != WZ_SCALE_F32;
   const bool cs = cr && d->shared_w_scale_kind == WZ_WSCALE_E8M0;
   const int Ti = int(T), dn13 = int(mt_dense * nb13d), dn2 = int(mt_dense * nb2d);
@@ -1136,7 +1144,7 @@ int launch_dense_fp4(const uint8_t* wp, const uint32_t* wp_s, const uint8_t* xq,
   w.hq = const_cast<uint8_t*>(xq);
   w.hs = const_cast<float*>(xs);
   w.sh_out = y;
-  const int nblk = int((N / 16 + 7) / 8);
+  const int nblk = int((N / 16 + 4 * ntw_of(4) - 1) / (4 * ntw_of(4)));
   const int blocks = int((M + kPM - 1) / kPM) * nblk;
   const dim3 grid{unsigned(blocks)}, blk{unsigned(kPThreads)};
   if (a_pow2) {
