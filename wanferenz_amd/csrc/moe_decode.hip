@@ -908,8 +908,8 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
 //
 // * The shared expert (FP8) is split over the 16 waves by K-block (wave w:
 //   K-block w, 2 KB of tiles and its scale).  Nothing about it depends on the
-//   routing, so its loads are the kernel's first: they stream while the
-//   routing tables load.
+//   routing, so its loads go out before any routed tile's and stream while the
+//   image is built; its partials meet in K order in the combine.
 // * The workgroup copies into LDS, act_quant-ed (torch_ops.py:33-49), every
 //   e4m3 h row it can need: one per routed (expert, token) pair, at its pair
 //   row q < P, then the T shared rows.
@@ -918,17 +918,21 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
 //   the NS = I / 128 one-KB tile slots of its job are in flight at once, and
 //   while it computes job j the tiles of job j + 16 are requested slot by slot
 //   into the registers just consumed.
-// * Every load instruction runs in every wave: a wave with no job (or no next
-//   job) re-reads one KB of the bank, which its L1 serves, and h chunks past
-//   the image clamp to its last one.  Counted waits (s_waitcnt vmcnt) then stay
-//   exact; with the loads behind branches the compiler waited for a whole batch
-//   of tiles before the first h chunk could be quantised.
-// * The image is built in passes of 8 chunks per thread.  The last pass
-//   requests its h chunks before the first half of the first job's tiles, so
-//   quantising it waits for the chunks alone; earlier passes (V4: T > 4) run
-//   with no tile in flight.  Before, a later pass's chunks were requested
-//   after the first job's 16 tile slots and waited for them (at T = 8 the
-//   image was ready at 18.6 us, the tiles' batch at ~10 us).
+// * Every load instruction runs in every wave, as a buffer load whose range
+//   is empty where there is nothing to read (a wave with no job or no next
+//   job, h chunks past the image): such a lane reads zeros without a memory
+//   request.  Counted waits (s_waitcnt vmcnt) then stay exact; with the loads
+//   behind branches the compiler waited for a whole batch of tiles before the
+//   first h chunk could be quantised, and clamped re-reads of one address
+//   piled onto one channel.
+// * Request order: the routing tables, the image's h chunks (NQ per thread,
+//   the host's smallest choice that holds the image in one pass, else 8 with
+//   the next pass requested ahead), the shared expert's K-block, then the
+//   first job's scales and its first tile slots.  The image is quantised while
+//   those are in flight; the rest of the first job's tiles follow the barrier.
+//   Loads return in issue order and a CU serves a bounded number at once, so
+//   the chunks queued behind a batch of tiles had waited for the batch (the
+//   image was ready at 10 / 14 us at T = 1 / 4, now at about 2).
 constexpr int kW2LdsBytes = 152 * 1024;
 
 // LDS bytes of w2_lds_kernel: A rows, their scales, umap, active ids and
