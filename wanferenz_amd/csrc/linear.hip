@@ -506,6 +506,226 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
   }
 }
 
+// Wave-tile GEMV, K = 128 KB (compile time), M <= 16: one 16-column tile per
+// WAVE over the whole K, W tiles per workgroup.  The workgroup quantises the
+// x rows into LDS once for its W tiles, exactly as fp8_gemv1_kernel does (the
+// dense bf16 passes, or with NORM the RMSNorm of x (+ b) in
+// rmsnorm_quant_kernel's thread mapping), and no partial crosses waves: a wave
+// computes the K slices of SL K-blocks (the K range one wave of the split
+// kernels owns) each from zero and folds them in K order, which is the split
+// kernels' wave-order sum, so every output has their bits.  Each wave requests
+// its tile's weights before the prologue.  Where a tile holds few bytes (K =
+// 1024: 16 KB) the split kernels spend a prologue and a cross-wave sum with a
+// barrier on every tile; here one prologue serves W tiles and the steady state
+// has no barrier.
+template <int W, int KB, int SL, int XP, bool AP2, bool BP2, bool NORM>
+__global__ __launch_bounds__(W * 64, 3) void fp8_gemv_wt_kernel(const void* __restrict__ x,
+                                                             const uint8_t* __restrict__ wp,
+                                                             const void* __restrict__ w_s,
+                                                             const uint16_t* __restrict__ res,
+                                                             uint16_t* __restrict__ y, uint16_t* __restrict__ y_hi,
+                                                             int n_split, int M, int N, const float* __restrict__ nw,
+                                                             float eps, const uint16_t* __restrict__ xb,
+                                                             uint16_t* __restrict__ hsum) {
+  static_assert(KB % SL == 0, "the slices cover K");
+  constexpr int K = KB * 128, ldk = K + 16;
+  // the norm's thread mapping: NWR waves (64 NWR threads) per row, thread t
+  // holding the 8-element chunks t + 256 j (GvNorm's, with W NKB = KB)
+  constexpr int NJ = (KB + 15) / 16, NWR = (KB + 3) / 4 < 4 ? (KB + 3) / 4 : 4, NROWS = W / NWR;
+  __shared__ float part[NORM ? NROWS : 1][4];
+  extern __shared__ __align__(16) uint8_t gv_lds[];
+  uint8_t* xq = gv_lds;
+  int2* xsc = reinterpret_cast<int2*>(gv_lds + M * ldk);
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nl = lane & 15, g = lane >> 4;
+  const int tiles = N / 16, item = int(blockIdx.x) * W + wave, it = item < tiles ? item : tiles - 1;
+  const int P = M * KB;
+
+  // ---- x: the loads of the prologue (fp8_gemv1_kernel's) ----
+  uint4 xr[NORM ? 1 : XP];
+  v4i nv[NORM ? NJ : 1], nbv[NORM ? NJ : 1], nwv[NORM ? NJ : 1][2];
+  if constexpr (NORM) {
+    const int nr = wave / NWR, rr = nr < M ? nr : M - 1, t = (wave % NWR) * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int64_t o = int64_t(rr) * K + (t + 256 * j) * 8;
+      nv[j] = load16(static_cast<const uint16_t*>(x) + o);
+      nbv[j] = load16((xb ? xb : static_cast<const uint16_t*>(x)) + o);
+      nwv[j][0] = load16(nw + (t + 256 * j) * 8);
+      nwv[j][1] = load16(nw + (t + 256 * j) * 8 + 4);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      int pr = 4 * (wave + j * W) + g;
+      pr = pr < P ? pr : P - 1;
+      const int r = pr / KB, kb = pr - r * KB;
+      xr[j] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + int64_t(r) * K + kb * 128 + nl * 8);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- this wave's tile: every K-block and its block scale ----
+  v8i w[KB];
+  int se[KB];
+  float sf[KB];
+  {
+    const uint8_t* t = wp + int64_t(it) * KB * 2048 + lane * 16;
+#pragma unroll
+    for (int q = 0; q < KB; ++q) {
+      const v4i lo = load16_nt(t + q * 2048), hi = load16_nt(t + q * 2048 + 1024);
+      w[q] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int q = 0; q < KB; ++q)
+      fp8_wscale(w_s, int64_t(it >> 3) * KB + q, BP2 ? WZ_WSCALE_E8M0 : WZ_WSCALE_F32, se[q], sf[q]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- the quantised rows into LDS (the arithmetic of fp8_gemv1_kernel) ----
+  if constexpr (NORM) {
+    const int nr = wave / NWR, nwi = wave % NWR, t = nwi * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) asm volatile("" ::"v"(nbv[j]));
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (xb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = bf16lo(uint32_t(nv[j][i])) + bf16lo(uint32_t(nbv[j][i]));
+          const float hi = bf16hi(uint32_t(nv[j][i])) + bf16hi(uint32_t(nbv[j][i]));
+          nv[j][i] = int(uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a0 = bf16lo(uint32_t(nv[j][i])), b0 = bf16hi(uint32_t(nv[j][i]));
+        ss += a0 * a0;
+        ss += b0 * b0;
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, kWave);
+    if (lane == 0 && nr < NROWS) part[nr][nwi] = ss;
+    __syncthreads();
+    if (nr < NROWS) {
+      const float* pp = part[nr];
+      const float p2 = NWR > 2 ? pp[2] : 0.0f, p3 = NWR > 3 ? pp[3] : 0.0f;
+      const float var = ((pp[0] + pp[1]) + (p2 + p3)) / float(K);
+      const float rs = 1.0f / sqrtf(var + eps);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int c = t + 256 * j;
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float w0 = __int_as_float(nwv[j][i >> 1][(i & 1) * 2]);
+          const float w1 = __int_as_float(nwv[j][i >> 1][(i & 1) * 2 + 1]);
+          f[2 * i] = bf16_round(w0 * (bf16lo(uint32_t(nv[j][i])) * rs));
+          f[2 * i + 1] = bf16_round(w1 * (bf16hi(uint32_t(nv[j][i])) * rs));
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = absmax(amax, f[i]);
+        amax = row16_absmax(amax);
+        const ActScale sc = act_scale(amax, AP2);
+        const uint32_t q0 = pack_fp8x4(quant_div(f[0], sc, AP2), quant_div(f[1], sc, AP2),
+                                       quant_div(f[2], sc, AP2), quant_div(f[3], sc, AP2));
+        const uint32_t q1 = pack_fp8x4(quant_div(f[4], sc, AP2), quant_div(f[5], sc, AP2),
+                                       quant_div(f[6], sc, AP2), quant_div(f[7], sc, AP2));
+        if (nr < M && c < K / 8) {
+          *reinterpret_cast<uint2*>(xq + nr * ldk + c * 8) = make_uint2(q0, q1);
+          if ((lane & 15) == 0) xsc[nr * KB + c / 16] = make_int2(AP2 ? sc.e8m0 : kE8m0One, __float_as_int(sc.s));
+        }
+      }
+    }
+  } else {
+    float lmax[XP];
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+      float m = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = absmax(absmax(m, bf16lo(v[i])), bf16hi(v[i]));
+      asm volatile("" ::"v"(m));
+      lmax[j] = m;
+    }
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const int pr = 4 * (wave + j * W) + g;
+      if (4 * (wave + j * W) < P) {
+        const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+        const float amax = row16_absmax(lmax[j]);
+        const ActScale sc = act_scale(amax, AP2);
+        const uint32_t q0 = pack_fp8x4(quant_div(bf16lo(v[0]), sc, AP2), quant_div(bf16hi(v[0]), sc, AP2),
+                                       quant_div(bf16lo(v[1]), sc, AP2), quant_div(bf16hi(v[1]), sc, AP2));
+        const uint32_t q1 = pack_fp8x4(quant_div(bf16lo(v[2]), sc, AP2), quant_div(bf16hi(v[2]), sc, AP2),
+                                       quant_div(bf16lo(v[3]), sc, AP2), quant_div(bf16hi(v[3]), sc, AP2));
+        if (pr < P) {
+          const int r = pr / KB, kb = pr - r * KB;
+          *reinterpret_cast<uint2*>(xq + r * ldk + kb * 128 + nl * 8) = make_uint2(q0, q1);
+          if (nl == 0) xsc[pr] = make_int2(AP2 ? sc.e8m0 : kE8m0One, __float_as_int(sc.s));
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- the tile: K slices from zero, folded in K order ----
+  v4f tot = {0.f, 0.f, 0.f, 0.f};
+  const int r = nl;
+#pragma unroll
+  for (int s = 0; s < KB / SL; ++s) {
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < SL; ++q) {
+      const int kb = s * SL + q;
+      AOp a = a_zero();
+      if (r < M) {
+        const uint8_t* pa = xq + r * ldk + kb * 128 + g * 16;
+        const uint4 lo = *reinterpret_cast<const uint4*>(pa), hi = *reinterpret_cast<const uint4*>(pa + 64);
+        a.v = v8i{int(lo.x), int(lo.y), int(lo.z), int(lo.w), int(hi.x), int(hi.y), int(hi.z), int(hi.w)};
+        const int2 s2 = xsc[r * KB + kb];
+        a.se8 = s2.x;
+        a.sf = __int_as_float(s2.y);
+      }
+      mma_step<kFmtFp8, kFmtFp8>(acc, a, w[kb], se[kb], sf[kb], AP2, BP2, lane);
+    }
+    if (s == 0) {
+      tot = acc;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tot[i] += acc[i];
+    }
+  }
+  if (item < tiles) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = g * 4 + i;
+      if (row < M) {
+        const float v = tot[i];
+        const int col = item * 16 + nl;
+        if (col < n_split) {
+          const int64_t o = int64_t(row) * n_split + col;
+          y[o] = f32_to_bf16(res ? bf16_round(v) + __uint_as_float(uint32_t(res[o]) << 16) : v);
+        } else {
+          y_hi[int64_t(row) * (N - n_split) + (col - n_split)] = f32_to_bf16(v);
+        }
+      }
+    }
+  }
+  if constexpr (NORM) {
+    // the residual step's sum, by workgroup 0, last (as fp8_gemv1_kernel)
+    const int nr = wave / NWR, t = (wave % NWR) * 64 + lane;
+    if (xb && hsum && blockIdx.x == 0 && nr < M && nr < NROWS) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (t + 256 * j < K / 8) *reinterpret_cast<v4i*>(hsum + int64_t(nr) * K + (t + 256 * j) * 8) = nv[j];
+    }
+  }
+}
+
 // dynamic LDS of the one-tile kernel's bf16 path: e4m3 rows + per-pair scales
 static size_t gemv1_lds_bytes(int64_t M, int64_t K) { return size_t(M) * size_t(K + 16) + size_t(M) * size_t(K / 128) * 8; }
 // ... and in total: that region, then the K-partials of RT row tiles in its place
@@ -839,12 +1059,73 @@ static int gemv_mt_dispatch(const void* xq, const void* xs, int a_kind, const ui
 #undef WZ_MT_
 }
 
+// The wave-tile GEMV (fp8_gemv_wt_kernel) at K = 1024 from WZ_GVWT_MIN_TILES
+// tiles up, where the split kernels pay a prologue and a cross-wave sum on
+// every 16-KB tile; its slices are the split kernels' (one_nkb), so all give
+// the same bits.  Twelve waves (three per SIMD at its ~150 registers) fill a
+// CU.  32768 x 1024 (2048 tiles) T = 1 / 4 / 8: 8.4 / 10.1 / 10.4 -> 7.6 /
+// 8.3 / 8.7 us; the stage's 40960-row q projection pair with its norm fused
+// (2560 tiles): the decode stage 1255 -> 1211 us per step.  Below ~1000 tiles
+// its few workgroups lose: 4096 x 1024 2.9 -> 5.3 us, 8192 x 1024 3.8 -> 5.5 us.
+#ifndef WZ_GVWT_MIN_TILES
+#define WZ_GVWT_MIN_TILES 2048
+#endif
+#ifndef WZ_GVWT_W
+#define WZ_GVWT_W 12
+#endif
+constexpr int kWtW = WZ_GVWT_W;
+// rows of the fused norm: two waves per row at K = 1024, and no more than the
+// split kernel serves (wz_fp8_norm_linear_max_rows), so every N has one limit
+constexpr int kWtNormRows = kWtW / 2 < GvNorm<one_w<WZ_GV1_K1024>(), one_nkb<WZ_GV1_K1024>()>::ROWS
+                                ? kWtW / 2
+                                : GvNorm<one_w<WZ_GV1_K1024>(), one_nkb<WZ_GV1_K1024>()>::ROWS;
+
+static bool gemv_wt_serves(bool norm, int64_t M, int64_t N, int64_t K) {
+  return K == 1024 && M >= 1 && M <= (norm ? kWtNormRows : 16) && N / 16 >= WZ_GVWT_MIN_TILES;
+}
+
+template <bool NORM>
+static int launch_gemv_wt(const void* x, const uint16_t* b, const float* nw, float eps, uint16_t* hsum,
+                          const uint8_t* w, const void* w_s, int w_kind, const uint16_t* res, uint16_t* y,
+                          uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N, bool pow2, hipStream_t stream) {
+  constexpr int W = kWtW, KB = 8, SL = one_nkb<WZ_GV1_K1024>();
+  const dim3 grid(unsigned((N / 16 + W - 1) / W)), block(W * 64);
+  const size_t lds = size_t(M) * (1024 + 16) + size_t(M) * KB * 8;
+  const bool bp = w_kind == WZ_WSCALE_E8M0;
+  const int xp = M * KB <= 4 * W ? 1 : M * KB <= 8 * W ? 2 : 4;
+#define WZ_WT(XP_, AP, BP)                                                                                     \
+  WZ_LAUNCH("fp8_gemv_wt", stream, (fp8_gemv_wt_kernel<W, KB, SL, XP_, AP, BP, NORM>), grid, block, lds, x, w, w_s, \
+            res, y, y_hi, int(n_split), int(M), int(N), nw, eps, b, hsum)
+#define WZ_WTK(XP_)                                 \
+  do {                                              \
+    if (pow2) {                                     \
+      if (bp) WZ_WT(XP_, true, true);               \
+      else WZ_WT(XP_, true, false);                 \
+    } else {                                        \
+      if (bp) WZ_WT(XP_, false, true);              \
+      else WZ_WT(XP_, false, false);                \
+    }                                               \
+  } while (0)
+  if (NORM || xp == 1)
+    WZ_WTK(1);
+  else if (xp == 2)
+    WZ_WTK(2);
+  else
+    WZ_WTK(4);
+#undef WZ_WTK
+#undef WZ_WT
+  return check_launch("fp8_gemv_wt");
+}
+
 static int gemv_dispatch(bool qa, const void* x, const void* xs, int a_kind, const uint8_t* w, const void* w_s,
                          int w_kind, const uint16_t* res, uint16_t* y, uint16_t* y_hi, int64_t n_split, int64_t M,
                          int64_t N, int64_t K, bool pow2, hipStream_t stream) {
   // the bf16 path quantises M x K / 128 pairs in passes of four per wave, the
   // fewest of 1, 2, 4, 8, 16 passes that cover them (at most the third value
   // of each WZ_GV1_K*), and holds them in LDS
+  if (!qa && gemv_wt_serves(false, M, N, K))
+    return launch_gemv_wt<false>(x, nullptr, nullptr, 0.0f, nullptr, w, w_s, w_kind, res, y, y_hi, n_split, M, N,
+                                 pow2, stream);
   const int rt = M <= 16 ? 1 : 2;
   auto fits1 = [&](int W_, int XP_) {
     return M * (K / 128) <= 4 * W_ * XP_ && gemv1_dyn_bytes(false, M, K, W_, rt) + 64 <= kLdsMax;
@@ -1111,6 +1392,9 @@ extern "C" int wz_fp8_norm_linear_packed_pair(const void* x_bf16, const void* b_
   uint16_t *y0 = static_cast<uint16_t*>(c0_bf16), *y1 = static_cast<uint16_t*>(c1_bf16),
            *hs = static_cast<uint16_t*>(sum_bf16);
   const bool pow2 = act_scale_kind != WZ_SCALE_F32;
+  if (gemv_wt_serves(true, M, N, K))
+    return launch_gemv_wt<true>(x_bf16, b, norm_weight, eps, hs, w, w_s, w_scale_kind, nullptr, y0, y1, N0, M, N, pow2,
+                                stream);
 #define WZ_NL_(W_, NKB_, XP_)                                                                                  \
   return launch_norm_gemv1<W_, NKB_>(x_bf16, b, norm_weight, eps, hs, w, w_s, w_scale_kind, y0, y1, N0, M, N, K, \
                                      pow2, stream)
