@@ -250,6 +250,18 @@ int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const int64_t* inpu
                    void* y_bf16, float* weights_out, int64_t* indices_out, void* ws,
                    size_t ws_bytes, hipStream_t stream);
 
+/* The block's ffn RMSNorm and the layer in one call: y_bf16 = MoE(RMSNorm(h_bf16)),
+ * x = self.ffn_norm(x); x = self.ffn(x, input_ids) of Block.forward
+ * (architecture.py:871-872); the norm is wz_rmsnorm's (RMSNorm.forward,
+ * architecture.py:225-230: fp32 mean of squares, times 1 / sqrt(mean + eps),
+ * times the fp32 weight, rounded to bf16).  norm_weight fp32 [D], D <= 4096.  Decode widths only,
+ * 1 <= T <= 8 (the norm runs inside the routing launch, whose workgroups each
+ * normalise the rows they read); other T: run the norm, then wz_moe_forward.
+ * Bit-for-bit the output of the norm followed by wz_moe_forward. */
+int wz_moe_forward_norm(const wz_moe_desc* d, const void* h_bf16, const float* norm_weight, float eps,
+                        const int64_t* input_ids, int64_t T, void* y_bf16, float* weights_out,
+                        int64_t* indices_out, void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* wz_moe_forward without a caller workspace: no counterpart in the reference.  For
  * callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  The scratch is a device array

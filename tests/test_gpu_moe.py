@@ -166,6 +166,63 @@ def test_v4_decode_parity(v4_layer, T):
     _v4_decode_check(cfg, w, host, moe, T)
 
 
+def _norm_weight(D, seed, dev):
+    rng = np.random.default_rng(seed)
+    return torch.from_numpy(rng.uniform(0.5, 1.5, D).astype(np.float32)).to(dev)
+
+
+def _forward_norm_check(moe, cfg, h, nw, ids=None):
+    """forward_norm(h) against rms_norm(h) then forward(): output and routing torch.equal."""
+    from wanferenz_amd import kernels
+
+    T, k = h.size(0), cfg.topk
+    dev = h.device
+    r1 = (torch.empty(T, k, dtype=torch.float32, device=dev), torch.empty(T, k, dtype=torch.int64, device=dev))
+    r2 = (torch.empty_like(r1[0]), torch.empty_like(r1[1]))
+    y1 = moe.forward_norm(h, nw, 1e-6, ids, routing_out=r1).clone()
+    m = kernels.rms_norm(h, nw, 1e-6)
+    y2 = moe.forward(m, ids, routing_out=r2).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(r1[1], r2[1]), "routing indices differ"
+    assert torch.equal(r1[0], r2[0]), "routing weights differ"
+    assert torch.equal(y1, y2), f"output differs at T={T}"
+    assert torch.isfinite(y1.float()).all()
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 7, 8, 9, 16])
+def test_v4_forward_norm_equals_norm_then_forward(v4_layer, T):
+    """The block's ffn RMSNorm folded into the layer's routing launch (every gate
+    and shared-expert workgroup normalises the rows it reads; T <= 8) gives the
+    bits of kernels.rms_norm followed by forward(), at every decode width (T = 9
+    and 16 run the norm launch first), on a residual-stream-sized h (std 3) and a
+    non-trivial norm weight."""
+    cfg, w, host, moe = v4_layer
+    dev = w.gate_w.device
+    h = bf16_tensor(synth.normal_bf16(synth.stream_key(900 + T, synth.S_X), (T, cfg.dim), 3.0), dev)
+    _forward_norm_check(moe, cfg, h, _norm_weight(cfg.dim, T, dev))
+
+
+@pytest.mark.parametrize("name", ["toy_t4", "hash_t3", "toy_t4_fp32scale", "top6_t8"])
+def test_forward_norm_golden_shapes(gpu, name):
+    """forward_norm at the golden cases' shapes: D = 1024 and 512, a hash-routed
+    layer (ids on the device), float activation scales, top-6 of 32 experts."""
+    case = CASES[name]
+    inp = make_inputs(case)
+    moe = upload_case(case, inp, gpu)
+    cfg = moe.cfg
+    h = bf16_tensor(synth.normal_bf16(synth.stream_key(77, synth.S_X), (case.T, case.dim), 2.0), gpu)
+    ids = torch.from_numpy(inp.input_ids).to(gpu)
+    _forward_norm_check(moe, cfg, h, _norm_weight(case.dim, 5, gpu), ids)
+
+
+def test_forward_norm_wide_batch_runs_the_norm_first(v4_layer):
+    """Above the decode widths forward_norm runs the norm launch, then forward."""
+    cfg, w, host, moe = v4_layer
+    dev = w.gate_w.device
+    h = bf16_tensor(synth.normal_bf16(synth.stream_key(901, synth.S_X), (24, cfg.dim), 3.0), dev)
+    _forward_norm_check(moe, cfg, h, _norm_weight(cfg.dim, 24, dev))
+
+
 def test_v4_decode_parity_fp32_act_scales(v4_layer):
     """Float (non power-of-two) activation scales at the V4 shape: the decode
     w2 then runs w2_combine_kernel (the LDS-staged kernel serves K-blocks of 16

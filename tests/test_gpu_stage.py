@@ -170,3 +170,25 @@ def test_stage_graph_replays_equal_eager(gpu):
         torch.cuda.synchronize()
         assert torch.equal(y_graph, y_eager), f"replay {s}"
         assert torch.isfinite(y_graph.float()).all()
+
+
+def test_stage_fused_norms_equal_unfused(gpu):
+    """The stage with every norm fused (attn_norm and q_norm in the projection
+    pairs, ffn_norm in the MoE layer's routing launch) gives the unfused stage's
+    bits (rms_norm_quant / rms_norm launches, then the layers), two V4 blocks at
+    T = 4, three inputs."""
+    cfg = MoEConfig(4096, 2048, 256, 6, "sqrtsoftplus", 1.5, 10.0, N.WZ_SCALE_UE8M0, N.WZ_WSCALE_E8M0)
+    T = 4
+    blocks = []
+    for l in range(2):
+        w, _ = synth.synthetic_moe(cfg, seed=0, layer=l, device=gpu)
+        blocks.append(stage.synthetic_block(HipMoE(cfg, w, max_tokens=T), 4096, seed=l, device=gpu))
+    fused, plain = stage.DecodeStage(blocks, T), stage.DecodeStage(blocks, T, fused_norms=False)
+    assert fused.fused_norms and not plain.fused_norms
+    for s in range(3):
+        x = bf16_tensor(synth.normal_bf16(synth.stream_key(40 + s, synth.S_X), (T, 4096), 1.0), gpu)
+        y0 = fused.step(x).clone()
+        y1 = plain.step(x).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(y0, y1), f"input {s}"
+

@@ -45,6 +45,7 @@ SIGNATURES = {
     "wz_moe_pack_shared": (_I, [_P, _P, _P, _P, _P]),
     "wz_moe_workspace_init": (_I, [_P, ctypes.c_size_t, _P]),
     "wz_moe_forward": (_I, [_P, _P, _P, _I64, _P, _P, _P, _P, ctypes.c_size_t, _P]),
+    "wz_moe_forward_norm": (_I, [_P, _P, _P, _F, _P, _I64, _P, _P, _P, _P, ctypes.c_size_t, _P]),
     "wz_moe_forward_noalloc": (_I, [_P, _P, _P, _I64, _P, _P, _P, _P]),
     "wz_moe_route": (_I, [_P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]),
     "wz_moe_replay_stage": (_I, [_P, _P, _P, _I64, _I, _P, _P, ctypes.c_size_t, _P]),

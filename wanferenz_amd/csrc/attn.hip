@@ -48,7 +48,7 @@ struct KsLayout {
 };
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return uint32_t(f32_to_bf16(a)) | (uint32_t(f32_to_bf16(b)) << 16);
+  return f32x2_to_bf16x2(a, b);
 }
 
 // Two floats -> packed bf16 pair with the hardware converter (round to nearest

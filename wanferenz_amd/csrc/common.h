@@ -34,13 +34,14 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
 __device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// float32 -> bfloat16 bits, round to nearest even (NaN kept quiet).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return uint16_t((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
+// float32 -> bfloat16 bits, round to nearest even (NaN stays NaN), by gfx950's
+// converter (v_cvt_pk_bf16_f32): one instruction for two values.
+typedef float wz_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 wz_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(wz_f32x2{lo, hi}, wz_bf16x2));
 }
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return uint16_t(f32x2_to_bf16x2(f, 0.0f)); }
 
 __device__ __forceinline__ float bf16_round(float f) {
   return __uint_as_float(uint32_t(f32_to_bf16(f)) << 16);

@@ -365,7 +365,7 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
         for (int i = 0; i < 4; ++i) {
           const float lo = bf16lo(uint32_t(nv[j][i])) + bf16lo(uint32_t(nbv[j][i]));
           const float hi = bf16hi(uint32_t(nv[j][i])) + bf16hi(uint32_t(nbv[j][i]));
-          nv[j][i] = int(uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16));
+          nv[j][i] = int(f32x2_to_bf16x2(lo, hi));
         }
       }
 #pragma unroll
@@ -595,7 +595,7 @@ __global__ __launch_bounds__(W * 64, 3) void fp8_gemv_wt_kernel(const void* __re
         for (int i = 0; i < 4; ++i) {
           const float lo = bf16lo(uint32_t(nv[j][i])) + bf16lo(uint32_t(nbv[j][i]));
           const float hi = bf16hi(uint32_t(nv[j][i])) + bf16hi(uint32_t(nbv[j][i]));
-          nv[j][i] = int(uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16));
+          nv[j][i] = int(f32x2_to_bf16x2(lo, hi));
         }
       }
 #pragma unroll

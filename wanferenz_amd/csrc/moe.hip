@@ -362,7 +362,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const MoeWs ws, int k, int
   for (int i = 0; i < 4; ++i) {
     const float lo = acc[2 * i] + bf16lo(uint32_t(sv[i]));
     const float hi = acc[2 * i + 1] + bf16hi(uint32_t(sv[i]));
-    o[i] = uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+    o[i] = f32x2_to_bf16x2(lo, hi);
   }
   *reinterpret_cast<v4i*>(y + int64_t(t) * D + c * 8) = v4i{int(o[0]), int(o[1]), int(o[2]), int(o[3])};
 }
@@ -388,7 +388,7 @@ __global__ void export_routing_kernel(const MoeWs ws, int P, float* __restrict__
 // ------------------------------------------------------------------ host ----
 
 int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* ids, int64_t T,
-                  void* y, hipStream_t stream, int only);
+                  void* y, hipStream_t stream, int only, const float* nw = nullptr, float eps = 0.0f);
 int launch_prefill_experts(const wz_moe_desc* d, const MoeWs& w, const void* x, int64_t T, hipStream_t stream,
                            int only);
 int launch_prefill_gate(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* input_ids, int64_t T,
@@ -547,6 +547,32 @@ extern "C" int wz_moe_forward(const wz_moe_desc* d, const void* x_bf16, const in
                                n, static_cast<uint16_t*>(y_bf16) + t0 * D, weights_out ? weights_out + t0 * k : nullptr,
                                indices_out ? indices_out + t0 * k : nullptr, ws, stream))
       return rc;
+  }
+  return WZ_OK;
+}
+
+extern "C" int wz_moe_forward_norm(const wz_moe_desc* d, const void* h_bf16, const float* norm_weight, float eps,
+                                   const int64_t* input_ids, int64_t T, void* y_bf16, float* weights_out,
+                                   int64_t* indices_out, void* ws, size_t ws_bytes, hipStream_t stream) {
+  using namespace wz;
+  if (int rc = validate(d, T, ws, ws_bytes, "moe_forward_norm", true)) return rc;
+  if (T == 0) return WZ_OK;
+  if (T > kNormMaxT)
+    return set_error(WZ_EINVAL, "moe_forward_norm: the fused norm serves T <= %d (T=%lld); run the norm, then "
+                     "wz_moe_forward", kNormMaxT, (long long)T);
+  if (!h_bf16 || !y_bf16 || !norm_weight) return set_error(WZ_EINVAL, "moe_forward_norm: null h, y or norm weight");
+  if (!d->w13p || !d->w13p_s || !d->w2p || !d->w2p_s || !d->sh13p || !d->sh2p)
+    return set_error(WZ_EINVAL, "moe_forward_norm: packed expert banks missing (build them with wz_moe_pack)");
+  if (!d->sh_w1_s || !d->sh_w3_s || !d->sh_w2_s)
+    return set_error(WZ_EINVAL, "moe_forward_norm: shared-expert block scales missing");
+  if (d->tid2eid && !input_ids) return set_error(WZ_EINVAL, "moe: hash-routed layer needs input_ids");
+  const MoeWs w = moe_ws_layout(d, T, static_cast<uint8_t*>(ws));
+  if (int rc = launch_decode(d, w, h_bf16, input_ids, T, y_bf16, stream, -1, norm_weight, eps)) return rc;
+  if (weights_out || indices_out) {
+    const int P = int(T * d->topk);
+    WZ_LAUNCH("moe_export", stream, export_routing_kernel, dim3(unsigned((P + 255) / 256)), dim3(256), 0, w, P,
+              weights_out, indices_out);
+    return check_launch("moe_forward_norm export");
   }
   return WZ_OK;
 }

@@ -10,6 +10,8 @@ constexpr int kMaxExperts = 512;
 constexpr int kMaxPairs = 16384;
 constexpr int kGateTok = 8;
 constexpr int kDecodeMaxT = 16;       // tokens served by the decode kernels
+constexpr int kNormMaxT = 8;          // rows the decode route launch normalises itself (fused ffn norm)
+constexpr int kNormMaxD = 4096;       // and their width
 constexpr int kPrefillTileRows = 64;  // pair rows per M-tile of the prefill / dense GEMMs
 constexpr int kCounterWords = 4096;   // arrival counters at the start of the workspace
 

@@ -104,7 +104,7 @@ struct RouteLds {
 };
 
 template <int KS, bool GEN>
-__device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t* ids, int T, int u_max,
+__device__ __forceinline__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t* ids, int T, int u_max,
                            RouteLds& L) {
   int* s_e = L.s_e;
   float* s_w = L.s_w;
@@ -324,7 +324,99 @@ __device__ void route_last(const wz_moe_desc& d, const MoeWs& ws, const int64_t*
   }
 }
 
-__device__ void quant_row(uint8_t* __restrict__ q, float* __restrict__ s, const uint16_t* __restrict__ x,
+// The token rows as a route-launch workgroup (512 threads) reads them, in
+// rmsnorm_kernel's thread mapping: thread (h, t) holds chunks t + 256 j
+// (8 bf16 each) of rows 2 p + h, the rows of pass p < kPass present when
+// 2 p < T (a row 2 p + 1 = T repeats row T - 1 and is not used).  D <= kNormMaxD.
+//
+// The ffn RMSNorm folded into the route launch (route_decode_kernel<KS, true>,
+// wz_moe_forward_norm): x is then the block's hidden state h, and each
+// workgroup forms 1 / sqrt(mean(h^2) + eps) of every row in rmsnorm_kernel's
+// arithmetic (the chunks summed in order, the wave butterfly, the four wave
+// partials as (p0 + p1) + (p2 + p3)) and the MoE input bf16(w (h r)) element by
+// element, so the codes and logits equal those of the unfused launches.
+constexpr int kRowCh = kNormMaxD / 2048;  // chunks per thread and row
+struct NormLds {
+  float rs[kDecodeMaxT];
+  float part[kDecodeMaxT][4];
+};
+
+template <int kPass>
+__device__ __forceinline__ void load_rows(v4i (&hv)[kPass][kRowCh], const uint16_t* __restrict__ x, int T, int D) {
+  const int half = threadIdx.x >> 8, vt = threadIdx.x & 255, nch = D / 8;
+#pragma unroll
+  for (int p = 0; p < kPass; ++p)
+    if (2 * p < T) {
+      const uint16_t* xr = x + int64_t(min(2 * p + half, T - 1)) * D;
+#pragma unroll
+      for (int j = 0; j < kRowCh; ++j) hv[p][j] = load16(xr + min(vt + 256 * j, nch - 1) * 8);
+    }
+}
+
+// the norm weight of the thread's chunks
+__device__ __forceinline__ void load_norm_w(float4 (&nwv)[kRowCh][2], const float* __restrict__ nw, int D) {
+  const int vt = threadIdx.x & 255, nch = D / 8;
+#pragma unroll
+  for (int j = 0; j < kRowCh; ++j) {
+    const float* w = nw + min(vt + 256 * j, nch - 1) * 8;
+    nwv[j][0] = *reinterpret_cast<const float4*>(w);
+    nwv[j][1] = *reinterpret_cast<const float4*>(w + 4);
+  }
+}
+
+// bf16(w (h r)) of the 8 elements packed in v (rmsnorm_kernel's value)
+__device__ __forceinline__ v4i norm_chunk(const v4i& v, const float4 (&w)[2], float r) {
+  const float wf[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
+  v4i o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = wf[2 * i] * (bf16lo(uint32_t(v[i])) * r);
+    const float b = wf[2 * i + 1] * (bf16hi(uint32_t(v[i])) * r);
+    o[i] = int(f32x2_to_bf16x2(a, b));
+  }
+  return o;
+}
+
+// Every row's norm factor from the loaded rows, then the rows normalised in place.
+template <int kPass>
+__device__ __forceinline__ void norm_rows(v4i (&hv)[kPass][kRowCh], const float4 (&nwv)[kRowCh][2], float eps,
+                                          int T, int D, NormLds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, half = tid >> 8, vt = tid & 255, nch = D / 8;
+#pragma unroll
+  for (int p = 0; p < kPass; ++p)
+    if (2 * p < T) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kRowCh; ++j)
+        if (vt + 256 * j < nch) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float a = bf16lo(uint32_t(hv[p][j][i])), c = bf16hi(uint32_t(hv[p][j][i]));
+            ss += a * a;
+            ss += c * c;
+          }
+        }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, kWave);
+      if (lane == 0 && 2 * p + half < T) L.part[2 * p + half][vt >> 6] = ss;
+    }
+  __syncthreads();
+  if (tid < T) {
+    const float* pp = L.part[tid];
+    const float var = ((pp[0] + pp[1]) + (pp[2] + pp[3])) / float(D);
+    L.rs[tid] = 1.0f / sqrtf(var + eps);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < kPass; ++p)
+    if (2 * p < T) {
+      const float r = L.rs[min(2 * p + half, T - 1)];
+#pragma unroll
+      for (int j = 0; j < kRowCh; ++j) hv[p][j] = norm_chunk(hv[p][j], nwv[j], r);
+    }
+}
+
+__device__ __forceinline__ void quant_row(uint8_t* __restrict__ q, float* __restrict__ s, const uint16_t* __restrict__ x,
                           int K, bool pow2) {
   // act_quant of one row (torch_ops.py:33-49): 8 elements per lane, 16 lanes per 128-block.
   for (int c0 = 0; c0 < K; c0 += int(blockDim.x) * 8) {
@@ -426,18 +518,158 @@ __device__ __forceinline__ void w13_shared_item_bf16(const wz_moe_desc& d, const
   }
 }
 
+// Shared expert w1 / w3 for features 16 b .. 16 b + 15, the token rows staged
+// in LDS (D <= kNormMaxD): the workgroup loads the T rows once (load_rows),
+// (NORM) normalises them (norm_rows), act_quant-s them into LDS, 16 lanes per
+// (row, 128-block) as quant_row does, so the codes equal the unfused path's,
+// and only then requests its weight tiles: the gate workgroups' loads, which
+// the routing waits on, reach HBM first.  Each wave reads its A operands from
+// LDS (rows past T repeat row T - 1; their outputs are not stored).  Item
+// b < T also writes token row b's codes and block scales to xq / xs for the
+// w1 / w3 launch.  Quantising each wave's K range in the MFMA layout instead
+// covered all 16 row slots (three quarters empty at T = 4) in every wave, and
+// with the norm folded in that cost the launch 5 us.
+struct ItemLds {
+  uint8_t xq[kDecodeMaxT][kNormMaxD + 16];  // e4m3 rows, padded against bank conflicts
+  float xs[kDecodeMaxT][kNormMaxD / 128];   // their block scales
+};
+// a route-launch workgroup's token rows: a shared item's codes, or a gate
+// block's bf16 rows (T <= kNormMaxT)
+union RowLds {
+  ItemLds il;
+  uint16_t xn[kNormMaxT][kNormMaxD];
+};
+template <bool AP2, bool WP2, bool NORM>
+__device__ __forceinline__ void w13_shared_item_lds(const wz_moe_desc& d, const MoeWs& ws,
+                                                    const uint16_t* __restrict__ x, const float* __restrict__ nw,
+                                                    float eps, int T, int b, float* red, NormLds& NL, ItemLds& IL) {
+  constexpr int kQ = 4, kPass = (NORM ? kNormMaxT : kDecodeMaxT) / 2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nl = lane & 15, g = lane >> 4, half = tid >> 8, vt = tid & 255;
+  const int D = d.dim, I = d.inter, KB = D / 128, nch = D / 8;
+  const int kb0 = (wave * KB) / kRouteWaves, kb1 = ((wave + 1) * KB) / kRouteWaves;
+  const int f0 = b * 16;
+  const uint8_t* tiles = static_cast<const uint8_t*>(d.sh13p) + int64_t(b) * KB * 4096;
+  const int wkind = WP2 ? WZ_WSCALE_E8M0 : WZ_WSCALE_F32;
+  const int64_t sbase = int64_t(f0 >> 7) * KB;
+  v4i hv[kPass][kRowCh];
+  load_rows<kPass>(hv, x, T, D);
+  if constexpr (NORM) {
+    float4 nwv[kRowCh][2];
+    load_norm_w(nwv, nw, D);
+    norm_rows<kPass>(hv, nwv, eps, T, D, NL);
+  }
+  // ---- act_quant of the rows into LDS (quant_row's arithmetic) ----
+#pragma unroll
+  for (int p = 0; p < kPass; ++p)
+    if (2 * p < T) {
+      const int row = 2 * p + half;
+#pragma unroll
+      for (int j = 0; j < kRowCh; ++j)
+        if (256 * j < nch) {  // uniform: the 16-lane groups of a chunk range are whole
+          const int c = vt + 256 * j, col = min(c, nch - 1) * 8;
+          const v4i v = hv[p][j];
+          float f[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            f[2 * i] = bf16lo(uint32_t(v[i]));
+            f[2 * i + 1] = bf16hi(uint32_t(v[i]));
+          }
+          float amax = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) amax = absmax(amax, f[i]);
+          amax = wave_absmax_xor(amax, 1);
+          amax = wave_absmax_xor(amax, 2);
+          amax = wave_absmax_xor(amax, 4);
+          amax = wave_absmax_xor(amax, 8);
+          const ActScale sc = act_scale(amax, AP2);
+          if (row < T && c < nch) {
+            const uint32_t lo = pack_fp8x4(quant_div(f[0], sc, AP2), quant_div(f[1], sc, AP2),
+                                           quant_div(f[2], sc, AP2), quant_div(f[3], sc, AP2));
+            const uint32_t hi = pack_fp8x4(quant_div(f[4], sc, AP2), quant_div(f[5], sc, AP2),
+                                           quant_div(f[6], sc, AP2), quant_div(f[7], sc, AP2));
+            *reinterpret_cast<uint2*>(&IL.xq[row][col]) = make_uint2(lo, hi);
+            if ((tid & 15) == 0) IL.xs[row][col / 128] = sc.s;
+          }
+        }
+    }
+  __syncthreads();
+  v8i w[2][kQ];
+  int se[2][kQ];
+  float sf[2][kQ];
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const int kk = min(kb + q, kb1 - 1);
+      w[0][q] = pk_fp8(tiles + int64_t(kk) * 4096, lane);
+      w[1][q] = pk_fp8(tiles + int64_t(kk) * 4096 + 2048, lane);
+      fp8_wscale(d.sh_w1_s, sbase + kk, wkind, se[0][q], sf[0][q]);
+      fp8_wscale(d.sh_w3_s, sbase + kk, wkind, se[1][q], sf[1][q]);
+    }
+  };
+  fetch(kb0);
+  // ---- item b < T: token row b's codes and scales for the w1 / w3 launch ----
+  if (b < T) {
+    for (int c = tid; c < nch; c += kRouteThreads_)
+      *reinterpret_cast<uint2*>(ws.xq + int64_t(b) * D + c * 8) = *reinterpret_cast<const uint2*>(&IL.xq[b][c * 8]);
+    if (tid < KB) ws.xs[int64_t(b) * KB + tid] = IL.xs[b][tid];
+  }
+  // ---- the K loop, A from LDS ----
+  const int arow = min(nl, T - 1);
+  v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  for (int kb = kb0; kb < kb1; kb += kQ) {
+    if (kb != kb0) fetch(kb);
+#pragma unroll
+    for (int q = 0; q < kQ; ++q)
+      if (kb + q < kb1) {
+        AOp a = a_zero();
+        const uint8_t* pa = &IL.xq[arow][(kb + q) * 128 + g * 16];
+        const v4i lo = *reinterpret_cast<const v4i*>(pa), hi = *reinterpret_cast<const v4i*>(pa + 64);
+        a.v = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const float sc = IL.xs[arow][kb + q];
+        a.sf = sc;
+        a.se8 = AP2 ? int((__float_as_uint(sc) >> 23) & 0xFFu) : kE8m0One;
+        mma_step<kFmtFp8, kFmtFp8>(acc[0], a, w[0][q], se[0][q], sf[0][q], AP2, WP2, lane);
+        mma_step<kFmtFp8, kFmtFp8>(acc[1], a, w[1][q], se[1][q], sf[1][q], AP2, WP2, lane);
+      }
+  }
+  // red: [kRouteWaves][2][4][64] floats; partials summed in wave order
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[((wave * 2 + m) * 4 + i) * kWave + lane] = acc[m][i];
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float gs = red[((0 * 2 + 0) * 4 + i) * kWave + lane], us = red[((0 * 2 + 1) * 4 + i) * kWave + lane];
+#pragma unroll
+      for (int w2 = 1; w2 < kRouteWaves; ++w2) {
+        gs += red[((w2 * 2 + 0) * 4 + i) * kWave + lane];
+        us += red[((w2 * 2 + 1) * 4 + i) * kWave + lane];
+      }
+      const int t = g * 4 + i;
+      if (t < T) ws.sh_h[int64_t(t) * I + f0 + nl] = f32_to_bf16(swiglu(gs, us, d.swiglu_limit));
+    }
+  }
+}
+
 // Blocks [0, n_gate): gate waves.  An expert's logits for all T tokens are
 // split over `split` consecutive waves of one block (a K range each, fp64
 // partials summed in wave order), so the gate's fp64 work spreads over
-// n_gate = E * split / 8 CUs; then the last block to arrive routes.
-// [n_gate, n_gate + T): act_quant of x.  The rest: the shared expert's w1 / w3
-// items, one per block (its waves split K), which do not depend on the routing
-// and so stream while it runs.
-template <int KS>
+// n_gate = E * split / 8 CUs; then the last block to arrive routes.  The
+// rest: the shared expert's w1 / w3 items, one per block (its waves split K),
+// which do not depend on the routing and so stream while it runs; item b < T
+// then writes act_quant of token row b.  NORM: x is the hidden state h and the MoE input
+// is its RMSNorm with weight nw (route_norm_prologue), formed where it is read.
+template <int KS, bool NORM>
 __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_desc d, MoeWs ws,
                                                                    const uint16_t* __restrict__ x,
                                                                    const int64_t* __restrict__ ids, int T,
-                                                                   int n_gate, int split, int u_max) {
+                                                                   int n_gate, int split, int u_max,
+                                                                   const float* __restrict__ nw, float eps) {
+  __shared__ NormLds nls;
+  __shared__ __align__(16) RowLds rows;
   __shared__ int s_last;
   __shared__ double part[kRouteWaves][kDecodeMaxT];
   // 16 KB: a gate block's per-lane partials (double [8][4][64]) or a shared
@@ -463,8 +695,40 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     double acc[kDecodeMaxT];
 #pragma unroll
     for (int t = 0; t < kDecodeMaxT; ++t) acc[t] = 0.0;
+    const uint16_t* wr = static_cast<const uint16_t*>(d.gate_w) + int64_t(min(e, E - 1)) * D;
+    // T <= kNormMaxT (D <= kNormMaxD): the rows are staged in LDS once for the
+    // block's waves (read in load_rows' mapping; NORM: normalised there), then
+    // the first weight chunks are requested: the staging waits on the rows (and
+    // the norm weight) alone
+    const bool staged = NORM || (T <= kNormMaxT && D <= kNormMaxD);
+    v4i hv[kNormMaxT / 2][kRowCh];
+    float4 nwv[kRowCh][2];
+    if (staged) load_rows<kNormMaxT / 2>(hv, x, T, D);
+    if constexpr (NORM) load_norm_w(nwv, nw, D);
+    __builtin_amdgcn_sched_barrier(0);
+    v4i wv0[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = c0 + lane + 64 * i;
+      wv0[i] = (e < E && c < c1) ? load16(wr + c * 8) : v4i{0, 0, 0, 0};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (staged) {
+      if constexpr (NORM) norm_rows<kNormMaxT / 2>(hv, nwv, eps, T, D, nls);
+      const int half = tid >> 8, vt = tid & 255, nch = D / 8;
+#pragma unroll
+      for (int p = 0; p < kNormMaxT / 2; ++p)
+        if (2 * p < T) {
+          const int row = 2 * p + half;
+#pragma unroll
+          for (int j = 0; j < kRowCh; ++j) {
+            const int c = vt + 256 * j;
+            if (row < T && c < nch) *reinterpret_cast<v4i*>(&rows.xn[row][c * 8]) = hv[p][j];
+          }
+        }
+      __syncthreads();
+    }
     if (e < E && c0 < c1) {
-      const uint16_t* wr = static_cast<const uint16_t*>(d.gate_w) + int64_t(e) * D;
 #pragma unroll 1
       for (int cb = c0; cb < c1; cb += 64 * 2) {
         // two 16-byte chunks per lane; a chunk past c1 gets w = 0 and a clamped,
@@ -474,7 +738,10 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int c = cb + lane + 64 * i;
-          wv[i] = c < c1 ? load16(wr + c * 8) : v4i{0, 0, 0, 0};
+          if (cb == c0)
+            wv[i] = wv0[i];
+          else
+            wv[i] = c < c1 ? load16(wr + c * 8) : v4i{0, 0, 0, 0};
           cx[i] = min(c, c1 - 1);
         }
         // tokens in groups of 8: a group's x chunks are all requested before any
@@ -483,10 +750,19 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
         for (int tg = 0; tg < kDecodeMaxT; tg += 8) {
           if (tg < T) {
             v4i xv[8][2];
+            if (staged) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
+              for (int j = 0; j < 8; ++j)
+                if (tg + j < T) {
 #pragma unroll
-              for (int i = 0; i < 2; ++i) xv[j][i] = load16(x + int64_t(min(tg + j, T - 1)) * D + cx[i] * 8);
+                  for (int i = 0; i < 2; ++i) xv[j][i] = *reinterpret_cast<const v4i*>(&rows.xn[tg + j][cx[i] * 8]);
+                }
+            } else {
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) xv[j][i] = load16(x + int64_t(min(tg + j, T - 1)) * D + cx[i] * 8);
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j)
               if (tg + j < T) {
@@ -552,12 +828,22 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     return;
   }
   b -= n_gate;
-  if (b < T) {
-    quant_row(ws.xq + int64_t(b) * D, ws.xs + int64_t(b) * (D / 128), x + int64_t(b) * D, D, a_pow2);
+  const bool wp2 = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  if (D <= kNormMaxD) {
+    // the token rows staged in LDS once for the item (and normalised: NORM)
+#define WZ_ITEM(AP, WP) w13_shared_item_lds<AP, WP, NORM>(d, ws, x, nw, eps, T, b, rbuf, nls, rows.il)
+    if (a_pow2 && wp2)
+      WZ_ITEM(true, true);
+    else if (a_pow2)
+      WZ_ITEM(true, false);
+    else if (wp2)
+      WZ_ITEM(false, true);
+    else
+      WZ_ITEM(false, false);
+#undef WZ_ITEM
     return;
   }
-  b -= T;
-  const bool wp2 = d.shared_w_scale_kind == WZ_WSCALE_E8M0;
+  // wider rows (never NORM: the launch refuses it): act_quant in the MFMA layout
   if (a_pow2 && wp2)
     w13_shared_item_bf16<true, true>(d, ws, x, T, b, rbuf);
   else if (a_pow2)
@@ -566,6 +852,11 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     w13_shared_item_bf16<false, true>(d, ws, x, T, b, rbuf);
   else
     w13_shared_item_bf16<false, false>(d, ws, x, T, b, rbuf);
+  // item b < T also quantises token row b (the w1 / w3 launch's A operand), so
+  // the launch is n_gate + I / 16 workgroups: one per CU at V4 (with separate
+  // act_quant workgroups, T of them waited for a second round)
+  if (b < T)
+    quant_row(ws.xq + int64_t(b) * D, ws.xs + int64_t(b) * (D / 128), x + int64_t(b) * D, D, a_pow2);
 }
 
 // -------------------------------------------------------------------- w13 ---
@@ -1415,8 +1706,10 @@ __global__ __launch_bounds__(256) void combine_decode_kernel(MoeWs ws, int T, in
 }
 
 // only < 0: the whole layer; otherwise the one stage WZ_STAGE_* (profiling replays).
+// nw: x is the hidden state and the MoE input its RMSNorm (weight nw, eps),
+// computed inside the route launch (D <= kNormMaxD, T <= kNormMaxT).
 int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int64_t* ids, int64_t T,
-                  void* y, hipStream_t stream, int only) {
+                  void* y, hipStream_t stream, int only, const float* nw, float eps) {
   const int E = d->n_experts, k = d->topk, D = d->dim, I = d->inter;
   // K-split of the gate: the largest of 8, 4, 2, 1 waves per expert that keeps
   // the gate within 128 workgroups (of 8 waves)
@@ -1430,15 +1723,21 @@ int launch_decode(const wz_moe_desc* d, const MoeWs& w, const void* x, const int
     return set_error(WZ_EINVAL, "moe decode: packed banks missing (wz_moe_pack)");
   if (only < 0 || only == WZ_STAGE_ROUTE) {
     // top-k lanes walk E / 64 slots: 4 for up to 256 experts, else 8
-    const dim3 rgrid{unsigned(n_gate + T + I / 16)};
+    if (T > I / 16) return set_error(WZ_EINVAL, "moe decode: T=%lld exceeds the %d shared items", (long long)T, I / 16);
+    const dim3 rgrid{unsigned(n_gate + I / 16)};
     const uint16_t* xb = static_cast<const uint16_t*>(x);
+    if (nw && (D > kNormMaxD || T > kNormMaxT))
+      return set_error(WZ_EINVAL, "moe decode: the fused norm serves D <= %d and T <= %d (D=%d, T=%lld)",
+                       kNormMaxD, kNormMaxT, D, (long long)T);
+#define WZ_RK(KS, NORM)                                                                                       \
+  WZ_LAUNCH("moe_route", stream, (route_decode_kernel<KS, NORM>), rgrid, dim3(kRouteThreads_), 0, *d, w, xb, ids, \
+            int(T), n_gate, split, u_max, nw, eps)
     if (E <= 256) {
-      WZ_LAUNCH("moe_route", stream, route_decode_kernel<4>, rgrid, dim3(kRouteThreads_), 0, *d, w, xb, ids, int(T),
-                n_gate, split, u_max);
+      if (nw) WZ_RK(4, true); else WZ_RK(4, false);
     } else {
-      WZ_LAUNCH("moe_route", stream, route_decode_kernel<8>, rgrid, dim3(kRouteThreads_), 0, *d, w, xb, ids, int(T),
-                n_gate, split, u_max);
+      if (nw) WZ_RK(8, true); else WZ_RK(8, false);
     }
+#undef WZ_RK
     if (int rc = check_launch("moe route")) return rc;
   }
   if (only < 0 || only == WZ_STAGE_W13) {

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
       const int d0 = c * 8 + 2 * i;
       const float a = w[d0] * (bf16lo(uint32_t(v[i])) * r);
       const float b = w[d0 + 1] * (bf16hi(uint32_t(v[i])) * r);
-      o[i] = uint32_t(f32_to_bf16(a)) | (uint32_t(f32_to_bf16(b)) << 16);
+      o[i] = f32x2_to_bf16x2(a, b);
     }
     *reinterpret_cast<v4i*>(y + row * D + c * 8) = v4i{int(o[0]), int(o[1]), int(o[2]), int(o[3])};
   }
@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256) void add_bf16_kernel(const uint16_t* __restric
   for (int j = 0; j < 4; ++j) {
     const float lo = bf16lo(uint32_t(va[j])) + bf16lo(uint32_t(vb[j]));
     const float hi = bf16hi(uint32_t(va[j])) + bf16hi(uint32_t(vb[j]));
-    o[j] = uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+    o[j] = f32x2_to_bf16x2(lo, hi);
   }
   *reinterpret_cast<v4i*>(out + i * 8) = v4i{int(o[0]), int(o[1]), int(o[2]), int(o[3])};
 }
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
       for (int i = 0; i < 4; ++i) {
         const float lo = bf16lo(uint32_t(v[j][i])) + bf16lo(uint32_t(vb[i]));
         const float hi = bf16hi(uint32_t(v[j][i])) + bf16hi(uint32_t(vb[i]));
-        v[j][i] = int(uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16));
+        v[j][i] = int(f32x2_to_bf16x2(lo, hi));
       }
       if (sum) *reinterpret_cast<v4i*>(sum + row * D + c * 8) = v[j];
     }
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256) void wire_unpack_kernel(const uint8_t* __restr
   uint32_t o[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k)
-    o[k] = uint32_t(f32_to_bf16(f[2 * k] * sf)) | (uint32_t(f32_to_bf16(f[2 * k + 1] * sf)) << 16);
+    o[k] = f32x2_to_bf16x2(f[2 * k] * sf, f[2 * k + 1] * sf);
   *reinterpret_cast<v4i*>(y + i * 8) = v4i{int(o[0]), int(o[1]), int(o[2]), int(o[3])};
 }
 

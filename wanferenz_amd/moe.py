@@ -354,6 +354,39 @@ class HipMoE:
 
     __call__ = forward
 
+    # widths the routing launch normalises itself (wz_moe_forward_norm)
+    NORM_MAX_T, NORM_MAX_D = 8, 4096
+
+    def forward_norm(self, h: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                     input_ids: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                     routing_out=None) -> torch.Tensor:
+        """forward(RMSNorm(h)): ``x = self.ffn_norm(x); x = self.ffn(x, input_ids)`` of
+        Block.forward (architecture.py:871-872) in one call, bit for bit the norm
+        (kernels.rms_norm) followed by forward().  For decode widths (T <= 8,
+        D <= 4096) the routing launch normalises the rows it reads, so no norm
+        launch runs; other widths run the norm, then forward."""
+        hv = self._tokens(h)
+        T, D, k = hv.size(0), self.cfg.dim, self.cfg.topk
+        nw = norm_weight.detach()
+        if nw.dtype != torch.float32 or nw.numel() != D or not nw.is_contiguous() or nw.device != hv.device:
+            raise ValueError(f"HipMoE.forward_norm: norm weight must be a contiguous fp32 [{D}] tensor on {hv.device}")
+        if T > self.NORM_MAX_T or D > self.NORM_MAX_D:
+            from . import kernels
+            return self.forward(kernels.rms_norm(h, norm_weight, eps), input_ids, out=out, routing_out=routing_out)
+        ids = self._ids(input_ids, T)
+        if out is not None:
+            self._check_out(out, (T, D), torch.bfloat16, "out")
+        y = out if out is not None else torch.empty_like(hv)
+        wp = ip = None
+        if routing_out is not None:
+            self._check_out(routing_out[0], (T, k), torch.float32, "routing weights")
+            self._check_out(routing_out[1], (T, k), torch.int64, "routing indices")
+            wp, ip = routing_out[0].data_ptr(), routing_out[1].data_ptr()
+        ws = self._ws_for(T)
+        N.call("wz_moe_forward_norm", ctypes.byref(self.desc), hv.data_ptr(), nw.data_ptr(), float(eps),
+               _ptr(ids), T, y.data_ptr(), wp, ip, ws.data_ptr(), ws.numel(), N.stream_handle(self.device))
+        return y.view(h.shape)
+
     def replay_stage(self, x: torch.Tensor, stage: int, out: torch.Tensor,
                      input_ids: Optional[torch.Tensor] = None) -> None:
         """Re-launch one stage (N.WZ_STAGE_*) of the preceding forward(x, input_ids, out) call.

@@ -31,7 +31,9 @@ wq_b with the indexer's wq_b: kernels.PackedFp8Pair), and the norm that feeds
 them (attn_norm with the previous block's MoE residual, q_norm) runs inside
 that launch (PackedFp8Pair.norm_gemm: the rms_norm_quant codes, bit for bit)
 when T fits its rows (T <= 4); otherwise each FP8 input is produced quantised
-by the norm that precedes it (rms_norm_quant).  The residual add of the
+by the norm that precedes it (rms_norm_quant).  With the fused norms the
+ffn_norm runs inside the MoE layer's routing launch as well
+(HipMoE.forward_norm: the rms_norm output, bit for bit).  The residual add of the
 attention side sits in wo_b's epilogue and that of the MoE side in the next
 block's norm.  Every buffer is allocated once, so a step is a fixed sequence of
 launches.
@@ -171,8 +173,12 @@ class DecodeStage:
                 b.q_idx.gemm(*self.qq, out=(self.q, self.iq))
             h1 = next(nxt)
             b.wo_b(self.iq, out=h1, residual=h)
-            kernels.rms_norm(h1, b.ffn_norm, eps, out=self.m)
-            b.moe.forward(self.m, out=self.e, routing_out=None if routing is None else routing[i])
+            ro = None if routing is None else routing[i]
+            if self.fused_norms and trace is None:
+                b.moe.forward_norm(h1, b.ffn_norm, eps, out=self.e, routing_out=ro)
+            else:
+                kernels.rms_norm(h1, b.ffn_norm, eps, out=self.m)
+                b.moe.forward(self.m, out=self.e, routing_out=ro)
             if trace is not None:
                 trace.append({"h_in": h_in, "e_in": e_in, "h": h.clone(), "hq": self.hq[0].clone(),
                               "hs": self.hq[1].clone(), "qa": self.qa.clone(), "kv": self.kv.clone(),
