@@ -120,7 +120,37 @@ __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float 
   return uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true));
 }
 
+// act_quant codes of eight values at scale sc, packed e4m3 (quant_div, then
+// the converter's RNE).  fast: the clamp to +-448 is left out, which holds for
+// power-of-two scales when the block amax is finite: s >= amax / 448 bounds
+// |x / s| by 448, up to the rounding of amax / 448, which converts to 448 all
+// the same.
+__device__ __forceinline__ uint2 quant8(const float (&f)[8], const ActScale& sc, bool pow2, bool fast) {
+  if (fast)
+    return make_uint2(pack_fp8x4(f[0] * sc.inv, f[1] * sc.inv, f[2] * sc.inv, f[3] * sc.inv),
+                      pack_fp8x4(f[4] * sc.inv, f[5] * sc.inv, f[6] * sc.inv, f[7] * sc.inv));
+  return make_uint2(pack_fp8x4(quant_div(f[0], sc, pow2), quant_div(f[1], sc, pow2), quant_div(f[2], sc, pow2),
+                               quant_div(f[3], sc, pow2)),
+                    pack_fp8x4(quant_div(f[4], sc, pow2), quant_div(f[5], sc, pow2), quant_div(f[6], sc, pow2),
+                               quant_div(f[7], sc, pow2)));
+}
+
+// the eight bf16 values packed in v, as floats
+__device__ __forceinline__ void bf16x8_unpack(const v4i& v, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(uint32_t(v[i]) << 16);
+    f[2 * i + 1] = __uint_as_float(uint32_t(v[i]) & 0xFFFF0000u);
+  }
+}
+
 // ---------------------------------------------------------------- wave ops ---
+
+// whether quant8 may leave out its clamp for every lane of the wave (the
+// active lanes' block amaxes): power-of-two scales, every amax finite
+__device__ __forceinline__ bool quant_fast(float amax, bool pow2) {
+  return pow2 && __ballot((__float_as_uint(amax) & 0x7F800000u) == 0x7F800000u) == 0ull;
+}
 
 // Block amax across lanes (see absmax: NaN wins).
 __device__ __forceinline__ float wave_absmax_xor(float v, int mask) {

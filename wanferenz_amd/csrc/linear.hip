@@ -333,6 +333,17 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
       xr[j] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + int64_t(r) * K + kb * 128 + nl * 8);
     }
   }
+  // the residual of this wave's first epilogue element, requested with the x
+  // rows: read in the epilogue it was a round trip after the reduction.  The
+  // load has no branch around it (clamped indices; without a residual it reads
+  // y's same element, unused): behind one, its use was moved into the branch
+  // and waited for every x load there, before the weights were requested
+  uint16_t res0;
+  {
+    const int row = min(m0 + ((wave >> 2) % RT) * 16 + g * 4 + (wave & 3), M - 1);
+    const int col = min(item * 16 + nl, n_split - 1);
+    res0 = (res ? res : y)[int64_t(row) * n_split + col];
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   v8i w[NKB];
@@ -400,10 +411,8 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
         for (int i = 0; i < 8; ++i) amax = absmax(amax, f[i]);
         amax = row16_absmax(amax);
         const ActScale sc = act_scale(amax, AP2);
-        const uint32_t q0 = pack_fp8x4(quant_div(f[0], sc, AP2), quant_div(f[1], sc, AP2),
-                                       quant_div(f[2], sc, AP2), quant_div(f[3], sc, AP2));
-        const uint32_t q1 = pack_fp8x4(quant_div(f[4], sc, AP2), quant_div(f[5], sc, AP2),
-                                       quant_div(f[6], sc, AP2), quant_div(f[7], sc, AP2));
+        const uint2 qv = quant8(f, sc, AP2, quant_fast(amax, AP2));
+        const uint32_t q0 = qv.x, q1 = qv.y;
         if (nr < M) {
           *reinterpret_cast<uint2*>(xq + nr * ldk + c * 8) = make_uint2(q0, q1);
           if ((lane & 15) == 0) xsc[nr * KB + c / 16] = make_int2(AP2 ? sc.e8m0 : kE8m0One, __float_as_int(sc.s));
@@ -421,10 +430,7 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
     float lmax[XP];
 #pragma unroll
     for (int j = 0; j < XP; ++j) {
-      const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
-      float m = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) m = absmax(absmax(m, bf16lo(v[i])), bf16hi(v[i]));
+      const float m = bf16x8_absmax(v4i{int(xr[j].x), int(xr[j].y), int(xr[j].z), int(xr[j].w)});
       asm volatile("" ::"v"(m));  // an unconditional use: the load stays here
       lmax[j] = m;
     }
@@ -432,13 +438,12 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
     for (int j = 0; j < XP; ++j) {
       const int pr = 4 * (wave + j * W) + g;
       if (4 * (wave + j * W) < P) {  // wave-uniform: the pass holds a pair
-        const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
         const float amax = row16_absmax(lmax[j]);
         const ActScale sc = act_scale(amax, AP2);
-        const uint32_t q0 = pack_fp8x4(quant_div(bf16lo(v[0]), sc, AP2), quant_div(bf16hi(v[0]), sc, AP2),
-                                       quant_div(bf16lo(v[1]), sc, AP2), quant_div(bf16hi(v[1]), sc, AP2));
-        const uint32_t q1 = pack_fp8x4(quant_div(bf16lo(v[2]), sc, AP2), quant_div(bf16hi(v[2]), sc, AP2),
-                                       quant_div(bf16lo(v[3]), sc, AP2), quant_div(bf16hi(v[3]), sc, AP2));
+        float f[8];
+        bf16x8_unpack(v4i{int(xr[j].x), int(xr[j].y), int(xr[j].z), int(xr[j].w)}, f);
+        const uint2 qv = quant8(f, sc, AP2, quant_fast(amax, AP2));
+        const uint32_t q0 = qv.x, q1 = qv.y;
         if (pr < P) {
           const int r = pr / KB, kb = pr - r * KB;
           *reinterpret_cast<uint2*>(xq + r * ldk + kb * 128 + nl * 8) = make_uint2(q0, q1);
@@ -489,7 +494,8 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
       const int col = item * 16 + nl;
       if (col < n_split) {
         const int64_t o = int64_t(row) * n_split + col;
-        y[o] = f32_to_bf16(res ? bf16_round(v) + __uint_as_float(uint32_t(res[o]) << 16) : v);
+        const uint16_t rv = res ? (pi == wave ? res0 : res[o]) : 0;
+        y[o] = f32_to_bf16(res ? bf16_round(v) + __uint_as_float(uint32_t(rv) << 16) : v);
       } else {
         y_hi[int64_t(row) * (N - n_split) + (col - n_split)] = f32_to_bf16(v);
       }
@@ -630,10 +636,8 @@ __global__ __launch_bounds__(W * 64, 3) void fp8_gemv_wt_kernel(const void* __re
         for (int i = 0; i < 8; ++i) amax = absmax(amax, f[i]);
         amax = row16_absmax(amax);
         const ActScale sc = act_scale(amax, AP2);
-        const uint32_t q0 = pack_fp8x4(quant_div(f[0], sc, AP2), quant_div(f[1], sc, AP2),
-                                       quant_div(f[2], sc, AP2), quant_div(f[3], sc, AP2));
-        const uint32_t q1 = pack_fp8x4(quant_div(f[4], sc, AP2), quant_div(f[5], sc, AP2),
-                                       quant_div(f[6], sc, AP2), quant_div(f[7], sc, AP2));
+        const uint2 qv = quant8(f, sc, AP2, quant_fast(amax, AP2));
+        const uint32_t q0 = qv.x, q1 = qv.y;
         if (nr < M && c < K / 8) {
           *reinterpret_cast<uint2*>(xq + nr * ldk + c * 8) = make_uint2(q0, q1);
           if ((lane & 15) == 0) xsc[nr * KB + c / 16] = make_int2(AP2 ? sc.e8m0 : kE8m0One, __float_as_int(sc.s));
@@ -644,10 +648,7 @@ __global__ __launch_bounds__(W * 64, 3) void fp8_gemv_wt_kernel(const void* __re
     float lmax[XP];
 #pragma unroll
     for (int j = 0; j < XP; ++j) {
-      const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
-      float m = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) m = absmax(absmax(m, bf16lo(v[i])), bf16hi(v[i]));
+      const float m = bf16x8_absmax(v4i{int(xr[j].x), int(xr[j].y), int(xr[j].z), int(xr[j].w)});
       asm volatile("" ::"v"(m));
       lmax[j] = m;
     }
@@ -655,13 +656,12 @@ __global__ __launch_bounds__(W * 64, 3) void fp8_gemv_wt_kernel(const void* __re
     for (int j = 0; j < XP; ++j) {
       const int pr = 4 * (wave + j * W) + g;
       if (4 * (wave + j * W) < P) {
-        const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
         const float amax = row16_absmax(lmax[j]);
         const ActScale sc = act_scale(amax, AP2);
-        const uint32_t q0 = pack_fp8x4(quant_div(bf16lo(v[0]), sc, AP2), quant_div(bf16hi(v[0]), sc, AP2),
-                                       quant_div(bf16lo(v[1]), sc, AP2), quant_div(bf16hi(v[1]), sc, AP2));
-        const uint32_t q1 = pack_fp8x4(quant_div(bf16lo(v[2]), sc, AP2), quant_div(bf16hi(v[2]), sc, AP2),
-                                       quant_div(bf16lo(v[3]), sc, AP2), quant_div(bf16hi(v[3]), sc, AP2));
+        float f[8];
+        bf16x8_unpack(v4i{int(xr[j].x), int(xr[j].y), int(xr[j].z), int(xr[j].w)}, f);
+        const uint2 qv = quant8(f, sc, AP2, quant_fast(amax, AP2));
+        const uint32_t q0 = qv.x, q1 = qv.y;
         if (pr < P) {
           const int r = pr / KB, kb = pr - r * KB;
           *reinterpret_cast<uint2*>(xq + r * ldk + kb * 128 + nl * 8) = make_uint2(q0, q1);

@@ -568,27 +568,13 @@ __device__ __forceinline__ void w13_shared_item_lds(const wz_moe_desc& d, const 
       for (int j = 0; j < kRowCh; ++j)
         if (256 * j < nch) {  // uniform: the 16-lane groups of a chunk range are whole
           const int c = vt + 256 * j, col = min(c, nch - 1) * 8;
-          const v4i v = hv[p][j];
-          float f[8];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            f[2 * i] = bf16lo(uint32_t(v[i]));
-            f[2 * i + 1] = bf16hi(uint32_t(v[i]));
-          }
-          float amax = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) amax = absmax(amax, f[i]);
-          amax = wave_absmax_xor(amax, 1);
-          amax = wave_absmax_xor(amax, 2);
-          amax = wave_absmax_xor(amax, 4);
-          amax = wave_absmax_xor(amax, 8);
+          const float amax = row16_absmax(bf16x8_absmax(hv[p][j]));
           const ActScale sc = act_scale(amax, AP2);
+          float f[8];
+          bf16x8_unpack(hv[p][j], f);
+          const uint2 qv = quant8(f, sc, AP2, quant_fast(amax, AP2));
           if (row < T && c < nch) {
-            const uint32_t lo = pack_fp8x4(quant_div(f[0], sc, AP2), quant_div(f[1], sc, AP2),
-                                           quant_div(f[2], sc, AP2), quant_div(f[3], sc, AP2));
-            const uint32_t hi = pack_fp8x4(quant_div(f[4], sc, AP2), quant_div(f[5], sc, AP2),
-                                           quant_div(f[6], sc, AP2), quant_div(f[7], sc, AP2));
-            *reinterpret_cast<uint2*>(&IL.xq[row][col]) = make_uint2(lo, hi);
+            *reinterpret_cast<uint2*>(&IL.xq[row][col]) = qv;
             if ((tid & 15) == 0) IL.xs[row][col / 128] = sc.s;
           }
         }
