@@ -62,6 +62,7 @@ constexpr int kGvMaxM = 32;
 static bool gemv_shape_ok(int64_t K) { return K == 1024 || K == 2048 || K == 4096 || K == 8192; }
 
 static bool gemv_serves(bool qa, int64_t M, int64_t N, int64_t K);
+static bool gemv_wt_serves(bool norm, int64_t M, int64_t N, int64_t K);
 static int gemv_nkb(int64_t K);
 
 // K-blocks per slice of the summation order every FP8 linear path shares (the
@@ -512,8 +513,9 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
   }
 }
 
-// Wave-tile GEMV, K = 128 KB (compile time), M <= 16: one 16-column tile per
-// WAVE over the whole K, W tiles per workgroup.  The workgroup quantises the
+// Wave-tile GEMV, K = 128 KB (compile time), M <= 16 RT: one 16-column tile per
+// WAVE over the whole K, W tiles per workgroup (RT row tiles of 16: each
+// weight K-block feeds RT MFMAs; the norm path serves one).  The workgroup quantises the
 // x rows into LDS once for its W tiles, exactly as fp8_gemv1_kernel does (the
 // dense bf16 passes, or with NORM the RMSNorm of x (+ b) in
 // rmsnorm_quant_kernel's thread mapping), and no partial crosses waves: a wave
@@ -524,8 +526,8 @@ __global__ __launch_bounds__(W * 64) void fp8_gemv1_kernel(const void* __restric
 // 1024: 16 KB) the split kernels spend a prologue and a cross-wave sum with a
 // barrier on every tile; here one prologue serves W tiles and the steady state
 // has no barrier.
-template <int W, int KB, int SL, int XP, bool AP2, bool BP2, bool NORM>
-__global__ __launch_bounds__(W * 64, 3) void fp8_gemv_wt_kernel(const void* __restrict__ x,
+template <int W, int KB, int SL, int XP, bool AP2, bool BP2, bool NORM, int RT>
+__global__ __launch_bounds__(W * 64, RT > 1 ? 2 : 3) void fp8_gemv_wt_kernel(const void* __restrict__ x,
                                                              const uint8_t* __restrict__ wp,
                                                              const void* __restrict__ w_s,
                                                              const uint16_t* __restrict__ res,
@@ -534,6 +536,7 @@ __global__ __launch_bounds__(W * 64, 3) void fp8_gemv_wt_kernel(const void* __re
                                                              float eps, const uint16_t* __restrict__ xb,
                                                              uint16_t* __restrict__ hsum) {
   static_assert(KB % SL == 0, "the slices cover K");
+  static_assert(!(NORM && RT > 1), "the norm path serves up to 16 rows");
   constexpr int K = KB * 128, ldk = K + 16;
   // the norm's thread mapping: NWR waves (64 NWR threads) per row, thread t
   // holding the 8-element chunks t + 256 j (GvNorm's, with W NKB = KB)
@@ -673,38 +676,47 @@ __global__ __launch_bounds__(W * 64, 3) void fp8_gemv_wt_kernel(const void* __re
   __syncthreads();
 
   // ---- the tile: K slices from zero, folded in K order ----
-  v4f tot = {0.f, 0.f, 0.f, 0.f};
-  const int r = nl;
+  v4f tot[RT];
 #pragma unroll
   for (int s = 0; s < KB / SL; ++s) {
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    v4f acc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < SL; ++q) {
       const int kb = s * SL + q;
-      AOp a = a_zero();
-      if (r < M) {
-        const uint8_t* pa = xq + r * ldk + kb * 128 + g * 16;
-        const uint4 lo = *reinterpret_cast<const uint4*>(pa), hi = *reinterpret_cast<const uint4*>(pa + 64);
-        a.v = v8i{int(lo.x), int(lo.y), int(lo.z), int(lo.w), int(hi.x), int(hi.y), int(hi.z), int(hi.w)};
-        const int2 s2 = xsc[r * KB + kb];
-        a.se8 = s2.x;
-        a.sf = __int_as_float(s2.y);
-      }
-      mma_step<kFmtFp8, kFmtFp8>(acc, a, w[kb], se[kb], sf[kb], AP2, BP2, lane);
-    }
-    if (s == 0) {
-      tot = acc;
-    } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) tot[i] += acc[i];
+      for (int rt = 0; rt < RT; ++rt) {
+        const int r = rt * 16 + nl;
+        AOp a = a_zero();
+        if (r < M) {
+          const uint8_t* pa = xq + r * ldk + kb * 128 + g * 16;
+          const uint4 lo = *reinterpret_cast<const uint4*>(pa), hi = *reinterpret_cast<const uint4*>(pa + 64);
+          a.v = v8i{int(lo.x), int(lo.y), int(lo.z), int(lo.w), int(hi.x), int(hi.y), int(hi.z), int(hi.w)};
+          const int2 s2 = xsc[r * KB + kb];
+          a.se8 = s2.x;
+          a.sf = __int_as_float(s2.y);
+        }
+        mma_step<kFmtFp8, kFmtFp8>(acc[rt], a, w[kb], se[kb], sf[kb], AP2, BP2, lane);
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      if (s == 0) {
+        tot[rt] = acc[rt];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tot[rt][i] += acc[rt][i];
+      }
     }
   }
   if (item < tiles) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = g * 4 + i;
+    for (int ri = 0; ri < 4 * RT; ++ri) {
+      const int rt = ri >> 2, i = ri & 3;
+      const int row = rt * 16 + g * 4 + i;
       if (row < M) {
-        const float v = tot[i];
+        const float v = tot[rt][i];
         const int col = item * 16 + nl;
         if (col < n_split) {
           const int64_t o = int64_t(row) * n_split + col;
@@ -1014,6 +1026,7 @@ static bool gemv_mt_serves(int64_t M, int64_t N, int64_t K) {
 static bool gemv_serves(bool qa, int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || !gemv_shape_ok(K)) return false;
   if (M <= 16) return true;
+  if (!qa && gemv_wt_serves(false, M, N, K)) return true;
   if (M > kGvMaxM || N / 16 > WZ_GV1_MAX_TILES) return false;
   if (qa) return true;
   int W = 0, XP = 0;
@@ -1081,7 +1094,7 @@ constexpr int kWtNormRows = kWtW / 2 < GvNorm<one_w<WZ_GV1_K1024>(), one_nkb<WZ_
                                 : GvNorm<one_w<WZ_GV1_K1024>(), one_nkb<WZ_GV1_K1024>()>::ROWS;
 
 static bool gemv_wt_serves(bool norm, int64_t M, int64_t N, int64_t K) {
-  return K == 1024 && M >= 1 && M <= (norm ? kWtNormRows : 16) && N / 16 >= WZ_GVWT_MIN_TILES;
+  return K == 1024 && M >= 1 && M <= (norm ? kWtNormRows : 32) && N / 16 >= WZ_GVWT_MIN_TILES;
 }
 
 template <bool NORM>
@@ -1089,29 +1102,42 @@ static int launch_gemv_wt(const void* x, const uint16_t* b, const float* nw, flo
                           const uint8_t* w, const void* w_s, int w_kind, const uint16_t* res, uint16_t* y,
                           uint16_t* y_hi, int64_t n_split, int64_t M, int64_t N, bool pow2, hipStream_t stream) {
   constexpr int W = kWtW, KB = 8, SL = one_nkb<WZ_GV1_K1024>();
-  const dim3 grid(unsigned((N / 16 + W - 1) / W)), block(W * 64);
+  // rows 17..32: two row tiles on eight waves (two per SIMD: the second row
+  // tile's fragments and sums did not fit the registers of three)
+  constexpr int W2 = 8;
+  const int wv = M <= 16 ? W : W2;
+  const dim3 grid(unsigned((N / 16 + wv - 1) / wv)), block(wv * 64);
   const size_t lds = size_t(M) * (1024 + 16) + size_t(M) * KB * 8;
   const bool bp = w_kind == WZ_WSCALE_E8M0;
-  const int xp = M * KB <= 4 * W ? 1 : M * KB <= 8 * W ? 2 : 4;
-#define WZ_WT(XP_, AP, BP)                                                                                     \
-  WZ_LAUNCH("fp8_gemv_wt", stream, (fp8_gemv_wt_kernel<W, KB, SL, XP_, AP, BP, NORM>), grid, block, lds, x, w, w_s, \
-            res, y, y_hi, int(n_split), int(M), int(N), nw, eps, b, hsum)
-#define WZ_WTK(XP_)                                 \
-  do {                                              \
-    if (pow2) {                                     \
-      if (bp) WZ_WT(XP_, true, true);               \
-      else WZ_WT(XP_, true, false);                 \
-    } else {                                        \
-      if (bp) WZ_WT(XP_, false, true);              \
-      else WZ_WT(XP_, false, false);                \
-    }                                               \
+  // passes of four (row, K-block) pairs per wave
+  const int xp = M * KB <= 4 * wv ? 1 : M * KB <= 8 * wv ? 2 : M * KB <= 16 * wv ? 4 : 8;
+  if (M > 32 || (NORM && M > 16) || M * KB > 4 * wv * 8)
+    return set_error(WZ_EINVAL, "fp8 gemv (wave tile): M=%lld outside its rows", (long long)M);
+#define WZ_WT(W_, XP_, AP, BP, RT_)                                                                                \
+  WZ_LAUNCH("fp8_gemv_wt", stream, (fp8_gemv_wt_kernel<W_, KB, SL, XP_, AP, BP, NORM, RT_>), grid, block, lds, x, \
+            w, w_s, res, y, y_hi, int(n_split), int(M), int(N), nw, eps, b, hsum)
+#define WZ_WTK(W_, XP_, RT_)                                 \
+  do {                                                       \
+    if (pow2) {                                              \
+      if (bp) WZ_WT(W_, XP_, true, true, RT_);               \
+      else WZ_WT(W_, XP_, true, false, RT_);                 \
+    } else {                                                 \
+      if (bp) WZ_WT(W_, XP_, false, true, RT_);              \
+      else WZ_WT(W_, XP_, false, false, RT_);                \
+    }                                                        \
   } while (0)
-  if (NORM || xp == 1)
-    WZ_WTK(1);
-  else if (xp == 2)
-    WZ_WTK(2);
-  else
-    WZ_WTK(4);
+  if constexpr (NORM) {
+    WZ_WTK(W, 1, 1);
+  } else {
+    if (M > 16)
+      WZ_WTK(W2, 8, 2);
+    else if (xp == 1)
+      WZ_WTK(W, 1, 1);
+    else if (xp == 2)
+      WZ_WTK(W, 2, 1);
+    else
+      WZ_WTK(W, 4, 1);
+  }
 #undef WZ_WTK
 #undef WZ_WT
   return check_launch("fp8_gemv_wt");
