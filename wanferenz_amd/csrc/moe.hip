@@ -204,6 +204,153 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
   return r;
 }
 
+// The permutation's tables from each expert's pair count c (thread e of the
+// block holds expert e; E <= 1024 = block size): offsets and the active-expert
+// list (offsets, counts), and the M-tile table of the prefill GEMMs (each
+// active expert's pair rows cut into tiles of kPrefillTileRows, in active
+// order).  Returns the expert's first slot.
+__device__ int perm_tables(int c, int E, int32_t* __restrict__ offsets, int32_t* __restrict__ active,
+                           int32_t* __restrict__ act_off, int32_t* __restrict__ act_cnt,
+                           int32_t* __restrict__ n_active, int32_t* __restrict__ mt_u,
+                           int32_t* __restrict__ mt_row0, int32_t* __restrict__ mt_n, int32_t* __restrict__ n_mt,
+                           int mt_cap, int* wsum) {
+  const int tid = threadIdx.x;
+  int total;
+  const int ex = block_excl_scan(c, wsum, total);
+  const int flag = c > 0 ? 1 : 0;
+  int nact;
+  const int u = block_excl_scan(flag, wsum, nact);
+  if (tid < E) {
+    offsets[tid] = ex;
+    if (flag) {
+      active[u] = tid;
+      act_off[u] = ex;
+      act_cnt[u] = c;
+    }
+  }
+  if (tid == 0) {
+    offsets[E] = total;
+    n_active[0] = nact;
+  }
+  const int ntile = flag ? (c + kPrefillTileRows - 1) / kPrefillTileRows : 0;
+  int ntiles;
+  const int mt0 = block_excl_scan(ntile, wsum, ntiles);
+  for (int i = 0; i < ntile && mt0 + i < mt_cap; ++i) {
+    mt_u[mt0 + i] = u;
+    mt_row0[mt0 + i] = ex + i * kPrefillTileRows;
+    mt_n[mt0 + i] = min(kPrefillTileRows, c - i * kPrefillTileRows);
+  }
+  if (tid == 0) n_mt[0] = min(ntiles, mt_cap);
+  return ex;
+}
+
+// Rank of each lane's expert e among the lanes below it with the same expert
+// (a match over e's nbits bits by ballots), and whether the lane is the lowest
+// with it; with the invalid lanes as one group of their own.
+__device__ __forceinline__ int wave_match_rank(int e, bool valid, int nbits, bool& leader,
+                                               unsigned long long& group) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  unsigned long long mask = __ballot(valid);
+  if (!valid) mask = ~mask;
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool on = (e >> bit) & 1;
+    const unsigned long long m = __ballot(on);
+    mask &= on ? m : ~m;
+  }
+  leader = (mask & lt) == 0ull;
+  group = mask;
+  return __popcll(mask & lt);
+}
+
+// P > 1024 pairs, in two launches (one workgroup walked every pair in turn:
+// 21 us at T = 2048).  perm_count_kernel: workgroup b counts the experts of
+// pairs [1024 b, 1024 (b + 1)) and publishes the counts (agent-scope stores,
+// drained, then the arrival count); the last to arrive sums them per expert in
+// workgroup order, writes the tables (perm_tables) and each workgroup's first
+// slot per expert.  perm_place_kernel: workgroup b places its pairs, a pair's
+// slot its workgroup's first slot for the expert plus the pairs of that
+// expert in the earlier waves and lanes: the pairs of an expert in pair order,
+// perm_kernel's placement.
+__global__ __launch_bounds__(kRouteThreads) void perm_count_kernel(
+    const int32_t* __restrict__ idx, int T, int E, int k, int32_t* __restrict__ cnt, int32_t* __restrict__ base,
+    uint32_t* __restrict__ counter, int32_t* __restrict__ offsets, int32_t* __restrict__ active,
+    int32_t* __restrict__ act_off, int32_t* __restrict__ act_cnt, int32_t* __restrict__ n_active,
+    int32_t* __restrict__ mt_u, int32_t* __restrict__ mt_row0, int32_t* __restrict__ mt_n,
+    int32_t* __restrict__ n_mt, int mt_cap) {
+  constexpr int kMaxBlocks = kMaxPairs / kRouteThreads;
+  __shared__ int hist[kMaxExperts];
+  __shared__ int wsum[128];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, b = blockIdx.x, nb = gridDim.x, P = T * k;
+  for (int e = tid; e < E; e += kRouteThreads) hist[e] = 0;
+  __syncthreads();
+  const int p = b * kRouteThreads + tid;
+  if (p < P) atomicAdd(&hist[clampi(idx[p], 0, E - 1)], 1);
+  __syncthreads();
+  for (int e = tid; e < E; e += kRouteThreads) store_agent_i(cnt + int64_t(b) * E + e, hist[e]);
+  vm_drain();  // this thread's counts are performed before the arrival below
+  __syncthreads();
+  if (tid == 0) s_last = arrive_last(counter, uint32_t(nb)) ? 1 : 0;
+  __syncthreads();
+  if (!s_last) return;
+  int v[kMaxBlocks];
+#pragma unroll
+  for (int bb = 0; bb < kMaxBlocks; ++bb)
+    v[bb] = (tid < E && bb < nb) ? load_agent_i(cnt + int64_t(bb) * E + tid) : 0;
+  int c = 0;
+#pragma unroll
+  for (int bb = 0; bb < kMaxBlocks; ++bb) c += v[bb];
+  const int ex = perm_tables(c, E, offsets, active, act_off, act_cnt, n_active, mt_u, mt_row0, mt_n, n_mt, mt_cap,
+                             wsum);
+  if (tid < E) {
+    int run = ex;
+#pragma unroll
+    for (int bb = 0; bb < kMaxBlocks; ++bb)
+      if (bb < nb) {
+        base[int64_t(bb) * E + tid] = run;
+        run += v[bb];
+      }
+  }
+}
+
+__global__ __launch_bounds__(kRouteThreads) void perm_place_kernel(const int32_t* __restrict__ idx, int T, int E,
+                                                                   int k, const int32_t* __restrict__ base,
+                                                                   int32_t* __restrict__ perm_token,
+                                                                   int32_t* __restrict__ perm_slot,
+                                                                   int32_t* __restrict__ pos) {
+  constexpr int kW = kRouteThreads / 64;
+  __shared__ int wcnt[kW][kMaxExperts];  // pairs of expert e in wave w, then their first slot
+  const int tid = threadIdx.x, wave = tid >> 6, b = blockIdx.x, P = T * k;
+  for (int i = tid; i < kW * kMaxExperts; i += kRouteThreads) (&wcnt[0][0])[i] = 0;
+  const int p = b * kRouteThreads + tid;
+  const bool valid = p < P;
+  const int e = valid ? clampi(idx[p], 0, E - 1) : 0;
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  bool leader;
+  unsigned long long group;
+  const int rank = wave_match_rank(e, valid, nbits, leader, group);
+  __syncthreads();
+  if (valid && leader) wcnt[wave][e] = __popcll(group);
+  __syncthreads();
+  if (tid < E) {
+    int run = base[int64_t(b) * E + tid];
+    for (int w = 0; w < kW; ++w) {
+      const int n = wcnt[w][tid];
+      wcnt[w][tid] = run;
+      run += n;
+    }
+  }
+  __syncthreads();
+  if (valid) {
+    const int q = wcnt[wave][e] + rank;
+    perm_token[q] = p / k;
+    perm_slot[q] = p % k;
+    pos[p] = q;
+  }
+}
+
 __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __restrict__ idx, int T,
                                                              int E, int k, int32_t* __restrict__ offsets,
                                                              int32_t* __restrict__ active,
@@ -230,23 +377,13 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
   for (int p = p0 + lane; p < p1; p += 64) atomicAdd(&wcnt[wave][clampi(idx[p], 0, E - 1)], 1);
   __syncthreads();
   // per expert: its count, then each wave's first slot (expert base + the
-  // pairs of the waves before it); offsets and the active-expert list
-  // (E <= 1024 = block size)
+  // pairs of the waves before it)
   int c = 0;
   if (tid < E)
     for (int w = 0; w < kW; ++w) c += wcnt[w][tid];
-  int total;
-  const int ex = block_excl_scan(c, wsum, total);
-  const int flag = c > 0 ? 1 : 0;
-  int nact;
-  const int u = block_excl_scan(flag, wsum, nact);
+  const int ex = perm_tables(c, E, offsets, active, act_off, act_cnt, n_active, mt_u, mt_row0, mt_n, n_mt, mt_cap,
+                             wsum);
   if (tid < E) {
-    offsets[tid] = ex;
-    if (flag) {
-      active[u] = tid;
-      act_off[u] = ex;
-      act_cnt[u] = c;
-    }
     int run = ex;
     for (int w = 0; w < kW; ++w) {
       const int n = wcnt[w][tid];
@@ -254,40 +391,18 @@ __global__ __launch_bounds__(kRouteThreads) void perm_kernel(const int32_t* __re
       run += n;
     }
   }
-  if (tid == 0) {
-    offsets[E] = total;
-    n_active[0] = nact;
-  }
-  // the M-tile table of the prefill GEMMs: each active expert's pair rows cut
-  // into tiles of kPrefillTileRows, in active order
-  const int ntile = flag ? (c + kPrefillTileRows - 1) / kPrefillTileRows : 0;
-  int ntiles;
-  const int mt0 = block_excl_scan(ntile, wsum, ntiles);
-  for (int i = 0; i < ntile && mt0 + i < mt_cap; ++i) {
-    mt_u[mt0 + i] = u;
-    mt_row0[mt0 + i] = ex + i * kPrefillTileRows;
-    mt_n[mt0 + i] = min(kPrefillTileRows, c - i * kPrefillTileRows);
-  }
-  if (tid == 0) n_mt[0] = min(ntiles, mt_cap);
   __syncthreads();
   // stable placement: a pair's slot is its wave's next slot for its expert
   // plus its rank among the round's lanes with the same expert
   int nbits = 1;
   while ((1 << nbits) < E) ++nbits;
-  const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int c0 = p0; c0 < p1; c0 += 64) {
     const int p = c0 + lane;
     const bool valid = p < p1;
     const int e = valid ? clampi(idx[p], 0, E - 1) : 0;
-    unsigned long long mask = __ballot(valid);
-    if (!valid) mask = ~mask;
-    for (int bit = 0; bit < nbits; ++bit) {
-      const bool on = (e >> bit) & 1;
-      const unsigned long long m = __ballot(on);
-      mask &= on ? m : ~m;
-    }
-    const int rank = __popcll(mask & lt);
-    const bool leader = (mask & lt) == 0ull;
+    bool leader;
+    unsigned long long mask;
+    const int rank = wave_match_rank(e, valid, nbits, leader, mask);
     if (valid) {
       const int q = wcnt[wave][e] + rank;
       perm_token[q] = p / k;
@@ -448,10 +563,26 @@ static int launch_routing(const wz_moe_desc* d, const MoeWs& w, const void* x,
     if (int rc = check_launch("moe topk")) return rc;
   }
   const int64_t P = T * k, mt_cap = P / kPrefillTileRows + (P < E ? P : E) + 1;
-  WZ_LAUNCH("moe_perm", stream, perm_kernel, dim3(1), dim3(kRouteThreads), 0, w.idx, int(T), E, k, w.offsets,
-            w.active, w.act_off, w.act_cnt, w.n_active, w.perm_token, w.perm_slot, w.pos, w.mt_u, w.mt_row0,
-            w.mt_n, w.n_mt, int(mt_cap));
-  return check_launch("moe perm");
+  if (P <= kRouteThreads) {
+    WZ_LAUNCH("moe_perm", stream, perm_kernel, dim3(1), dim3(kRouteThreads), 0, w.idx, int(T), E, k, w.offsets,
+              w.active, w.act_off, w.act_cnt, w.n_active, w.perm_token, w.perm_slot, w.pos, w.mt_u, w.mt_row0,
+              w.mt_n, w.n_mt, int(mt_cap));
+    return check_launch("moe perm");
+  }
+  // the gate scores are spent once the top-k is chosen: their [T, E] floats hold
+  // the per-workgroup counts and first slots ([nb, E] each; P > 1024 makes T >= 64)
+  const int nb = int((P + kRouteThreads - 1) / kRouteThreads);
+  if (int64_t(2) * nb * E > T * E || nb > kMaxPairs / kRouteThreads)
+    return set_error(WZ_EINVAL, "moe perm: %d count blocks do not fit the score buffer (T=%lld)", nb, (long long)T);
+  int32_t* cnt = reinterpret_cast<int32_t*>(w.scores);
+  int32_t* base = cnt + int64_t(nb) * E;
+  WZ_LAUNCH("moe_perm", stream, perm_count_kernel, dim3(unsigned(nb)), dim3(kRouteThreads), 0, w.idx, int(T), E, k,
+            cnt, base, &w.counters[kCounterWords - 1], w.offsets, w.active, w.act_off, w.act_cnt, w.n_active,
+            w.mt_u, w.mt_row0, w.mt_n, w.n_mt, int(mt_cap));
+  if (int rc = check_launch("moe perm count")) return rc;
+  WZ_LAUNCH("moe_perm", stream, perm_place_kernel, dim3(unsigned(nb)), dim3(kRouteThreads), 0, w.idx, int(T), E, k,
+            base, w.perm_token, w.perm_slot, w.pos);
+  return check_launch("moe perm place");
 }
 
 }  // namespace wz

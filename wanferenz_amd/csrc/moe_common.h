@@ -19,7 +19,7 @@ constexpr int kCounterWords = 4096;   // arrival counters at the start of the wo
 // arrival counters sit at offset 0 so wz_moe_workspace_init can zero them
 // without knowing T; every kernel that bumps a counter resets it to zero.
 struct MoeWs {
-  uint32_t* counters;  // [kCounterWords]: [0] route, [1 + d_tile] combine
+  uint32_t* counters;  // [kCounterWords]: [0] route, [1 + d_tile] combine, [kCounterWords - 1] permutation
   float* scores;       // [T, E] gate logits (general path) / scores (decode path)
   float* biased;       // [T, E] decode: scores + bias (the selection key); prefill: sum |x||w| (gate error bound)
   float* weights;      // [T, k]
@@ -232,6 +232,12 @@ __device__ __forceinline__ void store_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent_i(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t load_agent_i(const int32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0); }
