@@ -234,6 +234,56 @@ def test_v4_decode_parity_fp32_act_scales(v4_layer):
     _v4_decode_check(cfg32, w, host, moe32, 3, round_pow2=False)
 
 
+def test_v4_decode_routing_publication_over_many_steps(v4_layer):
+    """The decode routing launch hands the gate scores of its 128 gate
+    workgroups to the last one to arrive through relaxed agent-scope stores, a
+    drained wait and an agent-scope add (moe_common.h).  Over 96 distinct inputs
+    (T = 1, 2, 4, 8; eager calls and replays of one captured graph, the input
+    changed in place between replays, with eager work in between) the routing it
+    exports equals the oracle's gate every time: indices exactly, weights within
+    4 fp32 ulp (a top-k flip is allowed only at a relative key margin below
+    NEAR_TIE)."""
+    cfg, w, host, moe = v4_layer
+    gw = from_bf16_bits(host["gate_w"])
+    flips = 0
+    for T in (1, 2, 4, 8):
+        x = torch.empty(T, cfg.dim, dtype=torch.bfloat16, device="cuda")
+        out = torch.empty_like(x)
+        rw = torch.empty(T, cfg.topk, dtype=torch.float32, device="cuda")
+        ri = torch.empty(T, cfg.topk, dtype=torch.int64, device="cuda")
+        x.copy_(bf16_tensor(synth.normal_bf16(synth.stream_key(4000 + T, synth.S_X), (T, cfg.dim), 1.0), "cuda"))
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                moe.forward(x, out=out, routing_out=(rw, ri))
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            moe.forward(x, out=out, routing_out=(rw, ri))
+        for step in range(24):
+            xb = synth.normal_bf16(synth.stream_key(5000 + 100 * T + step, synth.S_X), (T, cfg.dim), 1.0)
+            x.copy_(bf16_tensor(xb, "cuda"))
+            ri.fill_(-1)
+            if step % 2:
+                graph.replay()
+            else:
+                moe.forward(x, out=out, routing_out=(rw, ri))
+            torch.cuda.synchronize()
+            g = om.gate(from_bf16_bits(xb), gw, host["gate_bias"], cfg.topk, cfg.score_func, cfg.route_scale)
+            got_i, got_w = ri.cpu().numpy(), rw.cpu().numpy()
+            for t in range(T):
+                if not np.array_equal(got_i[t], g.indices[t]):
+                    rel = g.margin[t] / max(abs(g.biased[t]).max(), 1e-30)
+                    assert rel < NEAR_TIE, f"T={T} step {step} token {t}: {got_i[t]} != {g.indices[t]}"
+                    flips += 1
+                    continue
+                wd = np.abs(got_w[t] - g.weights[t])
+                assert (wd <= 4 * np.spacing(np.abs(g.weights[t]).astype(np.float32))).all(), (T, step, t)
+        del graph
+    print(f"96 decode routings checked, near-tie flips {flips}")
+
+
 def test_v4_decode_graph_replay(v4_layer):
     """A captured decode step replays to the eager result, replay after replay."""
     cfg, w, host, moe = v4_layer
