@@ -379,6 +379,28 @@ def test_moe_prefill_oracle_cases(gpu, name):
     print(f"{name}: rel {rel:.2e} cos {cos:.8f} bit-equal {np.mean(got == ref.y):.4f} near-ties {near}")
 
 
+def test_prefill_gate_wide_batch(gpu):
+    """T >= 1024 takes the 32-token x 64-expert MFMA gate (at this width its rolled K
+    loop; 1100 leaves a ragged last token group) and the many-workgroup permutation:
+    every token's routing against the oracle's exact gate, the weights within 4 ulp,
+    and the offsets and permutation tables exact (check_routing), then the forward's
+    exported routing equal to it."""
+    import dataclasses
+    case = dataclasses.replace(CASES["top6_t8"], name="top6_t1100", T=1100)
+    inp = make_inputs(case)
+    moe = upload_case(case, inp, gpu)
+    x = bf16_tensor(inp.x, gpu)
+    g = om.gate(from_bf16_bits(inp.x), from_bf16_bits(inp.gate_w), inp.gate_bias, case.topk, case.score_func,
+                case.route_scale)
+    near = check_routing(moe, x, None, g, case.n_experts)
+    rw = torch.empty(case.T, case.topk, dtype=torch.float32, device=gpu)
+    ri = torch.empty(case.T, case.topk, dtype=torch.int64, device=gpu)
+    moe.forward(x, routing_out=(rw, ri))
+    if not near:
+        assert np.array_equal(ri.cpu().numpy(), g.indices)
+    print(f"{case.name}: routing of {case.T} tokens exact; near-ties {near}")
+
+
 def _torch_oracle_rows(cfg, w, xb, g, dev):
     """Every row of the layer by the torch float32 restatement of the reference CPU
     path (oracle/torch_ref.py: act_quant, dequantised fp4/fp8 GEMMs, clamp-SwiGLU,

@@ -583,10 +583,13 @@ __device__ __forceinline__ void w13_shared_item_lds(const wz_moe_desc& d, const 
   v8i w[2][kQ];
   int se[2][kQ];
   float sf[2][kQ];
+  // The first fetch runs before the K loop, also for a wave whose K range is
+  // empty (KB < kRouteWaves, D < 1024): its K-blocks are clamped into [0, KB)
+  // (kb1 - 1 alone is -1 for wave 0 there, 4 KB before the bank) and never used.
   auto fetch = [&](int kb) {
 #pragma unroll
     for (int q = 0; q < kQ; ++q) {
-      const int kk = min(kb + q, kb1 - 1);
+      const int kk = min(kb + q, max(kb1 - 1, 0));
       w[0][q] = pk_fp8(tiles + int64_t(kk) * 4096, lane);
       w[1][q] = pk_fp8(tiles + int64_t(kk) * 4096 + 2048, lane);
       fp8_wscale(d.sh_w1_s, sbase + kk, wkind, se[0][q], sf[0][q]);
