@@ -1211,8 +1211,10 @@ __global__ __launch_bounds__(kW2Threads) void w2_combine_kernel(wz_moe_desc d, M
 //   first job's scales and its first tile slots.  The image is quantised while
 //   those are in flight; the rest of the first job's tiles follow the barrier.
 //   Loads return in issue order and a CU serves a bounded number at once, so
-//   the chunks queued behind a batch of tiles had waited for the batch (the
-//   image was ready at 10 / 14 us at T = 1 / 4, now at about 2).
+//   the chunks queued behind a batch of tiles had waited for the batch (with
+//   the tiles first the image was ready at 10 / 14 us at T = 1 / 4); in this
+//   order it waits on the h read alone, which the tile stream still slows
+//   (ready at about 7.6 / 9 us).
 constexpr int kW2LdsBytes = 152 * 1024;
 
 // LDS bytes of w2_lds_kernel: A rows, their scales, umap, active ids and
@@ -1250,11 +1252,10 @@ __global__ __launch_bounds__(kW2Threads) void w2_lds_kernel(wz_moe_desc d, MoeWs
   float* sh_s = out_s + P * 16;                             // [16 waves][T][16] shared K-block partials
 
   // Order of requests: the routing tables, the h rows of the image (two passes'
-  // worth), the shared expert's K-block; the first job's tiles only once the
-  // image is in LDS.  Loads complete in issue order and every CU serves a
-  // bounded number of them at once, so a load requested behind a batch of
-  // tiles waits for the batch: with the tiles requested first, the image was
-  // ready at 10 / 14 us (T = 1 / 4) instead of about 2.
+  // worth), the shared expert's K-block, the first job's scales and its first
+  // kPre tile slots; the rest of its tiles once the image is in LDS.  Loads
+  // complete in issue order and every CU serves a bounded number of them at
+  // once, so a load requested behind a batch of tiles waits for the batch.
 
   // Buffer loads: a lane whose offset is past num_records reads zeros and
   // makes no memory request, so every thread issues every load with no lane
