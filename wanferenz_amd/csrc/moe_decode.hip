@@ -114,7 +114,7 @@ __device__ __forceinline__ void route_last(const wz_moe_desc& d, const MoeWs& ws
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr int kSlots = KS;
   // ---- top-k, one wave per token.  The gate waves already wrote each
-  // expert's score and biased score; softmax needs the whole row here.
+  // expert's score (softmax: its logit; the whole row is needed here).
   // (Loops in this single-workgroup phase stay rolled: it runs once per
   // launch, so its code is fetched cold and code size is its latency.) ----
 #pragma unroll 1
@@ -123,12 +123,19 @@ __device__ __forceinline__ void route_last(const wz_moe_desc& d, const MoeWs& ws
     uint32_t key[kSlots];
     float raw[kSlots], rawb[kSlots];
     const bool smax = GEN && d.score_func == WZ_SCORE_SOFTMAX;
+    // the selection key: the score plus the gate bias (a constant input, so
+    // read here beside the scores rather than published with them), the fp32
+    // add the reference's `scores + bias` makes
+    const bool addb = d.score_func != WZ_SCORE_SOFTMAX && d.tid2eid == nullptr && d.gate_bias != nullptr;
+    float bv[kSlots];
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       const int e = lane + 64 * i;
+      bv[i] = (addb && e < E) ? d.gate_bias[e] : 0.0f;
       raw[i] = e < E ? load_agent(ws.scores + int64_t(t) * E + e) : 0.0f;
-      rawb[i] = (e < E && !smax) ? load_agent(ws.biased + int64_t(t) * E + e) : 0.0f;
     }
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) rawb[i] = addb ? raw[i] + bv[i] : raw[i];
     double mx = -1e300, sum = 0.0;
     if (smax) {
 #pragma unroll
@@ -673,14 +680,10 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
     const int task = b * kRouteWaves + wave;
     const int e = task / split, sp = task % split;
     const int nc = D / 8, c0 = (sp * nc) / split, c1 = ((sp + 1) * nc) / split;
-    // the selection-key bias of the (expert, token) this thread finishes below,
-    // requested now: read after the partial sums it was a dependent round trip
-    // (about 1 us) in front of the arrival
+    // the (expert, token) this thread finishes below
     const int epb = kRouteWaves / split;
     const int fin_e = b * epb + tid / max(T, 1);
     const bool fin = tid < epb * T && fin_e < E;
-    const bool biased = d.score_func != WZ_SCORE_SOFTMAX && d.tid2eid == nullptr && d.gate_bias != nullptr;
-    const float fin_bias = (fin && biased) ? d.gate_bias[fin_e] : 0.0f;
     double acc[kDecodeMaxT];
 #pragma unroll
     for (int t = 0; t < kDecodeMaxT; ++t) acc[t] = 0.0;
@@ -795,13 +798,7 @@ __global__ __launch_bounds__(kRouteThreads_) void route_decode_kernel(wz_moe_des
       for (int s2 = 0; s2 < split; ++s2) v += part[es * split + s2][t];
       const int64_t o = int64_t(t) * E + e2;
       const float logit = float(v);
-      if (d.score_func == WZ_SCORE_SOFTMAX) {
-        store_agent(ws.scores + o, logit);
-      } else {
-        const float sc = score_of(logit, d.score_func);
-        store_agent(ws.scores + o, sc);
-        store_agent(ws.biased + o, biased ? sc + fin_bias : sc);
-      }
+      store_agent(ws.scores + o, d.score_func == WZ_SCORE_SOFTMAX ? logit : score_of(logit, d.score_func));
     }
     vm_drain();  // this wave's score stores are performed before the arrival below
     __syncthreads();
